@@ -1,0 +1,300 @@
+/*
+ * libdcn — MI355X (gfx950) modulated deformable convolution (DCNv2) behind a C ABI.
+ *
+ * This header is the drop-in boundary for the deformable-convolution operator of
+ * ken8303/jasnaMacOS. The reference's surface is Swift-internal; each declaration
+ * below names the reference item (file:line under Sources/JasnaMetalPoC/ unless
+ * stated) that it replaces. A SwiftPM C module target can wrap this header as is
+ * (module.modulemap: `module CDCN { header "dcn.h" link "dcn" export * }`).
+ *
+ * Conventions
+ *  - Plain pointers and element counts. Host-pointer entry points validate every
+ *    count against the shape and report name/expected/actual through
+ *    dcn_last_error(), as DeformConvCPU.require does (DeformConv.swift:140-144).
+ *  - FP16 data is passed as IEEE binary16 bit patterns (uint16_t).
+ *  - Tensors are NCHW, as in the reference: input [B][Cin][H][W],
+ *    offset [B][2*G*Kh*Kw][Ho][Wo] with channel 2*(g*Kh*Kw+k) = dy and +1 = dx,
+ *    mask [B][G*Kh*Kw][Ho][Wo], weight OIHW [Cout][Cin/groups][Kh][Kw],
+ *    output [B][Cout][Ho][Wo] (DeformConv.swift:110-132).
+ *  - One context per host thread; a context is not internally locked. Host-pointer
+ *    calls synchronise before returning. *_dev calls are asynchronous on the stream
+ *    given and never allocate once dcn_reserve() has sized the context's workspace,
+ *    so they can be captured into a hipGraph.
+ *  - The caller owns every buffer it passes. Packed weights are owned by their
+ *    handle (dcn_packed_free).
+ */
+#ifndef DCN_DCN_H
+#define DCN_DCN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DCN_ABI_VERSION 1
+
+/* Error taxonomy. Replaces DeformConvError (DeformConv.swift:44-73):
+ * invalidShape, invalidArrayCount, metalUnavailable, shaderResourceMissing,
+ * nonFiniteOutput, commandFailed. DCN_INVALID_ARGUMENT has no Swift counterpart:
+ * it reports a null pointer or a null context, which Swift arrays cannot be. */
+typedef enum dcn_status {
+    DCN_OK = 0,
+    DCN_INVALID_SHAPE = 1,
+    DCN_INVALID_ARRAY_COUNT = 2,
+    DCN_DEVICE_UNAVAILABLE = 3,
+    DCN_KERNEL_MISSING = 4,
+    DCN_NONFINITE_OUTPUT = 5,
+    DCN_COMMAND_FAILED = 6,
+    DCN_INVALID_ARGUMENT = 7
+} dcn_status;
+
+/* 1 only for DCN_NONFINITE_OUTPUT (isRecoverableNumericalFailure, DeformConv.swift:52-55). */
+int dcn_status_is_recoverable(dcn_status status);
+/* Static description of a status (DeformConvError.description, DeformConv.swift:57-72). */
+const char* dcn_status_string(dcn_status status);
+int dcn_abi_version(void);
+
+/* DeformConvShape (DeformConv.swift:3-20), same field order. Output H/W are given,
+ * not derived, as in the reference. */
+typedef struct dcn_shape {
+    int32_t batch;
+    int32_t input_channels;
+    int32_t input_height;
+    int32_t input_width;
+    int32_t output_channels;
+    int32_t output_height;
+    int32_t output_width;
+    int32_t kernel_height;
+    int32_t kernel_width;
+    int32_t pad_height;
+    int32_t pad_width;
+    int32_t stride_height;
+    int32_t stride_width;
+    int32_t dilation_height;
+    int32_t dilation_width;
+    int32_t groups;
+    int32_t offset_groups;
+} dcn_shape;
+
+/* Derived element counts (DeformConv.swift:22-27). */
+typedef struct dcn_counts {
+    size_t input;
+    size_t output;
+    size_t kernel_area;
+    size_t offset;
+    size_t mask;
+    size_t weight;
+    size_t bias;
+} dcn_counts;
+
+/* DeformConvShape.validate (DeformConv.swift:29-41): positive sizes, groups and
+ * offset groups; Cin % groups == 0, Cout % groups == 0, Cin % offsetGroups == 0.
+ * Returns DCN_INVALID_SHAPE otherwise. */
+dcn_status dcn_shape_validate(const dcn_shape* shape);
+dcn_status dcn_shape_counts(const dcn_shape* shape, dcn_counts* counts);
+/* 1 if the fused FP16 sampler+MFMA path serves this shape: groups == 1,
+ * (Cin/offsetGroups) % 8 == 0, Cout % 32 == 0 and Cout <= 128. The prepacked
+ * entry points return DCN_INVALID_SHAPE otherwise, as executeJasnaSIMDGroupGEMM
+ * does for shapes its kernels do not cover (MetalRunner.swift:696-710). */
+int dcn_shape_fused_supported(const dcn_shape* shape);
+
+/* ---- context: MetalDeformConv.init (MetalRunner.swift:107-144) ---------------- */
+typedef struct dcn_context dcn_context;
+dcn_status dcn_create(dcn_context** out, int device);
+void dcn_destroy(dcn_context* ctx);
+/* Detail of the last failure on this context ("offset has 3 elements; expected 4"). */
+const char* dcn_last_error(const dcn_context* ctx);
+/* Size the context's device workspace for `shape` so later *_dev calls do not
+ * allocate (call before hipGraph capture). */
+dcn_status dcn_reserve(dcn_context* ctx, const dcn_shape* shape);
+
+/* ---- host-pointer entry points (copy in, run, copy out, synchronise) ------------ */
+
+/* FP32 DCNv2. MetalDeformConv.runFloat32 (MetalRunner.swift:159-185) over
+ * deform_conv2d_fp32 (MetalShader.swift:76-124). Same summation order as
+ * DeformConvCPU.run (DeformConv.swift:98-135) with contraction off, so results
+ * are bit-identical to that oracle. Any valid shape. */
+dcn_status dcn_forward_f32(dcn_context* ctx, const dcn_shape* shape,
+                           const float* input, size_t input_count,
+                           const float* offset, size_t offset_count,
+                           const float* mask, size_t mask_count,
+                           const float* weight, size_t weight_count,
+                           const float* bias, size_t bias_count,
+                           float* output, size_t output_count);
+
+/* FP16 storage, FP32 accumulation in the oracle's order, half(sum) output:
+ * deform_conv2d_fp16 (MetalShader.swift:126-174) as dispatched by
+ * benchmarkJasnaShape's baseline (MetalRunner.swift:277-283). OIHW weights. */
+dcn_status dcn_forward_f16(dcn_context* ctx, const dcn_shape* shape,
+                           const uint16_t* input, size_t input_count,
+                           const uint16_t* offset, size_t offset_count,
+                           const uint16_t* mask, size_t mask_count,
+                           const uint16_t* weight, size_t weight_count,
+                           const uint16_t* bias, size_t bias_count,
+                           uint16_t* output, size_t output_count);
+
+/* ---- one-time weight prepack ---------------------------------------------------- */
+typedef enum dcn_weight_layout {
+    /* [Cout][Cin][Kh][Kw], PyTorch / DeformConvCPU order. */
+    DCN_LAYOUT_OIHW = 0,
+    /* [Cin][Kh*Kw][Cout], the .dcnfp16 / Metal packed order
+     * (tools/export_deform_weights.py:47, MetalRunner.swift:235-243). */
+    DCN_LAYOUT_IC_K_OC = 1
+} dcn_weight_layout;
+
+typedef struct dcn_packed dcn_packed;
+
+/* Pack FP16 weights + bias once into the MFMA B-fragment layout held on the
+ * context's device. Replaces the OIHW -> [ic][k][oc] packing of
+ * benchmarkJasnaShape (MetalRunner.swift:214-243) and the weight-buffer cache
+ * MetalResourceCache.deformConvWeightBuffers (MetalResourceCache.swift:86-106). */
+dcn_status dcn_prepack_f16(dcn_context* ctx, const dcn_shape* shape,
+                           const uint16_t* weight, size_t weight_count,
+                           dcn_weight_layout layout,
+                           const uint16_t* bias, size_t bias_count,
+                           dcn_packed** out);
+/* Same, from device buffers (stream-ordered; the handle is valid once the
+ * stream reaches this point). */
+dcn_status dcn_prepack_f16_dev(dcn_context* ctx, const dcn_shape* shape,
+                               const void* d_weight, dcn_weight_layout layout,
+                               const void* d_bias, void* stream, dcn_packed** out);
+void dcn_packed_free(dcn_packed* packed);
+/* Load a 147,584-byte .dcnfp16 file (FP16 weight [128][9][64] then bias [64])
+ * and prepack it for the 1x128xHxW -> 64, 3x3, 16-group shape.
+ * DeformConvWeightSet.init + makeBuffers (DeformConvWeights.swift:4-36). A file
+ * of another size fails with DCN_COMMAND_FAILED and the byte counts in
+ * dcn_last_error, as the reference does. */
+dcn_status dcn_load_dcnfp16(dcn_context* ctx, const char* path, dcn_packed** out);
+/* Expected .dcnfp16 size in bytes (DeformConvWeightSet.expectedBytes). */
+size_t dcn_dcnfp16_bytes(void);
+
+/* FP16 DCNv2 with prepacked weights: fused bilinear sampler + MFMA GEMM, FP32
+ * accumulation, half(acc + bias) output. Replaces the gather + SIMD-group GEMM pair
+ * executeJasnaSIMDGroupGEMM (MetalRunner.swift:696-761) over
+ * deform_conv2d_fp16_jasna_gather / _simdgroup_gemm_fused (MetalShader.swift:299-452).
+ * The im2col tile never reaches HBM. */
+dcn_status dcn_forward_f16_prepacked(dcn_context* ctx, const dcn_shape* shape,
+                                     const uint16_t* input, size_t input_count,
+                                     const uint16_t* offset, size_t offset_count,
+                                     const uint16_t* mask, size_t mask_count,
+                                     const dcn_packed* packed,
+                                     uint16_t* output, size_t output_count);
+
+/* ---- device-pointer, stream-ordered entry points (hipGraph capturable) -------- */
+/* `stream` is a hipStream_t (NULL = the default stream). Device pointers must
+ * hold the element counts dcn_shape_counts reports. */
+dcn_status dcn_forward_f32_dev(dcn_context* ctx, const dcn_shape* shape,
+                               const void* d_input, const void* d_offset, const void* d_mask,
+                               const void* d_weight, const void* d_bias, void* d_output,
+                               void* stream);
+dcn_status dcn_forward_f16_dev(dcn_context* ctx, const dcn_shape* shape,
+                               const void* d_input, const void* d_offset, const void* d_mask,
+                               const void* d_weight, const void* d_bias, void* d_output,
+                               void* stream);
+/* NCHW FP16 input; the context's workspace receives the padded channel-block copy. */
+dcn_status dcn_forward_f16_prepacked_dev(dcn_context* ctx, const dcn_shape* shape,
+                                         const void* d_input, const void* d_offset,
+                                         const void* d_mask, const dcn_packed* packed,
+                                         void* d_output, void* stream);
+
+/* The padded channel-block input layout the fused sampler reads:
+ * [B][Cin/8][H+2*DCN_CB8_PAD][W+2*DCN_CB8_PAD][8] FP16 with a zero border.
+ * Producers that can write it directly (the propagation body does) skip the
+ * NCHW repack. dcn_cb8_count gives its element count. */
+#define DCN_CB8_PAD 2
+size_t dcn_cb8_count(const dcn_shape* shape);
+/* Repack NCHW FP16 -> padded channel-block layout; writes interior and border. */
+dcn_status dcn_pack_input_cb8_dev(dcn_context* ctx, const dcn_shape* shape,
+                                  const void* d_input_nchw, void* d_cb8, void* stream);
+dcn_status dcn_forward_f16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape* shape,
+                                             const void* d_cb8, const void* d_offset,
+                                             const void* d_mask, const dcn_packed* packed,
+                                             void* d_output, void* stream);
+
+/* Fused-kernel tuning. sampler: 0 = reference arithmetic (FP32 bilinear in the
+ * reference's association, half(sampled*mask): the im2col values of
+ * deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into the
+ * bilinear weights, packed-FP16 blend). mt = 32-pixel row blocks per wave (1, 2),
+ * ks = waves splitting K (2, 4, 8). 0 / -1 = automatic choice. No counterpart in the
+ * reference (its tile size is the compile-time fusedGEMMRowsPerTile,
+ * MetalShader.swift:2). */
+dcn_status dcn_set_fused_config(dcn_context* ctx, int mt, int ks, int sampler);
+/* The configuration the next fused call on `shape` would use. */
+dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* mt, int* ks,
+                                int* sampler);
+
+/* Sampler alone: the modulated FP16 im2col matrix [B*Ho*Wo][Cin*Kh*Kw] with
+ * column ic*Kh*Kw + k and value half(bilinear * mask), exactly
+ * deform_conv2d_fp16_jasna_gather (MetalShader.swift:299-381) generalised to any
+ * offset-group count. Used for sampler parity and phase timing; the fused path
+ * never materialises it. */
+dcn_status dcn_im2col_f16_dev(dcn_context* ctx, const dcn_shape* shape,
+                              const void* d_input, const void* d_offset, const void* d_mask,
+                              void* d_columns, void* stream);
+
+/* Non-finite flag: *d_flag (uint32) is set to 1 if any of `count` FP16 values is
+ * NaN or Inf; it is never cleared here (flag_non_finite_fp16,
+ * MetalShader.swift:454-463). */
+dcn_status dcn_flag_nonfinite_f16_dev(dcn_context* ctx, const void* d_values, size_t count,
+                                      void* d_flag, void* stream);
+/* Host wrapper: clears a flag, runs the check, synchronises; DCN_NONFINITE_OUTPUT if
+ * set (FusedFourPassRecurrenceProbe.swift:714-743). */
+dcn_status dcn_check_nonfinite_f16_dev(dcn_context* ctx, const void* d_values, size_t count,
+                                       void* stream);
+
+/* ---- deterministic inputs, checksum, statistics (host only) -------------------- */
+
+/* SeededGenerator (DeformConv.swift:168-181): SplitMix64, seed 0 -> 0x9E3779B97F4A7C15. */
+uint64_t dcn_splitmix64_seed(uint64_t seed);
+uint64_t dcn_splitmix64_next(uint64_t* state);
+/* SeededGenerator.floats(count:range:) (DeformConv.swift:183-185): Swift's
+ * Float.random(in: lo...hi, using:) per element, in order. */
+void dcn_seeded_floats(uint64_t* state, size_t count, float lo, float hi, float* out);
+
+/* BASELINE configurations: 1 = FP32 1x128x64x64->64, 2 = same in FP16,
+ * 3 = 16 tiles batched FP16, 5 = 1x128x180x320 FP16. (4, the propagation body,
+ * has its own entry points.) */
+dcn_status dcn_config_shape(int config, dcn_shape* out);
+/* Fill FP32 arrays for `config` from `seed` (x ~ N(0,1); weight He-uniform bound
+ * sqrt(6/fan_in); bias U(-0.1,0.1); offsets 10*tanh(N(0,s)) + smooth flow; mask
+ * sigmoid(N(0,1)), with exact 0/1 sites for config 5). */
+dcn_status dcn_generate_config_inputs(int config, uint64_t seed,
+                                      float* input, size_t input_count,
+                                      float* offset, size_t offset_count,
+                                      float* mask, size_t mask_count,
+                                      float* weight, size_t weight_count,
+                                      float* bias, size_t bias_count);
+
+/* IEEE binary16 round-to-nearest-even conversions (Swift Float16(Float)). */
+uint16_t dcn_f32_to_f16(float value);
+float dcn_f16_to_f32(uint16_t bits);
+void dcn_f32_to_f16_array(const float* in, uint16_t* out, size_t count);
+void dcn_f16_to_f32_array(const uint16_t* in, float* out, size_t count);
+
+/* Benchmark checksum: sum in double of values at indices 0, 257, 514, ...
+ * (MetalRunner.swift:332-337; JasnaCLI.swift:1413-1420 for raw .dcnfp16 bytes). */
+double dcn_checksum_f32(const float* values, size_t count);
+double dcn_checksum_f16(const uint16_t* values, size_t count);
+
+/* BenchmarkStatistics (BenchmarkStatistics.swift:3-44): min, max, median, mean,
+ * population stddev, P10, P90 by linear interpolation. Empty or non-finite
+ * input -> DCN_INVALID_ARGUMENT (the Swift init returns nil). */
+typedef struct dcn_statistics {
+    double minimum;
+    double maximum;
+    double median;
+    double mean;
+    double standard_deviation;
+    double percentile10;
+    double percentile90;
+    size_t count;
+} dcn_statistics;
+dcn_status dcn_compute_statistics(const double* samples, size_t count, dcn_statistics* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DCN_DCN_H */

@@ -1,0 +1,129 @@
+"""ctypes binding of libdcn (include/dcn/dcn.h).
+
+The library is built in-tree by jasnamacos_amd.build into jasnamacos_amd/lib/libdcn.so.
+Loading fails loudly when it is missing: there is no CPU fallback behind this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libdcn.so"
+
+c_size = C.c_size_t
+c_u16p = C.POINTER(C.c_uint16)
+c_f32p = C.POINTER(C.c_float)
+c_f64p = C.POINTER(C.c_double)
+c_u64p = C.POINTER(C.c_uint64)
+c_void = C.c_void_p
+
+
+class DcnShape(C.Structure):
+    """dcn_shape: the 17 DeformConvShape fields (DeformConv.swift:3-20)."""
+
+    _fields_ = [
+        (name, C.c_int32)
+        for name in (
+            "batch", "input_channels", "input_height", "input_width",
+            "output_channels", "output_height", "output_width",
+            "kernel_height", "kernel_width", "pad_height", "pad_width",
+            "stride_height", "stride_width", "dilation_height", "dilation_width",
+            "groups", "offset_groups",
+        )
+    ]
+
+
+class DcnCounts(C.Structure):
+    _fields_ = [(n, c_size) for n in ("input", "output", "kernel_area", "offset", "mask", "weight", "bias")]
+
+
+class DcnStatistics(C.Structure):
+    _fields_ = [
+        ("minimum", C.c_double), ("maximum", C.c_double), ("median", C.c_double),
+        ("mean", C.c_double), ("standard_deviation", C.c_double),
+        ("percentile10", C.c_double), ("percentile90", C.c_double), ("count", c_size),
+    ]
+
+
+ShapeP = C.POINTER(DcnShape)
+CtxP = c_void
+PackedP = c_void
+
+# name -> (restype, argtypes). Every symbol declared in include/dcn/dcn.h.
+SIGNATURES: dict[str, tuple] = {
+    "dcn_abi_version": (C.c_int, []),
+    "dcn_status_is_recoverable": (C.c_int, [C.c_int]),
+    "dcn_status_string": (C.c_char_p, [C.c_int]),
+    "dcn_shape_validate": (C.c_int, [ShapeP]),
+    "dcn_shape_counts": (C.c_int, [ShapeP, C.POINTER(DcnCounts)]),
+    "dcn_shape_fused_supported": (C.c_int, [ShapeP]),
+    "dcn_create": (C.c_int, [C.POINTER(CtxP), C.c_int]),
+    "dcn_destroy": (None, [CtxP]),
+    "dcn_last_error": (C.c_char_p, [CtxP]),
+    "dcn_reserve": (C.c_int, [CtxP, ShapeP]),
+    "dcn_forward_f32": (C.c_int, [CtxP, ShapeP, c_f32p, c_size, c_f32p, c_size, c_f32p, c_size,
+                                  c_f32p, c_size, c_f32p, c_size, c_f32p, c_size]),
+    "dcn_forward_f16": (C.c_int, [CtxP, ShapeP, c_u16p, c_size, c_u16p, c_size, c_u16p, c_size,
+                                  c_u16p, c_size, c_u16p, c_size, c_u16p, c_size]),
+    "dcn_prepack_f16": (C.c_int, [CtxP, ShapeP, c_u16p, c_size, C.c_int, c_u16p, c_size,
+                                  C.POINTER(PackedP)]),
+    "dcn_prepack_f16_dev": (C.c_int, [CtxP, ShapeP, c_void, C.c_int, c_void, c_void,
+                                      C.POINTER(PackedP)]),
+    "dcn_packed_free": (None, [PackedP]),
+    "dcn_load_dcnfp16": (C.c_int, [CtxP, C.c_char_p, C.POINTER(PackedP)]),
+    "dcn_dcnfp16_bytes": (c_size, []),
+    "dcn_forward_f16_prepacked": (C.c_int, [CtxP, ShapeP, c_u16p, c_size, c_u16p, c_size,
+                                            c_u16p, c_size, PackedP, c_u16p, c_size]),
+    "dcn_forward_f32_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void, c_void, c_void,
+                                      c_void, c_void]),
+    "dcn_forward_f16_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void, c_void, c_void,
+                                      c_void, c_void]),
+    "dcn_forward_f16_prepacked_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void, PackedP,
+                                                c_void, c_void]),
+    "dcn_cb8_count": (c_size, [ShapeP]),
+    "dcn_pack_input_cb8_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void]),
+    "dcn_forward_f16_prepacked_cb8_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void,
+                                                    PackedP, c_void, c_void]),
+    "dcn_set_fused_config": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int]),
+    "dcn_get_fused_config": (C.c_int, [CtxP, ShapeP, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                       C.POINTER(C.c_int)]),
+    "dcn_im2col_f16_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void, c_void, c_void]),
+    "dcn_flag_nonfinite_f16_dev": (C.c_int, [CtxP, c_void, c_size, c_void, c_void]),
+    "dcn_check_nonfinite_f16_dev": (C.c_int, [CtxP, c_void, c_size, c_void]),
+    "dcn_splitmix64_seed": (C.c_uint64, [C.c_uint64]),
+    "dcn_splitmix64_next": (C.c_uint64, [c_u64p]),
+    "dcn_seeded_floats": (None, [c_u64p, c_size, C.c_float, C.c_float, c_f32p]),
+    "dcn_config_shape": (C.c_int, [C.c_int, ShapeP]),
+    "dcn_generate_config_inputs": (C.c_int, [C.c_int, C.c_uint64, c_f32p, c_size, c_f32p, c_size,
+                                             c_f32p, c_size, c_f32p, c_size, c_f32p, c_size]),
+    "dcn_f32_to_f16": (C.c_uint16, [C.c_float]),
+    "dcn_f16_to_f32": (C.c_float, [C.c_uint16]),
+    "dcn_f32_to_f16_array": (None, [c_f32p, c_u16p, c_size]),
+    "dcn_f16_to_f32_array": (None, [c_u16p, c_f32p, c_size]),
+    "dcn_checksum_f32": (C.c_double, [c_f32p, c_size]),
+    "dcn_checksum_f16": (C.c_double, [c_u16p, c_size]),
+    "dcn_compute_statistics": (C.c_int, [c_f64p, c_size, C.POINTER(DcnStatistics)]),
+}
+
+_LIB: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+    """Load libdcn.so once; raise ImportError if it has not been built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = Path(os.environ.get("DCN_LIBRARY", LIB_PATH))
+    if not path.exists():
+        raise ImportError(
+            f"libdcn.so not found at {path}; build it with `python -m jasnamacos_amd.build` "
+            "(there is no CPU fallback)"
+        )
+    lib = C.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib

@@ -1,0 +1,107 @@
+// Internal declarations shared by the C-ABI host layer and the HIP kernel files.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "dcn/dcn.h"
+
+namespace dcn {
+
+// Shape as seen by device code: the 17 reference fields, by value.
+struct KShape {
+    int32_t B, Cin, H, W, Cout, Ho, Wo, KH, KW, ph, pw, sh, sw, dh, dw, groups, og;
+};
+
+inline KShape to_kshape(const dcn_shape& s) {
+    return KShape{s.batch,         s.input_channels,  s.input_height,    s.input_width,
+                  s.output_channels, s.output_height, s.output_width,    s.kernel_height,
+                  s.kernel_width,  s.pad_height,      s.pad_width,       s.stride_height,
+                  s.stride_width,  s.dilation_height, s.dilation_width,  s.groups,
+                  s.offset_groups};
+}
+
+// Geometry of the fused FP16 path for one shape (see dcn_kernels_fused.hip).
+struct FusedGeometry {
+    int cblk;     // Cin / 8: number of 8-channel blocks (padded planes)
+    int cb;       // 8-channel blocks per offset group
+    int ka;       // Kh * Kw
+    int kb;       // K-blocks of 8 = G * KA * CB
+    int ksteps;   // MFMA K-steps of 16 = ceil(kb / 2)
+    int nb;       // N-blocks of 32 output channels
+    int hp, wp;   // padded input height / width
+    long long m;  // output pixels B * Ho * Wo
+};
+bool fused_geometry(const dcn_shape& s, FusedGeometry* g);
+
+// Sampler arithmetic of the fused kernel.
+enum SamplerMode : int {
+    // The reference's gather arithmetic, FP32, same association, then half(s * mask):
+    // bit-identical im2col values to deform_conv2d_fp16_jasna_gather.
+    kSamplerExact = 0,
+    // Mask folded into the four bilinear weights, packed-FP16 blend. Faster; within
+    // the FP16 tolerance against the FP32 oracle.
+    kSamplerFast = 1,
+};
+
+struct FusedConfig {
+    int mt;       // 32-pixel A fragments per wave (1 or 2)
+    int ks;       // waves per workgroup splitting the K range (2, 4 or 8)
+    int sampler;  // SamplerMode
+};
+
+// ---- launchers (return hipSuccess or the launch error) ---------------------------
+hipError_t launch_direct_f32(const KShape& s, const float* in, const float* off,
+                             const float* mask, const float* w, const float* b, float* out,
+                             hipStream_t stream);
+hipError_t launch_direct_f16(const KShape& s, const uint16_t* in, const uint16_t* off,
+                             const uint16_t* mask, const uint16_t* w, const uint16_t* b,
+                             uint16_t* out, hipStream_t stream);
+hipError_t launch_pack_cb8(const KShape& s, const FusedGeometry& g, const uint16_t* in_nchw,
+                           void* cb8, hipStream_t stream);
+hipError_t launch_prepack_weights(const KShape& s, const FusedGeometry& g, const uint16_t* w,
+                                  int layout, const uint16_t* bias, void* packed_w,
+                                  float* packed_b, hipStream_t stream);
+hipError_t launch_fused_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
+                            const void* cb8, const uint16_t* off, const uint16_t* mask,
+                            const void* packed_w, const float* packed_b, uint16_t* out,
+                            hipStream_t stream);
+hipError_t launch_im2col_f16(const KShape& s, const uint16_t* in, const uint16_t* off,
+                             const uint16_t* mask, uint16_t* columns, hipStream_t stream);
+hipError_t launch_flag_nonfinite_f16(const uint16_t* values, size_t count, uint32_t* flag,
+                                     hipStream_t stream);
+
+// Bytes of the prepacked B-fragment buffer for a geometry.
+inline size_t packed_weight_bytes(const FusedGeometry& g) {
+    return (size_t)g.ksteps * g.nb * 64 * 8 * sizeof(uint16_t);
+}
+inline size_t cb8_bytes(const dcn_shape& s, const FusedGeometry& g) {
+    return (size_t)s.batch * g.cblk * g.hp * g.wp * 16;
+}
+
+// Host utilities (dcn_host_util.cpp).
+uint16_t f32_to_f16_bits(float value);
+float f16_bits_to_f32(uint16_t bits);
+
+}  // namespace dcn
+
+// Opaque handle types of the C ABI.
+struct dcn_context {
+    int device = 0;
+    std::string last_error;
+    void* workspace = nullptr;  // padded channel-block input copy
+    size_t workspace_bytes = 0;
+    uint32_t* flag = nullptr;   // device flag for the non-finite check
+    dcn::FusedConfig fused_override{0, 0, -1};
+};
+
+struct dcn_packed {
+    dcn_shape shape{};          // the layer shape the weights were packed for
+    dcn::FusedGeometry geometry{};
+    void* weights = nullptr;    // B fragments, packed_weight_bytes(geometry)
+    float* bias = nullptr;      // Cout floats
+    int device = 0;
+};

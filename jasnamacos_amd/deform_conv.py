@@ -1,0 +1,442 @@
+"""Python mirror of the reference's deform-conv operator surface, over libdcn.
+
+Reference surface (ken8303/jasnaMacOS, Sources/JasnaMetalPoC/):
+  DeformConvShape / validate / counts     DeformConv.swift:3-42
+  DeformConvError, isRecoverable...        DeformConv.swift:44-73
+  SeededGenerator (SplitMix64), floats     DeformConv.swift:168-186
+  MetalDeformConv.init / runFloat32        MetalRunner.swift:107-185
+  benchmarkJasnaShape (inputs, packing)    MetalRunner.swift:187-388
+  DeformConvWeightSet, loadDeformConvWeightSets   DeformConvWeights.swift:4-46
+  BenchmarkStatistics                      BenchmarkStatistics.swift:3-44
+
+Every compute call goes through the HIP library; nothing here computes a convolution.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+
+OK = 0
+INVALID_SHAPE = 1
+INVALID_ARRAY_COUNT = 2
+DEVICE_UNAVAILABLE = 3
+KERNEL_MISSING = 4
+NONFINITE_OUTPUT = 5
+COMMAND_FAILED = 6
+INVALID_ARGUMENT = 7
+
+LAYOUT_OIHW = 0
+LAYOUT_IC_K_OC = 1
+
+SAMPLER_EXACT = 0
+SAMPLER_FAST = 1
+
+DIRECTIONS = ("backward_1", "forward_1", "backward_2", "forward_2")
+
+
+def lib() -> C.CDLL:
+    return _lib.load()
+
+
+class DeformConvError(Exception):
+    """DeformConvError (DeformConv.swift:44-73) carried by a dcn_status."""
+
+    def __init__(self, status: int, message: str = ""):
+        self.status = int(status)
+        self.message = message or lib().dcn_status_string(self.status).decode()
+        super().__init__(f"[{self.status}] {self.message}")
+
+    @property
+    def is_recoverable_numerical_failure(self) -> bool:
+        return bool(lib().dcn_status_is_recoverable(self.status))
+
+
+@dataclasses.dataclass(frozen=True)
+class DeformConvShape:
+    """DeformConvShape (DeformConv.swift:3-20); output H/W are given, not derived."""
+
+    batch: int
+    input_channels: int
+    input_height: int
+    input_width: int
+    output_channels: int
+    output_height: int
+    output_width: int
+    kernel_height: int = 3
+    kernel_width: int = 3
+    pad_height: int = 1
+    pad_width: int = 1
+    stride_height: int = 1
+    stride_width: int = 1
+    dilation_height: int = 1
+    dilation_width: int = 1
+    groups: int = 1
+    offset_groups: int = 1
+
+    def to_c(self) -> _lib.DcnShape:
+        return _lib.DcnShape(*[getattr(self, f.name) for f in dataclasses.fields(self)])
+
+    @classmethod
+    def from_c(cls, s: _lib.DcnShape) -> "DeformConvShape":
+        return cls(*[getattr(s, name) for name, _ in _lib.DcnShape._fields_])
+
+    def validate(self) -> None:
+        st = lib().dcn_shape_validate(C.byref(self.to_c()))
+        if st != OK:
+            raise DeformConvError(st)
+
+    def counts(self) -> dict:
+        c = _lib.DcnCounts()
+        st = lib().dcn_shape_counts(C.byref(self.to_c()), C.byref(c))
+        if st != OK:
+            raise DeformConvError(st)
+        return {name: getattr(c, name) for name, _ in _lib.DcnCounts._fields_}
+
+    @property
+    def input_count(self) -> int:
+        return self.counts()["input"]
+
+    @property
+    def output_count(self) -> int:
+        return self.counts()["output"]
+
+    @property
+    def kernel_area(self) -> int:
+        return self.kernel_height * self.kernel_width
+
+    @property
+    def offset_count(self) -> int:
+        return self.counts()["offset"]
+
+    @property
+    def mask_count(self) -> int:
+        return self.counts()["mask"]
+
+    @property
+    def weight_count(self) -> int:
+        return self.counts()["weight"]
+
+    @property
+    def fused_supported(self) -> bool:
+        return bool(lib().dcn_shape_fused_supported(C.byref(self.to_c())))
+
+    @property
+    def flops(self) -> int:
+        """2 * B * Ho * Wo * Cout * (Cin/groups) * Kh * Kw (GEMM-equivalent)."""
+        return (2 * self.batch * self.output_height * self.output_width * self.output_channels
+                * (self.input_channels // self.groups) * self.kernel_area)
+
+
+JASNA_SHAPE = DeformConvShape(1, 128, 64, 64, 64, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u16(a) -> np.ndarray:
+    a = np.asarray(a)
+    if a.dtype == np.float16:
+        return np.ascontiguousarray(a).view(np.uint16)
+    if a.dtype == np.uint16:
+        return np.ascontiguousarray(a)
+    raise TypeError(f"expected float16 or uint16 array, got {a.dtype}")
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(_lib.c_f32p)
+
+
+def _hp(a: np.ndarray):
+    return a.ctypes.data_as(_lib.c_u16p)
+
+
+def _ptr(t) -> Optional[int]:
+    """Device pointer of a torch tensor (or an int address)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+class PackedWeights:
+    """Handle of weights prepacked into the MFMA B-fragment layout (dcn_packed)."""
+
+    def __init__(self, handle: int, shape: DeformConvShape, direction: str = ""):
+        self.handle = C.c_void_p(handle)
+        self.shape = shape
+        self.direction = direction
+
+    def free(self) -> None:
+        if self.handle:
+            lib().dcn_packed_free(self.handle)
+            self.handle = C.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HipDeformConv:
+    """MetalDeformConv's role on MI355X: one libdcn context on one HIP device."""
+
+    def __init__(self, device: int = 0):
+        self._lib = lib()
+        ctx = C.c_void_p()
+        st = self._lib.dcn_create(C.byref(ctx), int(device))
+        if st != OK:
+            raise DeformConvError(st)
+        self.ctx = ctx
+        self.device = device
+
+    def close(self) -> None:
+        if self.ctx:
+            self._lib.dcn_destroy(self.ctx)
+            self.ctx = C.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def _check(self, st: int) -> None:
+        if st != OK:
+            raise DeformConvError(st, self._lib.dcn_last_error(self.ctx).decode())
+
+    @property
+    def last_error(self) -> str:
+        return self._lib.dcn_last_error(self.ctx).decode()
+
+    # ---- host-pointer entry points -------------------------------------------------
+    def run_float32(self, shape: DeformConvShape, input, offset, mask, weight, bias) -> np.ndarray:
+        """runFloat32 (MetalRunner.swift:159-185): bit-identical to DeformConvCPU.run."""
+        arrs = [_f32(a).ravel() for a in (input, offset, mask, weight, bias)]
+        out = np.empty(shape.output_count, dtype=np.float32)
+        args = []
+        for a in arrs:
+            args += [_fp(a), a.size]
+        self._check(self._lib.dcn_forward_f32(self.ctx, C.byref(shape.to_c()), *args, _fp(out), out.size))
+        return out
+
+    def run_float16(self, shape: DeformConvShape, input, offset, mask, weight, bias) -> np.ndarray:
+        """deform_conv2d_fp16 semantics (MetalShader.swift:126-174); float16 in/out."""
+        arrs = [_u16(a).ravel() for a in (input, offset, mask, weight, bias)]
+        out = np.empty(shape.output_count, dtype=np.uint16)
+        args = []
+        for a in arrs:
+            args += [_hp(a), a.size]
+        self._check(self._lib.dcn_forward_f16(self.ctx, C.byref(shape.to_c()), *args, _hp(out), out.size))
+        return out.view(np.float16)
+
+    def prepack(self, shape: DeformConvShape, weight, bias, layout: int = LAYOUT_OIHW) -> PackedWeights:
+        w = _u16(weight).ravel()
+        b = _u16(bias).ravel()
+        handle = C.c_void_p()
+        self._check(self._lib.dcn_prepack_f16(self.ctx, C.byref(shape.to_c()), _hp(w), w.size, int(layout),
+                                              _hp(b), b.size, C.byref(handle)))
+        return PackedWeights(handle.value, shape)
+
+    def load_dcnfp16(self, path, direction: str = "") -> PackedWeights:
+        """DeformConvWeightSet(direction:url:) + makeBuffers (DeformConvWeights.swift:11-36)."""
+        handle = C.c_void_p()
+        self._check(self._lib.dcn_load_dcnfp16(self.ctx, str(path).encode(), C.byref(handle)))
+        return PackedWeights(handle.value, JASNA_SHAPE, direction)
+
+    def load_weight_sets(self, directory) -> list[PackedWeights]:
+        """loadDeformConvWeightSets (DeformConvWeights.swift:39-46)."""
+        d = Path(directory)
+        return [self.load_dcnfp16(d / f"{name}.dcnfp16", name) for name in DIRECTIONS]
+
+    def run_float16_prepacked(self, shape: DeformConvShape, input, offset, mask,
+                              packed: PackedWeights) -> np.ndarray:
+        """Fused sampler + MFMA GEMM (replaces executeJasnaSIMDGroupGEMM)."""
+        arrs = [_u16(a).ravel() for a in (input, offset, mask)]
+        out = np.empty(shape.output_count, dtype=np.uint16)
+        args = []
+        for a in arrs:
+            args += [_hp(a), a.size]
+        self._check(self._lib.dcn_forward_f16_prepacked(self.ctx, C.byref(shape.to_c()), *args,
+                                                        packed.handle, _hp(out), out.size))
+        return out.view(np.float16)
+
+    # ---- device-pointer entry points (torch tensors as plumbing) ------------------
+    def forward_f32_dev(self, shape, x, off, msk, w, b, out, stream=None) -> None:
+        self._check(self._lib.dcn_forward_f32_dev(self.ctx, C.byref(shape.to_c()), _ptr(x), _ptr(off), _ptr(msk),
+                                                  _ptr(w), _ptr(b), _ptr(out), _stream(stream)))
+
+    def forward_f16_dev(self, shape, x, off, msk, w, b, out, stream=None) -> None:
+        self._check(self._lib.dcn_forward_f16_dev(self.ctx, C.byref(shape.to_c()), _ptr(x), _ptr(off), _ptr(msk),
+                                                  _ptr(w), _ptr(b), _ptr(out), _stream(stream)))
+
+    def prepack_dev(self, shape, w, b, layout: int = LAYOUT_OIHW, stream=None) -> PackedWeights:
+        handle = C.c_void_p()
+        self._check(self._lib.dcn_prepack_f16_dev(self.ctx, C.byref(shape.to_c()), _ptr(w), int(layout), _ptr(b),
+                                                  _stream(stream), C.byref(handle)))
+        return PackedWeights(handle.value, shape)
+
+    def forward_f16_prepacked_dev(self, shape, x, off, msk, packed: PackedWeights, out, stream=None) -> None:
+        self._check(self._lib.dcn_forward_f16_prepacked_dev(self.ctx, C.byref(shape.to_c()), _ptr(x), _ptr(off),
+                                                            _ptr(msk), packed.handle, _ptr(out), _stream(stream)))
+
+    def cb8_count(self, shape) -> int:
+        return int(self._lib.dcn_cb8_count(C.byref(shape.to_c())))
+
+    def pack_input_cb8_dev(self, shape, x, cb8, stream=None) -> None:
+        self._check(self._lib.dcn_pack_input_cb8_dev(self.ctx, C.byref(shape.to_c()), _ptr(x), _ptr(cb8),
+                                                     _stream(stream)))
+
+    def forward_f16_prepacked_cb8_dev(self, shape, cb8, off, msk, packed: PackedWeights, out, stream=None) -> None:
+        self._check(self._lib.dcn_forward_f16_prepacked_cb8_dev(self.ctx, C.byref(shape.to_c()), _ptr(cb8),
+                                                                _ptr(off), _ptr(msk), packed.handle, _ptr(out),
+                                                                _stream(stream)))
+
+    def im2col_f16_dev(self, shape, x, off, msk, columns, stream=None) -> None:
+        self._check(self._lib.dcn_im2col_f16_dev(self.ctx, C.byref(shape.to_c()), _ptr(x), _ptr(off), _ptr(msk),
+                                                 _ptr(columns), _stream(stream)))
+
+    def flag_nonfinite_f16_dev(self, values, count: int, flag, stream=None) -> None:
+        self._check(self._lib.dcn_flag_nonfinite_f16_dev(self.ctx, _ptr(values), int(count), _ptr(flag),
+                                                         _stream(stream)))
+
+    def check_nonfinite_f16_dev(self, values, count: int, stream=None) -> None:
+        """Raises DeformConvError(NONFINITE_OUTPUT) (recoverable) if any value is NaN/Inf."""
+        self._check(self._lib.dcn_check_nonfinite_f16_dev(self.ctx, _ptr(values), int(count), _stream(stream)))
+
+    def reserve(self, shape) -> None:
+        self._check(self._lib.dcn_reserve(self.ctx, C.byref(shape.to_c())))
+
+    def set_fused_config(self, mt: int = 0, ks: int = 0, sampler: int = -1) -> None:
+        self._check(self._lib.dcn_set_fused_config(self.ctx, int(mt), int(ks), int(sampler)))
+
+    def get_fused_config(self, shape) -> tuple[int, int, int]:
+        mt, ks, sm = C.c_int(), C.c_int(), C.c_int()
+        self._check(self._lib.dcn_get_fused_config(self.ctx, C.byref(shape.to_c()), C.byref(mt), C.byref(ks),
+                                                   C.byref(sm)))
+        return mt.value, ks.value, sm.value
+
+
+# ---- deterministic inputs ----------------------------------------------------------
+
+class SeededGenerator:
+    """SeededGenerator (DeformConv.swift:168-186): SplitMix64 + Swift's Float.random(in:)."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(lib().dcn_splitmix64_seed(C.c_uint64(seed)))
+
+    def next(self) -> int:
+        return int(lib().dcn_splitmix64_next(C.byref(self.state)))
+
+    def floats(self, count: int, lo: float, hi: float) -> np.ndarray:
+        out = np.empty(count, dtype=np.float32)
+        lib().dcn_seeded_floats(C.byref(self.state), count, lo, hi, _fp(out))
+        return out
+
+
+def config_shape(config: int) -> DeformConvShape:
+    s = _lib.DcnShape()
+    st = lib().dcn_config_shape(int(config), C.byref(s))
+    if st != OK:
+        raise DeformConvError(st)
+    return DeformConvShape.from_c(s)
+
+
+def generate_config_inputs(config: int, seed: int) -> dict:
+    """FP32 inputs of BASELINE config 1, 2, 3 or 5 (see dcn_generate_config_inputs)."""
+    shape = config_shape(config)
+    c = shape.counts()
+    arrays = {k: np.empty(c[k], dtype=np.float32) for k in ("input", "offset", "mask", "weight", "bias")}
+    args = []
+    for k in ("input", "offset", "mask", "weight", "bias"):
+        args += [_fp(arrays[k]), arrays[k].size]
+    st = lib().dcn_generate_config_inputs(int(config), C.c_uint64(seed), *args)
+    if st != OK:
+        raise DeformConvError(st)
+    arrays["shape"] = shape
+    return arrays
+
+
+def reference_benchmark_inputs(seed: int = 0x4A41534E41) -> dict:
+    """benchmarkJasnaShape's seeded inputs (MetalRunner.swift:210-213, 233-234): input
+    U(-1,1), offset U(-0.25,0.25), mask U(0.25,0.75), weight and bias U(-0.02,0.02),
+    each drawn in that order and rounded to FP16."""
+    shape = JASNA_SHAPE
+    rng = SeededGenerator(seed)
+    out = {
+        "input": rng.floats(shape.input_count, -1.0, 1.0).astype(np.float16),
+        "offset": rng.floats(shape.offset_count, -0.25, 0.25).astype(np.float16),
+        "mask": rng.floats(shape.mask_count, 0.25, 0.75).astype(np.float16),
+        "weight": rng.floats(shape.weight_count, -0.02, 0.02).astype(np.float16),
+        "bias": rng.floats(shape.output_channels, -0.02, 0.02).astype(np.float16),
+        "shape": shape,
+    }
+    return out
+
+
+def pack_ic_k_oc(weight_oihw: np.ndarray, shape: DeformConvShape) -> np.ndarray:
+    """OIHW -> [ic][k][oc] (MetalRunner.swift:235-243; tools/export_deform_weights.py:47)."""
+    w = np.asarray(weight_oihw).reshape(shape.output_channels, shape.input_channels, shape.kernel_area)
+    return np.ascontiguousarray(np.transpose(w, (1, 2, 0)))
+
+
+def checksum(values: np.ndarray) -> float:
+    """Sum in double of values[0::257] (MetalRunner.swift:332-337)."""
+    v = np.asarray(values).ravel()
+    if v.dtype == np.float32:
+        v = np.ascontiguousarray(v)
+        return float(lib().dcn_checksum_f32(_fp(v), v.size))
+    v = _u16(v)
+    return float(lib().dcn_checksum_f16(_hp(v), v.size))
+
+
+@dataclasses.dataclass
+class BenchmarkStatistics:
+    """BenchmarkStatistics (BenchmarkStatistics.swift:3-44)."""
+
+    samples: list
+    minimum: float
+    maximum: float
+    median: float
+    mean: float
+    standard_deviation: float
+    percentile10: float
+    percentile90: float
+
+    @classmethod
+    def of(cls, values) -> Optional["BenchmarkStatistics"]:
+        v = np.ascontiguousarray(values, dtype=np.float64)
+        s = _lib.DcnStatistics()
+        if lib().dcn_compute_statistics(v.ctypes.data_as(_lib.c_f64p), v.size, C.byref(s)) != OK:
+            return None
+        return cls(sorted(v.tolist()), s.minimum, s.maximum, s.median, s.mean,
+                   s.standard_deviation, s.percentile10, s.percentile90)
+
+
+def f32_to_f16(values) -> np.ndarray:
+    v = _f32(values).ravel()
+    out = np.empty(v.size, dtype=np.uint16)
+    lib().dcn_f32_to_f16_array(_fp(v), _hp(out), v.size)
+    return out.view(np.float16).reshape(np.shape(values))

@@ -1,0 +1,468 @@
+"""GPU parity of libdcn against the CPU oracle, through the C ABI.
+
+Bars:
+  * FP32 path and the FP16 direct path: bit-identical to the oracle (the reference
+    asks max relative error 1e-5; identical bits meet it with margin);
+  * sampler (im2col): bit-identical to the reference gather arithmetic;
+  * fused FP16 path: max |err| <= 2e-2 and mean |err| <= 1e-3 against the FP32 oracle
+    run on the same FP16-rounded inputs;
+  * zero padding for out-of-bounds samples exactly preserved.
+"""
+from __future__ import annotations
+
+import dataclasses
+import os
+import sys
+import tempfile
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS_F16 = 2e-2
+MEAN_ABS_F16 = 1e-3
+
+
+def log(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def f16_inputs(d):
+    return {k: np.asarray(d[k], np.float32).astype(np.float16) for k in ("input", "offset", "mask", "weight", "bias")}
+
+
+def widen(h):
+    return {k: v.astype(np.float32) for k, v in h.items()}
+
+
+def errors(got16, ref32):
+    e = np.abs(np.asarray(got16, np.float64) - np.asarray(ref32, np.float64))
+    return float(e.max()), float(e.mean())
+
+
+@pytest.fixture(scope="module")
+def c1(dcn, oracle):
+    d = dcn.generate_config_inputs(1, 1)
+    ref = oracle.forward_f32_threads(d["shape"], d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    return d, ref
+
+
+@pytest.fixture(scope="module")
+def c2(dcn, oracle):
+    d = dcn.generate_config_inputs(2, 2)
+    h = f16_inputs(d)
+    w = widen(h)
+    ref = oracle.forward_f32_threads(d["shape"], w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    return d["shape"], h, ref
+
+
+def rand_case(shape, seed, offset_scale=3.0):
+    rng = np.random.default_rng(seed)
+    c = shape.counts()
+    d = {
+        "input": rng.standard_normal(c["input"]),
+        "offset": rng.uniform(-offset_scale, offset_scale, c["offset"]),
+        "mask": rng.uniform(0, 1, c["mask"]),
+        "weight": rng.uniform(-0.2, 0.2, c["weight"]),
+        "bias": rng.uniform(-0.1, 0.1, c["bias"]),
+    }
+    return {k: v.astype(np.float32) for k, v in d.items()}
+
+
+GENERAL_SHAPES = [
+    # (batch, Cin, H, W, Cout, Ho, Wo, Kh, Kw, ph, pw, sh, sw, dh, dw, groups, offset_groups)
+    (1, 2, 5, 5, 3, 5, 5, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1),      # the reference self-test shape
+    (2, 8, 6, 6, 6, 6, 6, 3, 3, 1, 1, 1, 1, 1, 1, 2, 4),
+    (1, 6, 9, 8, 3, 4, 4, 3, 3, 1, 0, 2, 2, 1, 1, 1, 3),
+    (1, 4, 8, 8, 4, 6, 6, 3, 3, 1, 1, 1, 1, 2, 2, 2, 2),
+    (3, 16, 5, 7, 8, 5, 7, 1, 3, 0, 1, 1, 1, 1, 1, 1, 16),
+]
+
+
+# ---- FP32 ------------------------------------------------------------------------
+
+def test_fp32_bit_exact_c1(gpu_ctx, c1):
+    d, ref = c1
+    log("case: fp32 C1 1x128x64x64 -> 64, 16 dg")
+    out = gpu_ctx.run_float32(d["shape"], d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+def test_fp32_reference_self_test(gpu_ctx, dcn, oracle):
+    # correctnessTest (JasnaCLI.swift:68-110): SeededGenerator(0xC0FFEE), gate max abs < 2e-5.
+    s = dcn.DeformConvShape(*GENERAL_SHAPES[0])
+    rng = dcn.SeededGenerator(0xC0FFEE)
+    inp = rng.floats(s.input_count, -1, 1)
+    off = rng.floats(s.offset_count, -0.4, 0.4)
+    msk = rng.floats(s.mask_count, 0.1, 0.9)
+    w = rng.floats(s.weight_count, -0.2, 0.2)
+    b = rng.floats(s.output_channels, -0.1, 0.1)
+    log("case: fp32 self-test 1x2x5x5 -> 3")
+    out = gpu_ctx.run_float32(s, inp, off, msk, w, b)
+    ref = oracle.forward_f32(s, inp, off, msk, w, b)
+    assert np.abs(out - ref).max() < 2e-5
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("dims", GENERAL_SHAPES[1:], ids=lambda t: "x".join(map(str, t)))
+def test_fp32_general_shapes_bit_exact(gpu_ctx, dcn, oracle, dims):
+    s = dcn.DeformConvShape(*dims)
+    d = rand_case(s, sum(dims))
+    log("case: fp32", dims)
+    out = gpu_ctx.run_float32(s, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    ref = oracle.forward_f32(s, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+# ---- FP16 direct (reference semantics) ---------------------------------------------
+
+def test_fp16_direct_bit_exact_c2(gpu_ctx, c2):
+    s, h, ref = c2
+    log("case: fp16 direct C2")
+    out = gpu_ctx.run_float16(s, h["input"], h["offset"], h["mask"], h["weight"], h["bias"])
+    assert np.array_equal(out.view(np.uint16), ref.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("dims", GENERAL_SHAPES[1:3], ids=lambda t: "x".join(map(str, t)))
+def test_fp16_direct_general_bit_exact(gpu_ctx, dcn, oracle, dims):
+    s = dcn.DeformConvShape(*dims)
+    h = f16_inputs(rand_case(s, 7 + sum(dims)))
+    log("case: fp16 direct", dims)
+    out = gpu_ctx.run_float16(s, h["input"], h["offset"], h["mask"], h["weight"], h["bias"])
+    ref = oracle.forward_f16_direct(s, h["input"], h["offset"], h["mask"], h["weight"], h["bias"])
+    assert np.array_equal(out.view(np.uint16), ref.view(np.uint16))
+
+
+# ---- sampler --------------------------------------------------------------------
+
+def _dev(torch, a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return t.cuda()
+
+
+def test_im2col_bit_exact(gpu_ctx, dcn, oracle, c2):
+    import torch
+
+    s, h, _ = c2
+    log("case: im2col C2")
+    cols_ref = oracle.im2col_f16(s, h["input"], h["offset"], h["mask"])
+    x, o, m = (_dev(torch, h[k].view(np.int16)) for k in ("input", "offset", "mask"))
+    cols = torch.empty(cols_ref.size, dtype=torch.int16, device="cuda")
+    gpu_ctx.im2col_f16_dev(s, x, o, m, cols)
+    torch.cuda.synchronize()
+    assert np.array_equal(cols.cpu().numpy().view(np.uint16), cols_ref.view(np.uint16))
+
+
+# ---- fused FP16 ------------------------------------------------------------------
+
+def test_fused_exact_sampler_matches_gather_gemm(gpu_ctx, dcn, oracle, c2):
+    s, h, ref32 = c2
+    log("case: fused exact sampler C2")
+    cols = oracle.im2col_f16(s, h["input"], h["offset"], h["mask"])
+    ref_gemm = oracle.gemm_f16(s, cols, h["weight"], h["bias"]).astype(np.float64)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(0, 0, dcn.SAMPLER_EXACT)
+    try:
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed).astype(np.float64)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1)
+    # Same FP16 A and B operands; only the FP32 summation order differs (MFMA vs serial),
+    # so the two agree to about one FP16 ulp of the output.
+    diff = np.abs(out - ref_gemm)
+    ulp = np.maximum(np.abs(ref_gemm), 2.0 ** -14) * 2.0 ** -10
+    assert np.all(diff <= 2 * ulp + 1e-6), float((diff / ulp).max())
+    mx, mean = errors(out, ref32)
+    log(f"  exact sampler vs FP32 oracle: max {mx:.3e} mean {mean:.3e}")
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
+def test_fused_fast_c2_tolerance(gpu_ctx, dcn, c2):
+    s, h, ref32 = c2
+    log("case: fused fast C2")
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    mx, mean = errors(out, ref32)
+    log(f"  fast sampler vs FP32 oracle: max {mx:.3e} mean {mean:.3e}")
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
+@pytest.mark.parametrize("mt,ks", [(1, 8), (1, 4), (2, 4), (2, 2)])
+@pytest.mark.parametrize("sampler", [0, 1])
+def test_fused_configs(gpu_ctx, dcn, c2, mt, ks, sampler):
+    s, h, ref32 = c2
+    log("case: fused config", mt, ks, sampler)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(mt, ks, sampler)
+    try:
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+        again = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1)
+    assert np.array_equal(out.view(np.uint16), again.view(np.uint16))  # deterministic
+    mx, mean = errors(out, ref32)
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
+
+
+def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle):
+    d = dcn.generate_config_inputs(3, 3)
+    s = d["shape"]
+    h = f16_inputs(d)
+    log("case: fused C3 16 tiles")
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    tile = dataclasses.replace(s, batch=1)
+    c = tile.counts()
+    for b in (0, 7, 15):  # tiles are independent: check three against the oracle
+        w = widen(h)
+        ref = oracle.forward_f32_threads(tile, w["input"][b * c["input"]:(b + 1) * c["input"]],
+                                         w["offset"][b * c["offset"]:(b + 1) * c["offset"]],
+                                         w["mask"][b * c["mask"]:(b + 1) * c["mask"]], w["weight"], w["bias"])
+        mx, mean = errors(out[b * c["output"]:(b + 1) * c["output"]], ref)
+        log(f"  tile {b}: max {mx:.3e} mean {mean:.3e}")
+        assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
+def test_fused_c5_large_map(gpu_ctx, dcn, oracle):
+    d = dcn.generate_config_inputs(5, 5)
+    s = d["shape"]
+    h = f16_inputs(d)
+    log("case: fused C5 1x128x180x320")
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    w = widen(h)
+    plane = s.output_height * s.output_width
+    oc_end = 4  # a bounded slice of output channels: every pixel, every sample, 4 channels
+    ref = oracle.forward_f32_oc_range(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"], 0, oc_end)
+    mx, mean = errors(out[:oc_end * plane], ref[:oc_end * plane])
+    log(f"  C5 oc 0..3: max {mx:.3e} mean {mean:.3e}")
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+    assert np.all(np.isfinite(out.astype(np.float32)))
+
+
+EDGE_SHAPES = [
+    (1, 128, 7, 9, 64, 7, 9, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16),    # 63 pixels: tile tail
+    (2, 8, 11, 13, 32, 11, 13, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1),   # 9 K-blocks (odd), Cout 32
+    (1, 64, 10, 10, 96, 10, 10, 3, 3, 1, 1, 1, 1, 1, 1, 1, 8),  # Cout 96
+    (1, 32, 9, 12, 128, 9, 12, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2),   # Cout 128, 16 channels per group
+    (1, 16, 17, 15, 64, 8, 7, 3, 3, 1, 1, 2, 2, 1, 1, 1, 2),    # stride 2
+    (1, 16, 12, 12, 32, 10, 10, 3, 3, 1, 1, 1, 1, 2, 2, 1, 1),  # dilation 2
+    (3, 24, 6, 5, 32, 6, 5, 1, 3, 0, 1, 1, 1, 1, 1, 1, 3),      # 1x3 kernel, batch 3
+]
+
+
+@pytest.mark.parametrize("dims", EDGE_SHAPES, ids=lambda t: "x".join(map(str, t)))
+@pytest.mark.parametrize("sampler", [0, 1])
+def test_fused_edge_shapes(gpu_ctx, dcn, oracle, dims, sampler):
+    s = dcn.DeformConvShape(*dims)
+    assert s.fused_supported
+    d = rand_case(s, sum(dims), offset_scale=4.0)
+    d["weight"] *= 0.5
+    h = f16_inputs(d)
+    w = widen(h)
+    log("case: fused edge", dims, "sampler", sampler)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(0, 0, sampler)
+    try:
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1)
+    ref = oracle.forward_f32(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    mx, mean = errors(out, ref)
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
+
+
+def test_zero_padding_exact(gpu_ctx, dcn, c2):
+    s, h, _ = c2
+    log("case: zero padding")
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    bias_out = np.repeat(h["bias"], s.output_height * s.output_width)
+    for far in (1000.0, -1000.0, 66.0, -2.0 - 64.0):
+        off = np.full_like(h["offset"], far)
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], off, h["mask"], packed)
+        assert np.array_equal(out.view(np.uint16), bias_out.view(np.uint16)), far
+        out = gpu_ctx.run_float16(s, h["input"], off, h["mask"], h["weight"], h["bias"])
+        assert np.array_equal(out.view(np.uint16), bias_out.view(np.uint16)), far
+    zero_mask = np.zeros_like(h["mask"])
+    out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], zero_mask, packed)
+    assert np.array_equal(out.view(np.uint16), bias_out.view(np.uint16))
+
+
+def test_samples_straddling_the_border(gpu_ctx, dcn, oracle):
+    # Offsets that put corners exactly on -1, 0, H-1, H and just beyond, per corner.
+    s = dcn.DeformConvShape(1, 16, 6, 7, 32, 6, 7, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)
+    rng = np.random.default_rng(12)
+    d = rand_case(s, 12)
+    choices = np.array([-7.5, -6.0, -5.25, -1.0, -0.5, 0.0, 0.5, 1.0, 5.5, 6.0, 6.75, 7.0], np.float32)
+    d["offset"] = rng.choice(choices, d["offset"].size).astype(np.float32)
+    h = f16_inputs(d)
+    w = widen(h)
+    log("case: border straddle")
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    ref = oracle.forward_f32(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    mx, mean = errors(out, ref)
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+    direct = gpu_ctx.run_float16(s, h["input"], h["offset"], h["mask"], h["weight"], h["bias"])
+    assert np.array_equal(direct.view(np.uint16), ref.astype(np.float16).view(np.uint16))
+
+
+def test_zero_offsets_unit_mask_is_conv2d(gpu_ctx, dcn):
+    import torch
+    import torch.nn.functional as F
+
+    s = dcn.DeformConvShape(1, 128, 20, 24, 64, 20, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    d = rand_case(s, 21)
+    d["weight"] *= 0.1
+    d["offset"][:] = 0
+    d["mask"][:] = 1
+    h = f16_inputs(d)
+    log("case: zero offsets == conv2d")
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    ref = F.conv2d(torch.tensor(h["input"].astype(np.float64)).reshape(1, 128, 20, 24),
+                   torch.tensor(h["weight"].astype(np.float64)).reshape(64, 128, 3, 3),
+                   torch.tensor(h["bias"].astype(np.float64)), padding=1).numpy().ravel()
+    mx, mean = errors(out, ref)
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
+def test_prepack_layouts_and_dcnfp16_file(gpu_ctx, dcn, c2):
+    s, h, _ = c2
+    log("case: prepack layouts + .dcnfp16")
+    p1 = gpu_ctx.prepack(s, h["weight"], h["bias"], dcn.LAYOUT_OIHW)
+    packed_w = dcn.pack_ic_k_oc(h["weight"], s)
+    p2 = gpu_ctx.prepack(s, packed_w, h["bias"], dcn.LAYOUT_IC_K_OC)
+    o1 = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], p1)
+    o2 = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], p2)
+    assert np.array_equal(o1.view(np.uint16), o2.view(np.uint16))
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "forward_1.dcnfp16")
+        payload = packed_w.astype("<f2").tobytes() + h["bias"].astype("<f2").tobytes()
+        assert len(payload) == dcn.lib().dcn_dcnfp16_bytes() == 147584
+        with open(path, "wb") as f:
+            f.write(payload)
+        p3 = gpu_ctx.load_dcnfp16(path, "forward_1")
+        o3 = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], p3)
+        assert np.array_equal(o1.view(np.uint16), o3.view(np.uint16))
+        bad = os.path.join(tmp, "backward_1.dcnfp16")
+        with open(bad, "wb") as f:
+            f.write(payload[:-2])
+        with pytest.raises(dcn.DeformConvError) as e:
+            gpu_ctx.load_dcnfp16(bad)
+        assert e.value.status == dcn.COMMAND_FAILED
+        assert "backward_1.dcnfp16 has 147582 bytes; expected 147584" in e.value.message
+
+
+def test_count_mismatch_reports_name(gpu_ctx, dcn):
+    s = dcn.DeformConvShape(*GENERAL_SHAPES[0])
+    c = s.counts()
+    with pytest.raises(dcn.DeformConvError) as e:
+        gpu_ctx.run_float32(s, np.zeros(c["input"]), np.zeros(c["offset"] - 1), np.zeros(c["mask"]),
+                            np.zeros(c["weight"]), np.zeros(c["bias"]))
+    assert e.value.status == dcn.INVALID_ARRAY_COUNT
+    assert e.value.message == f"offset has {c['offset'] - 1} elements; expected {c['offset']}"
+    big = dataclasses.replace(s, groups=2, input_channels=4, output_channels=4, offset_groups=1)
+    with pytest.raises(dcn.DeformConvError) as e:
+        gpu_ctx.prepack(big, np.zeros(big.weight_count, np.float16), np.zeros(4, np.float16))
+    assert e.value.status == dcn.INVALID_SHAPE
+
+
+def test_nonfinite_flag(gpu_ctx, dcn):
+    import torch
+
+    # MetalNonFiniteFlagTests.swift:50-52
+    def flagged(values):
+        t = torch.tensor(np.array(values, np.float16).view(np.int16)).cuda()
+        flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+        gpu_ctx.flag_nonfinite_f16_dev(t, t.numel(), flag)
+        torch.cuda.synchronize()
+        return int(flag.item())
+
+    log("case: non-finite flag")
+    assert flagged([0, 1, -2, 0.5]) == 0
+    assert flagged([0, np.inf, 1]) == 1
+    assert flagged([0, np.nan, 1]) == 1
+    big = np.zeros(1 << 20, np.float16)
+    big[-1] = np.inf
+    assert flagged(big) == 1
+    t = torch.tensor(big.view(np.int16)).cuda()
+    with pytest.raises(dcn.DeformConvError) as e:
+        gpu_ctx.check_nonfinite_f16_dev(t, t.numel())
+    assert e.value.status == dcn.NONFINITE_OUTPUT and e.value.is_recoverable_numerical_failure
+    gpu_ctx.check_nonfinite_f16_dev(t, t.numel() - 1)  # finite prefix: no error
+
+
+def test_fp16_overflow_is_flagged(gpu_ctx, dcn, c2):
+    import torch
+
+    s, h, _ = c2
+    log("case: fp16 overflow")
+    w = (h["weight"].astype(np.float32) * 7e4).astype(np.float16)
+    packed = gpu_ctx.prepack(s, w, h["bias"])
+    out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    assert not np.all(np.isfinite(out.astype(np.float32)))
+    t = torch.tensor(out.view(np.int16)).cuda()
+    with pytest.raises(dcn.DeformConvError) as e:
+        gpu_ctx.check_nonfinite_f16_dev(t, t.numel())
+    assert e.value.is_recoverable_numerical_failure
+
+
+def test_device_entry_points_and_graph_replay(gpu_ctx, dcn, c2):
+    import torch
+
+    s, h, _ = c2
+    log("case: _dev entry points + hipGraph replay")
+    x, o, m = (torch.tensor(h[k].view(np.int16)).cuda() for k in ("input", "offset", "mask"))
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    host = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
+    gpu_ctx.reserve(s)
+    gpu_ctx.forward_f16_prepacked_dev(s, x, o, m, packed, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), host.view(np.uint16))
+    # CB8 repack equals the padded channel-block transpose of the input.
+    cb8 = torch.empty(gpu_ctx.cb8_count(s), dtype=torch.int16, device="cuda")
+    gpu_ctx.pack_input_cb8_dev(s, x, cb8)
+    torch.cuda.synchronize()
+    X = h["input"].view(np.uint16).reshape(1, 16, 8, 64, 64).transpose(0, 1, 3, 4, 2)
+    ref = np.zeros((1, 16, 68, 68, 8), np.uint16)
+    ref[:, :, 2:66, 2:66] = X
+    assert np.array_equal(cb8.cpu().numpy().view(np.uint16).reshape(ref.shape), ref)
+    out2 = torch.empty_like(out)
+    gpu_ctx.forward_f16_prepacked_cb8_dev(s, cb8, o, m, packed, out2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    # Graph capture of the stream-ordered call, replayed with eager work in between.
+    stream = torch.cuda.Stream()
+    graph_out = torch.zeros_like(out)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        gpu_ctx.forward_f16_prepacked_dev(s, x, o, m, packed, graph_out, stream=torch.cuda.current_stream())
+    scratch = torch.empty_like(out)
+    for i in range(3):
+        graph_out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(graph_out, out), i
+        gpu_ctx.forward_f16_prepacked_dev(s, x, o, m, packed, scratch)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_reference_benchmark_gate(gpu_ctx, dcn):
+    # benchmarkJasnaShape gates (MetalRunner.swift:345-354) on its own seeded inputs:
+    # gather + GEMM vs direct FP16 <= 2e-3.
+    d = dcn.reference_benchmark_inputs()
+    s = d["shape"]
+    log("case: reference benchmark gate")
+    direct = gpu_ctx.run_float16(s, d["input"], d["offset"], d["mask"], d["weight"], d["bias"]).astype(np.float32)
+    packed = gpu_ctx.prepack(s, d["weight"], d["bias"])
+    for sampler in (0, 1):
+        gpu_ctx.set_fused_config(0, 0, sampler)
+        try:
+            fused = gpu_ctx.run_float16_prepacked(s, d["input"], d["offset"], d["mask"], packed).astype(np.float32)
+        finally:
+            gpu_ctx.set_fused_config(0, 0, -1)
+        assert np.abs(fused - direct).max() <= 2e-3, sampler
+    log("  checksum (fused, reference inputs):", dcn.checksum(fused.astype(np.float16)))

@@ -1,0 +1,379 @@
+"""Pins the CPU oracle (oracle/dcn_oracle.c) before anything is compared against it.
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped bilinear term,
+a swapped dy/dx channel, a wrong offset-group index, a transposed weight, a missed
+padding case) fails at least one of them:
+  * the reference's own known-answer test (DeformConvCPUTests.swift:4-33);
+  * closed forms: zero offsets + mask 1 == torch conv2d; integer offsets == shifted
+    conv2d; mask 0 or far-away samples == bias; half-pixel offsets == 4-point means;
+  * an independent DCN built from torch.nn.functional.grid_sample (align_corners=True,
+    zero padding) in float64, over groups / offset groups / stride / dilation / padding;
+  * brute-force float64 Python loops on tiny shapes;
+  * IEEE binary16 conversion against numpy, exhaustively for binary16 -> binary32.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from jasnamacos_amd.deform_conv import DeformConvShape
+
+RNG = np.random.default_rng(20261201)
+
+
+def rand_inputs(shape: DeformConvShape, rng, offset_scale=2.5, mask_range=(0.0, 1.0)):
+    c = {
+        "input": rng.standard_normal(shape.batch * shape.input_channels * shape.input_height * shape.input_width),
+        "offset": rng.uniform(-offset_scale, offset_scale,
+                              shape.batch * 2 * shape.offset_groups * shape.kernel_area
+                              * shape.output_height * shape.output_width),
+        "mask": rng.uniform(*mask_range, shape.batch * shape.offset_groups * shape.kernel_area
+                            * shape.output_height * shape.output_width),
+        "weight": rng.uniform(-0.3, 0.3, shape.output_channels * (shape.input_channels // shape.groups)
+                              * shape.kernel_area),
+        "bias": rng.uniform(-0.1, 0.1, shape.output_channels),
+    }
+    return {k: v.astype(np.float32) for k, v in c.items()}
+
+
+def grid_sample_dcn(shape: DeformConvShape, inp, off, msk, w, b) -> np.ndarray:
+    """Independent float64 DCNv2 via grid_sample (bilinear, zeros, align_corners=True)."""
+    s = shape
+    x = torch.tensor(inp, dtype=torch.float64).reshape(s.batch, s.input_channels, s.input_height, s.input_width)
+    o = torch.tensor(off, dtype=torch.float64).reshape(s.batch, s.offset_groups, s.kernel_area, 2,
+                                                       s.output_height, s.output_width)
+    m = torch.tensor(msk, dtype=torch.float64).reshape(s.batch, s.offset_groups, s.kernel_area,
+                                                       s.output_height, s.output_width)
+    wt = torch.tensor(w, dtype=torch.float64).reshape(s.output_channels, s.input_channels // s.groups, s.kernel_area)
+    cg = s.input_channels // s.offset_groups
+    oy = torch.arange(s.output_height, dtype=torch.float64).view(-1, 1)
+    ox = torch.arange(s.output_width, dtype=torch.float64).view(1, -1)
+    cols = torch.zeros(s.batch, s.input_channels, s.kernel_area, s.output_height, s.output_width, dtype=torch.float64)
+    for g in range(s.offset_groups):
+        xg = x[:, g * cg:(g + 1) * cg]
+        for k in range(s.kernel_area):
+            ky, kx = divmod(k, s.kernel_width)
+            py = oy * s.stride_height - s.pad_height + ky * s.dilation_height + o[:, g, k, 0]
+            px = ox * s.stride_width - s.pad_width + kx * s.dilation_width + o[:, g, k, 1]
+            gx = 2.0 * px / (s.input_width - 1) - 1.0 if s.input_width > 1 else px * 0.0
+            gy = 2.0 * py / (s.input_height - 1) - 1.0 if s.input_height > 1 else py * 0.0
+            grid = torch.stack([gx, gy], dim=-1)
+            sampled = F.grid_sample(xg, grid, mode="bilinear", padding_mode="zeros", align_corners=True)
+            cols[:, g * cg:(g + 1) * cg, k] = sampled * m[:, g, k].unsqueeze(1)
+    out = torch.zeros(s.batch, s.output_channels, s.output_height, s.output_width, dtype=torch.float64)
+    cpg, opg = s.input_channels // s.groups, s.output_channels // s.groups
+    for grp in range(s.groups):
+        c = cols[:, grp * cpg:(grp + 1) * cpg]
+        out[:, grp * opg:(grp + 1) * opg] = torch.einsum("bckhw,ock->bohw", c, wt[grp * opg:(grp + 1) * opg])
+    out += torch.tensor(b, dtype=torch.float64).view(1, -1, 1, 1)
+    return out.numpy().ravel()
+
+
+def brute_force_dcn(shape: DeformConvShape, inp, off, msk, w, b) -> np.ndarray:
+    """Plain float64 loops; corners outside the input contribute zero."""
+    s = shape
+    X = np.asarray(inp, np.float64).reshape(s.batch, s.input_channels, s.input_height, s.input_width)
+    O = np.asarray(off, np.float64).reshape(s.batch, -1, s.output_height, s.output_width)
+    M = np.asarray(msk, np.float64).reshape(s.batch, -1, s.output_height, s.output_width)
+    W = np.asarray(w, np.float64).reshape(s.output_channels, s.input_channels // s.groups, s.kernel_height, s.kernel_width)
+    out = np.zeros((s.batch, s.output_channels, s.output_height, s.output_width))
+    cpg, opg = s.input_channels // s.groups, s.output_channels // s.groups
+    cpog = s.input_channels // s.offset_groups
+
+    def pix(n, c, yy, xx):
+        if 0 <= yy < s.input_height and 0 <= xx < s.input_width:
+            return X[n, c, yy, xx]
+        return 0.0
+
+    for n in range(s.batch):
+        for oc in range(s.output_channels):
+            grp = oc // opg
+            for oy in range(s.output_height):
+                for ox in range(s.output_width):
+                    acc = float(b[oc])
+                    for li in range(cpg):
+                        ic = grp * cpg + li
+                        og = ic // cpog
+                        for ky in range(s.kernel_height):
+                            for kx in range(s.kernel_width):
+                                k = ky * s.kernel_width + kx
+                                y = oy * s.stride_height - s.pad_height + ky * s.dilation_height + O[n, 2 * (og * s.kernel_area + k), oy, ox]
+                                x = ox * s.stride_width - s.pad_width + kx * s.dilation_width + O[n, 2 * (og * s.kernel_area + k) + 1, oy, ox]
+                                y0, x0 = math.floor(y), math.floor(x)
+                                ly, lx = y - y0, x - x0
+                                v = (pix(n, ic, y0, x0) * (1 - ly) * (1 - lx) + pix(n, ic, y0, x0 + 1) * (1 - ly) * lx
+                                     + pix(n, ic, y0 + 1, x0) * ly * (1 - lx) + pix(n, ic, y0 + 1, x0 + 1) * ly * lx)
+                                acc += v * M[n, og * s.kernel_area + k, oy, ox] * W[oc, li, ky, kx]
+                    out[n, oc, oy, ox] = acc
+    return out.ravel()
+
+
+def test_reference_known_answer(oracle):
+    # DeformConvCPUTests.swift:4-33: 1x1 kernel, zero offsets, mask 0.5, weight 2, bias 1.
+    s = DeformConvShape(1, 1, 2, 2, 1, 2, 2, 1, 1, 0, 0, 1, 1, 1, 1, 1, 1)
+    out = oracle.forward_f32(s, [1, 2, 3, 4], np.zeros(8), np.full(4, 0.5), [2], [1])
+    assert out.tolist() == [2.0, 3.0, 4.0, 5.0]
+
+
+def test_invalid_shape_rejected(oracle):
+    s = DeformConvShape(1, 3, 4, 4, 2, 4, 4, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)  # 3 % 2 != 0
+    with pytest.raises(ValueError):
+        oracle.forward_f32(s, np.zeros(48), np.zeros(2 * 2 * 9 * 16), np.zeros(2 * 9 * 16), np.zeros(54), np.zeros(2))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_zero_offsets_unit_mask_is_conv2d(oracle, seed):
+    rng = np.random.default_rng(seed)
+    s = DeformConvShape(2, 8, 9, 7, 6, 9, 7, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)
+    d = rand_inputs(s, rng)
+    d["offset"][:] = 0
+    d["mask"][:] = 1
+    out = oracle.forward_f32(s, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    x = torch.tensor(d["input"], dtype=torch.float64).reshape(2, 8, 9, 7)
+    w = torch.tensor(d["weight"], dtype=torch.float64).reshape(6, 8, 3, 3)
+    ref = F.conv2d(x, w, torch.tensor(d["bias"], dtype=torch.float64), padding=1).numpy().ravel()
+    np.testing.assert_allclose(out, ref, rtol=0, atol=2e-5)
+
+
+def test_integer_offsets_shift_the_input(oracle):
+    rng = np.random.default_rng(3)
+    s = DeformConvShape(1, 4, 10, 11, 5, 10, 11, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1)
+    d = rand_inputs(s, rng)
+    off = d["offset"].reshape(2 * 9, 10, 11)
+    off[0::2] = 2.0   # dy
+    off[1::2] = -3.0  # dx
+    d["mask"][:] = 1
+    out = oracle.forward_f32(s, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    x = torch.tensor(d["input"], dtype=torch.float64).reshape(1, 4, 10, 11)
+    # Tap (ky, kx) of pixel (oy, ox) reads x[oy - 1 + ky + 2, ox - 1 + kx - 3] (zero outside x):
+    # a valid conv over the zero-padded input cropped at (2 - 1, -3 - 1).
+    P = 5
+    xp = F.pad(x, (P, P, P, P))
+    crop = xp[:, :, P + 2 - 1:P + 2 - 1 + 12, P - 3 - 1:P - 3 - 1 + 13]
+    w = torch.tensor(d["weight"], dtype=torch.float64).reshape(5, 4, 3, 3)
+    ref = F.conv2d(crop, w, torch.tensor(d["bias"], dtype=torch.float64)).numpy().ravel()
+    np.testing.assert_allclose(out, ref, rtol=0, atol=2e-5)
+
+
+def test_zero_mask_and_far_samples_give_bias(oracle):
+    rng = np.random.default_rng(4)
+    s = DeformConvShape(1, 8, 6, 6, 4, 6, 6, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)
+    d = rand_inputs(s, rng)
+    bias_plane = np.repeat(d["bias"], 36)
+    m0 = d["mask"].copy()
+    m0[:] = 0
+    out = oracle.forward_f32(s, d["input"], d["offset"], m0, d["weight"], d["bias"])
+    assert np.array_equal(out, bias_plane)
+    for far in (1000.0, -1000.0, 7.0, -8.5):
+        off = np.full_like(d["offset"], far)
+        out = oracle.forward_f32(s, d["input"], off, d["mask"], d["weight"], d["bias"])
+        assert np.array_equal(out, bias_plane), far
+
+
+def test_half_pixel_offsets_average_four_neighbours(oracle):
+    # 1x1 kernel, weight 1, bias 0, mask 1, offset (+0.5, +0.5): mean of the 2x2 block.
+    s = DeformConvShape(1, 1, 4, 5, 1, 4, 5, 1, 1, 0, 0, 1, 1, 1, 1, 1, 1)
+    x = np.arange(20, dtype=np.float32) * 0.25 - 1.0
+    out = oracle.forward_f32(s, x, np.full(40, 0.5, np.float32), np.ones(20), [1.0], [0.0])
+    X = np.pad(x.reshape(4, 5).astype(np.float64), ((0, 1), (0, 1)))
+    ref = (X[:-1, :-1] + X[:-1, 1:] + X[1:, :-1] + X[1:, 1:]) / 4
+    np.testing.assert_allclose(out, ref.ravel(), rtol=0, atol=1e-6)
+
+
+SHAPES = [
+    DeformConvShape(1, 8, 7, 9, 4, 7, 9, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1),
+    DeformConvShape(2, 8, 6, 6, 6, 6, 6, 3, 3, 1, 1, 1, 1, 1, 1, 2, 4),   # groups 2, 4 offset groups
+    DeformConvShape(1, 6, 9, 8, 3, 4, 4, 3, 3, 1, 0, 2, 2, 1, 1, 1, 3),   # stride 2, asym pad
+    DeformConvShape(1, 4, 8, 8, 4, 6, 6, 3, 3, 1, 1, 1, 1, 2, 2, 2, 2),   # dilation 2
+    DeformConvShape(1, 16, 5, 5, 8, 5, 5, 1, 3, 0, 1, 1, 1, 1, 1, 1, 16),  # 1x3 kernel, Cg = 1
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: f"b{s.batch}c{s.input_channels}g{s.groups}og{s.offset_groups}s{s.stride_height}d{s.dilation_height}k{s.kernel_height}x{s.kernel_width}")
+def test_matches_grid_sample_dcn(oracle, shape):
+    d = rand_inputs(shape, np.random.default_rng(shape.input_channels * 7 + shape.groups))
+    out = oracle.forward_f32(shape, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    ref = grid_sample_dcn(shape, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    np.testing.assert_allclose(out, ref, rtol=0, atol=5e-5)
+
+
+@pytest.mark.parametrize("shape", SHAPES[:3], ids=["plain", "groups", "stride"])
+def test_matches_brute_force(oracle, shape):
+    d = rand_inputs(shape, np.random.default_rng(11))
+    out = oracle.forward_f32(shape, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    ref = brute_force_dcn(shape, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    np.testing.assert_allclose(out, ref, rtol=0, atol=5e-5)
+
+
+def test_swapping_dy_dx_changes_result(oracle):
+    # Guards the channel convention itself: channel 2k is dy, 2k+1 is dx.
+    s = DeformConvShape(1, 1, 5, 5, 1, 5, 5, 1, 1, 0, 0, 1, 1, 1, 1, 1, 1)
+    x = np.arange(25, dtype=np.float32)
+    off = np.zeros(50, np.float32)
+    off[:25] = 1.0  # dy = +1 -> value of the row below = x + 5
+    out = oracle.forward_f32(s, x, off, np.ones(25), [1.0], [0.0])
+    ref = np.where(np.arange(25) < 20, x + 5, 0)
+    assert np.array_equal(out, ref)
+
+
+def test_f16_direct_is_rounded_f32_oracle(oracle):
+    s = SHAPES[1]
+    d = rand_inputs(s, np.random.default_rng(5))
+    h = {k: v.astype(np.float16) for k, v in d.items()}
+    out16 = oracle.forward_f16_direct(s, h["input"], h["offset"], h["mask"], h["weight"], h["bias"])
+    out32 = oracle.forward_f32(s, *[h[k].astype(np.float32) for k in ("input", "offset", "mask", "weight", "bias")])
+    assert np.array_equal(out16.view(np.uint16), out32.astype(np.float16).view(np.uint16))
+
+
+def test_im2col_times_weights_is_forward(oracle):
+    s = DeformConvShape(2, 16, 7, 6, 8, 7, 6, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)
+    d = rand_inputs(s, np.random.default_rng(6))
+    h = {k: v.astype(np.float16) for k, v in d.items()}
+    cols = oracle.im2col_f16(s, h["input"], h["offset"], h["mask"]).astype(np.float64)
+    cols = cols.reshape(2, 42, 16 * 9)
+    W = h["weight"].astype(np.float64).reshape(8, 144)
+    ref = np.einsum("bpk,ok->bop", cols, W) + h["bias"].astype(np.float64)[None, :, None]
+    exact = oracle.forward_f32(s, *[h[k].astype(np.float32) for k in ("input", "offset", "mask", "weight", "bias")])
+    # im2col rounds each modulated sample to FP16: agreement to FP16 resolution only.
+    np.testing.assert_allclose(ref.ravel(), exact, rtol=0, atol=3e-3)
+    gem = oracle.gemm_f16(s, cols.astype(np.float16).ravel(), h["weight"], h["bias"]).astype(np.float64)
+    np.testing.assert_allclose(gem, ref.ravel(), rtol=0, atol=2e-3)
+
+
+def test_im2col_integer_offsets_copy_input(oracle):
+    s = DeformConvShape(1, 8, 5, 5, 8, 5, 5, 1, 1, 0, 0, 1, 1, 1, 1, 1, 1)
+    x = (np.arange(200) % 17 - 8).astype(np.float16)
+    off = np.zeros(50, np.float16)
+    off[:25] = -1  # dy = -1: row above
+    cols = oracle.im2col_f16(s, x, off, np.ones(25, np.float16)).reshape(25, 8)
+    X = x.reshape(8, 5, 5)
+    for p in range(25):
+        y, xx = divmod(p, 5)
+        ref = X[:, y - 1, xx] if y >= 1 else np.zeros(8, np.float16)
+        assert np.array_equal(cols[p], ref)
+
+
+def test_f16_to_f32_exhaustive(oracle):
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = oracle.f16_bits_to_f32(bits)
+    finite = np.isfinite(ref)
+    assert np.array_equal(got[finite].view(np.uint32), ref[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isinf(got), np.isinf(ref))
+
+
+def test_f32_to_f16_matches_numpy(oracle):
+    rng = np.random.default_rng(8)
+    vals = np.concatenate([
+        rng.standard_normal(4000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 4000).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e9, -1e9, 2.0 ** -24, 2.0 ** -25, 1.5 * 2.0 ** -25,
+                  2.0 ** -14, 2.0 ** -14 - 2.0 ** -30, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11], np.float32),
+        # ties: exactly halfway between two binary16 values
+        (np.arange(1, 2000, dtype=np.float32) * np.float32(2.0 ** -11) + np.float32(1.0)),
+    ])
+    got = oracle.f32_to_f16_bits(vals)
+    ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_nonfinite_flag(oracle):
+    # MetalNonFiniteFlagTests.swift:50-52
+    assert oracle.flag_nonfinite_f16(np.array([0, 1, -2, 0.5], np.float16)) == 0
+    assert oracle.flag_nonfinite_f16(np.array([0, np.inf, 1], np.float16)) == 1
+    assert oracle.flag_nonfinite_f16(np.array([0, np.nan, 1], np.float16)) == 1
+    assert oracle.flag_nonfinite_f16(np.array([65504, -65504], np.float16)) == 0
+
+
+def test_offset_transform_closed_form(oracle):
+    # JasnaCLI.swift:177-211: 10*tanh(raw) + flow[y for even / x for odd], sigmoid mask, tol 5e-3.
+    plane = 7
+    raw = np.array([((i * 13) % 101) / 50 - 1 for i in range(432 * plane)], np.float32).astype(np.float16)
+    flow1 = (np.arange(2 * plane) / 20 - 0.25).astype(np.float16)
+    flow2 = (0.3 - np.arange(2 * plane) / 30).astype(np.float16)
+    off, msk = oracle.offset_transform_f16(plane, raw, flow1, flow2)
+    r = raw.astype(np.float64).reshape(432, plane)
+    f1, f2 = flow1.astype(np.float64).reshape(2, plane), flow2.astype(np.float64).reshape(2, plane)
+    exp_off = np.empty((288, plane))
+    for c in range(288):
+        flow = f1 if c < 144 else f2
+        exp_off[c] = 10 * np.tanh(r[c]) + flow[1 if (c % 144) % 2 == 0 else 0]
+    exp_msk = 1 / (1 + np.exp(-r[288:]))
+    assert np.abs(off.astype(np.float64).reshape(288, plane) - exp_off).max() < 5e-3
+    assert np.abs(msk.astype(np.float64).reshape(144, plane) - exp_msk).max() < 5e-3
+
+
+def _warp_zero(values, y, x):
+    H, W = values.shape
+    y0, x0 = math.floor(y), math.floor(x)
+    ly, lx = y - y0, x - x0
+
+    def v(yy, xx):
+        return values[yy, xx] if 0 <= yy < H and 0 <= xx < W else 0.0
+
+    return (v(y0, x0) * (1 - ly) * (1 - lx) + v(y0, x0 + 1) * (1 - ly) * lx
+            + v(y0 + 1, x0) * ly * (1 - lx) + v(y0 + 1, x0 + 1) * ly * lx)
+
+
+def test_temporal_prepare_closed_form(oracle):
+    # JasnaCLI.swift:213-311 (tolerance 4e-3), first-order flow2 exactly 0 (:300-310).
+    w = h = 3
+    plane = 9
+    fp = np.array([((i * 11) % 71) / 50 - 0.7 for i in range(64 * plane)]).astype(np.float16)
+    fc = np.array([((i * 17) % 83) / 60 - 0.6 for i in range(64 * plane)]).astype(np.float16)
+    fn2 = np.array([((i * 23) % 97) / 70 - 0.65 for i in range(64 * plane)]).astype(np.float16)
+    f1 = np.array([((i * 7) % 19) / 20 - 0.4 for i in range(2 * plane)]).astype(np.float16)
+    pf = np.array([((i * 5) % 17) / 25 - 0.3 for i in range(2 * plane)]).astype(np.float16)
+    flow2, cond, dinp = oracle.temporal_prepare_f16(w, h, True, fp, fc, fn2, f1, pf)
+    F1 = f1.astype(np.float64).reshape(2, plane)
+    PF = pf.astype(np.float64).reshape(2, h, w)
+    exp_f2 = np.empty((2, plane))
+    for c in range(2):
+        for sp in range(plane):
+            y, x = divmod(sp, w)
+            exp_f2[c, sp] = F1[c, sp] + _warp_zero(PF[c], y + F1[1, sp], x + F1[0, sp])
+    exp_f2h = exp_f2.astype(np.float16).astype(np.float64)
+    FP = fp.astype(np.float64).reshape(64, h, w)
+    FN = fn2.astype(np.float64).reshape(64, h, w)
+    exp_cond = np.empty((196, plane))
+    for c in range(196):
+        for sp in range(plane):
+            y, x = divmod(sp, w)
+            if c < 64:
+                exp_cond[c, sp] = _warp_zero(FP[c], y + F1[1, sp], x + F1[0, sp])
+            elif c < 128:
+                exp_cond[c, sp] = fc.astype(np.float64)[(c - 64) * plane + sp]
+            elif c < 192:
+                exp_cond[c, sp] = _warp_zero(FN[c - 128], y + exp_f2h[1, sp], x + exp_f2h[0, sp])
+            elif c < 194:
+                exp_cond[c, sp] = F1[c - 192, sp]
+            else:
+                exp_cond[c, sp] = exp_f2h[c - 194, sp]
+    err = max(np.abs(flow2.astype(np.float64) - exp_f2.ravel()).max(),
+              np.abs(cond.astype(np.float64) - exp_cond.ravel()).max())
+    assert err < 4e-3
+    assert np.array_equal(dinp.view(np.uint16), np.concatenate([fp, fn2]).view(np.uint16))
+    flow2_first, _, _ = oracle.temporal_prepare_f16(w, h, False, fp, fc, np.zeros_like(fn2), f1, pf)
+    assert np.all(flow2_first.astype(np.float32) == 0)
+
+
+def test_conv3x3_matches_torch(oracle):
+    rng = np.random.default_rng(9)
+    cin, cout, hh, ww = 5, 4, 6, 7
+    x = rng.standard_normal(cin * hh * ww).astype(np.float16)
+    w = (rng.standard_normal(cout * cin * 9) * 0.2).astype(np.float16)
+    b = (rng.standard_normal(cout) * 0.1).astype(np.float16)
+    res = rng.standard_normal(cout * hh * ww).astype(np.float16)
+    ref = F.conv2d(torch.tensor(x.astype(np.float64)).reshape(1, cin, hh, ww),
+                   torch.tensor(w.astype(np.float64)).reshape(cout, cin, 3, 3),
+                   torch.tensor(b.astype(np.float64)), padding=1)
+    for act, fn in ((0, lambda t: t), (1, lambda t: F.leaky_relu(t, 0.1)), (2, F.relu)):
+        out = oracle.conv3x3_f16(cin, cout, hh, ww, x, w, b, act, 0.1)
+        np.testing.assert_allclose(out.astype(np.float64), fn(ref).numpy().ravel(), rtol=0, atol=4e-3)
+    out = oracle.conv3x3_f16(cin, cout, hh, ww, x, w, b, 2, 0.1, res)
+    np.testing.assert_allclose(out.astype(np.float64), F.relu(ref).numpy().ravel() + res.astype(np.float64),
+                               rtol=0, atol=8e-3)
