@@ -82,6 +82,17 @@ inline size_t cb8_bytes(const dcn_shape& s, const FusedGeometry& g) {
     return (size_t)s.batch * g.cblk * g.hp * g.wp * 16;
 }
 
+#if defined(__HIPCC__)
+// Round an FP32 value to FP16 (nearest even) *as an FP32 register value*. The empty
+// asm makes the value opaque, so the conversion cannot be folded into the operation
+// that produced it (v_fma_mixlo_f16 would round an exact product or sum once, where
+// the reference rounds to FP32 first and then to FP16).
+__device__ __forceinline__ _Float16 round_f16(float v) {
+    __asm__ volatile("" : "+v"(v));
+    return (_Float16)v;
+}
+#endif
+
 // Host utilities (dcn_host_util.cpp).
 uint16_t f32_to_f16_bits(float value);
 float f16_bits_to_f32(uint16_t bits);

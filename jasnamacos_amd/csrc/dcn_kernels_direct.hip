@@ -59,7 +59,7 @@ __device__ __forceinline__ void store_out<float>(float* out, long i, float v) {
 }
 template <>
 __device__ __forceinline__ void store_out<uint16_t>(uint16_t* out, long i, float v) {
-    out[i] = __builtin_bit_cast(uint16_t, (_Float16)v);  // half(sum), round to nearest even
+    out[i] = __builtin_bit_cast(uint16_t, round_f16(v));  // half(sum), round to nearest even
 }
 
 template <typename T>

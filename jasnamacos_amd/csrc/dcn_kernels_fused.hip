@@ -81,7 +81,7 @@ __device__ __forceinline__ h8 blend_exact(u32x4 q00, u32x4 q01, u32x4 q10, u32x4
     for (int e = 0; e < 8; ++e) {
         const float s = (float)a[e] * (1.0f - ly) * (1.0f - lx) + (float)b[e] * (1.0f - ly) * lx +
                         (float)c[e] * ly * (1.0f - lx) + (float)d[e] * ly * lx;
-        r[e] = (_Float16)(s * m);
+        r[e] = round_f16(s * m);
     }
     return r;
 }
@@ -92,21 +92,15 @@ __device__ __forceinline__ h8 blend_fast(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 
                                          float ly, float lx, float m) {
     const float t0 = m * (1.0f - ly);
     const float t1 = m * ly;
-    const _Float16 w00 = (_Float16)(t0 * (1.0f - lx));
-    const _Float16 w01 = (_Float16)(t0 * lx);
-    const _Float16 w10 = (_Float16)(t1 * (1.0f - lx));
-    const _Float16 w11 = (_Float16)(t1 * lx);
-    const h2 W00 = {w00, w00}, W01 = {w01, w01}, W10 = {w10, w10}, W11 = {w11, w11};
-    u32x4 r;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        h2 acc = W00 * __builtin_bit_cast(h2, q00[d]);
-        acc = __builtin_elementwise_fma(W01, __builtin_bit_cast(h2, q01[d]), acc);
-        acc = __builtin_elementwise_fma(W10, __builtin_bit_cast(h2, q10[d]), acc);
-        acc = __builtin_elementwise_fma(W11, __builtin_bit_cast(h2, q11[d]), acc);
-        r[d] = __builtin_bit_cast(uint32_t, acc);
-    }
-    return __builtin_bit_cast(h8, r);
+    const h8 w00 = (_Float16)(t0 * (1.0f - lx));  // scalar -> all 8 lanes
+    const h8 w01 = (_Float16)(t0 * lx);
+    const h8 w10 = (_Float16)(t1 * (1.0f - lx));
+    const h8 w11 = (_Float16)(t1 * lx);
+    h8 r = w00 * __builtin_bit_cast(h8, q00);
+    r = __builtin_elementwise_fma(w01, __builtin_bit_cast(h8, q01), r);
+    r = __builtin_elementwise_fma(w10, __builtin_bit_cast(h8, q10), r);
+    r = __builtin_elementwise_fma(w11, __builtin_bit_cast(h8, q11), r);
+    return r;
 }
 
 template <int NB, int MT, int KS, int SAMPLER>
@@ -234,7 +228,7 @@ __global__ __launch_bounds__(64 * KS) void fused_kernel(FusedArgs a) {
             const int b = p / a.HWo;
             const int sp = p - b * a.HWo;
             a.out[((size_t)b * a.Cout + oc) * a.HWo + sp] =
-                __builtin_bit_cast(uint16_t, (_Float16)(sum + a.bias[oc]));
+                __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
         }
     }
 }
@@ -341,7 +335,7 @@ __global__ __launch_bounds__(256) void im2col_kernel(const uint16_t* __restrict_
                           value(y0, x1) * (1.0f - ly) * lx + value(y1, x0) * ly * (1.0f - lx) +
                           value(y1, x1) * ly * lx;
     const float m = (float)__builtin_bit_cast(_Float16, mask[n * s.og * ka * plane + sample * plane + sp]);
-    columns[gid] = __builtin_bit_cast(uint16_t, (_Float16)(sampled * m));
+    columns[gid] = __builtin_bit_cast(uint16_t, round_f16(sampled * m));
 }
 
 // flag_non_finite_fp16 (MetalShader.swift:454-463): exponent all ones -> NaN or Inf.
