@@ -123,7 +123,7 @@ def main() -> int:
     ctx = dc.HipDeformConv(0)
     packed = ctx.prepack_dev(s, dev["weight"], dev["bias"])
     ctx.reserve(s)
-    mt, ks, sampler = ctx.get_fused_config(s)
+    fused_cfg = ctx.get_fused_config(s)
     out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
     cb8 = torch.empty(ctx.cb8_count(s), dtype=torch.int16, device="cuda")
     stream = torch.cuda.Stream()
@@ -207,7 +207,7 @@ def main() -> int:
             "workload": WORKLOADS[args.config],
             "batch": s.batch, "in_channels": s.input_channels, "height": s.input_height, "width": s.input_width,
             "out_channels": s.output_channels, "kernel": [s.kernel_height, s.kernel_width],
-            "deformable_groups": s.offset_groups, "fused_config": {"mt": mt, "ks": ks, "sampler": sampler},
+            "deformable_groups": s.offset_groups, "fused_config": fused_cfg,
             "timing": f"{args.steps} calls captured in one hipGraph, one replay timed with HIP events",
         },
         "tflops": flops / (us_per_call * 1e-6) / 1e12,

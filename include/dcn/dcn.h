@@ -213,17 +213,22 @@ dcn_status dcn_forward_f16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape* 
                                              const void* d_mask, const dcn_packed* packed,
                                              void* d_output, void* stream);
 
-/* Fused-kernel tuning. sampler: 0 = reference arithmetic (FP32 bilinear in the
- * reference's association, half(sampled*mask): the im2col values of
- * deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into the
- * bilinear weights, packed-FP16 blend). mt = 32-pixel row blocks per wave (1, 2),
- * ks = waves splitting K (2, 4, 8). 0 / -1 = automatic choice. No counterpart in the
- * reference (its tile size is the compile-time fusedGEMMRowsPerTile,
- * MetalShader.swift:2). */
-dcn_status dcn_set_fused_config(dcn_context* ctx, int mt, int ks, int sampler);
+/* Fused-kernel tuning. variant: 1 = register sampling (each lane gathers its MFMA A
+ * fragment directly), 2 = LDS-staged im2col tile (a sampler phase fills the tile for
+ * the whole K range, an MFMA phase consumes it), 3 = LDS input windows (3x3 kernels:
+ * per offset group, the bounding box of a 2D pixel tile's samples is copied to LDS and
+ * gathered from there; mt = tile rows, ks = waves = 32-pixel row blocks), 4 = variant 3
+ * with the lower corner row of each sample read through the L1 cache instead of LDS. sampler: 0 = reference arithmetic
+ * (FP32 bilinear in the reference's association, half(sampled*mask): the im2col
+ * values of deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into
+ * the bilinear weights, packed-FP16 blend). mt = 32-pixel row blocks per tile (1, 2),
+ * ks = waves per workgroup (register: 2, 4, 8; staged: 8, 16). 0 / -1 = automatic.
+ * No counterpart in the reference (its tile size is the compile-time
+ * fusedGEMMRowsPerTile, MetalShader.swift:2). */
+dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, int sampler);
 /* The configuration the next fused call on `shape` would use. */
-dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* mt, int* ks,
-                                int* sampler);
+dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* variant, int* mt,
+                                int* ks, int* sampler);
 
 /* Sampler alone: the modulated FP16 im2col matrix [B*Ho*Wo][Cin*Kh*Kw] with
  * column ic*Kh*Kw + k and value half(bilinear * mask), exactly

@@ -81,26 +81,48 @@ bool packed_matches(const dcn_packed* p, const dcn_shape* s) {
            p->shape.offset_groups == s->offset_groups;
 }
 
-dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry& g) {
-    dcn::FusedConfig cfg;
-    // Small problems (one 64x64 map) need every CU: 32-pixel tiles, K split over 8
-    // waves. Larger ones amortise each B fragment over two 32-pixel blocks.
+dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry& g,
+                               bool window_ok) {
+    const dcn::FusedConfig& o = ctx->fused_override;
     const long long tiles32 = (g.m + 31) / 32;
-    if (tiles32 <= 1024) {
-        cfg.mt = 1;
+    // Variant: small problems (one 64x64 map is 128 row blocks) need every CU busy and
+    // use 32-pixel tiles of the staged variant; large ones use LDS windows over 2D tiles.
+    int variant = o.variant > 0 ? o.variant
+                                : (window_ok && tiles32 > 1024 ? dcn::kVariantWindow : dcn::kVariantStaged);
+    const bool window = variant == dcn::kVariantWindow || variant == dcn::kVariantWindowSplit;
+    if (window && !window_ok) variant = dcn::kVariantStaged;
+    dcn::FusedConfig cfg{variant, 1, 8, dcn::kSamplerFast};
+    if (variant == dcn::kVariantWindow || variant == dcn::kVariantWindowSplit) {
+        // A 4 x 32 tile on 4 waves with single-buffered windows: two workgroups share a
+        // CU, so one copies its windows while the other multiplies.
+        cfg.mt = 4;  // tile rows
+        cfg.ks = 4;  // waves = 32-pixel row blocks
+        cfg.split = variant == dcn::kVariantWindowSplit ? 1 : 0;
+    } else if (variant == dcn::kVariantStaged) {
+        cfg.mt = tiles32 > 1024 ? 2 : 1;
         cfg.ks = 8;
     } else {
-        cfg.mt = 2;
-        cfg.ks = 4;
+        cfg.mt = tiles32 > 1024 ? 2 : 1;
+        cfg.ks = cfg.mt == 1 ? 8 : 4;
     }
-    cfg.sampler = dcn::kSamplerFast;
-    if (ctx->fused_override.mt > 0) cfg.mt = ctx->fused_override.mt;
-    if (ctx->fused_override.ks > 0) cfg.ks = ctx->fused_override.ks;
-    if (ctx->fused_override.sampler >= 0) cfg.sampler = ctx->fused_override.sampler;
+    if (o.mt > 0) cfg.mt = o.mt;
+    if (o.ks > 0) cfg.ks = o.ks;
+    if (o.sampler >= 0) cfg.sampler = o.sampler;
+    if (cfg.variant == dcn::kVariantStaged && dcn::staged_lds_bytes(g, cfg) > 160 * 1024 &&
+        o.variant != dcn::kVariantStaged) {
+        // The im2col tile does not fit: register sampling handles any K.
+        cfg.variant = dcn::kVariantRegister;
+        if (o.ks <= 0) cfg.ks = cfg.mt == 1 ? 8 : 4;
+    }
     return cfg;
 }
 
-bool config_supported(const dcn::FusedConfig& c) {
+bool config_supported(const dcn::FusedConfig& c, const dcn::FusedGeometry& g) {
+    if (c.variant == dcn::kVariantWindow || c.variant == dcn::kVariantWindowSplit)
+        return (c.ks == 8 && (c.mt == 8 || c.mt == 4)) || (c.ks == 4 && (c.mt == 4 || c.mt == 2));
+    if (c.variant == dcn::kVariantStaged)
+        return (c.mt == 1 || c.mt == 2) && (c.ks == 8 || c.ks == 16) &&
+               dcn::staged_lds_bytes(g, c) <= 160 * 1024;
     return (c.mt == 1 && (c.ks == 8 || c.ks == 4)) || (c.mt == 2 && (c.ks == 4 || c.ks == 2));
 }
 
@@ -153,14 +175,24 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
         return fail(ctx, DCN_INVALID_ARGUMENT, "packed weights live on another device");
     if (dcn::cb8_bytes(*shape, g) >= ((size_t)1 << 31))
         return fail(ctx, DCN_INVALID_SHAPE, "padded input too large for 32-bit device indexing");
-    const dcn::FusedConfig cfg = choose_config(ctx, g);
-    if (!config_supported(cfg)) return fail(ctx, DCN_INVALID_ARGUMENT, "unsupported fused config");
+    const dcn::FusedConfig cfg = choose_config(ctx, g, packed->weights_group != nullptr);
+    if (!config_supported(cfg, g))
+        return fail(ctx, DCN_INVALID_ARGUMENT,
+                    "unsupported fused config (variant " + std::to_string(cfg.variant) + ", mt " +
+                        std::to_string(cfg.mt) + ", ks " + std::to_string(cfg.ks) + ")");
+    if (g.kb >= (1 << 16)) return fail(ctx, DCN_INVALID_SHAPE, "K too large for the fused path");
     const dcn::KShape ks = dcn::to_kshape(*shape);
     const void* cb8 = d_input;
     if (!input_is_cb8) {
         DCN_TRY(ensure_workspace(ctx, dcn::cb8_bytes(*shape, g), stream));
         DCN_HIP(ctx, dcn::launch_pack_cb8(ks, g, (const uint16_t*)d_input, ctx->workspace, stream));
         cb8 = ctx->workspace;
+    }
+    if (cfg.variant == dcn::kVariantWindow || cfg.variant == dcn::kVariantWindowSplit) {
+        DCN_HIP(ctx, dcn::launch_window_f16(ks, g, cfg, cb8, (const uint16_t*)d_offset,
+                                            (const uint16_t*)d_mask, packed->weights_group,
+                                            packed->bias, (uint16_t*)d_output, stream));
+        return DCN_OK;
     }
     DCN_HIP(ctx, dcn::launch_fused_f16(ks, g, cfg, cb8, (const uint16_t*)d_offset,
                                        (const uint16_t*)d_mask, packed->weights, packed->bias,
@@ -297,24 +329,23 @@ dcn_status dcn_reserve(dcn_context* ctx, const dcn_shape* shape) {
     return ensure_workspace(ctx, dcn::cb8_bytes(*shape, g), nullptr);
 }
 
-dcn_status dcn_set_fused_config(dcn_context* ctx, int mt, int ks, int sampler) {
+dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, int sampler) {
     if (!ctx) return DCN_INVALID_ARGUMENT;
-    if (mt < 0 || ks < 0 || sampler < -1 || sampler > 1)
+    if (variant < 0 || variant > 4 || mt < 0 || mt > 8 || ks < 0 || sampler < -1 || sampler > 1)
         return fail(ctx, DCN_INVALID_ARGUMENT, "invalid fused config");
-    if (mt > 0 && ks > 0 && !config_supported(dcn::FusedConfig{mt, ks, 0}))
-        return fail(ctx, DCN_INVALID_ARGUMENT, "unsupported (mt, ks) pair");
-    ctx->fused_override = dcn::FusedConfig{mt, ks, sampler};
+    ctx->fused_override = dcn::FusedConfig{variant, mt, ks, sampler};
     return DCN_OK;
 }
 
-dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* mt, int* ks,
-                                int* sampler) {
-    if (!ctx || !mt || !ks || !sampler) return DCN_INVALID_ARGUMENT;
+dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* variant, int* mt,
+                                int* ks, int* sampler) {
+    if (!ctx || !variant || !mt || !ks || !sampler) return DCN_INVALID_ARGUMENT;
     dcn_counts c;
     DCN_TRY(validated_counts(ctx, shape, &c));
     dcn::FusedGeometry g;
     if (!dcn::fused_geometry(*shape, &g)) return fail(ctx, DCN_INVALID_SHAPE, "not a fused shape");
-    const dcn::FusedConfig cfg = choose_config(ctx, g);
+    const dcn::FusedConfig cfg = choose_config(ctx, g, dcn::window_supported(*shape));
+    *variant = cfg.variant;
     *mt = cfg.mt;
     *ks = cfg.ks;
     *sampler = cfg.sampler;
@@ -387,7 +418,9 @@ static dcn_status make_packed(dcn_context* ctx, const dcn_shape* shape, dcn_pack
     p->geometry = g;
     p->device = ctx->device;
     if (hipMalloc(&p->weights, dcn::packed_weight_bytes(g)) != hipSuccess ||
-        hipMalloc((void**)&p->bias, (size_t)shape->output_channels * sizeof(float)) != hipSuccess) {
+        hipMalloc((void**)&p->bias, (size_t)shape->output_channels * sizeof(float)) != hipSuccess ||
+        (dcn::window_supported(*shape) &&
+         hipMalloc(&p->weights_group, dcn::window_packed_bytes(*shape)) != hipSuccess)) {
         dcn_packed_free(p);
         return fail(ctx, DCN_COMMAND_FAILED, "hipMalloc of packed weights failed");
     }
@@ -408,10 +441,13 @@ dcn_status dcn_prepack_f16_dev(dcn_context* ctx, const dcn_shape* shape, const v
         return fail(ctx, DCN_INVALID_ARGUMENT, "unknown weight layout");
     dcn_packed* p = nullptr;
     DCN_TRY(make_packed(ctx, shape, &p));
-    const hipError_t e = dcn::launch_prepack_weights(dcn::to_kshape(*shape), p->geometry,
-                                                     (const uint16_t*)d_weight, (int)layout,
-                                                     (const uint16_t*)d_bias, p->weights, p->bias,
-                                                     (hipStream_t)stream);
+    hipError_t e = dcn::launch_prepack_weights(dcn::to_kshape(*shape), p->geometry,
+                                               (const uint16_t*)d_weight, (int)layout,
+                                               (const uint16_t*)d_bias, p->weights, p->bias,
+                                               (hipStream_t)stream);
+    if (e == hipSuccess && p->weights_group)
+        e = dcn::launch_prepack_group(dcn::to_kshape(*shape), (const uint16_t*)d_weight, (int)layout,
+                                      p->weights_group, (hipStream_t)stream);
     if (e != hipSuccess) {
         dcn_packed_free(p);
         return hip_fail(ctx, e, "prepack launch");
@@ -450,6 +486,7 @@ void dcn_packed_free(dcn_packed* p) {
     DeviceGuard guard(p->device);
     if (p->weights) (void)hipFree(p->weights);
     if (p->bias) (void)hipFree(p->bias);
+    if (p->weights_group) (void)hipFree(p->weights_group);
     delete p;
 }
 

@@ -47,11 +47,40 @@ enum SamplerMode : int {
     kSamplerFast = 1,
 };
 
-struct FusedConfig {
-    int mt;       // 32-pixel A fragments per wave (1 or 2)
-    int ks;       // waves per workgroup splitting the K range (2, 4 or 8)
-    int sampler;  // SamplerMode
+enum FusedVariant : int {
+    kVariantAuto = 0,
+    // Each wave samples its A fragments straight into registers (one K-block per lane
+    // per MFMA step); no LDS tile. Handles any K.
+    kVariantRegister = 1,
+    // A sampler phase fills an LDS im2col tile for the whole K range, then an MFMA
+    // phase consumes it. Needs the tile to fit in LDS.
+    kVariantStaged = 2,
+    // Per-group LDS windows of the input (3x3 kernels, 8 channels per offset group): a
+    // 2D pixel tile per workgroup, gathers served from LDS. Config: mt = tile rows,
+    // ks = waves (row blocks of 32 pixels).
+    kVariantWindow = 3,
+    // kVariantWindow with the lower corner row of each sample read through the L1
+    // (the window is there too after its copy), splitting gathers between LDS and L1.
+    kVariantWindowSplit = 4,
 };
+
+struct FusedConfig {
+    int variant;  // FusedVariant
+    int mt;       // 32-pixel row blocks per tile (1 or 2)
+    int ks;       // waves per workgroup splitting the K range
+    int sampler;  // SamplerMode
+    int split = 0;  // window variant: lower corner row from the L1
+};
+size_t staged_lds_bytes(const FusedGeometry& g, const FusedConfig& cfg);
+bool window_supported(const dcn_shape& s);
+int window_gps(const dcn_shape& s);
+size_t window_packed_bytes(const dcn_shape& s);
+hipError_t launch_prepack_group(const KShape& s, const uint16_t* w, int layout, void* wpk,
+                                hipStream_t stream);
+hipError_t launch_window_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
+                             const void* cb8, const uint16_t* off, const uint16_t* mask,
+                             const void* packed_w, const float* packed_b, uint16_t* out,
+                             hipStream_t stream);
 
 // ---- launchers (return hipSuccess or the launch error) ---------------------------
 hipError_t launch_direct_f32(const KShape& s, const float* in, const float* off,
@@ -106,13 +135,14 @@ struct dcn_context {
     void* workspace = nullptr;  // padded channel-block input copy
     size_t workspace_bytes = 0;
     uint32_t* flag = nullptr;   // device flag for the non-finite check
-    dcn::FusedConfig fused_override{0, 0, -1};
+    dcn::FusedConfig fused_override{0, 0, 0, -1};
 };
 
 struct dcn_packed {
     dcn_shape shape{};          // the layer shape the weights were packed for
     dcn::FusedGeometry geometry{};
     void* weights = nullptr;    // B fragments, packed_weight_bytes(geometry)
+    void* weights_group = nullptr;  // per-group B fragments of the window variant (or null)
     float* bias = nullptr;      // Cout floats
     int device = 0;
 };

@@ -44,6 +44,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPad = DCN_CB8_PAD;
+constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, gfx9 family
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
@@ -233,6 +234,184 @@ __global__ __launch_bounds__(64 * KS) void fused_kernel(FusedArgs a) {
     }
 }
 
+// ---- LDS-staged variant -----------------------------------------------------------
+// Phase 1 (sampler): thread t owns pixel t % TP of the tile and K-blocks
+// t / TP + i * (T / TP). It gathers UB units at a time with every load in flight
+// (offsets and mask, then the four 16-byte corners of each unit), blends them and
+// writes 16 bytes into the LDS A tile laid out [K-block][pixel][8 channels]: the
+// modulated im2col tile of the reference's gather kernel, kept on chip.
+// Phase 2 (GEMM): wave w takes K-steps [w*ksteps/NW, (w+1)*ksteps/NW) for all TP/32
+// pixel blocks and all Cout columns. A fragments are 16-byte LDS reads of 32
+// consecutive pixels (conflict-free), B fragments come from the prepacked buffer.
+// Phase 3: partial sums of the NW waves meet in LDS (reusing the A tile), then bias,
+// FP16 rounding and NCHW stores of consecutive pixels.
+struct StagedArgs {
+    FusedArgs f;
+    uint32_t magic_cb, magic_ka, magic_kw;  // ceil(2^32 / d) for d = CB, KA, KW
+};
+
+__device__ __forceinline__ int fast_div(int x, uint32_t magic) {
+    // floor(x / d) for 0 <= x < 2^16 and d < 2^16, magic = ceil(2^32 / d).
+    return (int)__umulhi((uint32_t)x, magic);
+}
+
+template <int NB, int MT, int NW, int UB, int SPW, int SAMPLER>
+__global__ __launch_bounds__(64 * NW) void staged_kernel(StagedArgs sa) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const FusedArgs& a = sa.f;
+    constexpr int TP = 32 * MT;
+    constexpr int T = 64 * NW;
+    constexpr int KSTRIDE = T / TP;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int p0 = blockIdx.x * TP;
+    const int kbp = 2 * a.ksteps;
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+
+    // ---- phase 1: sampler -> LDS ---------------------------------------------------
+    {
+        const int pl = tid % TP;
+        const int p = p0 + pl;
+        const bool pvalid = p < a.M;
+        const int pc = pvalid ? p : a.M - 1;
+        const int b = pc / a.HWo;
+        const int sp = pc - b * a.HWo;
+        const int oy = sp / a.Wo;
+        const int ox = sp - oy * a.Wo;
+        const int base_y = oy * a.sh - a.ph;
+        const int base_x = ox * a.sw - a.pw;
+        const uint32_t offb = (uint32_t)(b * 2 * a.G * a.KA) * a.HWo + sp;
+        const uint32_t mskb = (uint32_t)(b * a.G * a.KA) * a.HWo + sp;
+        const uint32_t xinb = (uint32_t)(b * a.CBLK * a.Hp + kPad) * a.Wp + kPad;
+        const int kb0 = tid / TP;
+        const int units = (kbp - kb0 + KSTRIDE - 1) / KSTRIDE;
+        for (int base = 0; base < units; base += UB) {
+            float dy[UB], dx[UB], m[UB];
+            int plane[UB], yb[UB], xb[UB];
+#pragma unroll
+            for (int i = 0; i < UB; ++i) {
+                const int kb = kb0 + (base + i) * KSTRIDE;
+                const int kbc = kb < a.KB ? kb : a.KB - 1;
+                const int gt = a.CB == 1 ? kbc : fast_div(kbc, sa.magic_cb);
+                const int cb = kbc - gt * a.CB;
+                const int g = fast_div(gt, sa.magic_ka);
+                const int tap = gt - g * a.KA;
+                const int ky = fast_div(tap, sa.magic_kw);
+                const int kx = tap - ky * a.KW;
+                plane[i] = g * a.CB + cb;
+                yb[i] = base_y + ky * a.dh;
+                xb[i] = base_x + kx * a.dw;
+                dy[i] = load_half(orr, (offb + (uint32_t)(2 * gt) * a.HWo) * 2u);
+                dx[i] = load_half(orr, (offb + (uint32_t)(2 * gt + 1) * a.HWo) * 2u);
+                m[i] = load_half(mr, (mskb + (uint32_t)gt * a.HWo) * 2u);
+            }
+            u32x4 q[UB][4];
+            float ly[UB], lx[UB];
+#pragma unroll
+            for (int i = 0; i < UB; ++i) {
+                const int kb = kb0 + (base + i) * KSTRIDE;
+                const bool live = pvalid && kb < a.KB;
+                // y = float(oy*sh - ph + ky*dh) + dy, as MetalShader.swift:327-332. Dead
+                // units (tile tail, K padding) sample the zero border with weight 0.
+                const float y = live ? (float)yb[i] + dy[i] : -16.0f;
+                const float x = live ? (float)xb[i] + dx[i] : -16.0f;
+                m[i] = live ? m[i] : 0.0f;
+                const float fy = floorf(y);
+                const float fx = floorf(x);
+                ly[i] = y - fy;
+                lx[i] = x - fx;
+                const int iy = (int)fminf(fmaxf(fy, (float)-kPad), (float)a.H);
+                const int ix = (int)fminf(fmaxf(fx, (float)-kPad), (float)a.W);
+                const uint32_t u = xinb + (uint32_t)(plane[i] * a.Hp + iy) * a.Wp + ix;
+                q[i][0] = load16(xr, u * 16u);
+                q[i][1] = load16(xr, u * 16u + 16u);
+                q[i][2] = load16(xr, (u + a.Wp) * 16u);
+                q[i][3] = load16(xr, (u + a.Wp) * 16u + 16u);
+            }
+#pragma unroll
+            for (int i = 0; i < UB; ++i) {
+                const int kb = kb0 + (base + i) * KSTRIDE;
+                if (kb < kbp) {
+                    const h8 v = SAMPLER == kSamplerExact
+                                     ? blend_exact(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], m[i])
+                                     : blend_fast(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], m[i]);
+                    *reinterpret_cast<h8*>(lds + ((size_t)kb * TP + pl) * 16) = v;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 2: MFMA over this wave's K-steps --------------------------------------
+    const int s0 = wave * a.ksteps / NW;
+    const int s1 = (wave + 1) * a.ksteps / NW;
+    f32x16 acc[MT][NB];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[mt][nb] = f32x16{};
+    for (int sb = s0; sb < s1; sb += SPW) {
+        h8 Bf[SPW][NB];
+#pragma unroll
+        for (int j = 0; j < SPW; ++j)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int s = sb + j < s1 ? sb + j : s1 - 1;
+                Bf[j][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)((s * NB + nb) * 64 + lane) * 16u));
+            }
+#pragma unroll
+        for (int j = 0; j < SPW; ++j) {
+            if (sb + j < s1) {
+                const int kb = 2 * (sb + j) + (lane >> 5);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const h8 A = *reinterpret_cast<const h8*>(lds + ((size_t)kb * TP + mt * 32 + (lane & 31)) * 16);
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc[mt][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bf[j][nb], acc[mt][nb], 0, 0, 0);
+                }
+            }
+        }
+    }
+    __syncthreads();  // the A tile is dead from here on
+
+    // ---- phase 3: cross-wave reduction, bias, FP16, NCHW store -----------------------
+    float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                red[(((wave * MT + mt) * NB + nb) * 16 + v) * 65 + lane] = acc[mt][nb][v];
+    __syncthreads();
+    for (int idx = tid; idx < TP * NB * 32; idx += T) {
+        const int pl = idx % TP;
+        const int oc = idx / TP;
+        const int mt = pl >> 5;
+        const int i = pl & 31;
+        const int nb = oc >> 5;
+        const int j = oc & 31;
+        const int v = 4 * (i >> 3) + (i & 3);
+        const int src = j + 32 * ((i >> 2) & 1);
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += red[(((w * MT + mt) * NB + nb) * 16 + v) * 65 + src];
+        const int p = p0 + pl;
+        if (p < a.M) {
+            const int b = p / a.HWo;
+            const int sp = p - b * a.HWo;
+            a.out[((size_t)b * a.Cout + oc) * a.HWo + sp] =
+                __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
+        }
+    }
+}
+
 // NCHW FP16 -> padded CB8. One thread per padded position and channel block: eight
 // 2-byte loads (coalesced along x) and one 16-byte store. Border positions get zeros.
 __global__ __launch_bounds__(256) void pack_cb8_kernel(const uint16_t* __restrict__ in,
@@ -370,6 +549,53 @@ hipError_t launch_fused_nb(const FusedArgs& a, const FusedConfig& cfg, hipStream
     return hipErrorInvalidValue;
 }
 
+template <int NB, int MT, int NW, int SAMPLER>
+hipError_t launch_staged_t(const StagedArgs& sa, long tiles, size_t lds, hipStream_t stream) {
+    // Units gathered per batch and K-steps whose B fragments are held at once, sized so
+    // the batch fits the register budget of the occupancy (2 or 4 waves per SIMD).
+    constexpr int UB = NW == 8 ? 9 : 5;
+    constexpr int kRegs = NW == 8 ? 200 : 96;
+    constexpr int kSpw = (kRegs - MT * NB * 16) / (NB * 4);
+    constexpr int SPW = kSpw < 1 ? 1 : (kSpw > (NW == 8 ? 9 : 5) ? (NW == 8 ? 9 : 5) : kSpw);
+    auto kernel = &staged_kernel<NB, MT, NW, UB, SPW, SAMPLER>;
+    static hipError_t attr = hipErrorNotReady;
+    static size_t attr_bytes = 0;
+    if (attr != hipSuccess || attr_bytes < lds) {
+        attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
+        attr_bytes = kMaxLds;
+        if (attr != hipSuccess) return attr;
+    }
+    hipLaunchKernelGGL(kernel, dim3((unsigned)tiles), dim3(64 * NW), lds, stream, sa);
+    return hipGetLastError();
+}
+
+template <int NB, int SAMPLER>
+hipError_t launch_staged_nb(const StagedArgs& sa, const FusedConfig& cfg, size_t lds, hipStream_t stream) {
+    const long tiles = ((long)sa.f.M + 32 * cfg.mt - 1) / (32 * cfg.mt);
+    if (cfg.mt == 1 && cfg.ks == 8) return launch_staged_t<NB, 1, 8, SAMPLER>(sa, tiles, lds, stream);
+    if (cfg.mt == 1 && cfg.ks == 16) return launch_staged_t<NB, 1, 16, SAMPLER>(sa, tiles, lds, stream);
+    if (cfg.mt == 2 && cfg.ks == 8) return launch_staged_t<NB, 2, 8, SAMPLER>(sa, tiles, lds, stream);
+    if (cfg.mt == 2 && cfg.ks == 16) return launch_staged_t<NB, 2, 16, SAMPLER>(sa, tiles, lds, stream);
+    return hipErrorInvalidValue;
+}
+
+template <int SAMPLER>
+hipError_t launch_staged_s(const StagedArgs& sa, int nb, const FusedConfig& cfg, size_t lds,
+                           hipStream_t stream) {
+    switch (nb) {
+        case 1: return launch_staged_nb<1, SAMPLER>(sa, cfg, lds, stream);
+        case 2: return launch_staged_nb<2, SAMPLER>(sa, cfg, lds, stream);
+        case 3: return launch_staged_nb<3, SAMPLER>(sa, cfg, lds, stream);
+        case 4: return launch_staged_nb<4, SAMPLER>(sa, cfg, lds, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+uint32_t magic_for(int d) {
+    return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) / (uint64_t)d);
+}
+
 template <int SAMPLER>
 hipError_t launch_fused_s(const FusedArgs& a, int nb, const FusedConfig& cfg, hipStream_t stream) {
     switch (nb) {
@@ -456,8 +682,21 @@ hipError_t launch_fused_f16(const KShape& s, const FusedGeometry& g, const Fused
     a.ksteps = g.ksteps;
     a.M = (int)g.m;
     a.Cout = s.Cout;
+    if (cfg.variant == kVariantStaged) {
+        StagedArgs sa{a, magic_for(g.cb), magic_for(g.ka), magic_for(s.KW)};
+        const size_t lds = staged_lds_bytes(g, cfg);
+        if (lds > kMaxLds) return hipErrorInvalidValue;
+        if (cfg.sampler == kSamplerExact) return launch_staged_s<kSamplerExact>(sa, g.nb, cfg, lds, stream);
+        return launch_staged_s<kSamplerFast>(sa, g.nb, cfg, lds, stream);
+    }
     if (cfg.sampler == kSamplerExact) return launch_fused_s<kSamplerExact>(a, g.nb, cfg, stream);
     return launch_fused_s<kSamplerFast>(a, g.nb, cfg, stream);
+}
+
+size_t staged_lds_bytes(const FusedGeometry& g, const FusedConfig& cfg) {
+    const size_t tile = (size_t)2 * g.ksteps * 32 * cfg.mt * 16;
+    const size_t red = (size_t)cfg.ks * cfg.mt * g.nb * 16 * 65 * sizeof(float);
+    return std::max(tile, red);
 }
 
 hipError_t launch_im2col_f16(const KShape& s, const uint16_t* in, const uint16_t* off,

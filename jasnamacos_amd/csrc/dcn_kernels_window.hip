@@ -1,0 +1,557 @@
+// Window-staged fused FP16 DCNv2 for gfx950 (3x3 kernels, 8 channels per offset group).
+//
+// Why: a deformable gather reads four random 16-byte corners per (pixel, group, tap).
+// Served from the vector L1 these reads miss about half the time and keep the texture
+// addresser stalled on the cache, and when tiles of many images share an XCD the 4 MB
+// L2 thrashes (measured 3.5x the compulsory HBM bytes). Here each workgroup owns a 2D
+// tile of output pixels and walks the offset groups in stages of GPS groups. For each
+// group it computes the exact bounding box of all its sample corners over the tile,
+// copies that window of the padded input plane into LDS with coalesced 16-byte loads,
+// and gathers from LDS (optionally the lower corner row from the L1, which then holds
+// the same window, to split the gather load between the two paths).
+//
+// Work split: NW waves, wave w owns one row block of 32 consecutive output pixels of the
+// tile (TR rows x NW/TR row blocks) and all Cout columns over the whole K range, so no
+// cross-wave reduction is needed. Within a stage, K-step k of v_mfma_f32_32x32x16_f16
+// takes unit u = 2k + l/32 (lane l): group u/9 of the stage, tap u%9 — one bilinear
+// coordinate and four 16-byte corners per lane. GPS = 2 pairs two groups into 9 K-steps
+// with no padding; GPS = 1 uses 5 K-steps with a zero tenth unit. The weights are
+// prepacked in the same order (prepack_group_kernel).
+//
+// Pipeline per stage (windows double-buffered): the next stage's offsets are loaded
+// before this stage is multiplied; its windows are computed and copied after.
+// A window larger than its LDS buffer makes that group gather from global memory
+// (same arithmetic), so any offset field is handled. Lanes past the image edge sample
+// a clamped in-image pixel: their accumulator rows are never stored.
+//
+// Tiles are ordered so that workgroup blockIdx lands on XCD blockIdx % 8 with a
+// contiguous eighth of the pixels: each XCD's L2 holds the inputs of its own images
+// (or image band) instead of all of them.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+
+#include "dcn_internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace dcn {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPad = DCN_CB8_PAD;
+constexpr int kBufferFlags = 0x00020000;
+// LDS for the windows of a workgroup: double-buffered (one workgroup per CU) or single
+// (two workgroups share a CU and overlap each other's copy and compute phases).
+__host__ __device__ constexpr int window_lds(int nbuf) { return nbuf == 2 ? 144 * 1024 : 72 * 1024; }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferFlags);
+}
+__device__ __forceinline__ u32x4 gload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ float gload_half(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const short v = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+    return (float)__builtin_bit_cast(_Float16, v);
+}
+
+struct WindowArgs {
+    const void* xin;      // CB8 input [B][CBLK][Hp][Wp][8]
+    const uint16_t* off;  // [B][2*G*9][HWo]
+    const uint16_t* msk;  // [B][G*9][HWo]
+    const void* wpk;      // [stages][KS][NB][64][8] FP16 (prepack_group_kernel)
+    const float* bias;    // [Cout]
+    uint16_t* out;        // [B][Cout][HWo]
+    uint32_t xin_bytes, off_bytes, msk_bytes, wpk_bytes;
+    int B, H, W, Ho, Wo, HWo, ph, pw, sh, sw, dh, dw;
+    int G, CBLK, Hp, Wp, Cout;
+    int tiles_y, tiles_x, tiles;  // tile grid per image, total
+};
+
+__device__ __forceinline__ h8 blend_exact_w(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 q11, float ly,
+                                            float lx, float m) {
+    const h8 a = __builtin_bit_cast(h8, q00), b = __builtin_bit_cast(h8, q01);
+    const h8 c = __builtin_bit_cast(h8, q10), d = __builtin_bit_cast(h8, q11);
+    h8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float s = (float)a[e] * (1.0f - ly) * (1.0f - lx) + (float)b[e] * (1.0f - ly) * lx +
+                        (float)c[e] * ly * (1.0f - lx) + (float)d[e] * ly * lx;
+        r[e] = round_f16(s * m);
+    }
+    return r;
+}
+__device__ __forceinline__ h8 blend_fast_w(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 q11, float ly,
+                                           float lx, float m) {
+    const float t0 = m * (1.0f - ly);
+    const float t1 = m * ly;
+    const h8 w00 = (_Float16)(t0 * (1.0f - lx));
+    const h8 w01 = (_Float16)(t0 * lx);
+    const h8 w10 = (_Float16)(t1 * (1.0f - lx));
+    const h8 w11 = (_Float16)(t1 * lx);
+    h8 r = w00 * __builtin_bit_cast(h8, q00);
+    r = __builtin_elementwise_fma(w01, __builtin_bit_cast(h8, q01), r);
+    r = __builtin_elementwise_fma(w10, __builtin_bit_cast(h8, q10), r);
+    r = __builtin_elementwise_fma(w11, __builtin_bit_cast(h8, q11), r);
+    return r;
+}
+
+// Unit u of a stage (0 .. 2*KS-1): group offset within the stage and tap.
+template <int GPS>
+__host__ __device__ constexpr int unit_group(int u) {
+    return GPS == 2 ? (u >= 9 ? 1 : 0) : 0;
+}
+template <int GPS>
+__host__ __device__ constexpr int unit_tap(int u) {
+    return GPS == 2 ? u - 9 * (u >= 9 ? 1 : 0) : (u < 9 ? u : 8);
+}
+
+template <int NB, int NW, int TR, int GPS, int SAMPLER, int SPLIT, int NBUF>
+__global__ __launch_bounds__(64 * NW) void window_kernel(WindowArgs a) {
+    constexpr int kWindowLds = window_lds(NBUF);
+    constexpr int TCB = NW / TR;              // row blocks across the tile
+    constexpr int T = 64 * NW;
+    constexpr int KS = GPS == 2 ? 9 : 5;      // K-steps per stage
+    constexpr int WIN = kWindowLds / (NBUF * GPS);  // bytes per window buffer
+    constexpr int CPT = (WIN / 16 + T - 1) / T;  // chunks per thread for a full window
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    int* box = reinterpret_cast<int*>(lds + kWindowLds);  // [2][GPS][NW][4]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int half = lane >> 5;
+
+    // XCD-aware tile order: blockIdx lands on XCD blockIdx % 8.
+    const int per_xcd = (a.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+    const int tiles_img = a.tiles_y * a.tiles_x;
+    const int b = tile / tiles_img;
+    const int trem = tile - b * tiles_img;
+    const int ty = trem / a.tiles_x;
+    const int tx = trem - ty * a.tiles_x;
+    const int oy_row = ty * TR + wave / TCB;
+    const int ox0 = (tx * TCB + wave % TCB) * 32;
+    // Lanes past the edge use a clamped pixel; their accumulator rows are not stored.
+    const int oyc = min(oy_row, a.Ho - 1);
+    const int oxc = min(ox0 + (lane & 31), a.Wo - 1);
+    const int sp = oyc * a.Wo + oxc;
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+
+    // Per-lane constants: base coordinates float(oy*sh - ph + ky*dh),
+    // float(ox*sw - pw + kx*dw) (MetalShader.swift:327-332) come from the pixel base
+    // plus the tap; offset/mask byte offsets from a per-lane base plus the channel.
+    const uint32_t hwo2 = (uint32_t)a.HWo * 2u;
+    const int by = oyc * a.sh - a.ph;
+    const int bx = oxc * a.sw - a.pw;
+    const uint32_t off_lane = ((uint32_t)b * 2 * a.G * 9 * a.HWo + sp) * 2u;
+    const uint32_t msk_lane = ((uint32_t)b * a.G * 9 * a.HWo + sp) * 2u;
+    const int stages = a.G / GPS;
+    // Tap and group offset of this lane's unit in K-step k (two compile-time choices).
+    auto unit_of = [&](int k, int& tap, int& go) {
+        tap = half ? unit_tap<GPS>(2 * k + 1) : unit_tap<GPS>(2 * k);
+        go = half ? unit_group<GPS>(2 * k + 1) : unit_group<GPS>(2 * k);
+    };
+
+    // Raw offsets/mask of a stage, then sample state.
+    float rdy[KS], rdx[KS], rm[KS];
+    auto load_raw = [&](int st) {
+        const uint32_t so = 2u * (uint32_t)(st * GPS * 9) * hwo2;  // dy of group st*GPS, tap 0
+        const uint32_t sm = (uint32_t)(st * GPS * 9) * hwo2;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            int tap, go;
+            unit_of(k, tap, go);
+            const uint32_t ch = (uint32_t)(go * 9 + tap);
+            rdy[k] = gload_half(orr, off_lane + 2u * ch * hwo2, so);
+            rdx[k] = gload_half(orr, off_lane + (2u * ch + 1u) * hwo2, so);
+            rm[k] = gload_half(mr, msk_lane + ch * hwo2, sm);
+        }
+    };
+    int iy[KS], ix[KS];
+    float ly[KS], lx[KS], mm[KS];
+    int bmin_y[GPS], bmax_y[GPS], bmin_x[GPS], bmax_x[GPS];
+    auto make_state = [&]() {
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) {
+            bmin_y[g] = INT_MAX;
+            bmax_y[g] = INT_MIN;
+            bmin_x[g] = INT_MAX;
+            bmax_x[g] = INT_MIN;
+        }
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            int tap, go;
+            unit_of(k, tap, go);
+            const int ky = tap / 3, kx = tap - 3 * (tap / 3);
+            const float y = (float)(by + ky * a.dh) + rdy[k];
+            const float x = (float)(bx + kx * a.dw) + rdx[k];
+            const float fy = floorf(y), fx = floorf(x);
+            ly[k] = y - fy;
+            lx[k] = x - fx;
+            mm[k] = rm[k];
+            // Clamped so both rows/columns of the corner pair stay in the padded plane.
+            iy[k] = (int)__builtin_amdgcn_fmed3f(fy, (float)-kPad, (float)a.H);
+            ix[k] = (int)__builtin_amdgcn_fmed3f(fx, (float)-kPad, (float)a.W);
+            const int g0 = unit_group<GPS>(2 * k), g1 = unit_group<GPS>(2 * k + 1);
+            if (g0 == g1) {
+                bmin_y[g0] = min(bmin_y[g0], iy[k]);
+                bmax_y[g0] = max(bmax_y[g0], iy[k]);
+                bmin_x[g0] = min(bmin_x[g0], ix[k]);
+                bmax_x[g0] = max(bmax_x[g0], ix[k]);
+            } else {  // the K-step straddles the two groups of the stage
+                bmin_y[g0] = min(bmin_y[g0], half ? INT_MAX : iy[k]);
+                bmax_y[g0] = max(bmax_y[g0], half ? INT_MIN : iy[k]);
+                bmin_x[g0] = min(bmin_x[g0], half ? INT_MAX : ix[k]);
+                bmax_x[g0] = max(bmax_x[g0], half ? INT_MIN : ix[k]);
+                bmin_y[g1] = min(bmin_y[g1], half ? iy[k] : INT_MAX);
+                bmax_y[g1] = max(bmax_y[g1], half ? iy[k] : INT_MIN);
+                bmin_x[g1] = min(bmin_x[g1], half ? ix[k] : INT_MAX);
+                bmax_x[g1] = max(bmax_x[g1], half ? ix[k] : INT_MIN);
+            }
+        }
+    };
+    auto publish_box = [&](int slot) {
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) {
+            const int v0 = __ockl_wfred_min_i32(bmin_y[g]);
+            const int v1 = __ockl_wfred_max_i32(bmax_y[g]);
+            const int v2 = __ockl_wfred_min_i32(bmin_x[g]);
+            const int v3 = __ockl_wfred_max_i32(bmax_x[g]);
+            if (lane == 0) {
+                int* sb = box + ((slot * GPS + g) * NW + wave) * 4;
+                sb[0] = v0;
+                sb[1] = v1;
+                sb[2] = v2;
+                sb[3] = v3;
+            }
+        }
+    };
+
+    struct Win {
+        int y0, x0, ww, hh;
+        bool in_lds;
+    };
+    auto read_box = [&](int slot, int g) {
+        int ymin = INT_MAX, ymax = INT_MIN, xmin = INT_MAX, xmax = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int4 v = *reinterpret_cast<const int4*>(box + ((slot * GPS + g) * NW + w) * 4);
+            ymin = min(ymin, v.x);
+            ymax = max(ymax, v.y);
+            xmin = min(xmin, v.z);
+            xmax = max(xmax, v.w);
+        }
+        Win win;
+        win.y0 = ymin;
+        win.x0 = xmin;
+        win.ww = xmax - xmin + 2;
+        win.hh = ymax - ymin + 2;
+        win.in_lds = win.hh * win.ww * 16 <= WIN;
+        return win;
+    };
+
+    // Copy a window of group `grp` into buffer slot/g. Branch-free: the tail lanes
+    // recopy the last position into itself.
+    auto copy_window = [&](int grp, const Win& w, uint8_t* dst) {
+        if (!w.in_lds) return;
+        const int count = w.hh * w.ww;
+        const uint32_t plane_row0 = (uint32_t)(b * a.CBLK + grp) * a.Hp + (uint32_t)(w.y0 + kPad);
+        const float inv_ww = 1.0f / (float)w.ww;
+        for (int c0 = 0; c0 < count; c0 += T * CPT) {
+            u32x4 v[CPT];
+            int cc[CPT];
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) {
+                const int c = min(c0 + i * T + tid, count - 1);
+                int r = (int)((float)c * inv_ww);
+                r -= (r * w.ww > c) ? 1 : 0;
+                r += ((r + 1) * w.ww <= c) ? 1 : 0;
+                const int col = c - r * w.ww;
+                const uint32_t gpos = (plane_row0 + (uint32_t)r) * a.Wp + (uint32_t)(w.x0 + col + kPad);
+                cc[i] = c;
+                v[i] = gload16(xr, gpos * 16u, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) *reinterpret_cast<u32x4*>(dst + (size_t)cc[i] * 16) = v[i];
+        }
+    };
+
+    f32x16 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x16{};
+
+    // B fragments in a ring of kBDepth K-steps: step k's fragment is requested kBDepth
+    // steps before it is used, across the stage boundary (the window copy hides it).
+    constexpr int kBDepth = 3;
+    h8 Bq[kBDepth][NB];
+    auto load_b = [&](int slot, int st, int k) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            Bq[slot][nb] = __builtin_bit_cast(
+                h8, gload16(wr, (uint32_t)(((st * KS + k) * NB + nb) * 64 + lane) * 16u, 0));
+    };
+
+    // ---- prologue: stage 0 ----
+    load_raw(0);
+    make_state();
+    publish_box(0);
+#pragma unroll
+    for (int j = 0; j < kBDepth; ++j) load_b(j, 0, j);
+    __syncthreads();
+    Win win[GPS];
+#pragma unroll
+    for (int g = 0; g < GPS; ++g) {
+        win[g] = read_box(0, g);
+        copy_window(g, win[g], lds + (size_t)g * WIN);
+    }
+    __syncthreads();
+
+    for (int st = 0; st < stages; ++st) {
+        const int buf = st & 1;
+        const bool more = st + 1 < stages;
+        // Prefetch the next stage's offsets; this stage's sample state stays in iy..mm
+        // until make_state() rebuilds it after the multiply.
+        if (more) load_raw(st + 1);
+
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const int g0 = unit_group<GPS>(2 * k), g1 = unit_group<GPS>(2 * k + 1);
+            const int gi = (g0 == g1) ? g0 : half;  // group of this lane's unit within the stage
+            const Win& w = (g0 == g1) ? win[g0] : (half ? win[g1] : win[g0]);
+            const int grp = st * GPS + gi;
+            u32x4 q00, q01, q10, q11;
+            const uint32_t gbase =
+                ((uint32_t)(b * a.CBLK + grp) * a.Hp + (uint32_t)(iy[k] + kPad)) * a.Wp +
+                (uint32_t)(ix[k] + kPad);
+            if (w.in_lds) {
+                const uint8_t* base = lds + (size_t)((NBUF == 2 ? buf : 0) * GPS + gi) * WIN;
+                const int idx = (iy[k] - w.y0) * w.ww + (ix[k] - w.x0);
+                const uint8_t* p = base + (size_t)idx * 16;
+                q00 = *reinterpret_cast<const u32x4*>(p);
+                q01 = *reinterpret_cast<const u32x4*>(p + 16);
+                if (SPLIT) {
+                    q10 = gload16(xr, (gbase + a.Wp) * 16u, 0);
+                    q11 = gload16(xr, (gbase + a.Wp) * 16u + 16u, 0);
+                } else {
+                    q10 = *reinterpret_cast<const u32x4*>(p + (size_t)w.ww * 16);
+                    q11 = *reinterpret_cast<const u32x4*>(p + (size_t)w.ww * 16 + 16);
+                }
+            } else {
+                q00 = gload16(xr, gbase * 16u, 0);
+                q01 = gload16(xr, gbase * 16u + 16u, 0);
+                q10 = gload16(xr, (gbase + a.Wp) * 16u, 0);
+                q11 = gload16(xr, (gbase + a.Wp) * 16u + 16u, 0);
+            }
+            h8 A = SAMPLER == kSamplerExact ? blend_exact_w(q00, q01, q10, q11, ly[k], lx[k], mm[k])
+                                            : blend_fast_w(q00, q01, q10, q11, ly[k], lx[k], mm[k]);
+            if (GPS == 1 && k == KS - 1 && half) A = h8{};  // the zero tenth unit
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bq[k % kBDepth][nb], acc[nb], 0, 0, 0);
+            if (k + kBDepth < KS) load_b(k % kBDepth, st, k + kBDepth);
+            else if (more) load_b(k % kBDepth, st + 1, k + kBDepth - KS);
+        }
+
+        if (more) {
+            make_state();
+            publish_box(buf ^ 1);
+            __syncthreads();  // boxes of stage st+1 visible; every wave is past its multiply
+#pragma unroll
+            for (int g = 0; g < GPS; ++g) {
+                win[g] = read_box(buf ^ 1, g);
+                copy_window((st + 1) * GPS + g, win[g],
+                            lds + (size_t)((NBUF == 2 ? (buf ^ 1) : 0) * GPS + g) * WIN);
+            }
+            __syncthreads();  // windows of stage st+1 complete
+        }
+    }
+
+    // ---- epilogue: bias, FP16, coalesced NCHW stores through LDS ----
+    __syncthreads();
+    uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + (size_t)wave * 32 * NB * 32;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int oc = nb * 32 + (lane & 31);
+        const float bias = a.bias[oc];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int i = 8 * (v >> 2) + 4 * half + (v & 3);  // pixel within the row block
+            stage[oc * 32 + i] = __builtin_bit_cast(uint16_t, round_f16(acc[nb][v] + bias));
+        }
+    }
+    __syncthreads();
+    if (oy_row < a.Ho) {
+        for (int idx = lane; idx < NB * 32 * 8; idx += 64) {
+            const int oc = idx >> 3;
+            const int q = (idx & 7) * 4;
+            const uint16_t* src = stage + oc * 32 + q;
+            uint16_t* dst = a.out + ((size_t)b * a.Cout + oc) * a.HWo + (size_t)oy_row * a.Wo + ox0 + q;
+            if (ox0 + q + 3 < a.Wo && ((((uintptr_t)dst) & 3u) == 0)) {
+                reinterpret_cast<uint32_t*>(dst)[0] = (uint32_t)src[0] | ((uint32_t)src[1] << 16);
+                reinterpret_cast<uint32_t*>(dst)[1] = (uint32_t)src[2] | ((uint32_t)src[3] << 16);
+            } else {
+                for (int e = 0; e < 4; ++e)
+                    if (ox0 + q + e < a.Wo) dst[e] = src[e];
+            }
+        }
+    }
+}
+
+// Weights -> B fragments [stages][KS][NB][64][8] for window_kernel: lane l of K-step k
+// of stage st holds unit u = 2k + l/32 (group st*GPS + u/9 (GPS 2) or st (GPS 1), tap
+// u%9; zero for the padding unit 9 of GPS 1) of output channel nb*32 + l%32, channels
+// group*8 .. group*8+7.
+__global__ __launch_bounds__(256) void prepack_group_kernel(const uint16_t* __restrict__ w, int layout,
+                                                            uint16_t* __restrict__ wpk, int Cin,
+                                                            int Cout, int NB, int gps, long total) {
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    const int ks = gps == 2 ? 9 : 5;
+    const int e = (int)(gid & 7);
+    const int lane = (int)((gid >> 3) & 63);
+    long q = gid >> 9;
+    const int nb = (int)(q % NB);
+    q /= NB;
+    const int k = (int)(q % ks);
+    const int st = (int)(q / ks);
+    const int u = 2 * k + (lane >> 5);
+    const int grp = gps == 2 ? st * 2 + (u >= 9 ? 1 : 0) : st;
+    const int tap = gps == 2 ? (u >= 9 ? u - 9 : u) : u;
+    const int oc = nb * 32 + (lane & 31);
+    const int ic = grp * 8 + e;
+    uint16_t v = 0;
+    if (tap < 9 && oc < Cout && ic < Cin)
+        v = layout == DCN_LAYOUT_OIHW ? w[((size_t)oc * Cin + ic) * 9 + tap]
+                                      : w[((size_t)ic * 9 + tap) * Cout + oc];
+    wpk[gid] = v;
+}
+
+template <int NB, int NW, int TR, int GPS, int SAMPLER, int SPLIT>
+hipError_t launch_window_t(const WindowArgs& a, hipStream_t stream) {
+    constexpr int NBUF = NW == 8 ? 2 : 1;
+    const size_t lds = (size_t)window_lds(NBUF) + 2 * GPS * NW * 4 * sizeof(int);
+    auto kernel = &window_kernel<NB, NW, TR, GPS, SAMPLER, SPLIT, NBUF>;
+    static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    const unsigned grid = (unsigned)(((a.tiles + 7) / 8) * 8);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * NW), lds, stream, a);
+    return hipGetLastError();
+}
+
+template <int NW, int TR, int GPS, int SAMPLER, int SPLIT>
+hipError_t launch_window_nb(const WindowArgs& a, int nb, hipStream_t stream) {
+    switch (nb) {
+        case 1: return launch_window_t<1, NW, TR, GPS, SAMPLER, SPLIT>(a, stream);
+        case 2: return launch_window_t<2, NW, TR, GPS, SAMPLER, SPLIT>(a, stream);
+        case 3: return launch_window_t<3, NW, TR, GPS, SAMPLER, SPLIT>(a, stream);
+        case 4: return launch_window_t<4, NW, TR, GPS, SAMPLER, SPLIT>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int GPS, int SAMPLER, int SPLIT>
+hipError_t launch_window_g(const WindowArgs& a, int nb, int nw, int tr, hipStream_t stream) {
+    if (nw == 8 && tr == 8) return launch_window_nb<8, 8, GPS, SAMPLER, SPLIT>(a, nb, stream);
+    if (nw == 8 && tr == 4) return launch_window_nb<8, 4, GPS, SAMPLER, SPLIT>(a, nb, stream);
+    if (nw == 4 && tr == 4) return launch_window_nb<4, 4, GPS, SAMPLER, SPLIT>(a, nb, stream);
+    if (nw == 4 && tr == 2) return launch_window_nb<4, 2, GPS, SAMPLER, SPLIT>(a, nb, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool window_supported(const dcn_shape& s) {
+    return s.groups == 1 && s.kernel_height == 3 && s.kernel_width == 3 &&
+           s.input_channels == 8 * s.offset_groups && s.output_channels % 32 == 0 &&
+           s.output_channels <= 128;
+}
+
+int window_gps(const dcn_shape& s) { return s.offset_groups % 2 == 0 ? 2 : 1; }
+
+size_t window_packed_bytes(const dcn_shape& s) {
+    const int gps = window_gps(s);
+    const int ks = gps == 2 ? 9 : 5;
+    return (size_t)(s.offset_groups / gps) * ks * (s.output_channels / 32) * 64 * 8 * sizeof(uint16_t);
+}
+
+hipError_t launch_prepack_group(const KShape& s, const uint16_t* w, int layout, void* wpk,
+                                hipStream_t stream) {
+    dcn_shape shape{s.B, s.Cin, s.H, s.W, s.Cout, s.Ho, s.Wo, s.KH, s.KW, s.ph, s.pw,
+                    s.sh, s.sw, s.dh, s.dw, s.groups, s.og};
+    const int gps = window_gps(shape);
+    const int nb = s.Cout / 32;
+    const long total = (long)(window_packed_bytes(shape) / sizeof(uint16_t));
+    const long grid = (total + 255) / 256;
+    hipLaunchKernelGGL(prepack_group_kernel, dim3((unsigned)grid), dim3(256), 0, stream, w, layout,
+                       (uint16_t*)wpk, s.Cin, s.Cout, nb, gps, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_window_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
+                             const void* cb8, const uint16_t* off, const uint16_t* mask,
+                             const void* packed_w, const float* packed_b, uint16_t* out,
+                             hipStream_t stream) {
+    WindowArgs a;
+    a.xin = cb8;
+    a.off = off;
+    a.msk = mask;
+    a.wpk = packed_w;
+    a.bias = packed_b;
+    a.out = out;
+    const size_t hwo = (size_t)s.Ho * s.Wo;
+    dcn_shape shape{s.B, s.Cin, s.H, s.W, s.Cout, s.Ho, s.Wo, s.KH, s.KW, s.ph, s.pw,
+                    s.sh, s.sw, s.dh, s.dw, s.groups, s.og};
+    a.xin_bytes = (uint32_t)((size_t)s.B * g.cblk * g.hp * g.wp * 16);
+    a.off_bytes = (uint32_t)((size_t)s.B * 2 * s.og * 9 * hwo * 2);
+    a.msk_bytes = (uint32_t)((size_t)s.B * s.og * 9 * hwo * 2);
+    a.wpk_bytes = (uint32_t)window_packed_bytes(shape);
+    a.B = s.B;
+    a.H = s.H;
+    a.W = s.W;
+    a.Ho = s.Ho;
+    a.Wo = s.Wo;
+    a.HWo = (int)hwo;
+    a.ph = s.ph;
+    a.pw = s.pw;
+    a.sh = s.sh;
+    a.sw = s.sw;
+    a.dh = s.dh;
+    a.dw = s.dw;
+    a.G = s.og;
+    a.CBLK = g.cblk;
+    a.Hp = g.hp;
+    a.Wp = g.wp;
+    a.Cout = s.Cout;
+    const int nw = cfg.ks;
+    const int tr = cfg.mt;  // for the window variant, mt carries the tile rows
+    const int tcb = nw / tr;
+    a.tiles_y = (s.Ho + tr - 1) / tr;
+    a.tiles_x = (s.Wo + 32 * tcb - 1) / (32 * tcb);
+    a.tiles = a.tiles_y * a.tiles_x * s.B;
+    const int gps = window_gps(shape);
+    const bool split = cfg.split != 0;
+    if (cfg.sampler == kSamplerExact) {
+        if (gps == 2) return split ? launch_window_g<2, kSamplerExact, 1>(a, g.nb, nw, tr, stream)
+                                   : launch_window_g<2, kSamplerExact, 0>(a, g.nb, nw, tr, stream);
+        return split ? launch_window_g<1, kSamplerExact, 1>(a, g.nb, nw, tr, stream)
+                     : launch_window_g<1, kSamplerExact, 0>(a, g.nb, nw, tr, stream);
+    }
+    if (gps == 2) return split ? launch_window_g<2, kSamplerFast, 1>(a, g.nb, nw, tr, stream)
+                               : launch_window_g<2, kSamplerFast, 0>(a, g.nb, nw, tr, stream);
+    return split ? launch_window_g<1, kSamplerFast, 1>(a, g.nb, nw, tr, stream)
+                 : launch_window_g<1, kSamplerFast, 0>(a, g.nb, nw, tr, stream);
+}
+
+}  // namespace dcn

@@ -37,6 +37,10 @@ LAYOUT_IC_K_OC = 1
 SAMPLER_EXACT = 0
 SAMPLER_FAST = 1
 
+VARIANT_AUTO = 0
+VARIANT_REGISTER = 1
+VARIANT_STAGED = 2
+
 DIRECTIONS = ("backward_1", "forward_1", "backward_2", "forward_2")
 
 
@@ -329,14 +333,15 @@ class HipDeformConv:
     def reserve(self, shape) -> None:
         self._check(self._lib.dcn_reserve(self.ctx, C.byref(shape.to_c())))
 
-    def set_fused_config(self, mt: int = 0, ks: int = 0, sampler: int = -1) -> None:
-        self._check(self._lib.dcn_set_fused_config(self.ctx, int(mt), int(ks), int(sampler)))
+    def set_fused_config(self, mt: int = 0, ks: int = 0, sampler: int = -1, variant: int = 0) -> None:
+        """Pin the fused kernel's configuration (0 / -1 = automatic)."""
+        self._check(self._lib.dcn_set_fused_config(self.ctx, int(variant), int(mt), int(ks), int(sampler)))
 
-    def get_fused_config(self, shape) -> tuple[int, int, int]:
-        mt, ks, sm = C.c_int(), C.c_int(), C.c_int()
-        self._check(self._lib.dcn_get_fused_config(self.ctx, C.byref(shape.to_c()), C.byref(mt), C.byref(ks),
-                                                   C.byref(sm)))
-        return mt.value, ks.value, sm.value
+    def get_fused_config(self, shape) -> dict:
+        v, mt, ks, sm = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        self._check(self._lib.dcn_get_fused_config(self.ctx, C.byref(shape.to_c()), C.byref(v), C.byref(mt),
+                                                   C.byref(ks), C.byref(sm)))
+        return {"variant": v.value, "mt": mt.value, "ks": ks.value, "sampler": sm.value}
 
 
 # ---- deterministic inputs ----------------------------------------------------------

@@ -188,13 +188,32 @@ def test_fused_fast_c2_tolerance(gpu_ctx, dcn, c2):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
 
 
-@pytest.mark.parametrize("mt,ks", [(1, 8), (1, 4), (2, 4), (2, 2)])
-@pytest.mark.parametrize("sampler", [0, 1])
-def test_fused_configs(gpu_ctx, dcn, c2, mt, ks, sampler):
-    s, h, ref32 = c2
-    log("case: fused config", mt, ks, sampler)
+FUSED_CONFIGS = [(1, 1, 8), (1, 1, 4), (1, 2, 4), (1, 2, 2),   # register variant (variant, mt, ks)
+                 (2, 1, 8), (2, 1, 16), (2, 2, 8),              # LDS-staged variant
+                 (3, 8, 8), (3, 4, 8), (3, 4, 4), (3, 2, 4),   # LDS windows (rows, waves)
+                 (4, 8, 8), (4, 4, 4)]                          # LDS windows + L1 lower rows
+
+
+def test_unsupported_fused_config_is_rejected(gpu_ctx, dcn, c2):
+    s, h, _ = c2
     packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
-    gpu_ctx.set_fused_config(mt, ks, sampler)
+    # 64-pixel tiles over 16 waves need 266 KB of LDS for the cross-wave reduction.
+    gpu_ctx.set_fused_config(2, 16, -1, dcn.VARIANT_STAGED)
+    try:
+        with pytest.raises(dcn.DeformConvError) as e:
+            gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+        assert e.value.status == dcn.INVALID_ARGUMENT and "unsupported fused config" in e.value.message
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+
+
+@pytest.mark.parametrize("variant,mt,ks", FUSED_CONFIGS)
+@pytest.mark.parametrize("sampler", [0, 1])
+def test_fused_configs(gpu_ctx, dcn, c2, variant, mt, ks, sampler):
+    s, h, ref32 = c2
+    log("case: fused config", variant, mt, ks, sampler)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(mt, ks, sampler, variant)
     try:
         out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
         again = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
@@ -254,21 +273,43 @@ EDGE_SHAPES = [
 
 @pytest.mark.parametrize("dims", EDGE_SHAPES, ids=lambda t: "x".join(map(str, t)))
 @pytest.mark.parametrize("sampler", [0, 1])
-def test_fused_edge_shapes(gpu_ctx, dcn, oracle, dims, sampler):
+@pytest.mark.parametrize("variant", [1, 2, 3, 4])
+def test_fused_edge_shapes(gpu_ctx, dcn, oracle, dims, sampler, variant):
     s = dcn.DeformConvShape(*dims)
     assert s.fused_supported
     d = rand_case(s, sum(dims), offset_scale=4.0)
     d["weight"] *= 0.5
     h = f16_inputs(d)
     w = widen(h)
-    log("case: fused edge", dims, "sampler", sampler)
+    log("case: fused edge", dims, "sampler", sampler, "variant", variant)
     packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
-    gpu_ctx.set_fused_config(0, 0, sampler)
+    gpu_ctx.set_fused_config(0, 0, sampler, variant)
     try:
         out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
     finally:
         gpu_ctx.set_fused_config(0, 0, -1)
     ref = oracle.forward_f32(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    mx, mean = errors(out, ref)
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
+
+
+@pytest.mark.parametrize("variant", [1, 2, 3, 4])
+def test_large_offsets_force_global_fallback(gpu_ctx, dcn, oracle, variant):
+    # Offsets up to +-40 px on a 64x64 map: a tile's sample box spans the whole plane
+    # (74 KB), larger than one LDS window, so the window variant gathers from global.
+    s = dcn.JASNA_SHAPE
+    d = rand_case(s, 40, offset_scale=40.0)
+    d["weight"] *= 0.3
+    h = f16_inputs(d)
+    w = widen(h)
+    log("case: offsets +-40, variant", variant)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(0, 0, -1, variant)
+    try:
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    ref = oracle.forward_f32_threads(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
     mx, mean = errors(out, ref)
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
@@ -280,8 +321,13 @@ def test_zero_padding_exact(gpu_ctx, dcn, c2):
     bias_out = np.repeat(h["bias"], s.output_height * s.output_width)
     for far in (1000.0, -1000.0, 66.0, -2.0 - 64.0):
         off = np.full_like(h["offset"], far)
-        out = gpu_ctx.run_float16_prepacked(s, h["input"], off, h["mask"], packed)
-        assert np.array_equal(out.view(np.uint16), bias_out.view(np.uint16)), far
+        for variant in (1, 2, 3, 4):
+            gpu_ctx.set_fused_config(0, 0, -1, variant)
+            try:
+                out = gpu_ctx.run_float16_prepacked(s, h["input"], off, h["mask"], packed)
+            finally:
+                gpu_ctx.set_fused_config(0, 0, -1, 0)
+            assert np.array_equal(out.view(np.uint16), bias_out.view(np.uint16)), (far, variant)
         out = gpu_ctx.run_float16(s, h["input"], off, h["mask"], h["weight"], h["bias"])
         assert np.array_equal(out.view(np.uint16), bias_out.view(np.uint16)), far
     zero_mask = np.zeros_like(h["mask"])
