@@ -39,6 +39,10 @@ WORKLOADS = {
 }
 
 
+KERNEL_NAMES = {1: "fused_kernel", 2: "staged_kernel", 3: "window_kernel", 4: "window_kernel",
+                5: "narrow_kernel"}
+
+
 def algorithmic_bytes(shape, elem=2) -> int:
     c = shape.counts()
     return elem * (c["input"] + c["offset"] + c["mask"] + c["output"] + c["weight"] + c["bias"])
@@ -100,6 +104,9 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=5, help="repetitions of the fused-only timing")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="after timing, run three device copies of this many MiB (the known-size "
+                         "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -181,6 +188,14 @@ def main() -> int:
         kernel_us.append(a.elapsed_time(b) * 1e3 / args.steps)
     k_us = statistics.median(kernel_us)
 
+    if args.calibration_copy_mib > 0:
+        src = torch.ones(args.calibration_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     # correctness of what was timed: finite output with the expected checksum scale
     res = out.cpu().numpy().view(np.float16)
     finite = bool(np.all(np.isfinite(res.astype(np.float32))))
@@ -224,7 +239,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
-            "kernel": "fused_kernel (sampler + MFMA GEMM)",
+            "kernel": KERNEL_NAMES.get(fused_cfg["variant"], "fused") + " (sampler + MFMA GEMM)",
             "algorithmic_bytes_per_launch": nbytes,
             "mfma_frac": flops / (k_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS,
         },

@@ -218,7 +218,9 @@ dcn_status dcn_forward_f16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape* 
  * the whole K range, an MFMA phase consumes it), 3 = LDS input windows (3x3 kernels:
  * per offset group, the bounding box of a 2D pixel tile's samples is copied to LDS and
  * gathered from there; mt = tile rows, ks = waves = 32-pixel row blocks), 4 = variant 3
- * with the lower corner row of each sample read through the L1 cache instead of LDS. sampler: 0 = reference arithmetic
+ * with the lower corner row of each sample read through the L1 cache instead of LDS,
+ * 5 = narrow 16-pixel tiles on 16x16x32 MFMA, one workgroup per CU on small maps
+ * (mt = 1, ks = waves splitting K: 8 or 12). sampler: 0 = reference arithmetic
  * (FP32 bilinear in the reference's association, half(sampled*mask): the im2col
  * values of deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into
  * the bilinear weights, packed-FP16 blend). mt = 32-pixel row blocks per tile (1, 2),

@@ -85,14 +85,17 @@ dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry&
                                bool window_ok) {
     const dcn::FusedConfig& o = ctx->fused_override;
     const long long tiles32 = (g.m + 31) / 32;
-    // Variant: small problems (one 64x64 map is 128 row blocks) need every CU busy and
-    // use 32-pixel tiles of the staged variant; large ones use LDS windows over 2D tiles.
+    // Variant: small problems (one 64x64 map is 128 row blocks of 32 pixels) need every
+    // CU busy and use 16-pixel tiles; large ones use LDS windows over 2D tiles.
     int variant = o.variant > 0 ? o.variant
-                                : (window_ok && tiles32 > 1024 ? dcn::kVariantWindow : dcn::kVariantStaged);
+                                : (window_ok && tiles32 > 1024 ? dcn::kVariantWindow : dcn::kVariantNarrow);
     const bool window = variant == dcn::kVariantWindow || variant == dcn::kVariantWindowSplit;
-    if (window && !window_ok) variant = dcn::kVariantStaged;
+    if (window && !window_ok) variant = dcn::kVariantNarrow;
     dcn::FusedConfig cfg{variant, 1, 8, dcn::kSamplerFast};
-    if (variant == dcn::kVariantWindow || variant == dcn::kVariantWindowSplit) {
+    if (variant == dcn::kVariantNarrow) {
+        cfg.mt = 1;
+        cfg.ks = 12;  // waves: 36 K-steps of the reference layer in 3 per wave
+    } else if (variant == dcn::kVariantWindow || variant == dcn::kVariantWindowSplit) {
         // A 4 x 32 tile on 4 waves with single-buffered windows: two workgroups share a
         // CU, so one copies its windows while the other multiplies.
         cfg.mt = 4;  // tile rows
@@ -118,6 +121,7 @@ dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry&
 }
 
 bool config_supported(const dcn::FusedConfig& c, const dcn::FusedGeometry& g) {
+    if (c.variant == dcn::kVariantNarrow) return c.mt == 1 && (c.ks == 8 || c.ks == 12);
     if (c.variant == dcn::kVariantWindow || c.variant == dcn::kVariantWindowSplit)
         return (c.ks == 8 && (c.mt == 8 || c.mt == 4)) || (c.ks == 4 && (c.mt == 4 || c.mt == 2));
     if (c.variant == dcn::kVariantStaged)
@@ -187,6 +191,12 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
         DCN_TRY(ensure_workspace(ctx, dcn::cb8_bytes(*shape, g), stream));
         DCN_HIP(ctx, dcn::launch_pack_cb8(ks, g, (const uint16_t*)d_input, ctx->workspace, stream));
         cb8 = ctx->workspace;
+    }
+    if (cfg.variant == dcn::kVariantNarrow) {
+        DCN_HIP(ctx, dcn::launch_narrow_f16(ks, g, cfg, cb8, (const uint16_t*)d_offset,
+                                            (const uint16_t*)d_mask, packed->weights_narrow,
+                                            packed->bias, (uint16_t*)d_output, stream));
+        return DCN_OK;
     }
     if (cfg.variant == dcn::kVariantWindow || cfg.variant == dcn::kVariantWindowSplit) {
         DCN_HIP(ctx, dcn::launch_window_f16(ks, g, cfg, cb8, (const uint16_t*)d_offset,
@@ -331,7 +341,7 @@ dcn_status dcn_reserve(dcn_context* ctx, const dcn_shape* shape) {
 
 dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, int sampler) {
     if (!ctx) return DCN_INVALID_ARGUMENT;
-    if (variant < 0 || variant > 4 || mt < 0 || mt > 8 || ks < 0 || sampler < -1 || sampler > 1)
+    if (variant < 0 || variant > 5 || mt < 0 || mt > 8 || ks < 0 || sampler < -1 || sampler > 1)
         return fail(ctx, DCN_INVALID_ARGUMENT, "invalid fused config");
     ctx->fused_override = dcn::FusedConfig{variant, mt, ks, sampler};
     return DCN_OK;
@@ -419,6 +429,7 @@ static dcn_status make_packed(dcn_context* ctx, const dcn_shape* shape, dcn_pack
     p->device = ctx->device;
     if (hipMalloc(&p->weights, dcn::packed_weight_bytes(g)) != hipSuccess ||
         hipMalloc((void**)&p->bias, (size_t)shape->output_channels * sizeof(float)) != hipSuccess ||
+        hipMalloc(&p->weights_narrow, dcn::narrow_packed_bytes(g)) != hipSuccess ||
         (dcn::window_supported(*shape) &&
          hipMalloc(&p->weights_group, dcn::window_packed_bytes(*shape)) != hipSuccess)) {
         dcn_packed_free(p);
@@ -445,6 +456,9 @@ dcn_status dcn_prepack_f16_dev(dcn_context* ctx, const dcn_shape* shape, const v
                                                (const uint16_t*)d_weight, (int)layout,
                                                (const uint16_t*)d_bias, p->weights, p->bias,
                                                (hipStream_t)stream);
+    if (e == hipSuccess)
+        e = dcn::launch_prepack_narrow(dcn::to_kshape(*shape), p->geometry, (const uint16_t*)d_weight,
+                                       (int)layout, p->weights_narrow, (hipStream_t)stream);
     if (e == hipSuccess && p->weights_group)
         e = dcn::launch_prepack_group(dcn::to_kshape(*shape), (const uint16_t*)d_weight, (int)layout,
                                       p->weights_group, (hipStream_t)stream);
@@ -487,6 +501,7 @@ void dcn_packed_free(dcn_packed* p) {
     if (p->weights) (void)hipFree(p->weights);
     if (p->bias) (void)hipFree(p->bias);
     if (p->weights_group) (void)hipFree(p->weights_group);
+    if (p->weights_narrow) (void)hipFree(p->weights_narrow);
     delete p;
 }
 

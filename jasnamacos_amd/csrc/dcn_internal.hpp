@@ -62,6 +62,9 @@ enum FusedVariant : int {
     // kVariantWindow with the lower corner row of each sample read through the L1
     // (the window is there too after its copy), splitting gathers between LDS and L1.
     kVariantWindowSplit = 4,
+    // 16-pixel tiles on v_mfma_f32_16x16x32_f16 with every load of a wave's K-steps in
+    // flight at once: one workgroup per CU on small problems. Config: ks = waves (8, 12).
+    kVariantNarrow = 5,
 };
 
 struct FusedConfig {
@@ -103,6 +106,21 @@ hipError_t launch_im2col_f16(const KShape& s, const uint16_t* in, const uint16_t
 hipError_t launch_flag_nonfinite_f16(const uint16_t* values, size_t count, uint32_t* flag,
                                      hipStream_t stream);
 
+// Narrow variant (16-pixel tiles, v_mfma_f32_16x16x32_f16; dcn_kernels_narrow.hip).
+int narrow_ksteps(const FusedGeometry& g);
+size_t narrow_packed_bytes(const FusedGeometry& g);
+hipError_t launch_prepack_narrow(const KShape& s, const FusedGeometry& g, const uint16_t* w,
+                                 int layout, void* packed_w, hipStream_t stream);
+hipError_t launch_narrow_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
+                             const void* cb8, const uint16_t* off, const uint16_t* mask,
+                             const void* packed_w, const float* packed_b, uint16_t* out,
+                             hipStream_t stream);
+
+// Constant of dev::fast_div: ceil(2^32 / d) for d > 1, 0 for d == 1.
+inline uint32_t magic_for(int d) {
+    return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) / (uint64_t)d);
+}
+
 // Bytes of the prepacked B-fragment buffer for a geometry.
 inline size_t packed_weight_bytes(const FusedGeometry& g) {
     return (size_t)g.ksteps * g.nb * 64 * 8 * sizeof(uint16_t);
@@ -143,6 +161,7 @@ struct dcn_packed {
     dcn::FusedGeometry geometry{};
     void* weights = nullptr;    // B fragments, packed_weight_bytes(geometry)
     void* weights_group = nullptr;  // per-group B fragments of the window variant (or null)
+    void* weights_narrow = nullptr; // 16-wide B fragments of the narrow variant
     float* bias = nullptr;      // Cout floats
     int device = 0;
 };

@@ -31,6 +31,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include "dcn_device.hpp"
 #include "dcn_internal.hpp"
 
 #pragma clang fp contract(off)
@@ -38,26 +39,9 @@
 namespace dcn {
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+using namespace dev;
 
-constexpr int kPad = DCN_CB8_PAD;
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
-constexpr int kBufferFlags = 0x00020000;  // raw buffer, gfx9 family
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
-                                             kBufferFlags);
-}
-__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_offset, 0, 0));
-}
-__device__ __forceinline__ float load_half(__amdgpu_buffer_rsrc_t r, uint32_t byte_offset) {
-    const short v = __builtin_amdgcn_raw_buffer_load_b16(r, (int)byte_offset, 0, 0);
-    return (float)__builtin_bit_cast(_Float16, v);
-}
 
 struct FusedArgs {
     const void* xin;       // CB8 input
@@ -70,39 +54,6 @@ struct FusedArgs {
     int H, W, Wo, HWo, KW, KA, ph, pw, sh, sw, dh, dw;
     int G, CB, CBLK, Hp, Wp, KB, ksteps, M, Cout;
 };
-
-// Reference arithmetic (MetalShader.swift:369-379): FP32 bilinear in the reference's
-// association, times the mask, rounded once to FP16.
-__device__ __forceinline__ h8 blend_exact(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 q11,
-                                          float ly, float lx, float m) {
-    const h8 a = __builtin_bit_cast(h8, q00), b = __builtin_bit_cast(h8, q01);
-    const h8 c = __builtin_bit_cast(h8, q10), d = __builtin_bit_cast(h8, q11);
-    h8 r;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float s = (float)a[e] * (1.0f - ly) * (1.0f - lx) + (float)b[e] * (1.0f - ly) * lx +
-                        (float)c[e] * ly * (1.0f - lx) + (float)d[e] * ly * lx;
-        r[e] = round_f16(s * m);
-    }
-    return r;
-}
-
-// Mask folded into the four FP32 bilinear weights, each rounded once to FP16, then
-// a packed-FP16 blend: 4 conversions + 16 packed FMAs per 8 channels.
-__device__ __forceinline__ h8 blend_fast(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 q11,
-                                         float ly, float lx, float m) {
-    const float t0 = m * (1.0f - ly);
-    const float t1 = m * ly;
-    const h8 w00 = (_Float16)(t0 * (1.0f - lx));  // scalar -> all 8 lanes
-    const h8 w01 = (_Float16)(t0 * lx);
-    const h8 w10 = (_Float16)(t1 * (1.0f - lx));
-    const h8 w11 = (_Float16)(t1 * lx);
-    h8 r = w00 * __builtin_bit_cast(h8, q00);
-    r = __builtin_elementwise_fma(w01, __builtin_bit_cast(h8, q01), r);
-    r = __builtin_elementwise_fma(w10, __builtin_bit_cast(h8, q10), r);
-    r = __builtin_elementwise_fma(w11, __builtin_bit_cast(h8, q11), r);
-    return r;
-}
 
 template <int NB, int MT, int KS, int SAMPLER>
 __global__ __launch_bounds__(64 * KS) void fused_kernel(FusedArgs a) {
@@ -185,8 +136,7 @@ __global__ __launch_bounds__(64 * KS) void fused_kernel(FusedArgs a) {
             const u32x4 q01 = load16(xr, byte0 + 16u);
             const u32x4 q10 = load16(xr, byte1);
             const u32x4 q11 = load16(xr, byte1 + 16u);
-            A[mt] = SAMPLER == kSamplerExact ? blend_exact(q00, q01, q10, q11, ly, lx, m)
-                                             : blend_fast(q00, q01, q10, q11, ly, lx, m);
+            A[mt] = blend<SAMPLER>(q00, q01, q10, q11, ly, lx, m);
         }
         h8 Bf[NB];
 #pragma unroll
@@ -250,10 +200,6 @@ struct StagedArgs {
     uint32_t magic_cb, magic_ka, magic_kw;  // ceil(2^32 / d) for d = CB, KA, KW
 };
 
-__device__ __forceinline__ int fast_div(int x, uint32_t magic) {
-    // floor(x / d) for 0 <= x < 2^16 and d < 2^16, magic = ceil(2^32 / d).
-    return (int)__umulhi((uint32_t)x, magic);
-}
 
 template <int NB, int MT, int NW, int UB, int SPW, int SAMPLER>
 __global__ __launch_bounds__(64 * NW) void staged_kernel(StagedArgs sa) {
@@ -337,9 +283,7 @@ __global__ __launch_bounds__(64 * NW) void staged_kernel(StagedArgs sa) {
             for (int i = 0; i < UB; ++i) {
                 const int kb = kb0 + (base + i) * KSTRIDE;
                 if (kb < kbp) {
-                    const h8 v = SAMPLER == kSamplerExact
-                                     ? blend_exact(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], m[i])
-                                     : blend_fast(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], m[i]);
+                    const h8 v = blend<SAMPLER>(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], m[i]);
                     *reinterpret_cast<h8*>(lds + ((size_t)kb * TP + pl) * 16) = v;
                 }
             }
@@ -412,51 +356,51 @@ __global__ __launch_bounds__(64 * NW) void staged_kernel(StagedArgs sa) {
     }
 }
 
-// NCHW FP16 -> padded CB8. One thread per padded position and channel block: eight
-// 2-byte loads (coalesced along x) and one 16-byte store. Border positions get zeros.
+// NCHW FP16 -> padded CB8. Grid (ceil(Hp*Wp / 256), B * Cin/8): one thread per padded
+// position of one channel block, eight 2-byte loads (coalesced along x) and one 16-byte
+// store; border positions get zeros. 32-bit index math only.
 __global__ __launch_bounds__(256) void pack_cb8_kernel(const uint16_t* __restrict__ in,
-                                                       u32x4* __restrict__ out, int B, int Cin,
-                                                       int H, int W, int Hp, int Wp,
-                                                       long total) {
-    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= total) return;
-    const int xp = (int)(gid % Wp);
-    long q = gid / Wp;
-    const int yp = (int)(q % Hp);
-    q /= Hp;
-    const int cblk = (int)(q % (Cin / 8));
-    const int b = (int)(q / (Cin / 8));
+                                                       u32x4* __restrict__ out, int H, int W,
+                                                       int Hp, int Wp) {
+    const int pos = blockIdx.x * 256 + threadIdx.x;
+    const int plane_p = Hp * Wp;
+    if (pos >= plane_p) return;
+    const int yp = pos / Wp;
     const int y = yp - kPad;
-    const int x = xp - kPad;
+    const int x = pos - yp * Wp - kPad;
     u32x4 v = {0u, 0u, 0u, 0u};
     if (y >= 0 && y < H && x >= 0 && x < W) {
         const size_t plane = (size_t)H * W;
-        const uint16_t* src = in + ((size_t)b * Cin + (size_t)cblk * 8) * plane + (size_t)y * W + x;
+        // blockIdx.y = b * Cin/8 + cblk: the first of its 8 NCHW planes is 8 * blockIdx.y.
+        const uint16_t* src = in + (size_t)blockIdx.y * 8 * plane + (size_t)y * W + x;
 #pragma unroll
         for (int d = 0; d < 4; ++d)
             v[d] = (uint32_t)src[(2 * d) * plane] | ((uint32_t)src[(2 * d + 1) * plane] << 16);
     }
-    out[gid] = v;
+    out[(size_t)blockIdx.y * plane_p + pos] = v;
 }
 
-// Weights -> MFMA B fragments [ksteps][NB][64 lanes][8], K order as in fused_kernel.
-// layout 0 = OIHW, 1 = [ic][k][oc] (.dcnfp16). Bias widened to FP32.
+// Weights -> MFMA B fragments [ksteps][NB][64 lanes][8] for column groups of MW
+// output channels (32: v_mfma_f32_32x32x16_f16, 16: v_mfma_f32_16x16x32_f16). Lane l
+// of K-step s holds output channel nb*MW + l%MW and K-block (64/MW)*s + l/MW, the
+// order in which the fused kernels sample A. layout 0 = OIHW, 1 = [ic][k][oc]
+// (.dcnfp16). Bias widened to FP32 (when bpk is non-null).
 __global__ __launch_bounds__(256) void prepack_kernel(const uint16_t* __restrict__ w, int layout,
                                                       const uint16_t* __restrict__ bias,
                                                       uint16_t* __restrict__ wpk,
                                                       float* __restrict__ bpk, int Cin, int Cout,
-                                                      int KA, int CB, int KB, int NB,
+                                                      int KA, int CB, int KB, int NB, int MW,
                                                       long total) {
     const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid < Cout) bpk[gid] = (float)__builtin_bit_cast(_Float16, bias[gid]);
+    if (bpk != nullptr && gid < Cout) bpk[gid] = (float)__builtin_bit_cast(_Float16, bias[gid]);
     if (gid >= total) return;
     const int e = (int)(gid & 7);
     const int lane = (int)((gid >> 3) & 63);
     const long q = gid >> 9;
     const int nb = (int)(q % NB);
     const int s = (int)(q / NB);
-    const int kb = 2 * s + (lane >> 5);
-    const int oc = nb * 32 + (lane & 31);
+    const int kb = (64 / MW) * s + lane / MW;
+    const int oc = nb * MW + lane % MW;
     uint16_t v = 0;
     if (kb < KB && oc < Cout) {
         const int gt = kb / CB;
@@ -592,10 +536,6 @@ hipError_t launch_staged_s(const StagedArgs& sa, int nb, const FusedConfig& cfg,
     }
 }
 
-uint32_t magic_for(int d) {
-    return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) / (uint64_t)d);
-}
-
 template <int SAMPLER>
 hipError_t launch_fused_s(const FusedArgs& a, int nb, const FusedConfig& cfg, hipStream_t stream) {
     switch (nb) {
@@ -627,10 +567,11 @@ bool fused_geometry(const dcn_shape& s, FusedGeometry* g) {
 
 hipError_t launch_pack_cb8(const KShape& s, const FusedGeometry& g, const uint16_t* in_nchw,
                            void* cb8, hipStream_t stream) {
-    const long total = (long)s.B * g.cblk * g.hp * g.wp;
-    const long grid = (total + 255) / 256;
-    hipLaunchKernelGGL(pack_cb8_kernel, dim3((unsigned)grid), dim3(256), 0, stream, in_nchw,
-                       (u32x4*)cb8, s.B, s.Cin, s.H, s.W, g.hp, g.wp, total);
+    const long planes = (long)s.B * g.cblk;
+    if (planes > 65535) return hipErrorInvalidValue;  // grid.y limit
+    const unsigned gx = (unsigned)(((long)g.hp * g.wp + 255) / 256);
+    hipLaunchKernelGGL(pack_cb8_kernel, dim3(gx, (unsigned)planes), dim3(256), 0, stream, in_nchw,
+                       (u32x4*)cb8, s.H, s.W, g.hp, g.wp);
     return hipGetLastError();
 }
 
@@ -640,8 +581,18 @@ hipError_t launch_prepack_weights(const KShape& s, const FusedGeometry& g, const
     const long total = (long)g.ksteps * g.nb * 64 * 8;
     const long grid = (std::max<long>(total, s.Cout) + 255) / 256;
     hipLaunchKernelGGL(prepack_kernel, dim3((unsigned)grid), dim3(256), 0, stream, w, layout, bias,
-                       (uint16_t*)packed_w, packed_b, s.Cin, s.Cout, g.ka, g.cb, g.kb, g.nb,
+                       (uint16_t*)packed_w, packed_b, s.Cin, s.Cout, g.ka, g.cb, g.kb, g.nb, 32,
                        total);
+    return hipGetLastError();
+}
+
+hipError_t launch_prepack_narrow(const KShape& s, const FusedGeometry& g, const uint16_t* w,
+                                 int layout, void* packed_w, hipStream_t stream) {
+    const long total = (long)narrow_ksteps(g) * (2 * g.nb) * 64 * 8;
+    const long grid = (total + 255) / 256;
+    hipLaunchKernelGGL(prepack_kernel, dim3((unsigned)grid), dim3(256), 0, stream, w, layout,
+                       (const uint16_t*)nullptr, (uint16_t*)packed_w, (float*)nullptr, s.Cin,
+                       s.Cout, g.ka, g.cb, g.kb, 2 * g.nb, 16, total);
     return hipGetLastError();
 }
 

@@ -1,0 +1,264 @@
+// Narrow-tile fused FP16 DCNv2 for gfx950: small problems (one 64x64 map is 4096
+// output pixels).
+//
+// Why: every gather corner and every weight fragment of the fused kernels passes
+// through the vector L1 of the CU that runs the workgroup. Per workgroup that is
+// (tile pixels x K-blocks x 64 B) of corners plus the whole packed weight matrix
+// (147 KB at 128 -> 64, 3x3). With 32-pixel tiles a 64x64 map has 128 workgroups:
+// half the CUs idle and 442 KB through each busy L1. 16-pixel tiles put one
+// workgroup on each of the 256 CUs with 295 KB each.
+//
+// MFMA: v_mfma_f32_16x16x32_f16. Lane l supplies A row l%16 with K elements
+// 8*(l/16) .. +7, and B column l%16 with the same K elements; output element v of
+// lane l is row 4*(l/16) + v, column l%16. K-step s covers K-blocks 4s .. 4s+3 (a
+// K-block is 8 channels of one offset group and tap, as in the other fused kernels),
+// so lane l samples K-block 4s + l/16 for pixel l%16: one bilinear coordinate, four
+// 16-byte corners of the CB8 input. prepack_kernel with 16-wide column groups writes
+// the weights in the same order.
+//
+// Workgroup: NW waves split the K-steps; every wave covers all 16 pixels and all Cout
+// columns. A wave issues all loads of U K-steps (weight fragments, offsets and mask,
+// then corners) before the first blend, so its critical path is two dependent memory
+// round trips rather than one per K-step. Partial sums meet in LDS; the epilogue adds
+// the bias, rounds to FP16 and stores 16 consecutive pixels per output channel.
+// Tiles are ordered so that the workgroups of one XCD cover consecutive pixels.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "dcn_device.hpp"
+#include "dcn_internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace dcn {
+namespace {
+
+using namespace dev;
+
+struct NarrowArgs {
+    const void* xin;       // CB8 input [B][CBLK][Hp][Wp][8]
+    const uint16_t* off;   // [B][2*G*KA][HWo]
+    const uint16_t* msk;   // [B][G*KA][HWo]
+    const void* wpk;       // [ksteps][NB][64][8] FP16, 16-wide column groups
+    const float* bias;     // [Cout]
+    uint16_t* out;         // [B][Cout][HWo]
+    uint32_t xin_bytes, off_bytes, msk_bytes, wpk_bytes;
+    int H, W, Wo, HWo, KW, KA, ph, pw, sh, sw, dh, dw;
+    int GKA, CB, CBLK, Hp, Wp, KB, ksteps, M, Cout, tiles;  // GKA = G * KA
+    uint32_t magic_cb, magic_ka, magic_kw;  // fast_div constants for CB, KA, KW
+};
+
+template <int NB, int NW, int U, int SAMPLER>
+__global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
+    extern __shared__ float red[];  // [NW][NB][4][65]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int quarter = lane >> 4;
+
+    const int per_xcd = (a.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+
+    const int p = tile * 16 + (lane & 15);
+    const bool pvalid = p < a.M;
+    const int pc = pvalid ? p : a.M - 1;
+    const int b = pc / a.HWo;
+    const int sp = pc - b * a.HWo;
+    const int oy = sp / a.Wo;
+    const int ox = sp - oy * a.Wo;
+    const int base_y = oy * a.sh - a.ph;
+    const int base_x = ox * a.sw - a.pw;
+    const uint32_t offb = (uint32_t)(b * 2 * a.GKA) * a.HWo + sp;
+    const uint32_t mskb = (uint32_t)(b * a.GKA) * a.HWo + sp;
+    // 16-byte units; includes the border shift so (iy, ix) may be negative down to -2.
+    const uint32_t xinb = (uint32_t)(b * a.CBLK * a.Hp + kPad) * a.Wp + kPad;
+
+    f32x4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{};
+
+    const int s0 = wave * a.ksteps / NW;
+    const int s1 = (wave + 1) * a.ksteps / NW;
+    for (int sb = s0; sb < s1; sb += U) {
+        h8 Bf[U][NB];
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int s = sb + i < s1 ? sb + i : s1 - 1;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)((s * NB + nb) * 64 + lane) * 16u));
+        }
+        float dy[U], dx[U], m[U];
+        int plane[U], yb[U], xb[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int kb = 4 * (sb + i) + quarter;
+            const int kbc = kb < a.KB ? kb : a.KB - 1;
+            const int gt = fast_div(kbc, a.magic_cb);  // g * KA + tap
+            const int cb = kbc - gt * a.CB;
+            const int g = fast_div(gt, a.magic_ka);
+            const int tap = gt - g * a.KA;
+            const int ky = fast_div(tap, a.magic_kw);
+            const int kx = tap - ky * a.KW;
+            plane[i] = g * a.CB + cb;
+            yb[i] = base_y + ky * a.dh;
+            xb[i] = base_x + kx * a.dw;
+            dy[i] = load_half(orr, (offb + (uint32_t)(2 * gt) * a.HWo) * 2u);
+            dx[i] = load_half(orr, (offb + (uint32_t)(2 * gt + 1) * a.HWo) * 2u);
+            m[i] = load_half(mr, (mskb + (uint32_t)gt * a.HWo) * 2u);
+        }
+        u32x4 q[U][4];
+        float ly[U], lx[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int kb = 4 * (sb + i) + quarter;
+            const bool live = pvalid && sb + i < s1 && kb < a.KB;
+            // y = float(oy*sh - ph + ky*dh) + dy, as MetalShader.swift:327-332. Dead
+            // units (tile tail, K padding) sample the zero border with weight 0.
+            const float y = live ? (float)yb[i] + dy[i] : -16.0f;
+            const float x = live ? (float)xb[i] + dx[i] : -16.0f;
+            m[i] = live ? m[i] : 0.0f;
+            const float fy = floorf(y);
+            const float fx = floorf(x);
+            ly[i] = y - fy;
+            lx[i] = x - fx;
+            const int iy = (int)fminf(fmaxf(fy, (float)-kPad), (float)a.H);
+            const int ix = (int)fminf(fmaxf(fx, (float)-kPad), (float)a.W);
+            const uint32_t u = xinb + (uint32_t)(plane[i] * a.Hp + iy) * a.Wp + ix;
+            q[i][0] = load16(xr, u * 16u);
+            q[i][1] = load16(xr, u * 16u + 16u);
+            q[i][2] = load16(xr, (u + a.Wp) * 16u);
+            q[i][3] = load16(xr, (u + a.Wp) * 16u + 16u);
+        }
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            if (sb + i < s1) {  // uniform across the wave
+                const h8 A = blend<SAMPLER>(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], m[i]);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+    __syncthreads();
+
+    for (int idx = tid; idx < 16 * NB * 16; idx += 64 * NW) {
+        const int pl = idx & 15;
+        const int oc = idx >> 4;
+        const int nb = oc >> 4;
+        const int src = ((pl >> 2) << 4) + (oc & 15);
+        const int v = pl & 3;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
+        const int pp = tile * 16 + pl;
+        if (pp < a.M) {
+            const int bb = pp / a.HWo;
+            const int spp = pp - bb * a.HWo;
+            a.out[((size_t)bb * a.Cout + oc) * a.HWo + spp] =
+                __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
+        }
+    }
+}
+
+template <int NB, int NW, int SAMPLER>
+hipError_t launch_narrow_t(const NarrowArgs& a, hipStream_t stream) {
+    // K-steps whose loads are in flight at once, sized to the register budget of
+    // NW / 4 waves per SIMD (more output columns hold more weight fragments).
+    constexpr int U = NB >= 6 ? (NW == 12 ? 2 : 3) : (NW == 12 ? 3 : 5);
+    const size_t lds = (size_t)NW * NB * 4 * 65 * sizeof(float);
+    auto kernel = &narrow_kernel<NB, NW, U, SAMPLER>;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    const int grid = (a.tiles + 7) / 8 * 8;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(64 * NW), lds, stream, a);
+    return hipGetLastError();
+}
+
+template <int SAMPLER>
+hipError_t launch_narrow_s(const NarrowArgs& a, int nb, int nw, hipStream_t stream) {
+    if (nw == 8) {
+        switch (nb) {
+            case 2: return launch_narrow_t<2, 8, SAMPLER>(a, stream);
+            case 4: return launch_narrow_t<4, 8, SAMPLER>(a, stream);
+            case 6: return launch_narrow_t<6, 8, SAMPLER>(a, stream);
+            case 8: return launch_narrow_t<8, 8, SAMPLER>(a, stream);
+        }
+    } else if (nw == 12) {
+        switch (nb) {
+            case 2: return launch_narrow_t<2, 12, SAMPLER>(a, stream);
+            case 4: return launch_narrow_t<4, 12, SAMPLER>(a, stream);
+            case 6: return launch_narrow_t<6, 12, SAMPLER>(a, stream);
+            case 8: return launch_narrow_t<8, 12, SAMPLER>(a, stream);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+int narrow_ksteps(const FusedGeometry& g) { return (g.kb + 3) / 4; }
+
+size_t narrow_packed_bytes(const FusedGeometry& g) {
+    return (size_t)narrow_ksteps(g) * (g.nb * 2) * 64 * 8 * sizeof(uint16_t);
+}
+
+hipError_t launch_narrow_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
+                             const void* cb8, const uint16_t* off, const uint16_t* mask,
+                             const void* packed_w, const float* packed_b, uint16_t* out,
+                             hipStream_t stream) {
+    NarrowArgs a;
+    a.xin = cb8;
+    a.off = off;
+    a.msk = mask;
+    a.wpk = packed_w;
+    a.bias = packed_b;
+    a.out = out;
+    const size_t hwo = (size_t)s.Ho * s.Wo;
+    a.xin_bytes = (uint32_t)((size_t)s.B * g.cblk * g.hp * g.wp * 16);
+    a.off_bytes = (uint32_t)((size_t)s.B * 2 * s.og * g.ka * hwo * 2);
+    a.msk_bytes = (uint32_t)((size_t)s.B * s.og * g.ka * hwo * 2);
+    a.wpk_bytes = (uint32_t)narrow_packed_bytes(g);
+    a.H = s.H;
+    a.W = s.W;
+    a.Wo = s.Wo;
+    a.HWo = (int)hwo;
+    a.KW = s.KW;
+    a.KA = g.ka;
+    a.ph = s.ph;
+    a.pw = s.pw;
+    a.sh = s.sh;
+    a.sw = s.sw;
+    a.dh = s.dh;
+    a.dw = s.dw;
+    a.GKA = s.og * g.ka;
+    a.CB = g.cb;
+    a.CBLK = g.cblk;
+    a.Hp = g.hp;
+    a.Wp = g.wp;
+    a.KB = g.kb;
+    a.ksteps = narrow_ksteps(g);
+    a.M = (int)g.m;
+    a.Cout = s.Cout;
+    a.tiles = (int)((g.m + 15) / 16);
+    a.magic_cb = magic_for(g.cb);
+    a.magic_ka = magic_for(g.ka);
+    a.magic_kw = magic_for(s.KW);
+    if (cfg.sampler == kSamplerExact) return launch_narrow_s<kSamplerExact>(a, g.nb * 2, cfg.ks, stream);
+    return launch_narrow_s<kSamplerFast>(a, g.nb * 2, cfg.ks, stream);
+}
+
+}  // namespace dcn

@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <climits>
 
+#include "dcn_device.hpp"
 #include "dcn_internal.hpp"
 
 #pragma clang fp contract(off)
@@ -39,26 +40,11 @@
 namespace dcn {
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+using namespace dev;
 
-constexpr int kPad = DCN_CB8_PAD;
-constexpr int kBufferFlags = 0x00020000;
 // LDS for the windows of a workgroup: double-buffered (one workgroup per CU) or single
 // (two workgroups share a CU and overlap each other's copy and compute phases).
 __host__ __device__ constexpr int window_lds(int nbuf) { return nbuf == 2 ? 144 * 1024 : 72 * 1024; }
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferFlags);
-}
-__device__ __forceinline__ u32x4 gload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
-}
-__device__ __forceinline__ float gload_half(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    const short v = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
-    return (float)__builtin_bit_cast(_Float16, v);
-}
 
 struct WindowArgs {
     const void* xin;      // CB8 input [B][CBLK][Hp][Wp][8]
@@ -72,34 +58,6 @@ struct WindowArgs {
     int G, CBLK, Hp, Wp, Cout;
     int tiles_y, tiles_x, tiles;  // tile grid per image, total
 };
-
-__device__ __forceinline__ h8 blend_exact_w(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 q11, float ly,
-                                            float lx, float m) {
-    const h8 a = __builtin_bit_cast(h8, q00), b = __builtin_bit_cast(h8, q01);
-    const h8 c = __builtin_bit_cast(h8, q10), d = __builtin_bit_cast(h8, q11);
-    h8 r;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const float s = (float)a[e] * (1.0f - ly) * (1.0f - lx) + (float)b[e] * (1.0f - ly) * lx +
-                        (float)c[e] * ly * (1.0f - lx) + (float)d[e] * ly * lx;
-        r[e] = round_f16(s * m);
-    }
-    return r;
-}
-__device__ __forceinline__ h8 blend_fast_w(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 q11, float ly,
-                                           float lx, float m) {
-    const float t0 = m * (1.0f - ly);
-    const float t1 = m * ly;
-    const h8 w00 = (_Float16)(t0 * (1.0f - lx));
-    const h8 w01 = (_Float16)(t0 * lx);
-    const h8 w10 = (_Float16)(t1 * (1.0f - lx));
-    const h8 w11 = (_Float16)(t1 * lx);
-    h8 r = w00 * __builtin_bit_cast(h8, q00);
-    r = __builtin_elementwise_fma(w01, __builtin_bit_cast(h8, q01), r);
-    r = __builtin_elementwise_fma(w10, __builtin_bit_cast(h8, q10), r);
-    r = __builtin_elementwise_fma(w11, __builtin_bit_cast(h8, q11), r);
-    return r;
-}
 
 // Unit u of a stage (0 .. 2*KS-1): group offset within the stage and tap.
 template <int GPS>
@@ -173,9 +131,9 @@ __global__ __launch_bounds__(64 * NW) void window_kernel(WindowArgs a) {
             int tap, go;
             unit_of(k, tap, go);
             const uint32_t ch = (uint32_t)(go * 9 + tap);
-            rdy[k] = gload_half(orr, off_lane + 2u * ch * hwo2, so);
-            rdx[k] = gload_half(orr, off_lane + (2u * ch + 1u) * hwo2, so);
-            rm[k] = gload_half(mr, msk_lane + ch * hwo2, sm);
+            rdy[k] = load_half(orr, off_lane + 2u * ch * hwo2, so);
+            rdx[k] = load_half(orr, off_lane + (2u * ch + 1u) * hwo2, so);
+            rm[k] = load_half(mr, msk_lane + ch * hwo2, sm);
         }
     };
     int iy[KS], ix[KS];
@@ -280,7 +238,7 @@ __global__ __launch_bounds__(64 * NW) void window_kernel(WindowArgs a) {
                 const int col = c - r * w.ww;
                 const uint32_t gpos = (plane_row0 + (uint32_t)r) * a.Wp + (uint32_t)(w.x0 + col + kPad);
                 cc[i] = c;
-                v[i] = gload16(xr, gpos * 16u, 0);
+                v[i] = load16(xr, gpos * 16u, 0);
             }
 #pragma unroll
             for (int i = 0; i < CPT; ++i) *reinterpret_cast<u32x4*>(dst + (size_t)cc[i] * 16) = v[i];
@@ -299,7 +257,7 @@ __global__ __launch_bounds__(64 * NW) void window_kernel(WindowArgs a) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
             Bq[slot][nb] = __builtin_bit_cast(
-                h8, gload16(wr, (uint32_t)(((st * KS + k) * NB + nb) * 64 + lane) * 16u, 0));
+                h8, load16(wr, (uint32_t)(((st * KS + k) * NB + nb) * 64 + lane) * 16u, 0));
     };
 
     // ---- prologue: stage 0 ----
@@ -341,20 +299,19 @@ __global__ __launch_bounds__(64 * NW) void window_kernel(WindowArgs a) {
                 q00 = *reinterpret_cast<const u32x4*>(p);
                 q01 = *reinterpret_cast<const u32x4*>(p + 16);
                 if (SPLIT) {
-                    q10 = gload16(xr, (gbase + a.Wp) * 16u, 0);
-                    q11 = gload16(xr, (gbase + a.Wp) * 16u + 16u, 0);
+                    q10 = load16(xr, (gbase + a.Wp) * 16u, 0);
+                    q11 = load16(xr, (gbase + a.Wp) * 16u + 16u, 0);
                 } else {
                     q10 = *reinterpret_cast<const u32x4*>(p + (size_t)w.ww * 16);
                     q11 = *reinterpret_cast<const u32x4*>(p + (size_t)w.ww * 16 + 16);
                 }
             } else {
-                q00 = gload16(xr, gbase * 16u, 0);
-                q01 = gload16(xr, gbase * 16u + 16u, 0);
-                q10 = gload16(xr, (gbase + a.Wp) * 16u, 0);
-                q11 = gload16(xr, (gbase + a.Wp) * 16u + 16u, 0);
+                q00 = load16(xr, gbase * 16u, 0);
+                q01 = load16(xr, gbase * 16u + 16u, 0);
+                q10 = load16(xr, (gbase + a.Wp) * 16u, 0);
+                q11 = load16(xr, (gbase + a.Wp) * 16u + 16u, 0);
             }
-            h8 A = SAMPLER == kSamplerExact ? blend_exact_w(q00, q01, q10, q11, ly[k], lx[k], mm[k])
-                                            : blend_fast_w(q00, q01, q10, q11, ly[k], lx[k], mm[k]);
+            h8 A = blend<SAMPLER>(q00, q01, q10, q11, ly[k], lx[k], mm[k]);
             if (GPS == 1 && k == KS - 1 && half) A = h8{};  // the zero tenth unit
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)

@@ -40,6 +40,9 @@ SAMPLER_FAST = 1
 VARIANT_AUTO = 0
 VARIANT_REGISTER = 1
 VARIANT_STAGED = 2
+VARIANT_WINDOW = 3
+VARIANT_WINDOW_SPLIT = 4
+VARIANT_NARROW = 5
 
 DIRECTIONS = ("backward_1", "forward_1", "backward_2", "forward_2")
 

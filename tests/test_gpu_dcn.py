@@ -191,7 +191,8 @@ def test_fused_fast_c2_tolerance(gpu_ctx, dcn, c2):
 FUSED_CONFIGS = [(1, 1, 8), (1, 1, 4), (1, 2, 4), (1, 2, 2),   # register variant (variant, mt, ks)
                  (2, 1, 8), (2, 1, 16), (2, 2, 8),              # LDS-staged variant
                  (3, 8, 8), (3, 4, 8), (3, 4, 4), (3, 2, 4),   # LDS windows (rows, waves)
-                 (4, 8, 8), (4, 4, 4)]                          # LDS windows + L1 lower rows
+                 (4, 8, 8), (4, 4, 4),                          # LDS windows + L1 lower rows
+                 (5, 1, 8), (5, 1, 12)]                         # narrow 16-pixel tiles (waves)
 
 
 def test_unsupported_fused_config_is_rejected(gpu_ctx, dcn, c2):
@@ -268,12 +269,14 @@ EDGE_SHAPES = [
     (1, 16, 17, 15, 64, 8, 7, 3, 3, 1, 1, 2, 2, 1, 1, 1, 2),    # stride 2
     (1, 16, 12, 12, 32, 10, 10, 3, 3, 1, 1, 1, 1, 2, 2, 1, 1),  # dilation 2
     (3, 24, 6, 5, 32, 6, 5, 1, 3, 0, 1, 1, 1, 1, 1, 1, 3),      # 1x3 kernel, batch 3
+    (2, 16, 7, 6, 32, 7, 6, 3, 1, 1, 0, 1, 1, 1, 1, 1, 2),      # 3x1 kernel (Kw 1)
+    (1, 32, 5, 9, 64, 5, 9, 1, 1, 0, 0, 1, 1, 1, 1, 1, 4),      # 1x1 kernel (Kh*Kw 1)
 ]
 
 
 @pytest.mark.parametrize("dims", EDGE_SHAPES, ids=lambda t: "x".join(map(str, t)))
 @pytest.mark.parametrize("sampler", [0, 1])
-@pytest.mark.parametrize("variant", [1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5])
 def test_fused_edge_shapes(gpu_ctx, dcn, oracle, dims, sampler, variant):
     s = dcn.DeformConvShape(*dims)
     assert s.fused_supported
@@ -293,7 +296,7 @@ def test_fused_edge_shapes(gpu_ctx, dcn, oracle, dims, sampler, variant):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5])
 def test_large_offsets_force_global_fallback(gpu_ctx, dcn, oracle, variant):
     # Offsets up to +-40 px on a 64x64 map: a tile's sample box spans the whole plane
     # (74 KB), larger than one LDS window, so the window variant gathers from global.
@@ -321,7 +324,7 @@ def test_zero_padding_exact(gpu_ctx, dcn, c2):
     bias_out = np.repeat(h["bias"], s.output_height * s.output_width)
     for far in (1000.0, -1000.0, 66.0, -2.0 - 64.0):
         off = np.full_like(h["offset"], far)
-        for variant in (1, 2, 3, 4):
+        for variant in (1, 2, 3, 4, 5):
             gpu_ctx.set_fused_config(0, 0, -1, variant)
             try:
                 out = gpu_ctx.run_float16_prepacked(s, h["input"], off, h["mask"], packed)
