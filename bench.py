@@ -49,7 +49,8 @@ def algorithmic_bytes(shape, elem=2) -> int:
 
 
 def read_traffic(name: str):
-    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if one exists."""
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated) from the committed
+    rocprofv3 --pmc summary of this kernel and workload, if one exists."""
     path = ROOT / "profiles" / f"{name}.md"
     if not path.exists():
         return None
@@ -204,7 +205,8 @@ def main() -> int:
     flops = s.flops
     achieved = nbytes / (k_us * 1e-6) / 1e9
     workload_name = {2: "dcn_c2_fp16", 3: "dcn_c3_fp16", 5: "dcn_c5_fp16"}[args.config]
-    traffic = read_traffic(f"fused_{workload_name}_traffic")
+    kernel_name = KERNEL_NAMES.get(fused_cfg["variant"], "fused_kernel")
+    traffic = read_traffic(f"{kernel_name}_{workload_name}")
     line = {
         "metric": METRIC,
         "value": round(us_per_call, 4),
@@ -239,7 +241,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic,
-            "kernel": KERNEL_NAMES.get(fused_cfg["variant"], "fused") + " (sampler + MFMA GEMM)",
+            "kernel": kernel_name + " (sampler + MFMA GEMM)",
+            "traffic_source": f"profiles/{kernel_name}_{workload_name}.md" if traffic else None,
             "algorithmic_bytes_per_launch": nbytes,
             "mfma_frac": flops / (k_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS,
         },
