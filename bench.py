@@ -36,6 +36,7 @@ WORKLOADS = {
     2: "C2: DCNv2 1x128x64x64 -> 64, 3x3, 16 deformable groups, FP16 storage, FP32 accumulate, prepacked weights",
     3: "C3: DCNv2 16x128x64x64 -> 64, 3x3, 16 deformable groups, FP16, prepacked weights (batched 8K-eye tiles)",
     5: "C5: DCNv2 1x128x180x320 -> 64, 3x3, 16 deformable groups, FP16, prepacked weights (large map)",
+    4: "C4: BasicVSR++ propagation body per frame (hipGraph)",
 }
 
 
@@ -96,6 +97,84 @@ def cpu_baseline(budget_s: float = 25.0) -> dict:
     }
 
 
+def bench_body(args) -> int:
+    """Config C4: one BasicVSR++ propagation body per frame, each frame one hipGraph launch.
+
+    30 frames of a synthetic clip are captured once (one graph per frame: frame t reads
+    the features of steps t-1 and t-2); a step is one frame's graph launch. The timed
+    region replays K frames, cycling through the clip."""
+    import numpy as np
+    import torch
+
+    from jasnamacos_amd import deform_conv as dc
+
+    clip = dc.generate_body_inputs(seed=args.seed)
+    H, W, frames, blocks = clip["height"], clip["width"], clip["frames"], clip["blocks"]
+    plane = H * W
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()  # noqa: E731
+    ctx = dc.HipDeformConv(0)
+    wd = {k: dev(v) for k, v in clip["weights"].items()}
+    body = ctx.body(H, W, wd, branch=0, blocks=blocks)
+    feats, flows = dev(clip["feats"]), dev(clip["flows"])
+    props = torch.zeros(frames, 64 * plane, dtype=torch.int16, device="cuda")
+    flow2s = torch.zeros(frames, 2 * plane, dtype=torch.int16, device="cuda")
+    zero_f = torch.zeros(64 * plane, dtype=torch.int16, device="cuda")
+    zero_flow = torch.zeros(2 * plane, dtype=torch.int16, device="cuda")
+    graphs = []
+    for t in range(frames):
+        # Frame 0 and 1 read the previous clip's last features, so that every replay
+        # of the cycle is a full second-order step.
+        graphs.append(body.capture(feats[t], flows[t], flows[t - 1], props[t - 1], props[t - 2], flow2s[t],
+                                   props[t], has_second_order=True))
+    stream = torch.cuda.Stream()
+    for i in range(max(args.warmup, frames)):
+        graphs[i % frames].launch(stream)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for i in range(args.steps):
+            graphs[i % frames].launch(stream)
+        end.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    step_ms = start.elapsed_time(end) / args.steps
+    out = props.cpu().numpy().view(np.float16)
+    flops = dc.body_flops(H, W, 0, blocks)
+    tflops = flops / (step_ms * 1e-3) / 1e12
+    line = {
+        "metric": "BasicVSR++ propagation body us/frame (C4: offset convs + DCNv2 + 5-block backbone, hipGraph per frame)",
+        "value": round(step_ms * 1e3, 3),
+        "unit": "us/frame",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (numpy PCG64 clip: N(0,1) features, smooth +-4 px flows, N(0,0.02) weights)",
+        "config": {"workload": "C4: one propagation body per frame, 1x64x64x64 features, branch 0, "
+                               f"{blocks} residual blocks, {frames}-frame clip, one hipGraph per frame",
+                   "height": H, "width": W, "frames": frames, "blocks": blocks},
+        "tflops": tflops,
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "whole body graph (conv3x3 x15, DCN, glue)", "flops_per_step": flops},
+        "wall_ms_timed_region": wall_ms,
+        "output_finite": bool(np.all(np.isfinite(out.astype(np.float32)))),
+        "cpu_baseline": None,
+    }
+    for g in graphs:
+        g.free()
+    body.free()
+    ctx.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,8 +190,8 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (tiles shard with no "
-              "exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (independent tiles "
+              "would shard with no exchange). Run with --gpus 1.", file=sys.stderr)
         return 2
     if args.steps < 1:
         print("--steps must be >= 1", file=sys.stderr)
@@ -124,6 +203,8 @@ def main() -> int:
     from jasnamacos_amd import deform_conv as dc
 
     torch.cuda.set_device(0)
+    if args.config == 4:
+        return bench_body(args)
     d = dc.generate_config_inputs(args.config, args.seed)
     s = d["shape"]
     h = {k: np.asarray(d[k], np.float32).astype(np.float16) for k in ("input", "offset", "mask", "weight", "bias")}

@@ -300,6 +300,135 @@ typedef struct dcn_statistics {
 } dcn_statistics;
 dcn_status dcn_compute_statistics(const double* samples, size_t count, dcn_statistics* out);
 
+/* ---- propagation body (BasicVSR++ second-order propagation, one branch) ----------
+ * The layers around the deformable convolution in one propagation step, FP16 storage:
+ * temporal alignment inputs, the conv_offset branch, the offset/mask transform, the
+ * DCN, the residual backbone and the alignment residual. Feature maps are one image,
+ * 64 channels; flows are [2][H][W] planes ordered (x, y). */
+
+/* Layout of a body tensor. NCHW: planar [C][H][W]. CB8: [ceil(C/8)][H+4][W+4][8], a
+ * 2-pixel zero border and 8 channels per 16-byte vector (the layout the fused kernels
+ * gather from). A CB8 buffer must be zero-filled once by its owner; writers only
+ * touch interior positions of real channels. */
+typedef enum dcn_tensor_layout {
+    DCN_TENSOR_NCHW = 0,
+    DCN_TENSOR_CB8 = 1
+} dcn_tensor_layout;
+
+/* Elements of a CB8 tensor of `channels` x height x width (uint16_t units). */
+size_t dcn_cb8_tensor_count(int channels, int height, int width);
+
+/* runDCNOffsetTransform (MetalRunner.swift:469-508), prepare_dcn_offsets_fp16
+ * (MetalShader.swift:815-839): raw [432][plane] = [o1, o2, mask logits] and flows
+ * flow1/flow2 [2][plane] -> offset [288][plane] = half(10*tanh(raw) + flow) with even
+ * channels dy (flow y) and odd dx (flow x), flow1 for the first 144 channels and
+ * flow2 for the rest; mask [144][plane] = half(sigmoid(raw[288 + c])). Count
+ * mismatches give DCN_INVALID_SHAPE, as the reference's guard. */
+dcn_status dcn_offset_transform_f16(dcn_context* ctx, size_t plane, const uint16_t* raw,
+                                    size_t raw_count, const uint16_t* flow1, size_t flow1_count,
+                                    const uint16_t* flow2, size_t flow2_count, uint16_t* offset,
+                                    size_t offset_count, uint16_t* mask, size_t mask_count);
+dcn_status dcn_offset_transform_f16_dev(dcn_context* ctx, size_t plane, const void* d_raw,
+                                        const void* d_flow1, const void* d_flow2, void* d_offset,
+                                        void* d_mask, void* stream);
+
+/* runTemporalPreparation (MetalRunner.swift:510-582): accumulate_second_order_flow_fp16
+ * + assemble_temporal_alignment_fp16 (MetalShader.swift:738-813).
+ * flow2 [2][plane] = has_second_order ? half(flow1 + warp(prev_flow, flow1)) : 0;
+ * conditions [196] = [warp(feat_prop, flow1), feat_current, warp(feat_n2, flow2), flow1,
+ * flow2]; deform_input [128] = [feat_prop, feat_n2]. Inputs are NCHW: features 64
+ * channels, flows 2. The host call returns NCHW outputs and checks counts like the
+ * reference (DCN_INVALID_SHAPE). */
+dcn_status dcn_temporal_prepare_f16(dcn_context* ctx, int width, int height,
+                                    const uint16_t* feat_prop, size_t feat_prop_count,
+                                    const uint16_t* feat_current, size_t feat_current_count,
+                                    const uint16_t* feat_n2, size_t feat_n2_count,
+                                    const uint16_t* flow1, size_t flow1_count,
+                                    const uint16_t* prev_flow, size_t prev_flow_count,
+                                    int has_second_order, uint16_t* conditions,
+                                    size_t conditions_count, uint16_t* deform_input,
+                                    size_t deform_input_count, uint16_t* flow2, size_t flow2_count);
+dcn_status dcn_temporal_prepare_f16_dev(dcn_context* ctx, int width, int height,
+                                        const void* d_feat_prop, const void* d_feat_current,
+                                        const void* d_feat_n2, const void* d_flow1,
+                                        const void* d_prev_flow, int has_second_order,
+                                        void* d_flow2, void* d_conditions,
+                                        dcn_tensor_layout conditions_layout, void* d_deform_input,
+                                        dcn_tensor_layout deform_input_layout, void* stream);
+
+/* assemble_temporal_backbone_fp16 / assemble_propagation_backbone_fp16
+ * (MetalShader.swift:841-855, 899-929): concatenate `count` (1..5) 64-channel NCHW
+ * sources into out (64 * count channels) in the given layout. */
+dcn_status dcn_assemble_backbone_f16_dev(dcn_context* ctx, int width, int height,
+                                         const void* const* d_sources, int count, void* d_out,
+                                         dcn_tensor_layout layout, void* stream);
+
+/* add_propagation_residual_fp16 (MetalShader.swift:857-867): out = half(aligned + backbone). */
+dcn_status dcn_add_residual_f16_dev(dcn_context* ctx, size_t count, const void* d_aligned,
+                                    const void* d_backbone, void* d_out, void* stream);
+
+/* CB8 -> NCHW copy of one image of `channels` channels. */
+dcn_status dcn_cb8_to_nchw_f16_dev(dcn_context* ctx, int channels, int height, int width,
+                                   const void* d_cb8, void* d_out, void* stream);
+
+/* 3x3 convolution, stride 1, pad 1, of the body's conv_offset branch and backbone
+ * (the conv modules exported by tools/convert_basicvsrpp.py:181-197): weights OIHW
+ * FP16 [cout][cin][3][3], packed once into MFMA fragments. */
+typedef struct dcn_conv dcn_conv;
+dcn_status dcn_conv3x3_create_dev(dcn_context* ctx, int cin, int cout, int height, int width,
+                                  const void* d_weight, const void* d_bias, void* stream,
+                                  dcn_conv** out);
+void dcn_conv3x3_free(dcn_conv* conv);
+/* out = half(r2 + half(r1 + act(conv(x) + bias))), each residual optional (null).
+ * activation: 0 none, 1 LeakyReLU(slope), 2 ReLU. x is CB8 (cin channels); out and the
+ * residuals (cout channels) in the layouts given. */
+dcn_status dcn_conv3x3_f16_dev(dcn_context* ctx, const dcn_conv* conv, const void* d_x_cb8,
+                               int activation, float slope, const void* d_res1,
+                               dcn_tensor_layout res1_layout, const void* d_res2,
+                               dcn_tensor_layout res2_layout, void* d_out,
+                               dcn_tensor_layout out_layout, void* stream);
+
+/* One propagation body: conv_offset (196->64->64->64->432, LeakyReLU 0.1 between), the
+ * offset transform, the 128->64 DCN (16 deformable groups, 3x3), the backbone
+ * ([feat_current, extra prefix features..., aligned] -> 64 conv + LeakyReLU 0.1, then
+ * `blocks` residual blocks conv-ReLU-conv + skip) and feat_prop = aligned + backbone.
+ * Replaces the per-step body of verifyFusedFourPassRecurrence
+ * (FusedFourPassRecurrenceProbe.swift:570-664) for one branch; prefix features = branch
+ * index (0: [spatial], 3: [spatial, b1, f1, b2], MetalShader.swift:899-929). All weights
+ * OIHW FP16 device pointers; the body packs them at creation and owns its
+ * intermediates, so a step allocates nothing. */
+#define DCN_BODY_MAX_BLOCKS 8
+typedef struct dcn_body_weights {
+    const void* offset_weight[4];
+    const void* offset_bias[4];
+    const void* dcn_weight;
+    const void* dcn_bias;
+    const void* backbone_weight[1 + 2 * DCN_BODY_MAX_BLOCKS];
+    const void* backbone_bias[1 + 2 * DCN_BODY_MAX_BLOCKS];
+} dcn_body_weights;
+typedef struct dcn_body dcn_body;
+dcn_status dcn_body_create(dcn_context* ctx, int height, int width, int branch, int blocks,
+                           const dcn_body_weights* weights, void* stream, dcn_body** out);
+void dcn_body_destroy(dcn_body* body);
+/* One step, stream-ordered. feat_current, feat_prop, feat_n2, feat_prop_out: NCHW
+ * [64][H][W]; flow1, prev_flow, flow2_out: [2][H][W]; d_prefix: `branch` further
+ * 64-channel NCHW backbone inputs (null when branch is 0). */
+dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                             const void* d_prev_flow, const void* d_feat_prop,
+                             const void* d_feat_n2, const void* const* d_prefix,
+                             int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                             void* stream);
+/* The same step captured into an executable hipGraph (the retained per-step graph of
+ * FusedFourPassRecurrenceProbe.swift:904-937); replay with dcn_graph_launch. */
+typedef struct dcn_graph dcn_graph;
+dcn_status dcn_body_capture(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                            const void* d_prev_flow, const void* d_feat_prop,
+                            const void* d_feat_n2, const void* const* d_prefix,
+                            int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                            dcn_graph** out);
+dcn_status dcn_graph_launch(dcn_graph* graph, void* stream);
+void dcn_graph_destroy(dcn_graph* graph);
+
 #ifdef __cplusplus
 }
 #endif

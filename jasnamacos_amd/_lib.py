@@ -7,6 +7,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import sys
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libdcn.so"
@@ -43,6 +44,22 @@ class DcnStatistics(C.Structure):
         ("minimum", C.c_double), ("maximum", C.c_double), ("median", C.c_double),
         ("mean", C.c_double), ("standard_deviation", C.c_double),
         ("percentile10", C.c_double), ("percentile90", C.c_double), ("count", c_size),
+    ]
+
+
+BODY_MAX_BLOCKS = 8
+
+
+class DcnBodyWeights(C.Structure):
+    """dcn_body_weights: OIHW FP16 device pointers of one propagation body."""
+
+    _fields_ = [
+        ("offset_weight", C.c_void_p * 4),
+        ("offset_bias", C.c_void_p * 4),
+        ("dcn_weight", C.c_void_p),
+        ("dcn_bias", C.c_void_p),
+        ("backbone_weight", C.c_void_p * (1 + 2 * BODY_MAX_BLOCKS)),
+        ("backbone_bias", C.c_void_p * (1 + 2 * BODY_MAX_BLOCKS)),
     ]
 
 
@@ -104,9 +121,53 @@ SIGNATURES: dict[str, tuple] = {
     "dcn_checksum_f32": (C.c_double, [c_f32p, c_size]),
     "dcn_checksum_f16": (C.c_double, [c_u16p, c_size]),
     "dcn_compute_statistics": (C.c_int, [c_f64p, c_size, C.POINTER(DcnStatistics)]),
+    # propagation body
+    "dcn_cb8_tensor_count": (c_size, [C.c_int, C.c_int, C.c_int]),
+    "dcn_offset_transform_f16": (C.c_int, [CtxP, c_size, c_u16p, c_size, c_u16p, c_size, c_u16p, c_size,
+                                           c_u16p, c_size, c_u16p, c_size]),
+    "dcn_offset_transform_f16_dev": (C.c_int, [CtxP, c_size, c_void, c_void, c_void, c_void, c_void, c_void]),
+    "dcn_temporal_prepare_f16": (C.c_int, [CtxP, C.c_int, C.c_int, c_u16p, c_size, c_u16p, c_size, c_u16p,
+                                           c_size, c_u16p, c_size, c_u16p, c_size, C.c_int, c_u16p, c_size,
+                                           c_u16p, c_size, c_u16p, c_size]),
+    "dcn_temporal_prepare_f16_dev": (C.c_int, [CtxP, C.c_int, C.c_int, c_void, c_void, c_void, c_void, c_void,
+                                               C.c_int, c_void, c_void, C.c_int, c_void, C.c_int, c_void]),
+    "dcn_assemble_backbone_f16_dev": (C.c_int, [CtxP, C.c_int, C.c_int, C.POINTER(c_void), C.c_int, c_void,
+                                                C.c_int, c_void]),
+    "dcn_add_residual_f16_dev": (C.c_int, [CtxP, c_size, c_void, c_void, c_void, c_void]),
+    "dcn_cb8_to_nchw_f16_dev": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, c_void, c_void, c_void]),
+    "dcn_conv3x3_create_dev": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int, c_void, c_void, c_void,
+                                         C.POINTER(c_void)]),
+    "dcn_conv3x3_free": (None, [c_void]),
+    "dcn_conv3x3_f16_dev": (C.c_int, [CtxP, c_void, c_void, C.c_int, C.c_float, c_void, C.c_int, c_void,
+                                      C.c_int, c_void, C.c_int, c_void]),
+    "dcn_body_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(DcnBodyWeights),
+                                  c_void, C.POINTER(c_void)]),
+    "dcn_body_destroy": (None, [c_void]),
+    "dcn_body_step_dev": (C.c_int, [c_void, c_void, c_void, c_void, c_void, c_void, C.POINTER(c_void),
+                                    C.c_int, c_void, c_void, c_void]),
+    "dcn_body_capture": (C.c_int, [c_void, c_void, c_void, c_void, c_void, c_void, C.POINTER(c_void),
+                                   C.c_int, c_void, c_void, C.POINTER(c_void)]),
+    "dcn_graph_launch": (C.c_int, [c_void, c_void]),
+    "dcn_graph_destroy": (None, [c_void]),
 }
 
 _LIB: C.CDLL | None = None
+
+
+def _share_hip_runtime_with_torch() -> None:
+    """Keep one HIP runtime per process.
+
+    PyTorch-ROCm ships its own libamdhip64 and links it by the unversioned name, while
+    libdcn links libamdhip64.so.7 from /opt/rocm. Loaded in the order libdcn-then-torch,
+    the loader maps both copies and the second runtime to initialise sees no device.
+    Importing torch first (when it is installed) lets libdcn bind to torch's already
+    loaded runtime, whose soname matches; without torch there is only ROCm's."""
+    if "torch" in sys.modules:
+        return
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
 
 
 def load() -> C.CDLL:
@@ -115,6 +176,7 @@ def load() -> C.CDLL:
     if _LIB is not None:
         return _LIB
     path = Path(os.environ.get("DCN_LIBRARY", LIB_PATH))
+    _share_hip_runtime_with_torch()
     if not path.exists():
         raise ImportError(
             f"libdcn.so not found at {path}; build it with `python -m jasnamacos_amd.build` "

@@ -8,56 +8,12 @@
 #include <string>
 #include <vector>
 
+#include "dcn_host.hpp"
 #include "dcn_internal.hpp"
 
 namespace {
 
-dcn_status fail(dcn_context* ctx, dcn_status status, const std::string& message) {
-    if (ctx) ctx->last_error = message;
-    return status;
-}
-
-dcn_status hip_fail(dcn_context* ctx, hipError_t e, const char* what) {
-    return fail(ctx, DCN_COMMAND_FAILED, std::string(what) + ": " + hipGetErrorString(e));
-}
-
-#define DCN_HIP(ctx, expr)                                        \
-    do {                                                          \
-        hipError_t e_ = (expr);                                   \
-        if (e_ != hipSuccess) return hip_fail((ctx), e_, #expr); \
-    } while (0)
-
-// Makes ctx->device current for the duration of a call.
-struct DeviceGuard {
-    int previous = -1;
-    explicit DeviceGuard(int device) {
-        if (hipGetDevice(&previous) == hipSuccess && previous != device) {
-            (void)hipSetDevice(device);
-        } else {
-            previous = -1;
-        }
-    }
-    ~DeviceGuard() {
-        if (previous >= 0) (void)hipSetDevice(previous);
-    }
-};
-
-// Owning device buffer for the host-pointer entry points.
-struct DevBuf {
-    void* p = nullptr;
-    ~DevBuf() {
-        if (p) (void)hipFree(p);
-    }
-};
-
-dcn_status check_count(dcn_context* ctx, const char* name, size_t actual, size_t expected) {
-    // DeformConvCPU.require (DeformConv.swift:140-144)
-    if (actual != expected)
-        return fail(ctx, DCN_INVALID_ARRAY_COUNT,
-                    std::string(name) + " has " + std::to_string(actual) +
-                        " elements; expected " + std::to_string(expected));
-    return DCN_OK;
-}
+using namespace dcn::host;
 
 dcn_status validated_counts(dcn_context* ctx, const dcn_shape* shape, dcn_counts* c) {
     if (!shape) return fail(ctx, DCN_INVALID_ARGUMENT, "shape is null");
@@ -147,19 +103,6 @@ dcn_status ensure_workspace(dcn_context* ctx, size_t bytes, hipStream_t stream) 
     ctx->workspace_bytes = bytes;
     return DCN_OK;
 }
-
-template <typename T>
-dcn_status upload(dcn_context* ctx, DevBuf& buf, const T* host, size_t count) {
-    DCN_HIP(ctx, hipMalloc(&buf.p, std::max<size_t>(count, 1) * sizeof(T)));
-    if (count) DCN_HIP(ctx, hipMemcpy(buf.p, host, count * sizeof(T), hipMemcpyHostToDevice));
-    return DCN_OK;
-}
-
-#define DCN_TRY(expr)                      \
-    do {                                   \
-        dcn_status st_ = (expr);           \
-        if (st_ != DCN_OK) return st_;     \
-    } while (0)
 
 dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const void* d_input,
                                bool input_is_cb8, const void* d_offset, const void* d_mask,

@@ -1,0 +1,498 @@
+// C-ABI host layer of the propagation body: glue entry points, conv3x3 layers and the
+// per-step body with hipGraph capture. Reference: runDCNOffsetTransform and
+// runTemporalPreparation (MetalRunner.swift:469-582), the body glue kernels
+// (MetalShader.swift:738-929) and the per-step body of verifyFusedFourPassRecurrence
+// (FusedFourPassRecurrenceProbe.swift:570-664, retained graph :904-937).
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "dcn_host.hpp"
+#include "dcn_internal.hpp"
+
+using namespace dcn::host;
+
+struct dcn_conv {
+    dcn::ConvGeometry g{};
+    void* wpk = nullptr;
+    float* bias = nullptr;
+    int device = 0;
+};
+
+struct dcn_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int device = 0;
+};
+
+struct dcn_body {
+    dcn_context* ctx = nullptr;
+    int h = 0, w = 0, branch = 0, blocks = 0;
+    dcn_conv* offset_conv[4] = {};
+    dcn_conv* backbone[1 + 2 * DCN_BODY_MAX_BLOCKS] = {};
+    dcn_packed* dcn = nullptr;
+    std::vector<void*> buffers;  // every device intermediate, freed with the body
+    uint16_t* cond_cb8 = nullptr;    // conditions, 196 channels
+    uint16_t* deform_cb8 = nullptr;  // DCN input [feat_prop, feat_n2], 128 channels
+    uint16_t* off_a = nullptr;       // conv_offset intermediates, 64 channels CB8
+    uint16_t* off_b = nullptr;
+    uint16_t* raw = nullptr;         // conv_offset output, 432 NCHW
+    uint16_t* offset = nullptr;      // 288 NCHW
+    uint16_t* mask = nullptr;        // 144 NCHW
+    uint16_t* aligned = nullptr;     // DCN output, 64 NCHW
+    uint16_t* bb_in = nullptr;       // backbone input, 64 * (branch + 2) channels CB8
+    uint16_t* feat[3] = {};          // backbone features, 64 channels CB8
+    hipStream_t capture_stream = nullptr;
+};
+
+namespace {
+
+dcn_status check_plane(dcn_context* ctx, int width, int height) {
+    if (width <= 0 || height <= 0 || (long long)width * height * 432 >= (1LL << 30))
+        return fail(ctx, DCN_INVALID_SHAPE, "invalid body plane size");
+    return DCN_OK;
+}
+
+dcn_status require_count(dcn_context* ctx, size_t actual, size_t expected) {
+    // The reference's guards throw invalidShape on any count mismatch
+    // (MetalRunner.swift:475-477, :520-526).
+    if (actual != expected) return fail(ctx, DCN_INVALID_SHAPE, "array count does not match the plane");
+    return DCN_OK;
+}
+
+template <typename T>
+dcn_status alloc(dcn_context* ctx, std::vector<void*>& owned, T** p, size_t elems) {
+    void* raw = nullptr;
+    DCN_HIP(ctx, hipMalloc(&raw, std::max<size_t>(elems, 1) * sizeof(uint16_t)));
+    owned.push_back(raw);
+    *p = static_cast<T*>(raw);
+    return DCN_OK;
+}
+
+dcn_status run_conv(dcn_context* ctx, const dcn_conv* c, const void* x, int act, const void* r1,
+                    int r1_layout, const void* r2, int r2_layout, void* out, int out_layout,
+                    hipStream_t stream) {
+    DCN_HIP(ctx, dcn::launch_conv3x3(c->g, x, c->wpk, c->bias, act, 0.1f, (const uint16_t*)r1,
+                                     r1_layout, (const uint16_t*)r2, r2_layout, (uint16_t*)out,
+                                     out_layout, stream));
+    return DCN_OK;
+}
+
+dcn_shape body_dcn_shape(int h, int w) {
+    return dcn_shape{1, 128, h, w, 64, h, w, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16};
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t dcn_cb8_tensor_count(int channels, int height, int width) {
+    if (channels <= 0 || height <= 0 || width <= 0) return 0;
+    return dcn::cb8_tensor_elems(channels, height, width);
+}
+
+dcn_status dcn_offset_transform_f16_dev(dcn_context* ctx, size_t plane, const void* d_raw,
+                                        const void* d_flow1, const void* d_flow2, void* d_offset,
+                                        void* d_mask, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    if (plane == 0 || plane * 432 >= ((size_t)1 << 30))
+        return fail(ctx, DCN_INVALID_SHAPE, "invalid plane size");
+    if (!d_raw || !d_flow1 || !d_flow2 || !d_offset || !d_mask)
+        return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    DeviceGuard guard(ctx->device);
+    DCN_HIP(ctx, dcn::launch_offset_transform((const uint16_t*)d_raw, (const uint16_t*)d_flow1,
+                                              (const uint16_t*)d_flow2, (uint16_t*)d_offset,
+                                              (uint16_t*)d_mask, (int)plane, (hipStream_t)stream));
+    return DCN_OK;
+}
+
+dcn_status dcn_offset_transform_f16(dcn_context* ctx, size_t plane, const uint16_t* raw,
+                                    size_t raw_count, const uint16_t* flow1, size_t flow1_count,
+                                    const uint16_t* flow2, size_t flow2_count, uint16_t* offset,
+                                    size_t offset_count, uint16_t* mask, size_t mask_count) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    if (plane == 0) return fail(ctx, DCN_INVALID_SHAPE, "plane is 0");
+    DCN_TRY(require_count(ctx, raw_count, 432 * plane));
+    DCN_TRY(require_count(ctx, flow1_count, 2 * plane));
+    DCN_TRY(require_count(ctx, flow2_count, 2 * plane));
+    DCN_TRY(require_count(ctx, offset_count, 288 * plane));
+    DCN_TRY(require_count(ctx, mask_count, 144 * plane));
+    if (!raw || !flow1 || !flow2 || !offset || !mask)
+        return fail(ctx, DCN_INVALID_ARGUMENT, "host pointer is null");
+    DeviceGuard guard(ctx->device);
+    DevBuf r, f1, f2, o, m;
+    DCN_TRY(upload(ctx, r, raw, raw_count));
+    DCN_TRY(upload(ctx, f1, flow1, flow1_count));
+    DCN_TRY(upload(ctx, f2, flow2, flow2_count));
+    DCN_HIP(ctx, hipMalloc(&o.p, offset_count * 2));
+    DCN_HIP(ctx, hipMalloc(&m.p, mask_count * 2));
+    DCN_TRY(dcn_offset_transform_f16_dev(ctx, plane, r.p, f1.p, f2.p, o.p, m.p, nullptr));
+    DCN_HIP(ctx, hipMemcpy(offset, o.p, offset_count * 2, hipMemcpyDeviceToHost));
+    DCN_HIP(ctx, hipMemcpy(mask, m.p, mask_count * 2, hipMemcpyDeviceToHost));
+    return DCN_OK;
+}
+
+dcn_status dcn_temporal_prepare_f16_dev(dcn_context* ctx, int width, int height,
+                                        const void* d_feat_prop, const void* d_feat_current,
+                                        const void* d_feat_n2, const void* d_flow1,
+                                        const void* d_prev_flow, int has_second_order,
+                                        void* d_flow2, void* d_conditions,
+                                        dcn_tensor_layout conditions_layout, void* d_deform_input,
+                                        dcn_tensor_layout deform_input_layout, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    DCN_TRY(check_plane(ctx, width, height));
+    if (!d_feat_prop || !d_feat_current || !d_feat_n2 || !d_flow1 || !d_prev_flow || !d_flow2 ||
+        !d_conditions || !d_deform_input)
+        return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    if ((conditions_layout != DCN_TENSOR_NCHW && conditions_layout != DCN_TENSOR_CB8) ||
+        (deform_input_layout != DCN_TENSOR_NCHW && deform_input_layout != DCN_TENSOR_CB8))
+        return fail(ctx, DCN_INVALID_ARGUMENT, "unknown tensor layout");
+    DeviceGuard guard(ctx->device);
+    const hipStream_t s = (hipStream_t)stream;
+    DCN_HIP(ctx, dcn::launch_second_order_flow((const uint16_t*)d_flow1, (const uint16_t*)d_prev_flow,
+                                               (uint16_t*)d_flow2, height, width,
+                                               has_second_order ? 1 : 0, s));
+    DCN_HIP(ctx, dcn::launch_temporal_assemble(
+                     (const uint16_t*)d_feat_prop, (const uint16_t*)d_feat_current,
+                     (const uint16_t*)d_feat_n2, (const uint16_t*)d_flow1, (const uint16_t*)d_flow2,
+                     (uint16_t*)d_conditions, conditions_layout, (uint16_t*)d_deform_input,
+                     deform_input_layout, height, width, s));
+    return DCN_OK;
+}
+
+dcn_status dcn_temporal_prepare_f16(dcn_context* ctx, int width, int height,
+                                    const uint16_t* feat_prop, size_t feat_prop_count,
+                                    const uint16_t* feat_current, size_t feat_current_count,
+                                    const uint16_t* feat_n2, size_t feat_n2_count,
+                                    const uint16_t* flow1, size_t flow1_count,
+                                    const uint16_t* prev_flow, size_t prev_flow_count,
+                                    int has_second_order, uint16_t* conditions,
+                                    size_t conditions_count, uint16_t* deform_input,
+                                    size_t deform_input_count, uint16_t* flow2, size_t flow2_count) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    DCN_TRY(check_plane(ctx, width, height));
+    const size_t plane = (size_t)width * height;
+    DCN_TRY(require_count(ctx, feat_prop_count, 64 * plane));
+    DCN_TRY(require_count(ctx, feat_current_count, 64 * plane));
+    DCN_TRY(require_count(ctx, feat_n2_count, 64 * plane));
+    DCN_TRY(require_count(ctx, flow1_count, 2 * plane));
+    DCN_TRY(require_count(ctx, prev_flow_count, 2 * plane));
+    DCN_TRY(require_count(ctx, conditions_count, 196 * plane));
+    DCN_TRY(require_count(ctx, deform_input_count, 128 * plane));
+    DCN_TRY(require_count(ctx, flow2_count, 2 * plane));
+    if (!feat_prop || !feat_current || !feat_n2 || !flow1 || !prev_flow || !conditions ||
+        !deform_input || !flow2)
+        return fail(ctx, DCN_INVALID_ARGUMENT, "host pointer is null");
+    DeviceGuard guard(ctx->device);
+    DevBuf fp, fc, fn, f1, pf, f2, c, d;
+    DCN_TRY(upload(ctx, fp, feat_prop, feat_prop_count));
+    DCN_TRY(upload(ctx, fc, feat_current, feat_current_count));
+    DCN_TRY(upload(ctx, fn, feat_n2, feat_n2_count));
+    DCN_TRY(upload(ctx, f1, flow1, flow1_count));
+    DCN_TRY(upload(ctx, pf, prev_flow, prev_flow_count));
+    DCN_HIP(ctx, hipMalloc(&f2.p, flow2_count * 2));
+    DCN_HIP(ctx, hipMalloc(&c.p, conditions_count * 2));
+    DCN_HIP(ctx, hipMalloc(&d.p, deform_input_count * 2));
+    DCN_TRY(dcn_temporal_prepare_f16_dev(ctx, width, height, fp.p, fc.p, fn.p, f1.p, pf.p,
+                                         has_second_order, f2.p, c.p, DCN_TENSOR_NCHW, d.p,
+                                         DCN_TENSOR_NCHW, nullptr));
+    DCN_HIP(ctx, hipMemcpy(conditions, c.p, conditions_count * 2, hipMemcpyDeviceToHost));
+    DCN_HIP(ctx, hipMemcpy(deform_input, d.p, deform_input_count * 2, hipMemcpyDeviceToHost));
+    DCN_HIP(ctx, hipMemcpy(flow2, f2.p, flow2_count * 2, hipMemcpyDeviceToHost));
+    return DCN_OK;
+}
+
+dcn_status dcn_assemble_backbone_f16_dev(dcn_context* ctx, int width, int height,
+                                         const void* const* d_sources, int count, void* d_out,
+                                         dcn_tensor_layout layout, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    DCN_TRY(check_plane(ctx, width, height));
+    if (!d_sources || count < 1 || count > 5 || !d_out)
+        return fail(ctx, DCN_INVALID_ARGUMENT, "assemble needs 1..5 sources and an output");
+    if (layout != DCN_TENSOR_NCHW && layout != DCN_TENSOR_CB8)
+        return fail(ctx, DCN_INVALID_ARGUMENT, "unknown tensor layout");
+    const uint16_t* src[5];
+    for (int i = 0; i < count; ++i) {
+        if (!d_sources[i]) return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+        src[i] = (const uint16_t*)d_sources[i];
+    }
+    DeviceGuard guard(ctx->device);
+    DCN_HIP(ctx, dcn::launch_assemble(src, count, (uint16_t*)d_out, layout, height, width,
+                                      (hipStream_t)stream));
+    return DCN_OK;
+}
+
+dcn_status dcn_add_residual_f16_dev(dcn_context* ctx, size_t count, const void* d_aligned,
+                                    const void* d_backbone, void* d_out, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    if (!d_aligned || !d_backbone || !d_out) return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    if (count == 0) return DCN_OK;
+    DeviceGuard guard(ctx->device);
+    DCN_HIP(ctx, dcn::launch_add_residual((const uint16_t*)d_aligned, (const uint16_t*)d_backbone,
+                                          (uint16_t*)d_out, (long)count, (hipStream_t)stream));
+    return DCN_OK;
+}
+
+dcn_status dcn_cb8_to_nchw_f16_dev(dcn_context* ctx, int channels, int height, int width,
+                                   const void* d_cb8, void* d_out, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    DCN_TRY(check_plane(ctx, width, height));
+    if (channels <= 0 || (long long)channels * width * height >= (1LL << 30))
+        return fail(ctx, DCN_INVALID_SHAPE, "invalid channel count");
+    if (!d_cb8 || !d_out) return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    DeviceGuard guard(ctx->device);
+    DCN_HIP(ctx, dcn::launch_cb8_to_nchw((const uint16_t*)d_cb8, (uint16_t*)d_out, channels, height,
+                                         width, (hipStream_t)stream));
+    return DCN_OK;
+}
+
+dcn_status dcn_conv3x3_create_dev(dcn_context* ctx, int cin, int cout, int height, int width,
+                                  const void* d_weight, const void* d_bias, void* stream,
+                                  dcn_conv** out) {
+    if (!ctx || !out) return DCN_INVALID_ARGUMENT;
+    *out = nullptr;
+    DCN_TRY(check_plane(ctx, width, height));
+    if (cin <= 0 || cout <= 0 || cin > 4096 || cout > 4096)
+        return fail(ctx, DCN_INVALID_SHAPE, "invalid conv channel counts");
+    if (!d_weight || !d_bias) return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    DeviceGuard guard(ctx->device);
+    auto* c = new dcn_conv();
+    c->g = dcn::conv_geometry(cin, cout, height, width);
+    c->device = ctx->device;
+    if (hipMalloc(&c->wpk, dcn::conv_packed_bytes(c->g)) != hipSuccess ||
+        hipMalloc((void**)&c->bias, (size_t)cout * sizeof(float)) != hipSuccess) {
+        dcn_conv3x3_free(c);
+        return fail(ctx, DCN_COMMAND_FAILED, "hipMalloc of packed conv weights failed");
+    }
+    const hipError_t e = dcn::launch_conv_prepack(c->g, (const uint16_t*)d_weight,
+                                                  (const uint16_t*)d_bias, c->wpk, c->bias,
+                                                  (hipStream_t)stream);
+    if (e != hipSuccess) {
+        dcn_conv3x3_free(c);
+        return hip_fail(ctx, e, "conv prepack launch");
+    }
+    *out = c;
+    return DCN_OK;
+}
+
+void dcn_conv3x3_free(dcn_conv* conv) {
+    if (!conv) return;
+    DeviceGuard guard(conv->device);
+    if (conv->wpk) (void)hipFree(conv->wpk);
+    if (conv->bias) (void)hipFree(conv->bias);
+    delete conv;
+}
+
+dcn_status dcn_conv3x3_f16_dev(dcn_context* ctx, const dcn_conv* conv, const void* d_x_cb8,
+                               int activation, float slope, const void* d_res1,
+                               dcn_tensor_layout res1_layout, const void* d_res2,
+                               dcn_tensor_layout res2_layout, void* d_out,
+                               dcn_tensor_layout out_layout, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    if (!conv || !d_x_cb8 || !d_out) return fail(ctx, DCN_INVALID_ARGUMENT, "null conv or pointer");
+    if (activation < 0 || activation > 2) return fail(ctx, DCN_INVALID_ARGUMENT, "unknown activation");
+    for (int l : {(int)res1_layout, (int)res2_layout, (int)out_layout})
+        if (l != DCN_TENSOR_NCHW && l != DCN_TENSOR_CB8)
+            return fail(ctx, DCN_INVALID_ARGUMENT, "unknown tensor layout");
+    DeviceGuard guard(ctx->device);
+    DCN_HIP(ctx, dcn::launch_conv3x3(conv->g, d_x_cb8, conv->wpk, conv->bias, activation, slope,
+                                     (const uint16_t*)d_res1, res1_layout, (const uint16_t*)d_res2,
+                                     res2_layout, (uint16_t*)d_out, out_layout, (hipStream_t)stream));
+    return DCN_OK;
+}
+
+void dcn_body_destroy(dcn_body* body) {
+    if (!body) return;
+    DeviceGuard guard(body->ctx ? body->ctx->device : 0);
+    for (auto* c : body->offset_conv) dcn_conv3x3_free(c);
+    for (auto* c : body->backbone) dcn_conv3x3_free(c);
+    dcn_packed_free(body->dcn);
+    for (void* p : body->buffers) (void)hipFree(p);
+    if (body->capture_stream) (void)hipStreamDestroy(body->capture_stream);
+    delete body;
+}
+
+dcn_status dcn_body_create(dcn_context* ctx, int height, int width, int branch, int blocks,
+                           const dcn_body_weights* weights, void* stream, dcn_body** out) {
+    if (!ctx || !out) return DCN_INVALID_ARGUMENT;
+    *out = nullptr;
+    DCN_TRY(check_plane(ctx, width, height));
+    if (branch < 0 || branch > 3 || blocks < 1 || blocks > DCN_BODY_MAX_BLOCKS || !weights)
+        return fail(ctx, DCN_INVALID_ARGUMENT, "body needs branch 0..3, 1..8 blocks and weights");
+    DeviceGuard guard(ctx->device);
+    auto* b = new dcn_body();
+    b->ctx = ctx;
+    b->h = height;
+    b->w = width;
+    b->branch = branch;
+    b->blocks = blocks;
+    const hipStream_t s = (hipStream_t)stream;
+    auto bail = [&](dcn_status st) {
+        dcn_body_destroy(b);
+        return st;
+    };
+    static const int kOffsetIn[4] = {196, 64, 64, 64};
+    static const int kOffsetOut[4] = {64, 64, 64, 432};
+    for (int i = 0; i < 4; ++i) {
+        const dcn_status st = dcn_conv3x3_create_dev(ctx, kOffsetIn[i], kOffsetOut[i], height, width,
+                                                     weights->offset_weight[i], weights->offset_bias[i],
+                                                     stream, &b->offset_conv[i]);
+        if (st != DCN_OK) return bail(st);
+    }
+    const int bb_in = 64 * (branch + 2);
+    for (int i = 0; i < 1 + 2 * blocks; ++i) {
+        const dcn_status st = dcn_conv3x3_create_dev(ctx, i == 0 ? bb_in : 64, 64, height, width,
+                                                     weights->backbone_weight[i],
+                                                     weights->backbone_bias[i], stream, &b->backbone[i]);
+        if (st != DCN_OK) return bail(st);
+    }
+    const dcn_shape ds = body_dcn_shape(height, width);
+    {
+        const dcn_status st = dcn_prepack_f16_dev(ctx, &ds, weights->dcn_weight, DCN_LAYOUT_OIHW,
+                                                  weights->dcn_bias, stream, &b->dcn);
+        if (st != DCN_OK) return bail(st);
+    }
+    const size_t plane = (size_t)width * height;
+    dcn_status st = DCN_OK;
+    auto a16 = [&](uint16_t** p, size_t elems) {
+        if (st == DCN_OK) st = alloc(ctx, b->buffers, p, elems);
+    };
+    a16(&b->cond_cb8, dcn::cb8_tensor_elems(196, height, width));
+    a16(&b->deform_cb8, dcn::cb8_tensor_elems(128, height, width));
+    a16(&b->off_a, dcn::cb8_tensor_elems(64, height, width));
+    a16(&b->off_b, dcn::cb8_tensor_elems(64, height, width));
+    a16(&b->raw, 432 * plane);
+    a16(&b->offset, 288 * plane);
+    a16(&b->mask, 144 * plane);
+    a16(&b->aligned, 64 * plane);
+    a16(&b->bb_in, dcn::cb8_tensor_elems(bb_in, height, width));
+    for (auto& f : b->feat) a16(&f, dcn::cb8_tensor_elems(64, height, width));
+    if (st != DCN_OK) return bail(st);
+    // CB8 borders and padding channels are zero once and never written again, so a
+    // step (and its captured graph) holds no memset.
+    for (uint16_t* p : {b->cond_cb8, b->deform_cb8, b->off_a, b->off_b, b->bb_in, b->feat[0],
+                        b->feat[1], b->feat[2]}) {
+        size_t elems = 0;
+        if (p == b->cond_cb8) elems = dcn::cb8_tensor_elems(196, height, width);
+        else if (p == b->deform_cb8) elems = dcn::cb8_tensor_elems(128, height, width);
+        else if (p == b->bb_in) elems = dcn::cb8_tensor_elems(bb_in, height, width);
+        else elems = dcn::cb8_tensor_elems(64, height, width);
+        if (hipMemsetAsync(p, 0, elems * 2, s) != hipSuccess)
+            return bail(fail(ctx, DCN_COMMAND_FAILED, "clearing body buffers failed"));
+    }
+    if (hipStreamCreateWithFlags(&b->capture_stream, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(ctx, DCN_COMMAND_FAILED, "hipStreamCreate failed"));
+    if (hipStreamSynchronize(s) != hipSuccess)
+        return bail(fail(ctx, DCN_COMMAND_FAILED, "body set-up failed"));
+    *out = b;
+    return DCN_OK;
+}
+
+dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                             const void* d_prev_flow, const void* d_feat_prop,
+                             const void* d_feat_n2, const void* const* d_prefix,
+                             int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                             void* stream) {
+    if (!body) return DCN_INVALID_ARGUMENT;
+    dcn_context* ctx = body->ctx;
+    if (!d_feat_current || !d_flow1 || !d_prev_flow || !d_feat_prop || !d_feat_n2 || !d_flow2_out ||
+        !d_feat_prop_out || (body->branch > 0 && !d_prefix))
+        return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    DeviceGuard guard(ctx->device);
+    const hipStream_t s = (hipStream_t)stream;
+    const int H = body->h, W = body->w;
+    const int NCHW = DCN_TENSOR_NCHW, CB8 = DCN_TENSOR_CB8;
+    // Temporal alignment inputs straight into the CB8 tensors the convs and the DCN read.
+    DCN_TRY(dcn_temporal_prepare_f16_dev(ctx, W, H, d_feat_prop, d_feat_current, d_feat_n2, d_flow1,
+                                         d_prev_flow, has_second_order, d_flow2_out, body->cond_cb8,
+                                         DCN_TENSOR_CB8, body->deform_cb8, DCN_TENSOR_CB8, stream));
+    // conv_offset: 196 -> 64 -> 64 -> 64 (LeakyReLU 0.1) -> 432.
+    DCN_TRY(run_conv(ctx, body->offset_conv[0], body->cond_cb8, 1, nullptr, NCHW, nullptr, NCHW,
+                     body->off_a, CB8, s));
+    DCN_TRY(run_conv(ctx, body->offset_conv[1], body->off_a, 1, nullptr, NCHW, nullptr, NCHW,
+                     body->off_b, CB8, s));
+    DCN_TRY(run_conv(ctx, body->offset_conv[2], body->off_b, 1, nullptr, NCHW, nullptr, NCHW,
+                     body->off_a, CB8, s));
+    DCN_TRY(run_conv(ctx, body->offset_conv[3], body->off_a, 0, nullptr, NCHW, nullptr, NCHW,
+                     body->raw, NCHW, s));
+    DCN_TRY(dcn_offset_transform_f16_dev(ctx, (size_t)H * W, body->raw, d_flow1, d_flow2_out,
+                                         body->offset, body->mask, stream));
+    const dcn_shape ds = body_dcn_shape(H, W);
+    DCN_TRY(dcn_forward_f16_prepacked_cb8_dev(ctx, &ds, body->deform_cb8, body->offset, body->mask,
+                                              body->dcn, body->aligned, stream));
+    // Backbone input [feat_current, prefix..., aligned].
+    const void* sources[5] = {d_feat_current};
+    for (int i = 0; i < body->branch; ++i) {
+        if (!d_prefix[i]) return fail(ctx, DCN_INVALID_ARGUMENT, "prefix pointer is null");
+        sources[1 + i] = d_prefix[i];
+    }
+    sources[1 + body->branch] = body->aligned;
+    DCN_TRY(dcn_assemble_backbone_f16_dev(ctx, W, H, sources, body->branch + 2, body->bb_in,
+                                          DCN_TENSOR_CB8, stream));
+    DCN_TRY(run_conv(ctx, body->backbone[0], body->bb_in, 1, nullptr, NCHW, nullptr, NCHW,
+                     body->feat[0], CB8, s));
+    // Residual blocks: t = ReLU(conv(x)); x = x + conv(t). The last one also adds the
+    // aligned feature: feat_prop = aligned + backbone (add_propagation_residual_fp16).
+    int x = 0;
+    for (int i = 0; i < body->blocks; ++i) {
+        const int t = (x + 1) % 3, y = (x + 2) % 3;
+        DCN_TRY(run_conv(ctx, body->backbone[1 + 2 * i], body->feat[x], 2, nullptr, NCHW, nullptr,
+                         NCHW, body->feat[t], CB8, s));
+        const bool last = i + 1 == body->blocks;
+        DCN_TRY(run_conv(ctx, body->backbone[2 + 2 * i], body->feat[t], 0, body->feat[x], CB8,
+                         last ? body->aligned : nullptr, NCHW,
+                         last ? d_feat_prop_out : (void*)body->feat[y], last ? NCHW : CB8, s));
+        x = y;
+    }
+    return DCN_OK;
+}
+
+dcn_status dcn_body_capture(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                            const void* d_prev_flow, const void* d_feat_prop,
+                            const void* d_feat_n2, const void* const* d_prefix,
+                            int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                            dcn_graph** out) {
+    if (!body || !out) return DCN_INVALID_ARGUMENT;
+    *out = nullptr;
+    dcn_context* ctx = body->ctx;
+    DeviceGuard guard(ctx->device);
+    const hipStream_t s = body->capture_stream;
+    DCN_HIP(ctx, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const dcn_status st = dcn_body_step_dev(body, d_feat_current, d_flow1, d_prev_flow, d_feat_prop,
+                                            d_feat_n2, d_prefix, has_second_order, d_flow2_out,
+                                            d_feat_prop_out, s);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(s, &graph);
+    if (st != DCN_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return st;
+    }
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamEndCapture");
+    auto* g = new dcn_graph();
+    g->graph = graph;
+    g->device = ctx->device;
+    const hipError_t ie = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+        dcn_graph_destroy(g);
+        return hip_fail(ctx, ie, "hipGraphInstantiate");
+    }
+    *out = g;
+    return DCN_OK;
+}
+
+dcn_status dcn_graph_launch(dcn_graph* graph, void* stream) {
+    if (!graph || !graph->exec) return DCN_INVALID_ARGUMENT;
+    DeviceGuard guard(graph->device);
+    return hipGraphLaunch(graph->exec, (hipStream_t)stream) == hipSuccess ? DCN_OK
+                                                                          : DCN_COMMAND_FAILED;
+}
+
+void dcn_graph_destroy(dcn_graph* graph) {
+    if (!graph) return;
+    DeviceGuard guard(graph->device);
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+}
+
+}  // extern "C"

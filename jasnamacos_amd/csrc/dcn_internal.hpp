@@ -116,6 +116,45 @@ hipError_t launch_narrow_f16(const KShape& s, const FusedGeometry& g, const Fuse
                              const void* packed_w, const float* packed_b, uint16_t* out,
                              hipStream_t stream);
 
+// Propagation-body kernels (dcn_kernels_body.hip, dcn_kernels_conv.hip).
+constexpr int kLayoutNCHW = DCN_TENSOR_NCHW;
+constexpr int kLayoutCB8 = DCN_TENSOR_CB8;
+
+struct ConvGeometry {
+    int cin, cout, h, w;
+    int cb;      // ceil(cin / 8) input channel blocks
+    int kb;      // K-blocks = 9 * cb
+    int ksteps;  // K-steps of 4 K-blocks
+    int chunks;  // 64-channel output chunks
+    int nbt;     // 16-column blocks over all chunks
+};
+ConvGeometry conv_geometry(int cin, int cout, int height, int width);
+size_t conv_packed_bytes(const ConvGeometry& g);
+hipError_t launch_conv_prepack(const ConvGeometry& g, const uint16_t* w, const uint16_t* bias,
+                               void* wpk, float* bpk, hipStream_t stream);
+hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,
+                          const float* bias, int act, float slope, const uint16_t* res1,
+                          int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,
+                          int out_layout, hipStream_t stream);
+hipError_t launch_second_order_flow(const uint16_t* flow1, const uint16_t* prev, uint16_t* flow2,
+                                    int H, int W, int has_second_order, hipStream_t stream);
+hipError_t launch_temporal_assemble(const uint16_t* feat_prop, const uint16_t* feat_current,
+                                    const uint16_t* feat_n2, const uint16_t* flow1,
+                                    const uint16_t* flow2, uint16_t* conditions, int cond_layout,
+                                    uint16_t* deform_input, int deform_layout, int H, int W,
+                                    hipStream_t stream);
+hipError_t launch_offset_transform(const uint16_t* raw, const uint16_t* flow1, const uint16_t* flow2,
+                                   uint16_t* offset, uint16_t* mask, int plane, hipStream_t stream);
+hipError_t launch_assemble(const uint16_t* const* sources, int count, uint16_t* out, int out_layout,
+                           int H, int W, hipStream_t stream);
+hipError_t launch_add_residual(const uint16_t* aligned, const uint16_t* backbone, uint16_t* out,
+                               long count, hipStream_t stream);
+hipError_t launch_cb8_to_nchw(const uint16_t* cb8, uint16_t* out, int C, int H, int W,
+                              hipStream_t stream);
+inline size_t cb8_tensor_elems(int channels, int h, int w) {
+    return (size_t)((channels + 7) / 8) * 8 * (h + 2 * DCN_CB8_PAD) * (w + 2 * DCN_CB8_PAD);
+}
+
 // Constant of dev::fast_div: ceil(2^32 / d) for d > 1, 0 for d == 1.
 inline uint32_t magic_for(int d) {
     return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + (uint64_t)d - 1) / (uint64_t)d);

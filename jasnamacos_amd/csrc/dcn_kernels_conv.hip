@@ -1,0 +1,249 @@
+// 3x3 convolution (stride 1, pad 1) for the propagation body's offset branch and
+// backbone: FP16 storage, FP32 accumulation on v_mfma_f32_16x16x32_f16.
+//
+// Implicit GEMM over the CB8 input ([Cin/8][H+4][W+4][8], 2-pixel zero border): out
+// [pixel][oc] = sum over K-blocks kb = tap * CB + cb of x[cb][y + ky - 1][x + kx - 1][0..7]
+// . W[oc][8 cb .. 8 cb + 7][ky][kx]. A K-block of one pixel is one 16-byte load and the
+// border supplies the zero padding, so the A fragment needs no arithmetic at all (the
+// deformable kernels' sampler with integer offsets and no blend). Lane layout, tiling,
+// K split over waves and the LDS reduction follow dcn_kernels_narrow.hip: 16-pixel tiles,
+// lane l takes pixel l%16 and K-block 4s + l/16 of K-step s.
+//
+// Workgroup (tile, chunk) computes 64 output channels (4 column blocks of 16) of 16
+// pixels; chunks split Cout (432 -> 7 chunks, the last one partly padded with zero
+// weights). Epilogue: + bias, activation (none / LeakyReLU(slope) / ReLU), optional
+// residual r1 and second residual r2, each add rounded to FP16 as a separate FP16 op:
+// out = half(r2 + half(r1 + act(acc))). Output NCHW or CB8.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "dcn_device.hpp"
+#include "dcn_internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace dcn {
+namespace {
+
+using namespace dev;
+
+constexpr int kConvChunk = 64;  // output channels per workgroup
+constexpr int kConvNbc = kConvChunk / 16;
+
+struct ConvArgs {
+    const void* xin;        // CB8 input
+    const void* wpk;        // [ksteps][NBT][64][8] FP16
+    const float* bias;      // [Cout] FP32
+    const uint16_t* res1;   // optional residual (layout res1_layout)
+    const uint16_t* res2;   // optional second residual (layout res2_layout)
+    uint16_t* out;
+    uint32_t xin_bytes, wpk_bytes;
+    int res1_layout, res2_layout, out_layout;
+    int H, W, Hp, Wp, CB, KB, ksteps, NBT, Cout, tiles, act;
+    float slope;
+    uint32_t magic_cb;
+};
+
+__device__ __forceinline__ size_t conv_index(int layout, int c, int y, int x, int H, int W, int Hp,
+                                             int Wp) {
+    if (layout == kLayoutCB8) return ((size_t)((c >> 3) * Hp + y + kPad) * Wp + x + kPad) * 8 + (c & 7);
+    return ((size_t)c * H + y) * W + x;
+}
+
+template <int NW, int U>
+__global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a) {
+    constexpr int NB = kConvNbc;
+    extern __shared__ float red[];  // [NW][NB][4][65]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int quarter = lane >> 4;
+
+    const int per_xcd = (a.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+    const int chunk = blockIdx.y;
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+
+    const int M = a.H * a.W;
+    const int p = tile * 16 + (lane & 15);
+    const bool pvalid = p < M;
+    const int pc = pvalid ? p : M - 1;
+    const int y = pc / a.W;
+    const int x = pc - y * a.W;
+    // 16-byte unit of (cb 0, y - 1, x - 1) in the padded plane.
+    const uint32_t base = (uint32_t)(y + kPad - 1) * a.Wp + x + kPad - 1;
+
+    f32x4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{};
+
+    const int s0 = wave * a.ksteps / NW;
+    const int s1 = (wave + 1) * a.ksteps / NW;
+    for (int sb = s0; sb < s1; sb += U) {
+        h8 Bf[U][NB];
+        u32x4 q[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int s = sb + i < s1 ? sb + i : s1 - 1;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                Bf[i][nb] = __builtin_bit_cast(
+                    h8, load16(wr, (uint32_t)((s * a.NBT + chunk * NB + nb) * 64 + lane) * 16u));
+            const int kb = 4 * s + quarter;
+            const int kbc = kb < a.KB ? kb : a.KB - 1;
+            const int tap = fast_div(kbc, a.magic_cb);
+            const int cb = kbc - tap * a.CB;
+            const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
+            const int kx = tap - ky * 3;
+            q[i] = load16(xr, (base + (uint32_t)(cb * a.Hp + ky) * a.Wp + kx) * 16u);
+        }
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            if (sb + i < s1) {  // uniform across the wave
+                const int kb = 4 * (sb + i) + quarter;
+                const u32x4 z = {0u, 0u, 0u, 0u};
+                // Padding K-blocks multiply zero weights; zero A keeps a non-finite
+                // input from turning 0 * inf into NaN there.
+                const h8 A = __builtin_bit_cast(h8, kb < a.KB ? q[i] : z);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+    __syncthreads();
+
+    for (int idx = tid; idx < 16 * kConvChunk; idx += 64 * NW) {
+        const int pl = idx & 15;
+        const int ocl = idx >> 4;
+        const int nb = ocl >> 4;
+        const int src = ((pl >> 2) << 4) + (ocl & 15);
+        const int v = pl & 3;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
+        const int oc = chunk * kConvChunk + ocl;
+        const int pp = tile * 16 + pl;
+        if (pp >= M || oc >= a.Cout) continue;
+        const int yy = pp / a.W;
+        const int xx = pp - yy * a.W;
+        float r = sum + a.bias[oc];
+        if (a.act == 1 && r < 0.0f) r = r * a.slope;
+        if (a.act == 2 && r < 0.0f) r = 0.0f;
+        if (a.res1 != nullptr) {
+            const float id = (float)__builtin_bit_cast(
+                _Float16, a.res1[conv_index(a.res1_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)]);
+            r = id + r;
+        }
+        if (a.res2 != nullptr) {
+            const float r1 = (float)round_f16(r);
+            const float id = (float)__builtin_bit_cast(
+                _Float16, a.res2[conv_index(a.res2_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)]);
+            r = id + r1;
+        }
+        a.out[conv_index(a.out_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)] =
+            __builtin_bit_cast(uint16_t, round_f16(r));
+    }
+}
+
+// Conv weights OIHW FP16 [Cout][Cin][3][3] -> B fragments [ksteps][NBT][64][8]:
+// lane l of K-step s holds output channel nb*16 + l%16 and K-block 4s + l/16 =
+// tap * CB + cb, channels 8 cb .. 8 cb + 7 (zero past Cin, past Cout and past KB).
+__global__ __launch_bounds__(256) void conv_prepack_kernel(const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ bias,
+                                                           uint16_t* __restrict__ wpk,
+                                                           float* __restrict__ bpk, int Cin,
+                                                           int Cout, int CB, int KB, int NBT,
+                                                           long total) {
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid < Cout) bpk[gid] = (float)__builtin_bit_cast(_Float16, bias[gid]);
+    if (gid >= total) return;
+    const int e = (int)(gid & 7);
+    const int lane = (int)((gid >> 3) & 63);
+    const long q = gid >> 9;
+    const int nb = (int)(q % NBT);
+    const int s = (int)(q / NBT);
+    const int kb = 4 * s + (lane >> 4);
+    const int oc = nb * 16 + (lane & 15);
+    uint16_t v = 0;
+    if (kb < KB && oc < Cout) {
+        const int tap = kb / CB;
+        const int ic = (kb - tap * CB) * 8 + e;
+        if (ic < Cin) v = w[((size_t)oc * Cin + ic) * 9 + tap];
+    }
+    wpk[gid] = v;
+}
+
+}  // namespace
+
+ConvGeometry conv_geometry(int cin, int cout, int height, int width) {
+    ConvGeometry g;
+    g.cin = cin;
+    g.cout = cout;
+    g.h = height;
+    g.w = width;
+    g.cb = (cin + 7) / 8;
+    g.kb = 9 * g.cb;
+    g.ksteps = (g.kb + 3) / 4;
+    g.chunks = (cout + kConvChunk - 1) / kConvChunk;
+    g.nbt = g.chunks * kConvNbc;
+    return g;
+}
+
+size_t conv_packed_bytes(const ConvGeometry& g) { return (size_t)g.ksteps * g.nbt * 64 * 8 * 2; }
+
+hipError_t launch_conv_prepack(const ConvGeometry& g, const uint16_t* w, const uint16_t* bias,
+                               void* wpk, float* bpk, hipStream_t stream) {
+    const long total = (long)g.ksteps * g.nbt * 64 * 8;
+    const long grid = (std::max<long>(total, g.cout) + 255) / 256;
+    hipLaunchKernelGGL(conv_prepack_kernel, dim3((unsigned)grid), dim3(256), 0, stream, w, bias,
+                       (uint16_t*)wpk, bpk, g.cin, g.cout, g.cb, g.kb, g.nbt, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,
+                          const float* bias, int act, float slope, const uint16_t* res1,
+                          int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,
+                          int out_layout, hipStream_t stream) {
+    constexpr int NW = 8, U = 4;
+    ConvArgs a;
+    a.xin = x_cb8;
+    a.wpk = wpk;
+    a.bias = bias;
+    a.res1 = res1;
+    a.res2 = res2;
+    a.out = out;
+    a.H = g.h;
+    a.W = g.w;
+    a.Hp = g.h + 2 * kPad;
+    a.Wp = g.w + 2 * kPad;
+    a.xin_bytes = (uint32_t)((size_t)g.cb * a.Hp * a.Wp * 16);
+    a.wpk_bytes = (uint32_t)conv_packed_bytes(g);
+    a.res1_layout = res1_layout;
+    a.res2_layout = res2_layout;
+    a.out_layout = out_layout;
+    a.CB = g.cb;
+    a.KB = g.kb;
+    a.ksteps = g.ksteps;
+    a.NBT = g.nbt;
+    a.Cout = g.cout;
+    a.tiles = (g.h * g.w + 15) / 16;
+    a.act = act;
+    a.slope = slope;
+    a.magic_cb = magic_for(g.cb);
+    const size_t lds = (size_t)NW * kConvNbc * 4 * 65 * sizeof(float);
+    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)g.chunks);
+    hipLaunchKernelGGL((conv3x3_kernel<NW, U>), grid, dim3(64 * NW), lds, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace dcn

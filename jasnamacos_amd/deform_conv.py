@@ -346,6 +346,179 @@ class HipDeformConv:
                                                    C.byref(ks), C.byref(sm)))
         return {"variant": v.value, "mt": mt.value, "ks": ks.value, "sampler": sm.value}
 
+    # ---- propagation body ------------------------------------------------------------
+
+    def offset_transform_f16(self, plane: int, raw, flow1, flow2):
+        """runDCNOffsetTransform (MetalRunner.swift:469-508): FP16 arrays in, (offset, mask) out."""
+        raw, flow1, flow2 = _u16(raw), _u16(flow1), _u16(flow2)
+        off = np.empty(288 * plane, np.uint16)
+        msk = np.empty(144 * plane, np.uint16)
+        self._check(self._lib.dcn_offset_transform_f16(self.ctx, int(plane), _hp(raw), raw.size, _hp(flow1),
+                                                       flow1.size, _hp(flow2), flow2.size, _hp(off), off.size,
+                                                       _hp(msk), msk.size))
+        return off.view(np.float16), msk.view(np.float16)
+
+    def offset_transform_f16_dev(self, plane: int, raw, flow1, flow2, offset, mask, stream=None) -> None:
+        self._check(self._lib.dcn_offset_transform_f16_dev(self.ctx, int(plane), _ptr(raw), _ptr(flow1),
+                                                           _ptr(flow2), _ptr(offset), _ptr(mask), _stream(stream)))
+
+    def temporal_prepare_f16(self, width: int, height: int, feat_prop, feat_current, feat_n2, flow1,
+                             prev_flow, has_second_order: bool) -> dict:
+        """runTemporalPreparation (MetalRunner.swift:510-582): conditions, deform_input, flow2."""
+        a = [_u16(x) for x in (feat_prop, feat_current, feat_n2, flow1, prev_flow)]
+        plane = width * height
+        cond = np.empty(196 * plane, np.uint16)
+        dinp = np.empty(128 * plane, np.uint16)
+        flow2 = np.empty(2 * plane, np.uint16)
+        args = []
+        for x in a:
+            args += [_hp(x), x.size]
+        self._check(self._lib.dcn_temporal_prepare_f16(self.ctx, int(width), int(height), *args,
+                                                       int(bool(has_second_order)), _hp(cond), cond.size,
+                                                       _hp(dinp), dinp.size, _hp(flow2), flow2.size))
+        return {"conditions": cond.view(np.float16), "deform_input": dinp.view(np.float16),
+                "flow2": flow2.view(np.float16)}
+
+    def temporal_prepare_f16_dev(self, width, height, feat_prop, feat_current, feat_n2, flow1, prev_flow,
+                                 has_second_order, flow2, conditions, conditions_layout, deform_input,
+                                 deform_input_layout, stream=None) -> None:
+        self._check(self._lib.dcn_temporal_prepare_f16_dev(
+            self.ctx, int(width), int(height), _ptr(feat_prop), _ptr(feat_current), _ptr(feat_n2), _ptr(flow1),
+            _ptr(prev_flow), int(bool(has_second_order)), _ptr(flow2), _ptr(conditions), int(conditions_layout),
+            _ptr(deform_input), int(deform_input_layout), _stream(stream)))
+
+    def assemble_backbone_f16_dev(self, width, height, sources, out, layout=0, stream=None) -> None:
+        arr = (C.c_void_p * len(sources))(*[_ptr(x) for x in sources])
+        self._check(self._lib.dcn_assemble_backbone_f16_dev(self.ctx, int(width), int(height), arr, len(sources),
+                                                            _ptr(out), int(layout), _stream(stream)))
+
+    def add_residual_f16_dev(self, count, aligned, backbone, out, stream=None) -> None:
+        self._check(self._lib.dcn_add_residual_f16_dev(self.ctx, int(count), _ptr(aligned), _ptr(backbone),
+                                                       _ptr(out), _stream(stream)))
+
+    def cb8_to_nchw_f16_dev(self, channels, height, width, cb8, out, stream=None) -> None:
+        self._check(self._lib.dcn_cb8_to_nchw_f16_dev(self.ctx, int(channels), int(height), int(width), _ptr(cb8),
+                                                      _ptr(out), _stream(stream)))
+
+    def conv3x3(self, cin, cout, height, width, weight, bias, stream=None) -> "Conv3x3":
+        handle = C.c_void_p()
+        self._check(self._lib.dcn_conv3x3_create_dev(self.ctx, int(cin), int(cout), int(height), int(width),
+                                                     _ptr(weight), _ptr(bias), _stream(stream), C.byref(handle)))
+        return Conv3x3(self, handle.value, cin, cout, height, width)
+
+    def body(self, height, width, weights: dict, branch: int = 0, blocks: int = 5, stream=None) -> "PropagationBody":
+        """weights: device tensors "offset_w{0..3}", "offset_b{0..3}", "dcn_w", "dcn_b",
+        "backbone_w{0..2*blocks}", "backbone_b{0..2*blocks}" (OIHW FP16)."""
+        w = _lib.DcnBodyWeights()
+        for i in range(4):
+            w.offset_weight[i] = _ptr(weights[f"offset_w{i}"])
+            w.offset_bias[i] = _ptr(weights[f"offset_b{i}"])
+        w.dcn_weight = _ptr(weights["dcn_w"])
+        w.dcn_bias = _ptr(weights["dcn_b"])
+        for i in range(1 + 2 * blocks):
+            w.backbone_weight[i] = _ptr(weights[f"backbone_w{i}"])
+            w.backbone_bias[i] = _ptr(weights[f"backbone_b{i}"])
+        handle = C.c_void_p()
+        self._check(self._lib.dcn_body_create(self.ctx, int(height), int(width), int(branch), int(blocks),
+                                              C.byref(w), _stream(stream), C.byref(handle)))
+        return PropagationBody(self, handle.value, height, width, branch, blocks)
+
+
+TENSOR_NCHW = 0
+TENSOR_CB8 = 1
+
+
+def cb8_tensor_count(channels: int, height: int, width: int) -> int:
+    return int(lib().dcn_cb8_tensor_count(int(channels), int(height), int(width)))
+
+
+class Conv3x3:
+    """A 3x3 body convolution with its weights packed into MFMA fragments (dcn_conv)."""
+
+    def __init__(self, ctx: HipDeformConv, handle: int, cin, cout, height, width):
+        self.ctx, self.handle = ctx, C.c_void_p(handle)
+        self.cin, self.cout, self.height, self.width = cin, cout, height, width
+
+    def run_dev(self, x_cb8, out, out_layout=TENSOR_NCHW, activation=0, slope=0.1, res1=None,
+                res1_layout=TENSOR_NCHW, res2=None, res2_layout=TENSOR_NCHW, stream=None) -> None:
+        self.ctx._check(self.ctx._lib.dcn_conv3x3_f16_dev(self.ctx.ctx, self.handle, _ptr(x_cb8), int(activation),
+                                                          float(slope), _ptr(res1), int(res1_layout), _ptr(res2),
+                                                          int(res2_layout), _ptr(out), int(out_layout),
+                                                          _stream(stream)))
+
+    def free(self) -> None:
+        if self.handle:
+            self.ctx._lib.dcn_conv3x3_free(self.handle)
+            self.handle = C.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class BodyGraph:
+    """An executable hipGraph of one body step (dcn_graph)."""
+
+    def __init__(self, ctx: HipDeformConv, handle: int):
+        self.ctx, self.handle = ctx, C.c_void_p(handle)
+
+    def launch(self, stream=None) -> None:
+        self.ctx._check(self.ctx._lib.dcn_graph_launch(self.handle, _stream(stream)))
+
+    def free(self) -> None:
+        if self.handle:
+            self.ctx._lib.dcn_graph_destroy(self.handle)
+            self.handle = C.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class PropagationBody:
+    """One BasicVSR++ propagation step for one branch (dcn_body)."""
+
+    def __init__(self, ctx: HipDeformConv, handle: int, height, width, branch, blocks):
+        self.ctx, self.handle = ctx, C.c_void_p(handle)
+        self.height, self.width, self.branch, self.blocks = height, width, branch, blocks
+
+    def _args(self, feat_current, flow1, prev_flow, feat_prop, feat_n2, prefix, has_second_order, flow2_out,
+              feat_prop_out):
+        pre = None
+        if prefix:
+            pre = (C.c_void_p * len(prefix))(*[_ptr(x) for x in prefix])
+        return (_ptr(feat_current), _ptr(flow1), _ptr(prev_flow), _ptr(feat_prop), _ptr(feat_n2), pre,
+                int(bool(has_second_order)), _ptr(flow2_out), _ptr(feat_prop_out))
+
+    def step_dev(self, feat_current, flow1, prev_flow, feat_prop, feat_n2, flow2_out, feat_prop_out,
+                 has_second_order=True, prefix=None, stream=None) -> None:
+        self.ctx._check(self.ctx._lib.dcn_body_step_dev(
+            self.handle, *self._args(feat_current, flow1, prev_flow, feat_prop, feat_n2, prefix, has_second_order,
+                                     flow2_out, feat_prop_out), _stream(stream)))
+
+    def capture(self, feat_current, flow1, prev_flow, feat_prop, feat_n2, flow2_out, feat_prop_out,
+                has_second_order=True, prefix=None) -> BodyGraph:
+        handle = C.c_void_p()
+        self.ctx._check(self.ctx._lib.dcn_body_capture(
+            self.handle, *self._args(feat_current, flow1, prev_flow, feat_prop, feat_n2, prefix, has_second_order,
+                                     flow2_out, feat_prop_out), C.byref(handle)))
+        return BodyGraph(self.ctx, handle.value)
+
+    def free(self) -> None:
+        if self.handle:
+            self.ctx._lib.dcn_body_destroy(self.handle)
+            self.handle = C.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
 
 # ---- deterministic inputs ----------------------------------------------------------
 
@@ -402,6 +575,50 @@ def reference_benchmark_inputs(seed: int = 0x4A41534E41) -> dict:
         "shape": shape,
     }
     return out
+
+
+def generate_body_inputs(height: int = 64, width: int = 64, frames: int = 30, branch: int = 0, blocks: int = 5,
+                         seed: int = 4, weight_std: float = 0.02, flow_px: float = 4.0) -> dict:
+    """Synthetic config-C4 clip: random-init body weights ~N(0, weight_std) (OIHW FP16),
+    per-frame spatial features ~N(0, 1) [frames][64*H*W] and first-order flows
+    [frames][2*H*W] (x, y) from a bilinearly upsampled 8x8 grid of U(-flow_px, flow_px),
+    all from numpy's PCG64 generator with the given seed."""
+    rng = np.random.default_rng(seed)
+    f16 = lambda a: np.asarray(a, np.float32).astype(np.float16)  # noqa: E731
+    w = {}
+    for i, (ci, co) in enumerate([(196, 64), (64, 64), (64, 64), (64, 432)]):
+        w[f"offset_w{i}"] = f16(rng.normal(0, weight_std, (co, ci, 3, 3)))
+        w[f"offset_b{i}"] = f16(rng.normal(0, weight_std, co))
+    w["dcn_w"] = f16(rng.normal(0, weight_std, (64, 128, 3, 3)))
+    w["dcn_b"] = f16(rng.normal(0, weight_std, 64))
+    for i in range(1 + 2 * blocks):
+        ci = 64 * (branch + 2) if i == 0 else 64
+        w[f"backbone_w{i}"] = f16(rng.normal(0, weight_std, (64, ci, 3, 3)))
+        w[f"backbone_b{i}"] = f16(rng.normal(0, weight_std, 64))
+    plane = height * width
+    feats = f16(rng.standard_normal((frames, 64 * plane)))
+    grid_y = np.linspace(0, 7, height)
+    grid_x = np.linspace(0, 7, width)
+    flows = np.empty((frames, 2, height, width), np.float32)
+    for t in range(frames):
+        for c in range(2):
+            g = rng.uniform(-flow_px, flow_px, (8, 8))
+            y0 = np.minimum(np.floor(grid_y).astype(int), 6)
+            x0 = np.minimum(np.floor(grid_x).astype(int), 6)
+            ly = (grid_y - y0)[:, None]
+            lx = (grid_x - x0)[None, :]
+            flows[t, c] = (g[y0][:, x0] * (1 - ly) * (1 - lx) + g[y0][:, x0 + 1] * (1 - ly) * lx +
+                           g[y0 + 1][:, x0] * ly * (1 - lx) + g[y0 + 1][:, x0 + 1] * ly * lx)
+    prefix = f16(rng.standard_normal((branch, frames, 64 * plane)))
+    return {"weights": w, "feats": feats, "flows": f16(flows.reshape(frames, 2 * plane)), "prefix": prefix,
+            "height": height, "width": width, "frames": frames, "branch": branch, "blocks": blocks}
+
+
+def body_flops(height: int, width: int, branch: int = 0, blocks: int = 5) -> int:
+    """GEMM-equivalent flops of one body: conv_offset, the DCN and the backbone."""
+    plane = height * width
+    convs = [(196, 64), (64, 64), (64, 64), (64, 432), (64 * (branch + 2), 64)] + [(64, 64)] * (2 * blocks)
+    return sum(2 * plane * 9 * ci * co for ci, co in convs) + 2 * plane * 9 * 128 * 64
 
 
 def pack_ic_k_oc(weight_oihw: np.ndarray, shape: DeformConvShape) -> np.ndarray:

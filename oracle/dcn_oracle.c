@@ -426,6 +426,8 @@ void oracle_conv3x3_f16(int cin, int cout, int height, int width, const uint16_t
                         float slope, const uint16_t* residual, uint16_t* output) {
     /* activation: 0 none, 1 LeakyReLU(slope), 2 ReLU. out = half(act(acc) [+ residual]). */
     const size_t plane = (size_t)width * height;
+    /* Output channels are independent; each element is computed by the same serial code. */
+#pragma omp parallel for schedule(static)
     for (int oc = 0; oc < cout; ++oc) {
         for (int oy = 0; oy < height; ++oy) {
             for (int ox = 0; ox < width; ++ox) {

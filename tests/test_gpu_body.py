@@ -1,0 +1,273 @@
+"""GPU parity of the propagation-body entry points (config C4) against the CPU oracle.
+
+Bars:
+  * temporal preparation (second-order flow, conditions, deform input), backbone
+    assembly and the alignment residual: bit-identical to the oracle / numpy (no
+    transcendental functions, same FP32 association, one rounding);
+  * offset transform: within one FP16 ulp of the oracle (device tanhf / expf against
+    the host's), and inside the reference's own 5e-3 gate (JasnaCLI.swift:177-211);
+  * conv3x3: within 2 FP16 ulp + 1e-4 of the oracle (only the FP32 summation order
+    differs);
+  * one whole body step: max |err| <= 2e-2, mean |err| <= 1e-3 against the oracle chain
+    (north-star FP16 tolerances), second-order flow bit-identical;
+  * a captured body graph replays bit-identically to the eager step.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import body_reference as br
+
+pytestmark = pytest.mark.gpu
+
+
+def log(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(np.asarray(a, np.float16)).view(np.int16)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy().view(np.float16)
+
+
+def ulp_close(got, ref, ulps=1, atol=0.0):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    ulp = np.maximum(np.abs(ref), 2.0 ** -14) * 2.0 ** -10
+    return np.abs(got - ref) <= ulps * ulp + atol
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+
+    return t
+
+
+def test_offset_transform_matches_oracle(gpu_ctx, oracle):
+    rng = np.random.default_rng(40)
+    plane = 13 * 17
+    raw = br.f16(rng.normal(0, 2.0, 432 * plane))
+    raw[:8] = np.array([0, -0, 30, -30, 1e-4, -1e-4, 65504, -65504], np.float16)
+    flow1 = br.f16(rng.uniform(-8, 8, 2 * plane))
+    flow2 = br.f16(rng.uniform(-8, 8, 2 * plane))
+    log("case: offset transform, plane", plane)
+    off, msk = gpu_ctx.offset_transform_f16(plane, raw, flow1, flow2)
+    roff, rmsk = oracle.offset_transform_f16(plane, raw, flow1, flow2)
+    assert np.all(ulp_close(off, roff)), float(np.abs(off.astype(np.float64) - roff).max())
+    assert np.all(ulp_close(msk, rmsk)), float(np.abs(msk.astype(np.float64) - rmsk).max())
+    assert np.abs(off.astype(np.float64) - roff).max() <= 5e-3 * 32  # offsets reach +-18 px
+    assert np.abs(msk.astype(np.float64) - rmsk).max() <= 5e-3
+    identical = float(np.mean(off.view(np.uint16) == roff.view(np.uint16)))
+    log(f"  offsets bit-identical: {identical:.4f}")
+
+
+def test_offset_transform_count_checks(gpu_ctx, dcn):
+    plane = 10
+    with pytest.raises(dcn.DeformConvError) as e:
+        gpu_ctx.offset_transform_f16(plane, np.zeros(431 * plane, np.float16), np.zeros(2 * plane, np.float16),
+                                     np.zeros(2 * plane, np.float16))
+    assert e.value.status == dcn.INVALID_SHAPE
+
+
+@pytest.mark.parametrize("second", [True, False])
+def test_temporal_prepare_bit_exact(gpu_ctx, oracle, second):
+    rng = np.random.default_rng(41)
+    h, w = 11, 14
+    x = br.body_inputs(rng, h, w, flow_px=6.0)
+    log("case: temporal prepare, second order", second)
+    got = gpu_ctx.temporal_prepare_f16(w, h, x["feat_prop"], x["feat_current"], x["feat_n2"], x["flow1"],
+                                       x["prev_flow"], second)
+    flow2, cond, dinp = oracle.temporal_prepare_f16(w, h, second, x["feat_prop"], x["feat_current"], x["feat_n2"],
+                                                    x["flow1"], x["prev_flow"])
+    assert np.array_equal(got["flow2"].view(np.uint16), flow2.view(np.uint16))
+    assert np.array_equal(got["conditions"].view(np.uint16), cond.view(np.uint16))
+    assert np.array_equal(got["deform_input"].view(np.uint16), dinp.view(np.uint16))
+    if not second:
+        assert not np.any(got["flow2"].view(np.uint16))
+
+
+def test_temporal_prepare_cb8_layout(gpu_ctx, dcn, oracle, torch):
+    rng = np.random.default_rng(42)
+    h, w = 9, 12
+    x = br.body_inputs(rng, h, w)
+    t = {k: dev(torch, x[k]) for k in ("feat_prop", "feat_current", "feat_n2", "flow1", "prev_flow")}
+    flow2 = torch.empty(2 * h * w, dtype=torch.int16, device="cuda")
+    cond = torch.zeros(dcn.cb8_tensor_count(196, h, w), dtype=torch.int16, device="cuda")
+    dinp = torch.zeros(dcn.cb8_tensor_count(128, h, w), dtype=torch.int16, device="cuda")
+    log("case: temporal prepare CB8")
+    gpu_ctx.temporal_prepare_f16_dev(w, h, t["feat_prop"], t["feat_current"], t["feat_n2"], t["flow1"],
+                                     t["prev_flow"], True, flow2, cond, dcn.TENSOR_CB8, dinp, dcn.TENSOR_CB8)
+    torch.cuda.synchronize()
+    _, rc, rd = oracle.temporal_prepare_f16(w, h, True, x["feat_prop"], x["feat_current"], x["feat_n2"],
+                                            x["flow1"], x["prev_flow"])
+    assert np.array_equal(host(cond).view(np.uint16).ravel(), br.to_cb8(rc, 196, h, w).view(np.uint16).ravel())
+    assert np.array_equal(host(dinp).view(np.uint16).ravel(), br.to_cb8(rd, 128, h, w).view(np.uint16).ravel())
+    back = torch.empty(196 * h * w, dtype=torch.int16, device="cuda")
+    gpu_ctx.cb8_to_nchw_f16_dev(196, h, w, cond, back)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(back).view(np.uint16), rc.view(np.uint16))
+
+
+@pytest.mark.parametrize("count", [1, 2, 5])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_assemble_backbone_and_residual(gpu_ctx, dcn, torch, count, layout):
+    rng = np.random.default_rng(43 + count)
+    h, w = 7, 10
+    srcs = [br.f16(rng.standard_normal(64 * h * w)) for _ in range(count)]
+    d = [dev(torch, s) for s in srcs]
+    n = 64 * count
+    out = torch.zeros(dcn.cb8_tensor_count(n, h, w) if layout else n * h * w, dtype=torch.int16, device="cuda")
+    log("case: assemble", count, "layout", layout)
+    gpu_ctx.assemble_backbone_f16_dev(w, h, d, out, layout)
+    torch.cuda.synchronize()
+    ref = np.concatenate(srcs)
+    if layout:
+        ref = br.to_cb8(ref, n, h, w)
+    assert np.array_equal(host(out).view(np.uint16).ravel(), ref.view(np.uint16).ravel())
+    a, b = srcs[0], br.f16(rng.standard_normal(64 * h * w))
+    r = torch.empty(64 * h * w, dtype=torch.int16, device="cuda")
+    gpu_ctx.add_residual_f16_dev(a.size, d[0], dev(torch, b), r)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(r).view(np.uint16), br.f16(a.astype(np.float32) + b.astype(np.float32)).view(np.uint16))
+
+
+CONV_CASES = [
+    # cin, cout, activation, residual layout (None = no residual), out layout
+    (196, 64, 1, None, 1),
+    (64, 432, 0, None, 0),
+    (128, 64, 1, None, 1),
+    (64, 64, 2, None, 1),
+    (64, 64, 0, 1, 1),
+    (64, 64, 0, 0, 0),
+    (24, 40, 1, None, 0),
+]
+
+
+@pytest.mark.parametrize("cin,cout,act,res,out_layout", CONV_CASES)
+def test_conv3x3_matches_oracle(gpu_ctx, dcn, oracle, torch, cin, cout, act, res, out_layout):
+    rng = np.random.default_rng(cin * 7 + cout + act)
+    h, w = 13, 21
+    x = br.f16(rng.standard_normal(cin * h * w))
+    wt = br.f16(rng.normal(0, 0.05, (cout, cin, 3, 3)))
+    b = br.f16(rng.normal(0, 0.05, cout))
+    r = br.f16(rng.standard_normal(cout * h * w)) if res is not None else None
+    log("case: conv3x3", cin, cout, act, res, out_layout)
+    conv = gpu_ctx.conv3x3(cin, cout, h, w, dev(torch, wt), dev(torch, b))
+    xd = dev(torch, br.to_cb8(x, cin, h, w))
+    rd = None
+    if r is not None:
+        rd = dev(torch, br.to_cb8(r, cout, h, w) if res == 1 else r)
+    n = dcn.cb8_tensor_count(cout, h, w) if out_layout else cout * h * w
+    out = torch.zeros(n, dtype=torch.int16, device="cuda")
+    conv.run_dev(xd, out, out_layout, act, 0.1, rd, res if res is not None else 0)
+    torch.cuda.synchronize()
+    got = host(out)
+    if out_layout:
+        full = got.reshape((cout + 7) // 8, h + 4, w + 4, 8).transpose(0, 3, 1, 2).reshape(-1, h + 4, w + 4)
+        assert not np.any(full[:, :2].view(np.uint16)) and not np.any(full[:, :, :2].view(np.uint16))
+        got = full[:cout, 2:2 + h, 2:2 + w].ravel()
+    ref = oracle.conv3x3_f16(cin, cout, h, w, x, wt, b, act, 0.1, r)
+    ok = ulp_close(got, ref, ulps=2, atol=1e-4)
+    assert np.all(ok), float(np.abs(got.astype(np.float64) - ref).max())
+    conv.free()
+
+
+def _body_case(torch, gpu_ctx, h, w, branch, blocks, seed):
+    rng = np.random.default_rng(seed)
+    weights = br.body_weights(rng, branch, blocks)
+    x = br.body_inputs(rng, h, w, branch)
+    wd = {k: dev(torch, v) for k, v in weights.items()}
+    body = gpu_ctx.body(h, w, wd, branch=branch, blocks=blocks)
+    xd = {k: dev(torch, x[k]) for k in ("feat_current", "flow1", "prev_flow", "feat_prop", "feat_n2")}
+    xd["prefix"] = [dev(torch, p) for p in x["prefix"]]
+    return weights, x, wd, body, xd
+
+
+@pytest.mark.parametrize("h,w,branch,blocks", [(16, 24, 0, 2), (12, 20, 2, 1), (64, 64, 0, 5)])
+def test_body_step_matches_oracle_chain(gpu_ctx, torch, h, w, branch, blocks):
+    weights, x, wd, body, xd = _body_case(torch, gpu_ctx, h, w, branch, blocks, 50 + h + branch)
+    flow2 = torch.empty(2 * h * w, dtype=torch.int16, device="cuda")
+    out = torch.empty(64 * h * w, dtype=torch.int16, device="cuda")
+    log("case: body step", h, w, "branch", branch, "blocks", blocks)
+    body.step_dev(xd["feat_current"], xd["flow1"], xd["prev_flow"], xd["feat_prop"], xd["feat_n2"], flow2, out,
+                  True, xd["prefix"] or None)
+    torch.cuda.synchronize()
+    rflow2, rout, _ = br.body_step(weights, x, h, w, blocks, True)
+    assert np.array_equal(host(flow2).view(np.uint16), rflow2.view(np.uint16))
+    got = host(out).astype(np.float64)
+    e = np.abs(got - rout.astype(np.float64))
+    log(f"  body out: max {e.max():.3e} mean {e.mean():.3e} (|ref| mean {np.abs(rout.astype(np.float64)).mean():.3f})")
+    assert np.all(np.isfinite(got))
+    assert e.max() <= 2e-2 and e.mean() <= 1e-3
+    body.free()
+
+
+def test_body_graph_replays_match_eager(gpu_ctx, torch):
+    h, w, blocks = 32, 32, 3
+    weights, x, wd, body, xd = _body_case(torch, gpu_ctx, h, w, 0, blocks, 77)
+    flow2 = torch.empty(2 * h * w, dtype=torch.int16, device="cuda")
+    eager = torch.empty(64 * h * w, dtype=torch.int16, device="cuda")
+    out = torch.empty(64 * h * w, dtype=torch.int16, device="cuda")
+    log("case: body graph replay")
+    body.step_dev(xd["feat_current"], xd["flow1"], xd["prev_flow"], xd["feat_prop"], xd["feat_n2"], flow2, eager)
+    torch.cuda.synchronize()
+    ref = host(eager).copy()
+    graph = body.capture(xd["feat_current"], xd["flow1"], xd["prev_flow"], xd["feat_prop"], xd["feat_n2"], flow2, out)
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        graph.launch()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out).view(np.uint16), ref.view(np.uint16)), i
+        # eager work between replays
+        body.step_dev(xd["feat_current"], xd["flow1"], xd["prev_flow"], xd["feat_prop"], xd["feat_n2"], flow2, eager)
+        torch.cuda.synchronize()
+    graph.free()
+    body.free()
+
+
+def test_body_recurrence_30_frames_graphs(gpu_ctx, dcn, torch):
+    """30 sequential frames, one captured graph per frame, against eager steps."""
+    h, w, blocks, frames = 32, 32, 2, 30
+    rng = np.random.default_rng(91)
+    weights = br.body_weights(rng, 0, blocks)
+    wd = {k: dev(torch, v) for k, v in weights.items()}
+    body = gpu_ctx.body(h, w, wd, branch=0, blocks=blocks)
+    plane = h * w
+    feats = dev(torch, br.f16(rng.standard_normal(frames * 64 * plane))).view(frames, 64 * plane)
+    flows = dev(torch, br.f16(rng.uniform(-3, 3, frames * 2 * plane))).view(frames, 2 * plane)
+    zero_f = torch.zeros(64 * plane, dtype=torch.int16, device="cuda")
+    zero_flow = torch.zeros(2 * plane, dtype=torch.int16, device="cuda")
+
+    def run(use_graphs):
+        props = torch.zeros(frames, 64 * plane, dtype=torch.int16, device="cuda")
+        flow2s = torch.zeros(frames, 2 * plane, dtype=torch.int16, device="cuda")
+        graphs = []
+        for t in range(frames):
+            args = (feats[t], flows[t], flows[t - 1] if t >= 1 else zero_flow, props[t - 1] if t >= 1 else zero_f,
+                    props[t - 2] if t >= 2 else zero_f, flow2s[t], props[t])
+            if use_graphs:
+                g = body.capture(*args, has_second_order=t >= 1)
+                graphs.append(g)
+                g.launch()
+            else:
+                body.step_dev(*args, has_second_order=t >= 1)
+        torch.cuda.synchronize()
+        for g in graphs:
+            g.free()
+        return host(props).copy()
+
+    log("case: 30-frame recurrence")
+    a = run(False)
+    b = run(True)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    assert np.all(np.isfinite(a.astype(np.float32)))
+    body.free()
