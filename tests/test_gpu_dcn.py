@@ -404,6 +404,25 @@ def test_prepack_layouts_and_dcnfp16_file(gpu_ctx, dcn, c2):
         assert "backward_1.dcnfp16 has 147582 bytes; expected 147584" in e.value.message
 
 
+def test_exported_weight_sets_load_and_run(gpu_ctx, dcn, c2):
+    from jasnamacos_amd import weights as W
+
+    s, h, _ = c2
+    log("case: exported weight sets")
+    rng = np.random.default_rng(8)
+    sets = {d: ((h["weight"].astype(np.float32) * rng.uniform(0.5, 1.5)).astype(np.float16), h["bias"])
+            for d in W.DIRECTIONS}
+    with tempfile.TemporaryDirectory() as tmp:
+        W.export_weight_sets(tmp, sets)
+        assert len(W.validate_weight_sets(tmp)) == 4
+        loaded = gpu_ctx.load_weight_sets(tmp)
+        for p in loaded:
+            ref = gpu_ctx.prepack(s, sets[p.direction][0], sets[p.direction][1])
+            a = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], p)
+            b = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], ref)
+            assert np.array_equal(a.view(np.uint16), b.view(np.uint16)), p.direction
+
+
 def test_count_mismatch_reports_name(gpu_ctx, dcn):
     s = dcn.DeformConvShape(*GENERAL_SHAPES[0])
     c = s.counts()
