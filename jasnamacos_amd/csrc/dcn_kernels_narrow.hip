@@ -44,7 +44,7 @@ struct NarrowArgs {
     const float* bias;     // [Cout]
     uint16_t* out;         // [B][Cout][HWo]
     uint32_t xin_bytes, off_bytes, msk_bytes, wpk_bytes;
-    int H, W, Wo, HWo, KW, KA, ph, pw, sh, sw, dh, dw;
+    int H, W, Ho, Wo, HWo, KW, KA, ph, pw, sh, sw, dh, dw;
     int GKA, CB, CBLK, Hp, Wp, KB, ksteps, M, Cout, tiles;  // GKA = G * KA
     uint32_t magic_cb, magic_ka, magic_kw;  // fast_div constants for CB, KA, KW
 };
@@ -66,13 +66,25 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
     const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
 
-    const int p = tile * 16 + (lane & 15);
-    const bool pvalid = p < a.M;
-    const int pc = pvalid ? p : a.M - 1;
-    const int b = pc / a.HWo;
-    const int sp = pc - b * a.HWo;
-    const int oy = sp / a.Wo;
-    const int ox = sp - oy * a.Wo;
+    // Pixel of this lane (and of every epilogue element it stores: the epilogue stride is
+    // a multiple of 16). The tile's first pixel is split on the scalar unit; the lane's
+    // 0..15 step is carried across rows and images without a per-lane division. Lanes
+    // past the last pixel take the last pixel (their results are never stored).
+    const int p0 = tile * 16;
+    const bool pvalid = p0 + (lane & 15) < a.M;
+    const int step = pvalid ? (lane & 15) : (a.M - 1 - p0);
+    int b = p0 / a.HWo;
+    const int sp0 = p0 - b * a.HWo;
+    int oy = sp0 / a.Wo;
+    int ox = sp0 - oy * a.Wo + step;
+    while (ox >= a.Wo) {  // at most 15 / Wo + 1 steps
+        ox -= a.Wo;
+        if (++oy == a.Ho) {
+            oy = 0;
+            ++b;
+        }
+    }
+    const int sp = oy * a.Wo + ox;
     const int base_y = oy * a.sh - a.ph;
     const int base_x = ox * a.sw - a.pw;
     const uint32_t offb = (uint32_t)(b * 2 * a.GKA) * a.HWo + sp;
@@ -163,13 +175,9 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
         float sum = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
-        const int pp = tile * 16 + pl;
-        if (pp < a.M) {
-            const int bb = pp / a.HWo;
-            const int spp = pp - bb * a.HWo;
-            a.out[((size_t)bb * a.Cout + oc) * a.HWo + spp] =
+        if (pvalid)  // pl == lane % 16: this lane's pixel (b, sp)
+            a.out[((size_t)b * a.Cout + oc) * a.HWo + sp] =
                 __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
-        }
     }
 }
 
@@ -234,6 +242,7 @@ hipError_t launch_narrow_f16(const KShape& s, const FusedGeometry& g, const Fuse
     a.wpk_bytes = (uint32_t)narrow_packed_bytes(g);
     a.H = s.H;
     a.W = s.W;
+    a.Ho = s.Ho;
     a.Wo = s.Wo;
     a.HWo = (int)hwo;
     a.KW = s.KW;

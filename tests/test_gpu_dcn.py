@@ -410,8 +410,8 @@ def test_exported_weight_sets_load_and_run(gpu_ctx, dcn, c2):
     s, h, _ = c2
     log("case: exported weight sets")
     rng = np.random.default_rng(8)
-    sets = {d: ((h["weight"].astype(np.float32) * rng.uniform(0.5, 1.5)).astype(np.float16), h["bias"])
-            for d in W.DIRECTIONS}
+    sets = {d: ((h["weight"].astype(np.float32) * rng.uniform(0.5, 1.5)).astype(np.float16).reshape(64, 128, 3, 3),
+                h["bias"]) for d in W.DIRECTIONS}
     with tempfile.TemporaryDirectory() as tmp:
         W.export_weight_sets(tmp, sets)
         assert len(W.validate_weight_sets(tmp)) == 4
