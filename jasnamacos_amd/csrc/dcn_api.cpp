@@ -45,12 +45,17 @@ dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry&
     // CU busy and use 16-pixel tiles; large ones use LDS windows over 2D tiles.
     int variant = o.variant > 0 ? o.variant
                                 : (window_ok && tiles32 > 1024 ? dcn::kVariantWindow : dcn::kVariantNarrow);
-    const bool window = variant == dcn::kVariantWindow || variant == dcn::kVariantWindowSplit;
+    const bool window = variant == dcn::kVariantWindow || variant == dcn::kVariantWindowSplit ||
+                        variant == dcn::kVariantWindowAsync;
     if (window && !window_ok) variant = dcn::kVariantNarrow;
     dcn::FusedConfig cfg{variant, 1, 8, dcn::kSamplerFast};
     if (variant == dcn::kVariantNarrow) {
         cfg.mt = 1;
         cfg.ks = 12;  // waves: 36 K-steps of the reference layer in 3 per wave
+    } else if (variant == dcn::kVariantWindowAsync) {
+        cfg.mt = 8;  // tile rows = waves
+        cfg.ks = 8;
+        if (g.kb % 18 != 0) cfg.variant = dcn::kVariantWindow;  // needs two groups per stage
     } else if (variant == dcn::kVariantWindow || variant == dcn::kVariantWindowSplit) {
         // A 4 x 32 tile on 4 waves with single-buffered windows: two workgroups share a
         // CU, so one copies its windows while the other multiplies.
@@ -77,6 +82,7 @@ dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry&
 }
 
 bool config_supported(const dcn::FusedConfig& c, const dcn::FusedGeometry& g) {
+    if (c.variant == dcn::kVariantWindowAsync) return c.mt == 8 && c.ks == 8;
     if (c.variant == dcn::kVariantNarrow) return c.mt == 1 && (c.ks == 8 || c.ks == 12);
     if (c.variant == dcn::kVariantWindow || c.variant == dcn::kVariantWindowSplit)
         return (c.ks == 8 && (c.mt == 8 || c.mt == 4)) || (c.ks == 4 && (c.mt == 4 || c.mt == 2));
@@ -141,7 +147,8 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
                                             packed->bias, (uint16_t*)d_output, stream));
         return DCN_OK;
     }
-    if (cfg.variant == dcn::kVariantWindow || cfg.variant == dcn::kVariantWindowSplit) {
+    if (cfg.variant == dcn::kVariantWindow || cfg.variant == dcn::kVariantWindowSplit ||
+        cfg.variant == dcn::kVariantWindowAsync) {
         DCN_HIP(ctx, dcn::launch_window_f16(ks, g, cfg, cb8, (const uint16_t*)d_offset,
                                             (const uint16_t*)d_mask, packed->weights_group,
                                             packed->bias, (uint16_t*)d_output, stream));
@@ -284,7 +291,7 @@ dcn_status dcn_reserve(dcn_context* ctx, const dcn_shape* shape) {
 
 dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, int sampler) {
     if (!ctx) return DCN_INVALID_ARGUMENT;
-    if (variant < 0 || variant > 5 || mt < 0 || mt > 8 || ks < 0 || sampler < -1 || sampler > 1)
+    if (variant < 0 || variant > 6 || mt < 0 || mt > 8 || ks < 0 || sampler < -1 || sampler > 1)
         return fail(ctx, DCN_INVALID_ARGUMENT, "invalid fused config");
     ctx->fused_override = dcn::FusedConfig{variant, mt, ks, sampler};
     return DCN_OK;

@@ -65,6 +65,10 @@ enum FusedVariant : int {
     // 16-pixel tiles on v_mfma_f32_16x16x32_f16 with every load of a wave's K-steps in
     // flight at once: one workgroup per CU on small problems. Config: ks = waves (8, 12).
     kVariantNarrow = 5,
+    // kVariantWindow (8 x 32 tiles, 8 waves, two groups per stage) with the next stage's
+    // windows and B fragments streamed into a double buffer by LDS DMA while the current
+    // stage is multiplied. Needs an even group count.
+    kVariantWindowAsync = 6,
 };
 
 struct FusedConfig {

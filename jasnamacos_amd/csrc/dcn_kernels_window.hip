@@ -365,6 +365,339 @@ __global__ __launch_bounds__(64 * NW) void window_kernel(WindowArgs a) {
     }
 }
 
+// ---- asynchronous window pipeline (LDS DMA) ------------------------------------------
+// Same K order, tiles and weights as window_kernel with GPS = 2, one workgroup of eight
+// waves per CU on an 8 x 32 tile, but the copies run in the background: while stage s is
+// multiplied from LDS, global_load_lds_dwordx4 streams stage s+1's two input windows and
+// its 18 KB of B fragments straight into the other half of a double buffer (no VGPRs, no
+// LDS store instructions), and the offsets of stage s+2 are loaded. The stage loop then
+// reads only LDS, so the copy latency that bounds window_kernel is hidden behind the
+// multiply. B fragments come from LDS once per workgroup instead of once per wave.
+
+// 64 lanes x 16 bytes from `g` (one per lane) into LDS [lds_addr, lds_addr + 1 KB) at
+// lds_addr + lane * 16. lds_addr is wave-uniform and goes through M0, which nothing else
+// in these kernels uses (checked in the generated code). The caller keeps every g inside
+// its buffer and waits with wait_dma() before reading.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
+    asm volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %0, off"
+        :
+        : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+        : "memory");
+}
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
+constexpr int kAsyncNw = 8;     // waves per workgroup = tile rows
+constexpr int kAsyncLds = 160 * 1024;
+template <int NB>
+struct AsyncLayout {
+    static constexpr int kStageB = 9 * NB * 1024;  // B fragments of one stage
+    static constexpr int kBox = 2 * 2 * kAsyncNw * 4 * (int)sizeof(int);
+    static constexpr int kWin = ((kAsyncLds - 2 * kStageB - kBox) / 4) & ~1023;  // bytes per window
+    static constexpr int kBufB = 4 * kWin;           // offset of the B double buffer
+    static constexpr int kBoxes = kBufB + 2 * kStageB;
+    static constexpr int kBytes = kBoxes + kBox;
+};
+
+template <int NB, int SAMPLER>
+__global__ __launch_bounds__(64 * kAsyncNw) void window_async_kernel(WindowArgs a) {
+    using L = AsyncLayout<NB>;
+    constexpr int NW = kAsyncNw, GPS = 2, KS = 9;
+    static_assert(L::kBytes <= kAsyncLds && L::kWin >= 8 * 1024, "LDS plan");
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    int* box = reinterpret_cast<int*>(lds + L::kBoxes);  // [2][GPS][NW][4]
+    auto win_buf = [&](int buf, int g) { return lds + (buf * GPS + g) * L::kWin; };
+    auto b_buf = [&](int buf) { return lds + L::kBufB + buf * L::kStageB; };
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int half = lane >> 5;
+
+    const int per_xcd = (a.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+    const int tiles_img = a.tiles_y * a.tiles_x;
+    const int b = tile / tiles_img;
+    const int trem = tile - b * tiles_img;
+    const int ty = trem / a.tiles_x;
+    const int tx = trem - ty * a.tiles_x;
+    const int oy_row = ty * NW + wave;
+    const int ox0 = tx * 32;
+    const int oyc = min(oy_row, a.Ho - 1);
+    const int oxc = min(ox0 + (lane & 31), a.Wo - 1);
+    const int sp = oyc * a.Wo + oxc;
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
+    const uint8_t* xin = static_cast<const uint8_t*>(a.xin);
+    const uint8_t* wpk = static_cast<const uint8_t*>(a.wpk);
+
+    const uint32_t hwo2 = (uint32_t)a.HWo * 2u;
+    const int by = oyc * a.sh - a.ph;
+    const int bx = oxc * a.sw - a.pw;
+    const uint32_t off_lane = ((uint32_t)b * 2 * a.G * 9 * a.HWo + sp) * 2u;
+    const uint32_t msk_lane = ((uint32_t)b * a.G * 9 * a.HWo + sp) * 2u;
+    const int stages = a.G / GPS;
+
+    auto unit_of = [&](int k, int& tap, int& go) {
+        tap = half ? unit_tap<GPS>(2 * k + 1) : unit_tap<GPS>(2 * k);
+        go = half ? unit_group<GPS>(2 * k + 1) : unit_group<GPS>(2 * k);
+    };
+    float rdy[KS], rdx[KS], rm[KS];
+    auto load_raw = [&](int st) {
+        const uint32_t so = 2u * (uint32_t)(st * GPS * 9) * hwo2;
+        const uint32_t sm = (uint32_t)(st * GPS * 9) * hwo2;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            int tap, go;
+            unit_of(k, tap, go);
+            const uint32_t ch = (uint32_t)(go * 9 + tap);
+            rdy[k] = load_half(orr, off_lane + 2u * ch * hwo2, so);
+            rdx[k] = load_half(orr, off_lane + (2u * ch + 1u) * hwo2, so);
+            rm[k] = load_half(mr, msk_lane + ch * hwo2, sm);
+        }
+    };
+    // Sample state of a stage (from rdy/rdx/rm) and the bounding box of its corners.
+    int iy[KS], ix[KS], niy[KS], nix[KS];
+    float ly[KS], lx[KS], mm[KS], nly[KS], nlx[KS], nmm[KS];
+    int bmin_y[GPS], bmax_y[GPS], bmin_x[GPS], bmax_x[GPS];
+    auto make_next_state = [&]() {
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) {
+            bmin_y[g] = INT_MAX;
+            bmax_y[g] = INT_MIN;
+            bmin_x[g] = INT_MAX;
+            bmax_x[g] = INT_MIN;
+        }
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            int tap, go;
+            unit_of(k, tap, go);
+            const int ky = tap / 3, kx = tap - 3 * (tap / 3);
+            const float y = (float)(by + ky * a.dh) + rdy[k];
+            const float x = (float)(bx + kx * a.dw) + rdx[k];
+            const float fy = floorf(y), fx = floorf(x);
+            nly[k] = y - fy;
+            nlx[k] = x - fx;
+            nmm[k] = rm[k];
+            niy[k] = (int)__builtin_amdgcn_fmed3f(fy, (float)-kPad, (float)a.H);
+            nix[k] = (int)__builtin_amdgcn_fmed3f(fx, (float)-kPad, (float)a.W);
+            const int g0 = unit_group<GPS>(2 * k), g1 = unit_group<GPS>(2 * k + 1);
+            if (g0 == g1) {
+                bmin_y[g0] = min(bmin_y[g0], niy[k]);
+                bmax_y[g0] = max(bmax_y[g0], niy[k]);
+                bmin_x[g0] = min(bmin_x[g0], nix[k]);
+                bmax_x[g0] = max(bmax_x[g0], nix[k]);
+            } else {
+                bmin_y[g0] = min(bmin_y[g0], half ? INT_MAX : niy[k]);
+                bmax_y[g0] = max(bmax_y[g0], half ? INT_MIN : niy[k]);
+                bmin_x[g0] = min(bmin_x[g0], half ? INT_MAX : nix[k]);
+                bmax_x[g0] = max(bmax_x[g0], half ? INT_MIN : nix[k]);
+                bmin_y[g1] = min(bmin_y[g1], half ? niy[k] : INT_MAX);
+                bmax_y[g1] = max(bmax_y[g1], half ? niy[k] : INT_MIN);
+                bmin_x[g1] = min(bmin_x[g1], half ? nix[k] : INT_MAX);
+                bmax_x[g1] = max(bmax_x[g1], half ? nix[k] : INT_MIN);
+            }
+        }
+    };
+    auto take_next_state = [&]() {
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            iy[k] = niy[k];
+            ix[k] = nix[k];
+            ly[k] = nly[k];
+            lx[k] = nlx[k];
+            mm[k] = nmm[k];
+        }
+    };
+    auto publish_box = [&](int slot) {
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) {
+            const int v0 = __ockl_wfred_min_i32(bmin_y[g]);
+            const int v1 = __ockl_wfred_max_i32(bmax_y[g]);
+            const int v2 = __ockl_wfred_min_i32(bmin_x[g]);
+            const int v3 = __ockl_wfred_max_i32(bmax_x[g]);
+            if (lane == 0) {
+                int* sb = box + ((slot * GPS + g) * NW + wave) * 4;
+                sb[0] = v0;
+                sb[1] = v1;
+                sb[2] = v2;
+                sb[3] = v3;
+            }
+        }
+    };
+    struct Win {
+        int y0, x0, ww, hh;
+        bool in_lds;
+    };
+    auto read_box = [&](int slot, int g) {
+        int ymin = INT_MAX, ymax = INT_MIN, xmin = INT_MAX, xmax = INT_MIN;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int4 v = *reinterpret_cast<const int4*>(box + ((slot * GPS + g) * NW + w) * 4);
+            ymin = min(ymin, v.x);
+            ymax = max(ymax, v.y);
+            xmin = min(xmin, v.z);
+            xmax = max(xmax, v.w);
+        }
+        Win w;
+        w.y0 = ymin;
+        w.x0 = xmin;
+        w.ww = xmax - xmin + 2;
+        w.hh = ymax - ymin + 2;
+        // whole 64-chunk blocks: the last block's tail lanes land in the window's slack
+        w.in_lds = ((w.hh * w.ww + 63) / 64) * 1024 <= L::kWin;
+        return w;
+    };
+    // Background copies of a stage: its two windows (if they fit) and its B fragments.
+    // Block j of 64 chunks goes to wave j % NW. Every source address lies inside the
+    // CB8 input (the box is clamped into the padded plane) or the packed weights.
+    auto dma_stage = [&](int st, int buf, const Win (&w)[GPS]) {
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) {
+            if (!w[g].in_lds) continue;
+            const int count = w[g].hh * w[g].ww;
+            const int blocks = (count + 63) / 64;
+            const uint32_t row0 = (uint32_t)(b * a.CBLK + st * GPS + g) * a.Hp + (uint32_t)(w[g].y0 + kPad);
+            const float inv_ww = 1.0f / (float)w[g].ww;
+            const uint32_t dst = lds_address(win_buf(buf, g));
+            for (int j = wave; j < blocks; j += NW) {
+                const int c = min(j * 64 + lane, count - 1);
+                int r = (int)((float)c * inv_ww);
+                r -= (r * w[g].ww > c) ? 1 : 0;
+                r += ((r + 1) * w[g].ww <= c) ? 1 : 0;
+                const int col = c - r * w[g].ww;
+                const uint32_t unit = (row0 + (uint32_t)r) * a.Wp + (uint32_t)(w[g].x0 + col + kPad);
+                dma16(xin + (size_t)unit * 16, dst + (uint32_t)j * 1024u);
+            }
+        }
+        const uint8_t* src = wpk + (size_t)st * L::kStageB;
+        const uint32_t dst = lds_address(b_buf(buf));
+        for (int j = wave; j < 9 * NB; j += NW)
+            dma16(src + (size_t)j * 1024 + (size_t)lane * 16, dst + (uint32_t)j * 1024u);
+    };
+
+    f32x16 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x16{};
+
+    // ---- prologue: stage 0 state and copies, stage 1 offsets ----
+    load_raw(0);
+    make_next_state();
+    take_next_state();
+    publish_box(0);
+    __syncthreads();
+    Win win[GPS];
+#pragma unroll
+    for (int g = 0; g < GPS; ++g) win[g] = read_box(0, g);
+    dma_stage(0, 0, win);
+    if (stages > 1) load_raw(1);
+
+    for (int st = 0; st < stages; ++st) {
+        const int buf = st & 1;
+        const bool more = st + 1 < stages;
+        // Stage st's copies and stage st+1's offsets have landed.
+        wait_dma();
+        Win cur[GPS];
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) cur[g] = win[g];
+        if (more) {
+            make_next_state();
+            publish_box(buf ^ 1);
+        }
+        // Copies of stage st visible to all waves; every wave is done with stage st-1,
+        // whose buffers the next copies overwrite.
+        __syncthreads();
+        if (more) {
+#pragma unroll
+            for (int g = 0; g < GPS; ++g) win[g] = read_box(buf ^ 1, g);
+            dma_stage(st + 1, buf ^ 1, win);
+            if (st + 2 < stages) load_raw(st + 2);
+        }
+
+        const uint8_t* bsrc = b_buf(buf);
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const int g0 = unit_group<GPS>(2 * k), g1 = unit_group<GPS>(2 * k + 1);
+            const int gi = (g0 == g1) ? g0 : half;
+            const Win& w = (g0 == g1) ? cur[g0] : (half ? cur[g1] : cur[g0]);
+            u32x4 q0, q1, q2, q3;
+            if (w.in_lds) {
+                // 0 <= iy - y0 < hh and 0 <= ix - x0 < ww by construction of the box.
+                const uint8_t* p = win_buf(buf, gi) +
+                                   (size_t)((iy[k] - w.y0) * w.ww + (ix[k] - w.x0)) * 16;
+                q0 = *reinterpret_cast<const u32x4*>(p);
+                q1 = *reinterpret_cast<const u32x4*>(p + 16);
+                q2 = *reinterpret_cast<const u32x4*>(p + (size_t)w.ww * 16);
+                q3 = *reinterpret_cast<const u32x4*>(p + (size_t)w.ww * 16 + 16);
+            } else {
+                const uint32_t g = ((uint32_t)(b * a.CBLK + st * GPS + gi) * a.Hp + (uint32_t)(iy[k] + kPad)) *
+                                       a.Wp + (uint32_t)(ix[k] + kPad);
+                q0 = load16(xr, g * 16u, 0);
+                q1 = load16(xr, g * 16u + 16u, 0);
+                q2 = load16(xr, (g + a.Wp) * 16u, 0);
+                q3 = load16(xr, (g + a.Wp) * 16u + 16u, 0);
+            }
+            const h8 A = blend<SAMPLER>(q0, q1, q2, q3, ly[k], lx[k], mm[k]);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const h8 B = *reinterpret_cast<const h8*>(bsrc + ((k * NB + nb) * 64 + lane) * 16);
+                acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, acc[nb], 0, 0, 0);
+            }
+        }
+        if (more) take_next_state();
+    }
+
+    // ---- epilogue: bias, FP16, coalesced NCHW stores through LDS ----
+    __syncthreads();
+    uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + (size_t)wave * 32 * NB * 32;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int oc = nb * 32 + (lane & 31);
+        const float bias = a.bias[oc];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int i = 8 * (v >> 2) + 4 * half + (v & 3);
+            stage[oc * 32 + i] = __builtin_bit_cast(uint16_t, round_f16(acc[nb][v] + bias));
+        }
+    }
+    __syncthreads();
+    if (oy_row < a.Ho) {
+        for (int idx = lane; idx < NB * 32 * 8; idx += 64) {
+            const int oc = idx >> 3;
+            const int q = (idx & 7) * 4;
+            const uint16_t* src = stage + oc * 32 + q;
+            uint16_t* dst = a.out + ((size_t)b * a.Cout + oc) * a.HWo + (size_t)oy_row * a.Wo + ox0 + q;
+            if (ox0 + q + 3 < a.Wo && ((((uintptr_t)dst) & 3u) == 0)) {
+                reinterpret_cast<uint32_t*>(dst)[0] = (uint32_t)src[0] | ((uint32_t)src[1] << 16);
+                reinterpret_cast<uint32_t*>(dst)[1] = (uint32_t)src[2] | ((uint32_t)src[3] << 16);
+            } else {
+                for (int e = 0; e < 4; ++e)
+                    if (ox0 + q + e < a.Wo) dst[e] = src[e];
+            }
+        }
+    }
+}
+
+template <int NB, int SAMPLER>
+hipError_t launch_window_async_t(const WindowArgs& a, hipStream_t stream) {
+    auto kernel = &window_async_kernel<NB, SAMPLER>;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+        AsyncLayout<NB>::kBytes);
+    if (attr != hipSuccess) return attr;
+    const unsigned grid = (unsigned)(((a.tiles + 7) / 8) * 8);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kAsyncNw), AsyncLayout<NB>::kBytes, stream, a);
+    return hipGetLastError();
+}
+
 // Weights -> B fragments [stages][KS][NB][64][8] for window_kernel: lane l of K-step k
 // of stage st holds unit u = 2k + l/32 (group st*GPS + u/9 (GPS 2) or st (GPS 1), tap
 // u%9; zero for the padding unit 9 of GPS 1) of output channel nb*32 + l%32, channels
@@ -491,6 +824,24 @@ hipError_t launch_window_f16(const KShape& s, const FusedGeometry& g, const Fuse
     a.Hp = g.hp;
     a.Wp = g.wp;
     a.Cout = s.Cout;
+    if (cfg.variant == kVariantWindowAsync) {
+        if (window_gps(shape) != 2) return hipErrorInvalidValue;
+        a.tiles_y = (s.Ho + kAsyncNw - 1) / kAsyncNw;
+        a.tiles_x = (s.Wo + 31) / 32;
+        a.tiles = a.tiles_y * a.tiles_x * s.B;
+        const bool exact = cfg.sampler == kSamplerExact;
+        switch (g.nb) {
+            case 1: return exact ? launch_window_async_t<1, kSamplerExact>(a, stream)
+                                 : launch_window_async_t<1, kSamplerFast>(a, stream);
+            case 2: return exact ? launch_window_async_t<2, kSamplerExact>(a, stream)
+                                 : launch_window_async_t<2, kSamplerFast>(a, stream);
+            case 3: return exact ? launch_window_async_t<3, kSamplerExact>(a, stream)
+                                 : launch_window_async_t<3, kSamplerFast>(a, stream);
+            case 4: return exact ? launch_window_async_t<4, kSamplerExact>(a, stream)
+                                 : launch_window_async_t<4, kSamplerFast>(a, stream);
+            default: return hipErrorInvalidValue;
+        }
+    }
     const int nw = cfg.ks;
     const int tr = cfg.mt;  // for the window variant, mt carries the tile rows
     const int tcb = nw / tr;

@@ -43,6 +43,7 @@ VARIANT_STAGED = 2
 VARIANT_WINDOW = 3
 VARIANT_WINDOW_SPLIT = 4
 VARIANT_NARROW = 5
+VARIANT_WINDOW_ASYNC = 6
 
 DIRECTIONS = ("backward_1", "forward_1", "backward_2", "forward_2")
 

@@ -192,7 +192,8 @@ FUSED_CONFIGS = [(1, 1, 8), (1, 1, 4), (1, 2, 4), (1, 2, 2),   # register varian
                  (2, 1, 8), (2, 1, 16), (2, 2, 8),              # LDS-staged variant
                  (3, 8, 8), (3, 4, 8), (3, 4, 4), (3, 2, 4),   # LDS windows (rows, waves)
                  (4, 8, 8), (4, 4, 4),                          # LDS windows + L1 lower rows
-                 (5, 1, 8), (5, 1, 12)]                         # narrow 16-pixel tiles (waves)
+                 (5, 1, 8), (5, 1, 12),                         # narrow 16-pixel tiles (waves)
+                 (6, 8, 8)]                                     # LDS windows streamed by DMA
 
 
 def test_unsupported_fused_config_is_rejected(gpu_ctx, dcn, c2):
@@ -225,13 +226,18 @@ def test_fused_configs(gpu_ctx, dcn, c2, variant, mt, ks, sampler):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
-def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle):
+@pytest.mark.parametrize("variant", [0, 6])
+def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle, variant):
     d = dcn.generate_config_inputs(3, 3)
     s = d["shape"]
     h = f16_inputs(d)
-    log("case: fused C3 16 tiles")
+    log("case: fused C3 16 tiles, variant", variant)
     packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
-    out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    gpu_ctx.set_fused_config(0, 0, -1, variant)
+    try:
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
     tile = dataclasses.replace(s, batch=1)
     c = tile.counts()
     for b in (0, 7, 15):  # tiles are independent: check three against the oracle
@@ -244,13 +250,18 @@ def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle):
         assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
 
 
-def test_fused_c5_large_map(gpu_ctx, dcn, oracle):
+@pytest.mark.parametrize("variant", [0, 6])
+def test_fused_c5_large_map(gpu_ctx, dcn, oracle, variant):
     d = dcn.generate_config_inputs(5, 5)
     s = d["shape"]
     h = f16_inputs(d)
-    log("case: fused C5 1x128x180x320")
+    log("case: fused C5 1x128x180x320, variant", variant)
     packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
-    out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    gpu_ctx.set_fused_config(0, 0, -1, variant)
+    try:
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
     w = widen(h)
     plane = s.output_height * s.output_width
     oc_end = 4  # a bounded slice of output channels: every pixel, every sample, 4 channels
@@ -276,7 +287,7 @@ EDGE_SHAPES = [
 
 @pytest.mark.parametrize("dims", EDGE_SHAPES, ids=lambda t: "x".join(map(str, t)))
 @pytest.mark.parametrize("sampler", [0, 1])
-@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 6])
 def test_fused_edge_shapes(gpu_ctx, dcn, oracle, dims, sampler, variant):
     s = dcn.DeformConvShape(*dims)
     assert s.fused_supported
@@ -296,7 +307,7 @@ def test_fused_edge_shapes(gpu_ctx, dcn, oracle, dims, sampler, variant):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 6])
 def test_large_offsets_force_global_fallback(gpu_ctx, dcn, oracle, variant):
     # Offsets up to +-40 px on a 64x64 map: a tile's sample box spans the whole plane
     # (74 KB), larger than one LDS window, so the window variant gathers from global.
@@ -324,7 +335,7 @@ def test_zero_padding_exact(gpu_ctx, dcn, c2):
     bias_out = np.repeat(h["bias"], s.output_height * s.output_width)
     for far in (1000.0, -1000.0, 66.0, -2.0 - 64.0):
         off = np.full_like(h["offset"], far)
-        for variant in (1, 2, 3, 4, 5):
+        for variant in (1, 2, 3, 4, 5, 6):
             gpu_ctx.set_fused_config(0, 0, -1, variant)
             try:
                 out = gpu_ctx.run_float16_prepacked(s, h["input"], off, h["mask"], packed)
