@@ -36,11 +36,9 @@ struct dcn_body {
     uint16_t* deform_cb8 = nullptr;  // DCN input [feat_prop, feat_n2], 128 channels
     uint16_t* off_a = nullptr;       // conv_offset intermediates, 64 channels CB8
     uint16_t* off_b = nullptr;
-    uint16_t* raw = nullptr;         // conv_offset output, 432 NCHW
     uint16_t* offset = nullptr;      // 288 NCHW
     uint16_t* mask = nullptr;        // 144 NCHW
-    uint16_t* aligned = nullptr;     // DCN output, 64 NCHW
-    uint16_t* bb_in = nullptr;       // backbone input, 64 * (branch + 2) channels CB8
+    uint16_t* bb_in = nullptr;       // backbone input [feat_current, prefix..., aligned] CB8
     uint16_t* feat[3] = {};          // backbone features, 64 channels CB8
     hipStream_t capture_stream = nullptr;
 };
@@ -361,10 +359,8 @@ dcn_status dcn_body_create(dcn_context* ctx, int height, int width, int branch, 
     a16(&b->deform_cb8, dcn::cb8_tensor_elems(128, height, width));
     a16(&b->off_a, dcn::cb8_tensor_elems(64, height, width));
     a16(&b->off_b, dcn::cb8_tensor_elems(64, height, width));
-    a16(&b->raw, 432 * plane);
     a16(&b->offset, 288 * plane);
     a16(&b->mask, 144 * plane);
-    a16(&b->aligned, 64 * plane);
     a16(&b->bb_in, dcn::cb8_tensor_elems(bb_in, height, width));
     for (auto& f : b->feat) a16(&f, dcn::cb8_tensor_elems(64, height, width));
     if (st != DCN_OK) return bail(st);
@@ -402,33 +398,43 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
     const hipStream_t s = (hipStream_t)stream;
     const int H = body->h, W = body->w;
     const int NCHW = DCN_TENSOR_NCHW, CB8 = DCN_TENSOR_CB8;
-    // Temporal alignment inputs straight into the CB8 tensors the convs and the DCN read.
-    DCN_TRY(dcn_temporal_prepare_f16_dev(ctx, W, H, d_feat_prop, d_feat_current, d_feat_n2, d_flow1,
-                                         d_prev_flow, has_second_order, d_flow2_out, body->cond_cb8,
-                                         DCN_TENSOR_CB8, body->deform_cb8, DCN_TENSOR_CB8, stream));
-    // conv_offset: 196 -> 64 -> 64 -> 64 (LeakyReLU 0.1) -> 432.
+    const uint16_t* prefix[3] = {};
+    for (int i = 0; i < body->branch; ++i) {
+        if (!d_prefix[i]) return fail(ctx, DCN_INVALID_ARGUMENT, "prefix pointer is null");
+        prefix[i] = (const uint16_t*)d_prefix[i];
+    }
+    // Second-order flow, conditions, DCN input and the backbone input's leading
+    // [feat_current, prefix...] in one kernel, straight into the CB8 tensors.
+    DCN_HIP(ctx, dcn::launch_body_temporal((const uint16_t*)d_feat_prop, (const uint16_t*)d_feat_current,
+                                           (const uint16_t*)d_feat_n2, (const uint16_t*)d_flow1,
+                                           (const uint16_t*)d_prev_flow, has_second_order ? 1 : 0,
+                                           prefix, body->branch, (uint16_t*)d_flow2_out, body->cond_cb8,
+                                           body->deform_cb8, body->bb_in, H, W, s));
+    // conv_offset: 196 -> 64 -> 64 -> 64 (LeakyReLU 0.1) -> 432, the last one turning its
+    // output into offsets and masks in its epilogue.
     DCN_TRY(run_conv(ctx, body->offset_conv[0], body->cond_cb8, 1, nullptr, NCHW, nullptr, NCHW,
                      body->off_a, CB8, s));
     DCN_TRY(run_conv(ctx, body->offset_conv[1], body->off_a, 1, nullptr, NCHW, nullptr, NCHW,
                      body->off_b, CB8, s));
     DCN_TRY(run_conv(ctx, body->offset_conv[2], body->off_b, 1, nullptr, NCHW, nullptr, NCHW,
                      body->off_a, CB8, s));
-    DCN_TRY(run_conv(ctx, body->offset_conv[3], body->off_a, 0, nullptr, NCHW, nullptr, NCHW,
-                     body->raw, NCHW, s));
-    DCN_TRY(dcn_offset_transform_f16_dev(ctx, (size_t)H * W, body->raw, d_flow1, d_flow2_out,
-                                         body->offset, body->mask, stream));
+    const dcn_conv* c3 = body->offset_conv[3];
+    DCN_HIP(ctx, dcn::launch_conv3x3_offsets(c3->g, body->off_a, c3->wpk, c3->bias,
+                                             (const uint16_t*)d_flow1, (const uint16_t*)d_flow2_out,
+                                             body->offset, body->mask, s));
+    // The DCN writes the aligned feature into the backbone input (CB8, after the prefix).
     const dcn_shape ds = body_dcn_shape(H, W);
-    DCN_TRY(dcn_forward_f16_prepacked_cb8_dev(ctx, &ds, body->deform_cb8, body->offset, body->mask,
-                                              body->dcn, body->aligned, stream));
-    // Backbone input [feat_current, prefix..., aligned].
-    const void* sources[5] = {d_feat_current};
-    for (int i = 0; i < body->branch; ++i) {
-        if (!d_prefix[i]) return fail(ctx, DCN_INVALID_ARGUMENT, "prefix pointer is null");
-        sources[1 + i] = d_prefix[i];
-    }
-    sources[1 + body->branch] = body->aligned;
-    DCN_TRY(dcn_assemble_backbone_f16_dev(ctx, W, H, sources, body->branch + 2, body->bb_in,
-                                          DCN_TENSOR_CB8, stream));
+    dcn::FusedGeometry g;
+    dcn::fused_geometry(ds, &g);
+    const dcn::FusedConfig cfg{dcn::kVariantNarrow, 1, 12, dcn::kSamplerFast};
+    const int aligned_c = 64 * (body->branch + 1);
+    dcn::OutPlacement place;
+    place.cb8 = 1;
+    place.coff = aligned_c;
+    place.cblk = 8 * (body->branch + 2);
+    DCN_HIP(ctx, dcn::launch_narrow_f16(dcn::to_kshape(ds), g, cfg, body->deform_cb8, body->offset,
+                                        body->mask, body->dcn->weights_narrow, body->dcn->bias,
+                                        body->bb_in, s, place));
     DCN_TRY(run_conv(ctx, body->backbone[0], body->bb_in, 1, nullptr, NCHW, nullptr, NCHW,
                      body->feat[0], CB8, s));
     // Residual blocks: t = ReLU(conv(x)); x = x + conv(t). The last one also adds the
@@ -439,9 +445,11 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
         DCN_TRY(run_conv(ctx, body->backbone[1 + 2 * i], body->feat[x], 2, nullptr, NCHW, nullptr,
                          NCHW, body->feat[t], CB8, s));
         const bool last = i + 1 == body->blocks;
-        DCN_TRY(run_conv(ctx, body->backbone[2 + 2 * i], body->feat[t], 0, body->feat[x], CB8,
-                         last ? body->aligned : nullptr, NCHW,
-                         last ? d_feat_prop_out : (void*)body->feat[y], last ? NCHW : CB8, s));
+        const dcn_conv* c = body->backbone[2 + 2 * i];
+        DCN_HIP(ctx, dcn::launch_conv3x3(c->g, body->feat[t], c->wpk, c->bias, 0, 0.1f, body->feat[x], CB8,
+                                         last ? body->bb_in : nullptr, CB8,
+                                         last ? (uint16_t*)d_feat_prop_out : body->feat[y],
+                                         last ? NCHW : CB8, s, aligned_c));
         x = y;
     }
     return DCN_OK;

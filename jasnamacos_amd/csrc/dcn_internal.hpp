@@ -115,10 +115,17 @@ int narrow_ksteps(const FusedGeometry& g);
 size_t narrow_packed_bytes(const FusedGeometry& g);
 hipError_t launch_prepack_narrow(const KShape& s, const FusedGeometry& g, const uint16_t* w,
                                  int layout, void* packed_w, hipStream_t stream);
+// Where a kernel writes its output: NCHW, or channels coff.. of a CB8 tensor with cblk
+// 8-channel blocks per image.
+struct OutPlacement {
+    int cb8 = 0;
+    int coff = 0;
+    int cblk = 0;
+};
 hipError_t launch_narrow_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
                              const void* cb8, const uint16_t* off, const uint16_t* mask,
                              const void* packed_w, const float* packed_b, uint16_t* out,
-                             hipStream_t stream);
+                             hipStream_t stream, OutPlacement place = OutPlacement{});
 
 // Propagation-body kernels (dcn_kernels_body.hip, dcn_kernels_conv.hip).
 constexpr int kLayoutNCHW = DCN_TENSOR_NCHW;
@@ -139,7 +146,20 @@ hipError_t launch_conv_prepack(const ConvGeometry& g, const uint16_t* w, const u
 hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                           const float* bias, int act, float slope, const uint16_t* res1,
                           int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,
-                          int out_layout, hipStream_t stream);
+                          int out_layout, hipStream_t stream, int res2_coff = 0);
+// The last conv_offset layer (cout 432) with prepare_dcn_offsets_fp16 in its epilogue:
+// raw = half(conv + bias), offsets = half(10 tanh(raw) + flow), masks = half(sigmoid(raw)).
+hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, const void* wpk,
+                                  const float* bias, const uint16_t* flow1, const uint16_t* flow2,
+                                  uint16_t* offset, uint16_t* mask, hipStream_t stream);
+// One kernel for the body's temporal inputs: second-order flow (NCHW), conditions and
+// the DCN input in CB8, and the backbone input's leading [feat_current, prefix...] in CB8.
+hipError_t launch_body_temporal(const uint16_t* feat_prop, const uint16_t* feat_current,
+                                const uint16_t* feat_n2, const uint16_t* flow1,
+                                const uint16_t* prev_flow, int has_second_order,
+                                const uint16_t* const* prefix, int nprefix, uint16_t* flow2,
+                                uint16_t* cond_cb8, uint16_t* deform_cb8, uint16_t* bb_cb8, int H,
+                                int W, hipStream_t stream);
 hipError_t launch_second_order_flow(const uint16_t* flow1, const uint16_t* prev, uint16_t* flow2,
                                     int H, int W, int has_second_order, hipStream_t stream);
 hipError_t launch_temporal_assemble(const uint16_t* feat_prop, const uint16_t* feat_current,

@@ -183,6 +183,112 @@ __global__ __launch_bounds__(256) void cb8_to_nchw_kernel(const uint16_t* __rest
     out[gid] = cb8[tensor_index(kLayoutCB8, channel, y, x, H, W)];
 }
 
+// Bilinear sample of eight consecutive planes at one coordinate: sample_zero's arithmetic
+// per plane (same association), the corner set computed once.
+__device__ __forceinline__ void sample8_zero(const uint16_t* planes, size_t plane, int H, int W,
+                                             float y, float x, float (&v)[8]) {
+    const float fy = floorf(y), fx = floorf(x);
+    const int y0 = (int)fminf(fmaxf(fy, -4.0f), (float)H + 4.0f);
+    const int x0 = (int)fminf(fmaxf(fx, -4.0f), (float)W + 4.0f);
+    const int y1 = y0 + 1, x1 = x0 + 1;
+    const float ly = y - fy, lx = x - fx;
+    const bool r0 = y0 >= 0 && y0 < H, r1 = y1 >= 0 && y1 < H;
+    const bool c0 = x0 >= 0 && x0 < W, c1 = x1 >= 0 && x1 < W;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const uint16_t* p = planes + (size_t)c * plane;
+        const float v00 = (r0 && c0) ? h2f(p[(size_t)y0 * W + x0]) : 0.0f;
+        const float v01 = (r0 && c1) ? h2f(p[(size_t)y0 * W + x1]) : 0.0f;
+        const float v10 = (r1 && c0) ? h2f(p[(size_t)y1 * W + x0]) : 0.0f;
+        const float v11 = (r1 && c1) ? h2f(p[(size_t)y1 * W + x1]) : 0.0f;
+        v[c] = v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx + v10 * ly * (1.0f - lx) +
+               v11 * ly * lx;
+    }
+}
+
+struct BodyTemporalArgs {
+    const uint16_t *feat_prop, *feat_current, *feat_n2, *flow1, *prev_flow;
+    const uint16_t* prefix[3];
+    int nprefix, has_second_order, H, W;
+    uint16_t *flow2, *cond, *deform, *bb;
+};
+
+// The body's temporal inputs in one pass. Workgroup row blockIdx.y selects an 8-channel
+// output block: 0-24 the conditions [warp(feat_prop, flow1), feat_current,
+// warp(feat_n2, flow2), flow1, flow2, 4 zero channels], 25-40 the DCN input
+// [feat_prop, feat_n2], then the backbone input's [feat_current, prefix...]; one thread
+// per pixel writes the block's 16 bytes of CB8. The second-order flow of a pixel is
+// recomputed by each thread that needs it (same arithmetic, same bits) and stored by
+// the flow block's thread.
+__global__ __launch_bounds__(256) void body_temporal_kernel(BodyTemporalArgs a) {
+    const int plane = a.H * a.W;
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= plane) return;
+    const int kind = blockIdx.y;
+    const int y = p / a.W;
+    const int x = p - y * a.W;
+    const size_t pl = (size_t)plane;
+    const float fx1 = h2f(a.flow1[p]);
+    const float fy1 = h2f(a.flow1[pl + p]);
+    float f2[2] = {0.0f, 0.0f};
+    uint16_t f2h16[2] = {0, 0};
+    if (kind >= 16 && kind < 25 && a.has_second_order) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const float prev = sample_zero(a.prev_flow + (size_t)c * pl, a.H, a.W, (float)y + fy1, (float)x + fx1);
+            f2h16[c] = f2h(h2f(a.flow1[(size_t)c * pl + p]) + prev);
+            f2[c] = h2f(f2h16[c]);
+        }
+    }
+    float v[8];
+    const uint16_t* copy_src = nullptr;  // eight planes copied as they are
+    uint16_t* dst;
+    int dblock;
+    if (kind < 25) {
+        dst = a.cond;
+        dblock = kind;
+        if (kind < 8) {
+            sample8_zero(a.feat_prop + (size_t)kind * 8 * pl, pl, a.H, a.W, (float)y + fy1, (float)x + fx1, v);
+        } else if (kind < 16) {
+            copy_src = a.feat_current + (size_t)(kind - 8) * 8 * pl;
+        } else if (kind < 24) {
+            sample8_zero(a.feat_n2 + (size_t)(kind - 16) * 8 * pl, pl, a.H, a.W, (float)y + f2[1],
+                         (float)x + f2[0], v);
+        } else {
+            a.flow2[p] = f2h16[0];
+            a.flow2[pl + p] = f2h16[1];
+        }
+    } else if (kind < 41) {
+        dst = a.deform;
+        dblock = kind - 25;
+        copy_src = dblock < 8 ? a.feat_prop + (size_t)dblock * 8 * pl : a.feat_n2 + (size_t)(dblock - 8) * 8 * pl;
+    } else {
+        dst = a.bb;
+        dblock = kind - 41;
+        const int src = dblock >> 3;
+        const uint16_t* base = src == 0 ? a.feat_current : a.prefix[src - 1];
+        copy_src = base + (size_t)(dblock & 7) * 8 * pl;
+    }
+    u32x4 out;
+    if (copy_src) {
+        uint16_t h[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) h[c] = copy_src[(size_t)c * pl + p];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) out[d] = (uint32_t)h[2 * d] | ((uint32_t)h[2 * d + 1] << 16);
+    } else if (kind == 24) {
+        out[0] = (uint32_t)a.flow1[p] | ((uint32_t)a.flow1[pl + p] << 16);
+        out[1] = (uint32_t)f2h16[0] | ((uint32_t)f2h16[1] << 16);
+        out[2] = 0u;
+        out[3] = 0u;
+    } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) out[d] = (uint32_t)f2h(v[2 * d]) | ((uint32_t)f2h(v[2 * d + 1]) << 16);
+    }
+    const int Hp = a.H + 2 * kPad, Wp = a.W + 2 * kPad;
+    reinterpret_cast<u32x4*>(dst)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = out;
+}
+
 unsigned blocks_for(long n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -202,6 +308,33 @@ hipError_t launch_temporal_assemble(const uint16_t* feat_prop, const uint16_t* f
     hipLaunchKernelGGL(temporal_assemble_kernel, dim3(blocks_for(196L * H * W)), dim3(256), 0, stream,
                        feat_prop, feat_current, feat_n2, flow1, flow2, conditions, cond_layout,
                        deform_input, deform_layout, H, W);
+    return hipGetLastError();
+}
+
+hipError_t launch_body_temporal(const uint16_t* feat_prop, const uint16_t* feat_current,
+                                const uint16_t* feat_n2, const uint16_t* flow1,
+                                const uint16_t* prev_flow, int has_second_order,
+                                const uint16_t* const* prefix, int nprefix, uint16_t* flow2,
+                                uint16_t* cond_cb8, uint16_t* deform_cb8, uint16_t* bb_cb8, int H,
+                                int W, hipStream_t stream) {
+    if (nprefix < 0 || nprefix > 3) return hipErrorInvalidValue;
+    BodyTemporalArgs a{};
+    a.feat_prop = feat_prop;
+    a.feat_current = feat_current;
+    a.feat_n2 = feat_n2;
+    a.flow1 = flow1;
+    a.prev_flow = prev_flow;
+    for (int i = 0; i < 3; ++i) a.prefix[i] = i < nprefix ? prefix[i] : feat_current;
+    a.nprefix = nprefix;
+    a.has_second_order = has_second_order;
+    a.H = H;
+    a.W = W;
+    a.flow2 = flow2;
+    a.cond = cond_cb8;
+    a.deform = deform_cb8;
+    a.bb = bb_cb8;
+    const dim3 grid(blocks_for((long)H * W), (unsigned)(41 + 8 * (1 + nprefix)));
+    hipLaunchKernelGGL(body_temporal_kernel, grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

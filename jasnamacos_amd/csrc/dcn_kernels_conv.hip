@@ -13,7 +13,8 @@
 // pixels; chunks split Cout (432 -> 7 chunks, the last one partly padded with zero
 // weights). Epilogue: + bias, activation (none / LeakyReLU(slope) / ReLU), optional
 // residual r1 and second residual r2, each add rounded to FP16 as a separate FP16 op:
-// out = half(r2 + half(r1 + act(acc))). Output NCHW or CB8.
+// out = half(r2 + half(r1 + act(acc))). Output NCHW or CB8. A second epilogue (the
+// body's last conv_offset layer) turns the FP16 conv output into DCN offsets and masks.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -40,6 +41,13 @@ struct ConvArgs {
     uint16_t* out;
     uint32_t xin_bytes, wpk_bytes;
     int res1_layout, res2_layout, out_layout;
+    int res2_coff;          // channel offset of the second residual inside its tensor
+    // Offsets epilogue (cout 432): out unused; offsets and masks from half(conv + bias).
+    int offsets;
+    const uint16_t* flow1;  // [2][H][W] (x, y)
+    const uint16_t* flow2;
+    uint16_t* offset;       // [288][H][W]
+    uint16_t* mask;         // [144][H][W]
     int H, W, Hp, Wp, CB, KB, ksteps, NBT, Cout, tiles, act;
     float slope;
     uint32_t magic_cb;
@@ -137,6 +145,23 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a) {
         const int yy = pp / a.W;
         const int xx = pp - yy * a.W;
         float r = sum + a.bias[oc];
+        if (a.offsets) {
+            // prepare_dcn_offsets_fp16 (MetalShader.swift:815-839) on the FP16 conv output.
+            const float raw = (float)round_f16(r);
+            const size_t px = (size_t)yy * a.W + xx;
+            const size_t plane = (size_t)M;
+            if (oc < 288) {
+                const uint16_t* flow = oc < 144 ? a.flow1 : a.flow2;
+                const int flow_channel = ((oc % 144) & 1) == 0 ? 1 : 0;  // even = dy = flow y
+                const float residue = 10.0f * tanhf(raw);
+                const float f = (float)__builtin_bit_cast(_Float16, flow[flow_channel * plane + px]);
+                a.offset[(size_t)oc * plane + px] = __builtin_bit_cast(uint16_t, round_f16(residue + f));
+            } else {
+                a.mask[(size_t)(oc - 288) * plane + px] =
+                    __builtin_bit_cast(uint16_t, round_f16(1.0f / (1.0f + expf(-raw))));
+            }
+            continue;
+        }
         if (a.act == 1 && r < 0.0f) r = r * a.slope;
         if (a.act == 2 && r < 0.0f) r = 0.0f;
         if (a.res1 != nullptr) {
@@ -147,7 +172,7 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a) {
         if (a.res2 != nullptr) {
             const float r1 = (float)round_f16(r);
             const float id = (float)__builtin_bit_cast(
-                _Float16, a.res2[conv_index(a.res2_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)]);
+                _Float16, a.res2[conv_index(a.res2_layout, a.res2_coff + oc, yy, xx, a.H, a.W, a.Hp, a.Wp)]);
             r = id + r1;
         }
         a.out[conv_index(a.out_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)] =
@@ -210,40 +235,65 @@ hipError_t launch_conv_prepack(const ConvGeometry& g, const uint16_t* w, const u
     return hipGetLastError();
 }
 
-hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,
-                          const float* bias, int act, float slope, const uint16_t* res1,
-                          int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,
-                          int out_layout, hipStream_t stream) {
+namespace {
+
+hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, hipStream_t stream) {
     constexpr int NW = 8, U = 4;
-    ConvArgs a;
-    a.xin = x_cb8;
-    a.wpk = wpk;
-    a.bias = bias;
-    a.res1 = res1;
-    a.res2 = res2;
-    a.out = out;
     a.H = g.h;
     a.W = g.w;
     a.Hp = g.h + 2 * kPad;
     a.Wp = g.w + 2 * kPad;
     a.xin_bytes = (uint32_t)((size_t)g.cb * a.Hp * a.Wp * 16);
     a.wpk_bytes = (uint32_t)conv_packed_bytes(g);
-    a.res1_layout = res1_layout;
-    a.res2_layout = res2_layout;
-    a.out_layout = out_layout;
     a.CB = g.cb;
     a.KB = g.kb;
     a.ksteps = g.ksteps;
     a.NBT = g.nbt;
     a.Cout = g.cout;
     a.tiles = (g.h * g.w + 15) / 16;
-    a.act = act;
-    a.slope = slope;
     a.magic_cb = magic_for(g.cb);
     const size_t lds = (size_t)NW * kConvNbc * 4 * 65 * sizeof(float);
     const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)g.chunks);
     hipLaunchKernelGGL((conv3x3_kernel<NW, U>), grid, dim3(64 * NW), lds, stream, a);
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, const void* wpk,
+                                  const float* bias, const uint16_t* flow1, const uint16_t* flow2,
+                                  uint16_t* offset, uint16_t* mask, hipStream_t stream) {
+    if (g.cout != 432) return hipErrorInvalidValue;
+    ConvArgs a{};
+    a.xin = x_cb8;
+    a.wpk = wpk;
+    a.bias = bias;
+    a.offsets = 1;
+    a.flow1 = flow1;
+    a.flow2 = flow2;
+    a.offset = offset;
+    a.mask = mask;
+    return run_conv(g, a, stream);
+}
+
+hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,
+                          const float* bias, int act, float slope, const uint16_t* res1,
+                          int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,
+                          int out_layout, hipStream_t stream, int res2_coff) {
+    ConvArgs a{};
+    a.res2_coff = res2_coff;
+    a.xin = x_cb8;
+    a.wpk = wpk;
+    a.bias = bias;
+    a.res1 = res1;
+    a.res2 = res2;
+    a.out = out;
+    a.res1_layout = res1_layout;
+    a.res2_layout = res2_layout;
+    a.out_layout = out_layout;
+    a.act = act;
+    a.slope = slope;
+    return run_conv(g, a, stream);
 }
 
 }  // namespace dcn

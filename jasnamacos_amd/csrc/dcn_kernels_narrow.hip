@@ -47,6 +47,9 @@ struct NarrowArgs {
     int H, W, Ho, Wo, HWo, KW, KA, ph, pw, sh, sw, dh, dw;
     int GKA, CB, CBLK, Hp, Wp, KB, ksteps, M, Cout, tiles;  // GKA = G * KA
     uint32_t magic_cb, magic_ka, magic_kw;  // fast_div constants for CB, KA, KW
+    // Output placement: NCHW [B][Cout][HWo], or channels out_coff.. of a CB8 tensor with
+    // out_cblk 8-channel blocks per image ([B][out_cblk][Ho+4][Wo+4][8]).
+    int out_cb8, out_coff, out_cblk;
 };
 
 template <int NB, int NW, int U, int SAMPLER>
@@ -175,9 +178,17 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
         float sum = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
-        if (pvalid)  // pl == lane % 16: this lane's pixel (b, sp)
-            a.out[((size_t)b * a.Cout + oc) * a.HWo + sp] =
-                __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
+        if (pvalid) {  // pl == lane % 16: this lane's pixel (b, sp)
+            size_t dst;
+            if (a.out_cb8) {
+                const int c = a.out_coff + oc;
+                dst = (((size_t)b * a.out_cblk + (c >> 3)) * (a.Ho + 2 * kPad) + oy + kPad) *
+                          (size_t)(a.Wo + 2 * kPad) * 8 + (size_t)(ox + kPad) * 8 + (c & 7);
+            } else {
+                dst = ((size_t)b * a.Cout + oc) * a.HWo + sp;
+            }
+            a.out[dst] = __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
+        }
     }
 }
 
@@ -227,8 +238,11 @@ size_t narrow_packed_bytes(const FusedGeometry& g) {
 hipError_t launch_narrow_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
                              const void* cb8, const uint16_t* off, const uint16_t* mask,
                              const void* packed_w, const float* packed_b, uint16_t* out,
-                             hipStream_t stream) {
+                             hipStream_t stream, OutPlacement place) {
     NarrowArgs a;
+    a.out_cb8 = place.cb8;
+    a.out_coff = place.coff;
+    a.out_cblk = place.cblk;
     a.xin = cb8;
     a.off = off;
     a.msk = mask;
