@@ -184,6 +184,8 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=5, help="repetitions of the fused-only timing")
+    ap.add_argument("--cold-calls", type=int, default=20,
+                    help="single calls timed after flushing the caches with a 512 MB write (0: skip)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run three device copies of this many MiB (the known-size "
                          "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -270,6 +272,30 @@ def main() -> int:
         kernel_us.append(a.elapsed_time(b) * 1e3 / args.steps)
     k_us = statistics.median(kernel_us)
 
+    # ---- cold cache: a 512 MB scratch write (twice the 256 MB MALL) before each call --
+    cold_us = warm_single_us = None
+    if args.cold_calls > 0:
+        scratch = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+
+        def single_calls(flush: bool) -> float:
+            samples = []
+            with torch.cuda.stream(stream):
+                for i in range(args.cold_calls):
+                    if flush:
+                        scratch.fill_(i & 0xFF)
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record(stream)
+                    step(stream)
+                    b.record(stream)
+                    b.synchronize()
+                    samples.append(a.elapsed_time(b) * 1e3)
+            torch.cuda.synchronize()
+            return statistics.median(samples)
+
+        cold_us = single_calls(True)
+        warm_single_us = single_calls(False)
+        del scratch
+
     if args.calibration_copy_mib > 0:
         src = torch.ones(args.calibration_copy_mib << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -312,6 +338,11 @@ def main() -> int:
         "step_hbm_frac": nbytes / (us_per_call * 1e-6) / 1e9 / HBM_PEAK_GBS,
         "step_mfma_frac": flops / (us_per_call * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS,
         "kernel_us": k_us,
+        "cold_us_per_call": cold_us,
+        "warm_single_us_per_call": warm_single_us,
+        "cold_note": ("medians of single eager calls timed with HIP events on the call's stream "
+                      "(launch latency included), cold = each after a 512 MB scratch write, warm = "
+                      "back to back") if cold_us is not None else None,
         "kernel_tflops": flops / (k_us * 1e-6) / 1e12,
         "wall_ms_timed_region": wall_ms,
         "output_finite": finite,

@@ -347,6 +347,69 @@ class HipDeformConv:
                                                    C.byref(ks), C.byref(sm)))
         return {"variant": v.value, "mt": mt.value, "ks": ks.value, "sampler": sm.value}
 
+    # ---- benchmark harness --------------------------------------------------------------
+
+    def benchmark_jasna_shape(self, iterations: int = 20, weight_set=None, stream=None) -> "BenchmarkResult":
+        """benchmarkJasnaShape (MetalRunner.swift:187-388) on this device.
+
+        Seeded inputs of the reference (SeededGenerator(0x4A41534E41): input, offset, mask,
+        then weight and bias unless `weight_set`, a .dcnfp16 path, supplies them), FP16
+        device buffers, 2 warm-up calls then `iterations` timed calls per variant, each timed
+        with HIP events around one call: the direct FP16 kernel (the baseline), the
+        reference-arithmetic gather (im2col) alone, and the fused prepacked path. Checksum
+        over the fused output (stride 257) and the reference's gate: the fused result within
+        2e-3 of the baseline, else DeformConvError(COMMAND_FAILED)."""
+        import torch
+
+        from . import weights as _weights
+
+        d = reference_benchmark_inputs()
+        shape = d["shape"]
+        w16, b16 = d["weight"], d["bias"]
+        if weight_set is not None:
+            packed_w, bias = _weights.unpack_weight_set(_weights.read_weight_set(weight_set))
+            w16 = np.ascontiguousarray(np.transpose(packed_w, (2, 0, 1))).reshape(-1).astype(np.float16)
+            b16 = np.asarray(bias, np.float16)
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(np.asarray(a, np.float16)).view(np.int16)).cuda()  # noqa: E731
+        x, off, msk, w, b = (dev(a) for a in (d["input"], d["offset"], d["mask"], w16, b16))
+        base_out = torch.empty(shape.output_count, dtype=torch.int16, device="cuda")
+        fused_out = torch.empty_like(base_out)
+        cols = torch.empty(shape.output_height * shape.output_width * shape.input_channels * shape.kernel_area,
+                           dtype=torch.int16, device="cuda")
+        packed = self.prepack_dev(shape, w, b)
+        self.reserve(shape)
+        st = stream or torch.cuda.current_stream()
+        variants = {
+            "baseline": lambda: self.forward_f16_dev(shape, x, off, msk, w, b, base_out, stream=st),
+            "gather": lambda: self.im2col_f16_dev(shape, x, off, msk, cols, stream=st),
+            "fused": lambda: self.forward_f16_prepacked_dev(shape, x, off, msk, packed, fused_out, stream=st),
+        }
+        stats = {}
+        for name, call in variants.items():
+            for _ in range(2):
+                call()
+            samples = []
+            for _ in range(max(iterations, 1)):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(st)
+                call()
+                e1.record(st)
+                e1.synchronize()
+                samples.append(e0.elapsed_time(e1))
+            stats[name] = BenchmarkStatistics.of(samples)
+            if stats[name] is None:
+                raise DeformConvError(COMMAND_FAILED, "invalid DCNv2 benchmark samples")
+        torch.cuda.synchronize()
+        packed.free()
+        base = base_out.cpu().numpy().view(np.float16).astype(np.float32)
+        fused = fused_out.cpu().numpy().view(np.float16)
+        max_diff = float(np.abs(fused.astype(np.float32) - base).max())
+        if max_diff > 0.002:
+            raise DeformConvError(COMMAND_FAILED, f"fused FP16 result differs from baseline by {max_diff}")
+        return BenchmarkResult(baseline=stats["baseline"], gather=stats["gather"], fused=stats["fused"],
+                               checksum=checksum(fused), max_difference_from_baseline=max_diff,
+                               iterations=max(iterations, 1))
+
     # ---- propagation body ------------------------------------------------------------
 
     def offset_transform_f16(self, plane: int, raw, flow1, flow2):
@@ -659,6 +722,19 @@ class BenchmarkStatistics:
             return None
         return cls(sorted(v.tolist()), s.minimum, s.maximum, s.median, s.mean,
                    s.standard_deviation, s.percentile10, s.percentile90)
+
+
+@dataclasses.dataclass
+class BenchmarkResult:
+    """BenchmarkResult (MetalRunner.swift:67-90) for the variants this build has: the
+    direct FP16 baseline, the gather alone and the fused path (milliseconds)."""
+
+    baseline: BenchmarkStatistics
+    gather: BenchmarkStatistics
+    fused: BenchmarkStatistics
+    checksum: float
+    max_difference_from_baseline: float
+    iterations: int
 
 
 def f32_to_f16(values) -> np.ndarray:

@@ -545,3 +545,101 @@ def test_reference_benchmark_gate(gpu_ctx, dcn):
             gpu_ctx.set_fused_config(0, 0, -1)
         assert np.abs(fused - direct).max() <= 2e-3, sampler
     log("  checksum (fused, reference inputs):", dcn.checksum(fused.astype(np.float16)))
+
+
+def test_benchmark_jasna_shape_harness(gpu_ctx, dcn):
+    # benchmarkJasnaShape (MetalRunner.swift:187-388): statistics per variant, the gate,
+    # a checksum over the fused output; with a .dcnfp16 weight set the weights come from
+    # the file and the result equals a run with the same weights prepacked directly.
+    from jasnamacos_amd import weights as W
+
+    log("case: benchmark harness")
+    r = gpu_ctx.benchmark_jasna_shape(iterations=5)
+    assert r.iterations == 5 and len(r.fused.samples) == 5
+    for st in (r.baseline, r.gather, r.fused):
+        assert 0 < st.minimum <= st.median <= st.maximum
+    assert r.max_difference_from_baseline <= 2e-3 and np.isfinite(r.checksum)
+    log(f"  baseline {r.baseline.median:.4f} ms, gather {r.gather.median:.4f} ms, fused {r.fused.median:.4f} ms, "
+        f"checksum {r.checksum:.6f}")
+    rng = np.random.default_rng(17)
+    w = rng.uniform(-0.02, 0.02, (64, 128, 3, 3)).astype(np.float16)
+    b = rng.uniform(-0.02, 0.02, 64).astype(np.float16)
+    with tempfile.TemporaryDirectory() as tmp:
+        W.export_weight_sets(tmp, {"backward_1": (w, b)})
+        r2 = gpu_ctx.benchmark_jasna_shape(iterations=2, weight_set=os.path.join(tmp, "backward_1.dcnfp16"))
+    d = dcn.reference_benchmark_inputs()
+    packed = gpu_ctx.prepack(d["shape"], w, b)
+    ref = gpu_ctx.run_float16_prepacked(d["shape"], d["input"], d["offset"], d["mask"], packed)
+    assert r2.checksum == dcn.checksum(ref)
+
+
+# ---- property tests over random shapes (Hypothesis) ---------------------------------
+
+from hypothesis import HealthCheck, given, settings  # noqa: E402
+from hypothesis import strategies as st  # noqa: E402
+
+
+@st.composite
+def _direct_cases(draw):
+    groups = draw(st.sampled_from([1, 2]))
+    og = draw(st.sampled_from([1, 2, 4]))
+    unit = groups * og // np.gcd(groups, og)
+    cin = int(unit * draw(st.integers(1, 3)))
+    cout = groups * draw(st.integers(1, 3))
+    kh, kw = draw(st.integers(1, 3)), draw(st.integers(1, 3))
+    sh, sw, dh, dw = (draw(st.integers(1, 2)) for _ in range(4))
+    ph, pw = draw(st.integers(0, 2)), draw(st.integers(0, 2))
+    h, w = draw(st.integers(2, 9)), draw(st.integers(2, 9))
+    ho = max(1, (h + 2 * ph - dh * (kh - 1) - 1) // sh + 1)
+    wo = max(1, (w + 2 * pw - dw * (kw - 1) - 1) // sw + 1)
+    return (draw(st.integers(1, 2)), cin, h, w, cout, ho, wo, kh, kw, ph, pw, sh, sw, dh, dw, groups, og), \
+        draw(st.integers(0, 2**31 - 1)), draw(st.sampled_from([0.5, 3.0, 12.0]))
+
+
+@settings(max_examples=25, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@given(_direct_cases())
+def test_property_fp32_direct_bit_exact(gpu_ctx, dcn, oracle, case):
+    dims, seed, scale = case
+    s = dcn.DeformConvShape(*dims)
+    d = rand_case(s, seed % 100000, offset_scale=scale)
+    log("case: property fp32", dims, seed, scale)
+    out = gpu_ctx.run_float32(s, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    ref = oracle.forward_f32(s, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
+@st.composite
+def _fused_cases(draw):
+    og = draw(st.sampled_from([1, 2, 4, 8, 16]))
+    cin = og * 8 * draw(st.integers(1, 2))
+    cout = 32 * draw(st.integers(1, 4))
+    kh, kw = draw(st.sampled_from([(3, 3), (3, 3), (1, 3), (3, 1), (1, 1)]))
+    sh, sw, dh, dw = (draw(st.integers(1, 2)) for _ in range(4))
+    ph, pw = kh // 2 * dh, kw // 2 * dw
+    h, w = draw(st.integers(3, 20)), draw(st.integers(3, 40))
+    ho = max(1, (h + 2 * ph - dh * (kh - 1) - 1) // sh + 1)
+    wo = max(1, (w + 2 * pw - dw * (kw - 1) - 1) // sw + 1)
+    return (draw(st.integers(1, 3)), cin, h, w, cout, ho, wo, kh, kw, ph, pw, sh, sw, dh, dw, 1, og), \
+        draw(st.integers(0, 2**31 - 1)), draw(st.sampled_from([1, 2, 3, 5, 6])), draw(st.sampled_from([0, 1]))
+
+
+@settings(max_examples=30, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@given(_fused_cases())
+def test_property_fused_f16_tolerance(gpu_ctx, dcn, oracle, case):
+    dims, seed, variant, sampler = case
+    s = dcn.DeformConvShape(*dims)
+    assert s.fused_supported
+    d = rand_case(s, seed % 100000, offset_scale=4.0)
+    d["weight"] *= 0.5
+    h = f16_inputs(d)
+    w = widen(h)
+    log("case: property fused", dims, "variant", variant, "sampler", sampler)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(0, 0, sampler, variant)
+    try:
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    ref = oracle.forward_f32_threads(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    mx, mean = errors(out, ref)
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)

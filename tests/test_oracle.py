@@ -377,3 +377,43 @@ def test_conv3x3_matches_torch(oracle):
     out = oracle.conv3x3_f16(cin, cout, hh, ww, x, w, b, 2, 0.1, res)
     np.testing.assert_allclose(out.astype(np.float64), F.relu(ref).numpy().ravel() + res.astype(np.float64),
                                rtol=0, atol=8e-3)
+
+
+# ---- property test over random shapes (Hypothesis) ------------------------------------
+
+from hypothesis import HealthCheck, given, settings  # noqa: E402
+from hypothesis import strategies as st  # noqa: E402
+
+
+@st.composite
+def dcn_cases(draw):
+    groups = draw(st.sampled_from([1, 2]))
+    offset_groups = draw(st.sampled_from([1, 2, 4]))
+    unit = groups * offset_groups // math.gcd(groups, offset_groups)
+    cin = unit * draw(st.integers(1, 2))
+    cout = groups * draw(st.integers(1, 2))
+    kh, kw = draw(st.integers(1, 3)), draw(st.integers(1, 3))
+    sh, sw = draw(st.integers(1, 2)), draw(st.integers(1, 2))
+    dh, dw = draw(st.integers(1, 2)), draw(st.integers(1, 2))
+    ph, pw = draw(st.integers(0, 2)), draw(st.integers(0, 2))
+    h, w = draw(st.integers(2, 6)), draw(st.integers(2, 6))
+    # Output size as a standard convolution would give it (the reference takes it as given).
+    ho = max(1, (h + 2 * ph - dh * (kh - 1) - 1) // sh + 1)
+    wo = max(1, (w + 2 * pw - dw * (kw - 1) - 1) // sw + 1)
+    shape = DeformConvShape(draw(st.integers(1, 2)), cin, h, w, cout, ho, wo, kh, kw, ph, pw, sh, sw, dh, dw,
+                            groups, offset_groups)
+    seed = draw(st.integers(0, 2**31 - 1))
+    scale = draw(st.sampled_from([0.5, 2.5, 8.0]))
+    return shape, seed, scale
+
+
+@settings(max_examples=60, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@given(dcn_cases())
+def test_property_random_shapes_match_brute_force(oracle, case):
+    # Any valid shape: the oracle equals float64 brute force to FP32 rounding, including
+    # samples far outside the map (offset scale 8 on maps of 2..6 pixels).
+    shape, seed, scale = case
+    d = rand_inputs(shape, np.random.default_rng(seed), offset_scale=scale)
+    out = oracle.forward_f32(shape, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    ref = brute_force_dcn(shape, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    np.testing.assert_allclose(out, ref, rtol=0, atol=5e-5)
