@@ -431,6 +431,64 @@ dcn_status dcn_body_capture(dcn_body* body, const void* d_feat_current, const vo
 dcn_status dcn_graph_launch(dcn_graph* graph, void* stream);
 void dcn_graph_destroy(dcn_graph* graph);
 
+/* The first step of a branch (position 0 of its traversal): no alignment, so the
+ * backbone input is [feat_current, prefix..., 0] and feat_prop_out = half(0 + backbone)
+ * (initialAssemblyArguments / initialResidualArguments,
+ * FusedFourPassRecurrenceProbe.swift:300-318, encoded at :528-566). */
+dcn_status dcn_body_initial_step_dev(dcn_body* body, const void* d_feat_current,
+                                     const void* const* d_prefix, void* d_feat_prop_out,
+                                     void* stream);
+
+/* ---- temporal schedule and the four-branch clip ------------------------------------
+ * TemporalSchedule (TemporalSchedule.swift:27-68): branches backward_1, forward_1,
+ * backward_2, forward_2 (branch index 0..3, backbone inputs (2 + index) * 64 channels)
+ * each walk the frames backward (T-1 .. 0) or forward (0 .. T-1). -1 stands for the
+ * reference's nil. */
+typedef struct dcn_schedule_step {
+    int branch;              /* 0..3 */
+    int position;            /* index within the branch's traversal */
+    int frame;
+    int flow_index;          /* backward: frame, forward: frame - 1; -1 at position 0 */
+    int second_order_frame;  /* traversal[position - 2]; -1 below position 2 */
+} dcn_schedule_step;
+/* The 4 * frame_count steps, branch-major, into steps[0 .. capacity); *count receives
+ * 4 * frame_count. DCN_INVALID_SHAPE for frame_count <= 0, DCN_INVALID_ARGUMENT when
+ * capacity is too small. */
+dcn_status dcn_temporal_schedule(int frame_count, dcn_schedule_step* steps, size_t capacity,
+                                 size_t* count);
+/* TemporalSchedule.persistentTensorBytes: FP16 LQ frames 3x256x256, five 64x64x64
+ * feature sets per frame and both directions' flows 2x64x64. */
+size_t dcn_schedule_persistent_bytes(int frame_count);
+/* SideBySideRestoration.temporalChunkRanges (SideBySideRestoration.swift:1213-1230):
+ * frame_count frames cut into max(1, min(ceil(T / n), T / 3)) balanced chunks, the
+ * first T % chunks one frame longer. starts/sizes receive *count ranges.
+ * DCN_INVALID_SHAPE unless frame_count >= 3 and max_frames_per_chunk >= 3. */
+dcn_status dcn_temporal_chunk_ranges(int frame_count, int max_frames_per_chunk, int* starts,
+                                     int* sizes, size_t capacity, size_t* count);
+
+/* A four-branch propagation clip: one body per branch (weights[0..3] = backward_1,
+ * forward_1, backward_2, forward_2), frames x height x width, owning its scratch
+ * (second-order flow, a zero feature). */
+typedef struct dcn_clip dcn_clip;
+dcn_status dcn_clip_create(dcn_context* ctx, int height, int width, int frames, int blocks,
+                           const dcn_body_weights* weights, void* stream, dcn_clip** out);
+void dcn_clip_destroy(dcn_clip* clip);
+/* The whole clip in schedule order, stream-ordered: spatial [frames][64][H][W];
+ * backward_flows / forward_flows [frames-1][2][H][W] indexed by the schedule's
+ * flow_index; propagated [4][frames][64][H][W] receives every branch's feat_prop (the
+ * propagationBuffers of FusedFourPassRecurrenceProbe.swift:221-225), which later
+ * branches read as their prefix features. max_frames_per_chunk = 0 runs one
+ * recurrence over the clip; n >= 3 runs each range of dcn_temporal_chunk_ranges as an
+ * independent clip (restoreTileFrames, SideBySideRestoration.swift:1174-1211). */
+dcn_status dcn_clip_run_dev(dcn_clip* clip, const void* d_spatial, const void* d_backward_flows,
+                            const void* d_forward_flows, void* d_propagated,
+                            int max_frames_per_chunk, void* stream);
+/* The same clip captured into one executable hipGraph (the retained whole-clip command
+ * buffer of FusedFourPassRecurrenceProbe.swift:904-937). */
+dcn_status dcn_clip_capture(dcn_clip* clip, const void* d_spatial, const void* d_backward_flows,
+                            const void* d_forward_flows, void* d_propagated,
+                            int max_frames_per_chunk, dcn_graph** out);
+
 #ifdef __cplusplus
 }
 #endif

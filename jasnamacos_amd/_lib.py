@@ -50,6 +50,12 @@ class DcnStatistics(C.Structure):
 BODY_MAX_BLOCKS = 8
 
 
+class DcnScheduleStep(C.Structure):
+    """dcn_schedule_step: one PropagationStep of TemporalSchedule (-1 for nil)."""
+
+    _fields_ = [(n, C.c_int) for n in ("branch", "position", "frame", "flow_index", "second_order_frame")]
+
+
 class DcnBodyWeights(C.Structure):
     """dcn_body_weights: OIHW FP16 device pointers of one propagation body."""
 
@@ -149,6 +155,17 @@ SIGNATURES: dict[str, tuple] = {
                                    C.c_int, c_void, c_void, C.POINTER(c_void)]),
     "dcn_graph_launch": (C.c_int, [c_void, c_void]),
     "dcn_graph_destroy": (None, [c_void]),
+    "dcn_body_initial_step_dev": (C.c_int, [c_void, c_void, C.POINTER(c_void), c_void, c_void]),
+    # temporal schedule and the four-branch clip
+    "dcn_temporal_schedule": (C.c_int, [C.c_int, C.POINTER(DcnScheduleStep), c_size, C.POINTER(c_size)]),
+    "dcn_schedule_persistent_bytes": (c_size, [C.c_int]),
+    "dcn_temporal_chunk_ranges": (C.c_int, [C.c_int, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int), c_size,
+                                            C.POINTER(c_size)]),
+    "dcn_clip_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(DcnBodyWeights), c_void,
+                                  C.POINTER(c_void)]),
+    "dcn_clip_destroy": (None, [c_void]),
+    "dcn_clip_run_dev": (C.c_int, [c_void, c_void, c_void, c_void, c_void, C.c_int, c_void]),
+    "dcn_clip_capture": (C.c_int, [c_void, c_void, c_void, c_void, c_void, C.c_int, C.POINTER(c_void)]),
 }
 
 _LIB: C.CDLL | None = None

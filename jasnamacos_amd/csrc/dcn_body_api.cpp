@@ -25,6 +25,16 @@ struct dcn_graph {
     int device = 0;
 };
 
+struct dcn_clip {
+    dcn_context* ctx = nullptr;
+    int h = 0, w = 0, frames = 0, blocks = 0;
+    dcn_body* body[4] = {};
+    uint16_t* zero_feat = nullptr;  // 64 x plane zeros: the feat_n2 of positions 0 and 1
+    uint16_t* flow2 = nullptr;      // 2 x plane second-order flow scratch
+    std::vector<void*> buffers;
+    hipStream_t capture_stream = nullptr;
+};
+
 struct dcn_body {
     dcn_context* ctx = nullptr;
     int h = 0, w = 0, branch = 0, blocks = 0;
@@ -384,6 +394,40 @@ dcn_status dcn_body_create(dcn_context* ctx, int height, int width, int branch, 
     return DCN_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Backbone of a step from the body's backbone input (aligned slot filled): conv 128+ -> 64
+// with LeakyReLU 0.1, then residual blocks t = ReLU(conv(x)); x = x + conv(t). The last
+// one also adds the aligned feature: feat_prop = aligned + backbone
+// (add_propagation_residual_fp16).
+dcn_status run_backbone(dcn_body* body, void* d_feat_prop_out, hipStream_t s) {
+    dcn_context* ctx = body->ctx;
+    const int NCHW = DCN_TENSOR_NCHW, CB8 = DCN_TENSOR_CB8;
+    const int aligned_c = 64 * (body->branch + 1);
+    DCN_TRY(run_conv(ctx, body->backbone[0], body->bb_in, 1, nullptr, NCHW, nullptr, NCHW,
+                     body->feat[0], CB8, s));
+    int x = 0;
+    for (int i = 0; i < body->blocks; ++i) {
+        const int t = (x + 1) % 3, y = (x + 2) % 3;
+        DCN_TRY(run_conv(ctx, body->backbone[1 + 2 * i], body->feat[x], 2, nullptr, NCHW, nullptr,
+                         NCHW, body->feat[t], CB8, s));
+        const bool last = i + 1 == body->blocks;
+        const dcn_conv* c = body->backbone[2 + 2 * i];
+        DCN_HIP(ctx, dcn::launch_conv3x3(c->g, body->feat[t], c->wpk, c->bias, 0, 0.1f, body->feat[x], CB8,
+                                         last ? body->bb_in : nullptr, CB8,
+                                         last ? (uint16_t*)d_feat_prop_out : body->feat[y],
+                                         last ? NCHW : CB8, s, aligned_c));
+        x = y;
+    }
+    return DCN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const void* d_flow1,
                              const void* d_prev_flow, const void* d_feat_prop,
                              const void* d_feat_n2, const void* const* d_prefix,
@@ -435,24 +479,26 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
     DCN_HIP(ctx, dcn::launch_narrow_f16(dcn::to_kshape(ds), g, cfg, body->deform_cb8, body->offset,
                                         body->mask, body->dcn->weights_narrow, body->dcn->bias,
                                         body->bb_in, s, place));
-    DCN_TRY(run_conv(ctx, body->backbone[0], body->bb_in, 1, nullptr, NCHW, nullptr, NCHW,
-                     body->feat[0], CB8, s));
-    // Residual blocks: t = ReLU(conv(x)); x = x + conv(t). The last one also adds the
-    // aligned feature: feat_prop = aligned + backbone (add_propagation_residual_fp16).
-    int x = 0;
-    for (int i = 0; i < body->blocks; ++i) {
-        const int t = (x + 1) % 3, y = (x + 2) % 3;
-        DCN_TRY(run_conv(ctx, body->backbone[1 + 2 * i], body->feat[x], 2, nullptr, NCHW, nullptr,
-                         NCHW, body->feat[t], CB8, s));
-        const bool last = i + 1 == body->blocks;
-        const dcn_conv* c = body->backbone[2 + 2 * i];
-        DCN_HIP(ctx, dcn::launch_conv3x3(c->g, body->feat[t], c->wpk, c->bias, 0, 0.1f, body->feat[x], CB8,
-                                         last ? body->bb_in : nullptr, CB8,
-                                         last ? (uint16_t*)d_feat_prop_out : body->feat[y],
-                                         last ? NCHW : CB8, s, aligned_c));
-        x = y;
+    return run_backbone(body, d_feat_prop_out, s);
+}
+
+dcn_status dcn_body_initial_step_dev(dcn_body* body, const void* d_feat_current,
+                                     const void* const* d_prefix, void* d_feat_prop_out,
+                                     void* stream) {
+    if (!body) return DCN_INVALID_ARGUMENT;
+    dcn_context* ctx = body->ctx;
+    if (!d_feat_current || !d_feat_prop_out || (body->branch > 0 && !d_prefix))
+        return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    DeviceGuard guard(ctx->device);
+    const hipStream_t s = (hipStream_t)stream;
+    const uint16_t* prefix[3] = {};
+    for (int i = 0; i < body->branch; ++i) {
+        if (!d_prefix[i]) return fail(ctx, DCN_INVALID_ARGUMENT, "prefix pointer is null");
+        prefix[i] = (const uint16_t*)d_prefix[i];
     }
-    return DCN_OK;
+    DCN_HIP(ctx, dcn::launch_body_initial((const uint16_t*)d_feat_current, prefix, body->branch, body->bb_in,
+                                          body->h, body->w, s));
+    return run_backbone(body, d_feat_prop_out, s);
 }
 
 dcn_status dcn_body_capture(dcn_body* body, const void* d_feat_current, const void* d_flow1,
@@ -501,6 +547,138 @@ void dcn_graph_destroy(dcn_graph* graph) {
     if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
     if (graph->graph) (void)hipGraphDestroy(graph->graph);
     delete graph;
+}
+
+
+void dcn_clip_destroy(dcn_clip* clip) {
+    if (!clip) return;
+    DeviceGuard guard(clip->ctx ? clip->ctx->device : 0);
+    for (auto* b : clip->body) dcn_body_destroy(b);
+    for (void* p : clip->buffers) (void)hipFree(p);
+    if (clip->capture_stream) (void)hipStreamDestroy(clip->capture_stream);
+    delete clip;
+}
+
+dcn_status dcn_clip_create(dcn_context* ctx, int height, int width, int frames, int blocks,
+                           const dcn_body_weights* weights, void* stream, dcn_clip** out) {
+    if (!ctx || !out) return DCN_INVALID_ARGUMENT;
+    *out = nullptr;
+    if (frames <= 0) return fail(ctx, DCN_INVALID_SHAPE, "a clip needs at least one frame");
+    if (!weights) return fail(ctx, DCN_INVALID_ARGUMENT, "clip weights are null");
+    DCN_TRY(check_plane(ctx, width, height));
+    DeviceGuard guard(ctx->device);
+    auto* c = new dcn_clip();
+    c->ctx = ctx;
+    c->h = height;
+    c->w = width;
+    c->frames = frames;
+    c->blocks = blocks;
+    auto bail = [&](dcn_status st) {
+        dcn_clip_destroy(c);
+        return st;
+    };
+    for (int b = 0; b < 4; ++b) {
+        const dcn_status st = dcn_body_create(ctx, height, width, b, blocks, &weights[b], stream, &c->body[b]);
+        if (st != DCN_OK) return bail(st);
+    }
+    const size_t plane = (size_t)width * height;
+    dcn_status st = alloc(ctx, c->buffers, &c->zero_feat, 64 * plane);
+    if (st == DCN_OK) st = alloc(ctx, c->buffers, &c->flow2, 2 * plane);
+    if (st != DCN_OK) return bail(st);
+    const hipStream_t s = (hipStream_t)stream;
+    if (hipMemsetAsync(c->zero_feat, 0, 64 * plane * 2, s) != hipSuccess ||
+        hipMemsetAsync(c->flow2, 0, 2 * plane * 2, s) != hipSuccess)
+        return bail(fail(ctx, DCN_COMMAND_FAILED, "clearing clip buffers failed"));
+    if (hipStreamCreateWithFlags(&c->capture_stream, hipStreamNonBlocking) != hipSuccess)
+        return bail(fail(ctx, DCN_COMMAND_FAILED, "hipStreamCreate failed"));
+    if (hipStreamSynchronize(s) != hipSuccess) return bail(fail(ctx, DCN_COMMAND_FAILED, "clip set-up failed"));
+    *out = c;
+    return DCN_OK;
+}
+
+dcn_status dcn_clip_run_dev(dcn_clip* clip, const void* d_spatial, const void* d_backward_flows,
+                            const void* d_forward_flows, void* d_propagated,
+                            int max_frames_per_chunk, void* stream) {
+    if (!clip) return DCN_INVALID_ARGUMENT;
+    dcn_context* ctx = clip->ctx;
+    const int T = clip->frames;
+    if (!d_spatial || !d_propagated || (T > 1 && (!d_backward_flows || !d_forward_flows)))
+        return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    std::vector<int> starts(1, 0), sizes(1, T);
+    if (max_frames_per_chunk != 0) {
+        size_t n = 0;
+        starts.assign((size_t)T, 0);
+        sizes.assign((size_t)T, 0);
+        DCN_TRY(dcn_temporal_chunk_ranges(T, max_frames_per_chunk, starts.data(), sizes.data(),
+                                          starts.size(), &n));
+        starts.resize(n);
+        sizes.resize(n);
+    }
+    DeviceGuard guard(ctx->device);
+    const size_t plane = (size_t)clip->w * clip->h;
+    const uint16_t* spatial = (const uint16_t*)d_spatial;
+    const uint16_t* bflows = (const uint16_t*)d_backward_flows;
+    const uint16_t* fflows = (const uint16_t*)d_forward_flows;
+    uint16_t* prop = (uint16_t*)d_propagated;
+    auto feat = [&](int frame) { return spatial + (size_t)frame * 64 * plane; };
+    auto propagated = [&](int branch, int frame) { return prop + ((size_t)branch * T + frame) * 64 * plane; };
+    for (size_t r = 0; r < starts.size(); ++r) {
+        const int c0 = starts[r], n = sizes[r];
+        for (int b = 0; b < 4; ++b) {
+            const bool backward = b % 2 == 0;
+            const uint16_t* flows = backward ? bflows : fflows;
+            auto frame_at = [&](int position) { return backward ? c0 + n - 1 - position : c0 + position; };
+            auto flow_of = [&](int frame) { return flows + (size_t)(backward ? frame : frame - 1) * 2 * plane; };
+            for (int p = 0; p < n; ++p) {
+                const int frame = frame_at(p);
+                const void* prefix[3] = {};
+                for (int i = 0; i < b; ++i) prefix[i] = propagated(i, frame);
+                if (p == 0) {
+                    DCN_TRY(dcn_body_initial_step_dev(clip->body[b], feat(frame), prefix, propagated(b, frame),
+                                                      stream));
+                    continue;
+                }
+                const int prev = frame_at(p - 1);
+                const uint16_t* flow1 = flow_of(frame);
+                const uint16_t* prev_flow = p >= 2 ? flow_of(prev) : flow1;
+                const uint16_t* feat_n2 = p >= 2 ? propagated(b, frame_at(p - 2)) : clip->zero_feat;
+                DCN_TRY(dcn_body_step_dev(clip->body[b], feat(frame), flow1, prev_flow, propagated(b, prev),
+                                          feat_n2, prefix, p >= 2 ? 1 : 0, clip->flow2, propagated(b, frame),
+                                          stream));
+            }
+        }
+    }
+    return DCN_OK;
+}
+
+dcn_status dcn_clip_capture(dcn_clip* clip, const void* d_spatial, const void* d_backward_flows,
+                            const void* d_forward_flows, void* d_propagated,
+                            int max_frames_per_chunk, dcn_graph** out) {
+    if (!clip || !out) return DCN_INVALID_ARGUMENT;
+    *out = nullptr;
+    dcn_context* ctx = clip->ctx;
+    DeviceGuard guard(ctx->device);
+    const hipStream_t s = clip->capture_stream;
+    DCN_HIP(ctx, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const dcn_status st = dcn_clip_run_dev(clip, d_spatial, d_backward_flows, d_forward_flows,
+                                           d_propagated, max_frames_per_chunk, s);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(s, &graph);
+    if (st != DCN_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return st;
+    }
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamEndCapture");
+    auto* g = new dcn_graph();
+    g->graph = graph;
+    g->device = ctx->device;
+    const hipError_t ie = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+        dcn_graph_destroy(g);
+        return hip_fail(ctx, ie, "hipGraphInstantiate");
+    }
+    *out = g;
+    return DCN_OK;
 }
 
 }  // extern "C"

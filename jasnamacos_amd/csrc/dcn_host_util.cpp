@@ -282,3 +282,56 @@ dcn_status dcn_compute_statistics(const double* samples, size_t count, dcn_stati
 }
 
 }  // extern "C"
+
+extern "C" {
+
+dcn_status dcn_temporal_schedule(int frame_count, dcn_schedule_step* steps, size_t capacity,
+                                 size_t* count) {
+    if (frame_count <= 0) return DCN_INVALID_SHAPE;
+    const size_t total = 4 * (size_t)frame_count;
+    if (count) *count = total;
+    if (!steps || capacity < total) return DCN_INVALID_ARGUMENT;
+    size_t i = 0;
+    for (int b = 0; b < 4; ++b) {
+        const bool backward = b % 2 == 0;  // backward_1, forward_1, backward_2, forward_2
+        auto frame_at = [&](int position) { return backward ? frame_count - 1 - position : position; };
+        for (int p = 0; p < frame_count; ++p) {
+            dcn_schedule_step& st = steps[i++];
+            st.branch = b;
+            st.position = p;
+            st.frame = frame_at(p);
+            st.flow_index = p == 0 ? -1 : (backward ? st.frame : st.frame - 1);
+            st.second_order_frame = p > 1 ? frame_at(p - 2) : -1;
+        }
+    }
+    return DCN_OK;
+}
+
+size_t dcn_schedule_persistent_bytes(int frame_count) {
+    if (frame_count <= 0) return 0;
+    const size_t fp16 = 2, t = (size_t)frame_count;
+    const size_t lq = t * 3 * 256 * 256 * fp16;
+    const size_t features = t * 5 * 64 * 64 * 64 * fp16;
+    const size_t flows = 2 * (t - 1) * 2 * 64 * 64 * fp16;
+    return lq + features + flows;
+}
+
+dcn_status dcn_temporal_chunk_ranges(int frame_count, int max_frames_per_chunk, int* starts,
+                                     int* sizes, size_t capacity, size_t* count) {
+    if (frame_count < 3 || max_frames_per_chunk < 3) return DCN_INVALID_SHAPE;
+    const int requested = (frame_count + max_frames_per_chunk - 1) / max_frames_per_chunk;
+    const int chunks = std::max(1, std::min(requested, frame_count / 3));
+    if (count) *count = (size_t)chunks;
+    if (!starts || !sizes || capacity < (size_t)chunks) return DCN_INVALID_ARGUMENT;
+    const int base = frame_count / chunks, larger = frame_count % chunks;
+    int start = 0;
+    for (int i = 0; i < chunks; ++i) {
+        const int size = base + (i < larger ? 1 : 0);
+        starts[i] = start;
+        sizes[i] = size;
+        start += size;
+    }
+    return DCN_OK;
+}
+
+}  // extern "C"

@@ -154,6 +154,10 @@ hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, cons
                                   uint16_t* offset, uint16_t* mask, hipStream_t stream);
 // One kernel for the body's temporal inputs: second-order flow (NCHW), conditions and
 // the DCN input in CB8, and the backbone input's leading [feat_current, prefix...] in CB8.
+// Backbone input of a branch's first step: [feat_current, prefix...] and a zero aligned
+// slot, CB8 with 64 * (nprefix + 2) channels.
+hipError_t launch_body_initial(const uint16_t* feat_current, const uint16_t* const* prefix, int nprefix,
+                               uint16_t* bb_cb8, int H, int W, hipStream_t stream);
 hipError_t launch_body_temporal(const uint16_t* feat_prop, const uint16_t* feat_current,
                                 const uint16_t* feat_n2, const uint16_t* flow1,
                                 const uint16_t* prev_flow, int has_second_order,

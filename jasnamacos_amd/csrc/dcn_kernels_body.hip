@@ -289,6 +289,32 @@ __global__ __launch_bounds__(256) void body_temporal_kernel(BodyTemporalArgs a) 
     reinterpret_cast<u32x4*>(dst)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = out;
 }
 
+// The backbone input of a branch's first step: [feat_current, prefix...] copied into CB8
+// and the aligned slot (the last 64 channels) written as zeros. Workgroup row blockIdx.y
+// is the 8-channel output block.
+__global__ __launch_bounds__(256) void body_initial_kernel(BodyTemporalArgs a) {
+    const int plane = a.H * a.W;
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= plane) return;
+    const int dblock = blockIdx.y;
+    const int y = p / a.W;
+    const int x = p - y * a.W;
+    const size_t pl = (size_t)plane;
+    const int src = dblock >> 3;
+    u32x4 out = {0u, 0u, 0u, 0u};
+    if (src <= a.nprefix) {
+        const uint16_t* base = src == 0 ? a.feat_current : a.prefix[src - 1];
+        const uint16_t* copy_src = base + (size_t)(dblock & 7) * 8 * pl;
+        uint16_t h[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) h[c] = copy_src[(size_t)c * pl + p];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) out[d] = (uint32_t)h[2 * d] | ((uint32_t)h[2 * d + 1] << 16);
+    }
+    const int Hp = a.H + 2 * kPad, Wp = a.W + 2 * kPad;
+    reinterpret_cast<u32x4*>(a.bb)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = out;
+}
+
 unsigned blocks_for(long n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
@@ -335,6 +361,21 @@ hipError_t launch_body_temporal(const uint16_t* feat_prop, const uint16_t* feat_
     a.bb = bb_cb8;
     const dim3 grid(blocks_for((long)H * W), (unsigned)(41 + 8 * (1 + nprefix)));
     hipLaunchKernelGGL(body_temporal_kernel, grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_body_initial(const uint16_t* feat_current, const uint16_t* const* prefix, int nprefix,
+                               uint16_t* bb_cb8, int H, int W, hipStream_t stream) {
+    if (nprefix < 0 || nprefix > 3) return hipErrorInvalidValue;
+    BodyTemporalArgs a{};
+    a.feat_current = feat_current;
+    for (int i = 0; i < 3; ++i) a.prefix[i] = i < nprefix ? prefix[i] : feat_current;
+    a.nprefix = nprefix;
+    a.H = H;
+    a.W = W;
+    a.bb = bb_cb8;
+    const dim3 grid(blocks_for((long)H * W), (unsigned)(8 * (2 + nprefix)));
+    hipLaunchKernelGGL(body_initial_kernel, grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -473,19 +473,22 @@ class HipDeformConv:
     def body(self, height, width, weights: dict, branch: int = 0, blocks: int = 5, stream=None) -> "PropagationBody":
         """weights: device tensors "offset_w{0..3}", "offset_b{0..3}", "dcn_w", "dcn_b",
         "backbone_w{0..2*blocks}", "backbone_b{0..2*blocks}" (OIHW FP16)."""
-        w = _lib.DcnBodyWeights()
-        for i in range(4):
-            w.offset_weight[i] = _ptr(weights[f"offset_w{i}"])
-            w.offset_bias[i] = _ptr(weights[f"offset_b{i}"])
-        w.dcn_weight = _ptr(weights["dcn_w"])
-        w.dcn_bias = _ptr(weights["dcn_b"])
-        for i in range(1 + 2 * blocks):
-            w.backbone_weight[i] = _ptr(weights[f"backbone_w{i}"])
-            w.backbone_bias[i] = _ptr(weights[f"backbone_b{i}"])
+        w = _body_weights(weights, blocks)
         handle = C.c_void_p()
         self._check(self._lib.dcn_body_create(self.ctx, int(height), int(width), int(branch), int(blocks),
                                               C.byref(w), _stream(stream), C.byref(handle)))
         return PropagationBody(self, handle.value, height, width, branch, blocks)
+
+    def clip(self, height, width, frames, weights, blocks: int = 5, stream=None) -> "PropagationClip":
+        """The four propagation branches over `frames` frames; weights: four body weight dicts
+        (backward_1, forward_1, backward_2, forward_2), as for body()."""
+        if len(weights) != 4:
+            raise DeformConvError(INVALID_ARGUMENT, "a clip needs four branch weight sets")
+        ws = (_lib.DcnBodyWeights * 4)(*[_body_weights(w, blocks) for w in weights])
+        handle = C.c_void_p()
+        self._check(self._lib.dcn_clip_create(self.ctx, int(height), int(width), int(frames), int(blocks), ws,
+                                              _stream(stream), C.byref(handle)))
+        return PropagationClip(self, handle.value, height, width, frames, blocks)
 
 
 TENSOR_NCHW = 0
@@ -564,6 +567,14 @@ class PropagationBody:
             self.handle, *self._args(feat_current, flow1, prev_flow, feat_prop, feat_n2, prefix, has_second_order,
                                      flow2_out, feat_prop_out), _stream(stream)))
 
+    def initial_step_dev(self, feat_current, feat_prop_out, prefix=None, stream=None) -> None:
+        """A branch's first step: backbone on [feat_current, prefix..., 0], no alignment."""
+        pre = None
+        if prefix:
+            pre = (C.c_void_p * len(prefix))(*[_ptr(x) for x in prefix])
+        self.ctx._check(self.ctx._lib.dcn_body_initial_step_dev(self.handle, _ptr(feat_current), pre,
+                                                                _ptr(feat_prop_out), _stream(stream)))
+
     def capture(self, feat_current, flow1, prev_flow, feat_prop, feat_n2, flow2_out, feat_prop_out,
                 has_second_order=True, prefix=None) -> BodyGraph:
         handle = C.c_void_p()
@@ -582,6 +593,153 @@ class PropagationBody:
             self.free()
         except Exception:
             pass
+
+
+def _body_weights(weights: dict, blocks: int) -> "_lib.DcnBodyWeights":
+    w = _lib.DcnBodyWeights()
+    for i in range(4):
+        w.offset_weight[i] = _ptr(weights[f"offset_w{i}"])
+        w.offset_bias[i] = _ptr(weights[f"offset_b{i}"])
+    w.dcn_weight = _ptr(weights["dcn_w"])
+    w.dcn_bias = _ptr(weights["dcn_b"])
+    for i in range(1 + 2 * blocks):
+        w.backbone_weight[i] = _ptr(weights[f"backbone_w{i}"])
+        w.backbone_bias[i] = _ptr(weights[f"backbone_b{i}"])
+    return w
+
+
+class PropagationClip:
+    """Four propagation branches over a clip (dcn_clip): the per-frame spatial features
+    [frames][64][H][W] and both directions' flows [frames-1][2][H][W] in, every branch's
+    propagated feature [4][frames][64][H][W] out (verifyFusedFourPassRecurrence,
+    FusedFourPassRecurrenceProbe.swift:493-664, without the flow and reconstruction nets)."""
+
+    def __init__(self, ctx: HipDeformConv, handle: int, height, width, frames, blocks):
+        self.ctx, self.handle = ctx, C.c_void_p(handle)
+        self.height, self.width, self.frames, self.blocks = height, width, frames, blocks
+
+    def run_dev(self, spatial, backward_flows, forward_flows, propagated, max_frames_per_chunk: int = 0,
+                stream=None) -> None:
+        self.ctx._check(self.ctx._lib.dcn_clip_run_dev(self.handle, _ptr(spatial), _ptr(backward_flows),
+                                                       _ptr(forward_flows), _ptr(propagated),
+                                                       int(max_frames_per_chunk), _stream(stream)))
+
+    def capture(self, spatial, backward_flows, forward_flows, propagated, max_frames_per_chunk: int = 0) -> BodyGraph:
+        handle = C.c_void_p()
+        self.ctx._check(self.ctx._lib.dcn_clip_capture(self.handle, _ptr(spatial), _ptr(backward_flows),
+                                                       _ptr(forward_flows), _ptr(propagated),
+                                                       int(max_frames_per_chunk), C.byref(handle)))
+        return BodyGraph(self.ctx, handle.value)
+
+    def free(self) -> None:
+        if self.handle:
+            self.ctx._lib.dcn_clip_destroy(self.handle)
+            self.handle = C.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def propagate_with_fallback(run, frame_count: int, report=None) -> int:
+    """The recoverable-error ladder of restoreTileWithFallback
+    (SideBySideRestoration.swift:1065-1110) for the propagation: run(0) propagates the
+    whole clip; when it fails with the recoverable nonFiniteOutput, run(n) is retried with
+    shorter recurrence chunks n = 10, 5, 3 (those below frame_count). Returns the chunk
+    size that succeeded (0 = whole clip). Any other error propagates at once; when every
+    chunk size fails the last nonFiniteOutput is re-raised as commandFailed."""
+    report = report or (lambda msg: None)
+    try:
+        run(0)
+        return 0
+    except DeformConvError as e:
+        if not e.is_recoverable_numerical_failure:
+            raise
+        last = e
+        report(f"full temporal window failed ({e}); retrying shorter recurrence chunks")
+    for chunk in (10, 5, 3):
+        if chunk >= frame_count:
+            continue
+        try:
+            run(chunk)
+            report(f"recovered with at most {chunk} frames per recurrence chunk")
+            return chunk
+        except DeformConvError as e:
+            if not e.is_recoverable_numerical_failure:
+                raise
+            last = e
+            report(f"also failed with {chunk}-frame chunks ({e})")
+    raise DeformConvError(COMMAND_FAILED, f"every recurrence chunk size failed: {last}")
+
+
+# ---- temporal schedule ----------------------------------------------------------------
+
+BRANCH_NAMES = ("backward_1", "forward_1", "backward_2", "forward_2")
+
+
+@dataclasses.dataclass(frozen=True)
+class PropagationBranch:
+    """PropagationBranch (TemporalSchedule.swift:8-17)."""
+
+    name: str
+    direction: str
+    pass_: int
+    branch_index: int
+
+    @property
+    def backbone_input_channels(self) -> int:
+        return (2 + self.branch_index) * 64
+
+
+@dataclasses.dataclass(frozen=True)
+class PropagationStep:
+    """PropagationStep (TemporalSchedule.swift:19-25); None for the reference's nil."""
+
+    branch: PropagationBranch
+    position: int
+    frame_index: int
+    flow_index: int | None
+    second_order_frame_index: int | None
+
+
+class TemporalSchedule:
+    """TemporalSchedule (TemporalSchedule.swift:27-101) from dcn_temporal_schedule."""
+
+    def __init__(self, frame_count: int):
+        self.frame_count = int(frame_count)
+        self.branches = tuple(PropagationBranch(n, "backward" if i % 2 == 0 else "forward", 1 + i // 2, i)
+                              for i, n in enumerate(BRANCH_NAMES))
+        n = C.c_size_t()
+        cap = max(4 * self.frame_count, 0)
+        raw = (_lib.DcnScheduleStep * max(cap, 1))()
+        st = lib().dcn_temporal_schedule(self.frame_count, raw, cap, C.byref(n))
+        if st != OK:
+            raise DeformConvError(st)
+        nil = lambda v: None if v < 0 else int(v)  # noqa: E731
+        self.steps = tuple(PropagationStep(self.branches[r.branch], r.position, r.frame, nil(r.flow_index),
+                                           nil(r.second_order_frame)) for r in raw[:n.value])
+
+    @property
+    def flow_count_per_direction(self) -> int:
+        return max(self.frame_count - 1, 0)
+
+    @property
+    def persistent_tensor_bytes(self) -> int:
+        return int(lib().dcn_schedule_persistent_bytes(self.frame_count))
+
+
+def temporal_chunk_ranges(frame_count: int, maximum_frames_per_chunk: int) -> list[range]:
+    """SideBySideRestoration.temporalChunkRanges (SideBySideRestoration.swift:1213-1230)."""
+    starts = (C.c_int * max(frame_count, 1))()
+    sizes = (C.c_int * max(frame_count, 1))()
+    n = C.c_size_t()
+    st = lib().dcn_temporal_chunk_ranges(int(frame_count), int(maximum_frames_per_chunk), starts, sizes,
+                                         max(frame_count, 1), C.byref(n))
+    if st != OK:
+        raise DeformConvError(st)
+    return [range(starts[i], starts[i] + sizes[i]) for i in range(n.value)]
 
 
 # ---- deterministic inputs ----------------------------------------------------------

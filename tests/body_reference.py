@@ -74,6 +74,28 @@ def body_step(weights: dict, x: dict, height: int, width: int, blocks: int, has_
                         "deform_input": dinp}
 
 
+def backbone(weights: dict, bb: np.ndarray, height: int, width: int, blocks: int) -> np.ndarray:
+    """Backbone of one step on the CPU: conv (LeakyReLU 0.1), then residual blocks."""
+    plane = height * width
+    feat = oracle.conv3x3_f16(bb.size // plane, 64, height, width, bb, weights["backbone_w0"],
+                              weights["backbone_b0"], 1, 0.1)
+    for i in range(blocks):
+        t = oracle.conv3x3_f16(64, 64, height, width, feat, weights[f"backbone_w{1 + 2 * i}"],
+                               weights[f"backbone_b{1 + 2 * i}"], 2, 0.1)
+        feat = oracle.conv3x3_f16(64, 64, height, width, t, weights[f"backbone_w{2 + 2 * i}"],
+                                  weights[f"backbone_b{2 + 2 * i}"], 0, 0.1, feat)
+    return feat
+
+
+def body_initial_step(weights: dict, feat_current, prefix, height: int, width: int, blocks: int) -> np.ndarray:
+    """A branch's first step (FusedFourPassRecurrenceProbe.swift:528-566): backbone on
+    [feat_current, prefix..., 0] and feat_prop = half(0 + backbone)."""
+    zero = np.zeros(64 * height * width, np.float16)
+    bb = np.concatenate([feat_current, *prefix, zero])
+    feat = backbone(weights, bb, height, width, blocks)
+    return f16(zero.astype(np.float32) + feat.astype(np.float32))
+
+
 def to_cb8(x_nchw: np.ndarray, channels: int, height: int, width: int, pad: int = 2) -> np.ndarray:
     """NCHW FP16 -> CB8 [ceil(C/8)][H+2p][W+2p][8] with zero border and padding channels."""
     cb = (channels + 7) // 8

@@ -1,0 +1,202 @@
+"""GPU tests of the four-branch propagation clip (dcn_clip).
+
+Bars:
+  * orchestration: the clip equals the same steps driven one at a time from the
+    TemporalSchedule through single bodies, bit for bit (same kernels, same inputs);
+  * semantics, teacher-forced: every step's output (first steps without alignment
+    included) against the oracle chain run on that step's GPU inputs, within the one-step
+    FP16 tolerance (max 2e-2, mean 1e-3), so errors do not compound over the recurrence;
+  * one captured graph for the whole clip replays bit-identically to the eager run;
+  * chunked recurrences equal independent clips over the chunk ranges;
+  * non-finite features are detected, and the fallback ladder ends in commandFailed.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import body_reference as br
+
+pytestmark = pytest.mark.gpu
+
+
+def log(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(np.asarray(a, np.float16)).view(np.int16)).cuda()
+
+
+def host(t):
+    return t.cpu().numpy().view(np.float16)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+
+    return t
+
+
+def _clip_case(torch, frames, h, w, blocks, seed, flow_px=3.0):
+    rng = np.random.default_rng(seed)
+    weights = [br.body_weights(rng, b, blocks) for b in range(4)]
+    plane = h * w
+    x = {
+        "spatial": br.f16(rng.standard_normal(frames * 64 * plane)),
+        "bflows": br.f16(rng.uniform(-flow_px, flow_px, max(frames - 1, 1) * 2 * plane)),
+        "fflows": br.f16(rng.uniform(-flow_px, flow_px, max(frames - 1, 1) * 2 * plane)),
+    }
+    wd = [{k: dev(torch, v) for k, v in wb.items()} for wb in weights]
+    xd = {k: dev(torch, v) for k, v in x.items()}
+    return weights, wd, x, xd
+
+
+def _run_clip(torch, ctx, wd, xd, frames, h, w, blocks, chunk=0):
+    clip = ctx.clip(h, w, frames, wd, blocks=blocks)
+    prop = torch.zeros(4 * frames * 64 * h * w, dtype=torch.int16, device="cuda")
+    clip.run_dev(xd["spatial"], xd["bflows"], xd["fflows"], prop, chunk)
+    torch.cuda.synchronize()
+    out = host(prop).copy().reshape(4, frames, 64 * h * w)
+    clip.free()
+    return out
+
+
+def test_clip_matches_schedule_driven_bodies(gpu_ctx, dcn, torch):
+    frames, h, w, blocks = 4, 16, 24, 2
+    weights, wd, x, xd = _clip_case(torch, frames, h, w, blocks, 3)
+    log("case: clip vs schedule-driven bodies", frames, h, w)
+    got = _run_clip(torch, gpu_ctx, wd, xd, frames, h, w, blocks)
+    plane = h * w
+    bodies = [gpu_ctx.body(h, w, wd[b], branch=b, blocks=blocks) for b in range(4)]
+    prop = torch.zeros(4, frames, 64 * plane, dtype=torch.int16, device="cuda")
+    spatial = xd["spatial"].view(frames, 64 * plane)
+    flows = {"backward": xd["bflows"].view(-1, 2 * plane), "forward": xd["fflows"].view(-1, 2 * plane)}
+    zero = torch.zeros(64 * plane, dtype=torch.int16, device="cuda")
+    flow2 = torch.zeros(2 * plane, dtype=torch.int16, device="cuda")
+    schedule = dcn.TemporalSchedule(frames)
+    for s in schedule.steps:
+        b = s.branch.branch_index
+        prefix = [prop[i, s.frame_index] for i in range(b)] or None
+        if s.position == 0:
+            bodies[b].initial_step_dev(spatial[s.frame_index], prop[b, s.frame_index], prefix=prefix)
+            continue
+        steps = [t for t in schedule.steps if t.branch == s.branch]
+        prev = steps[s.position - 1]
+        f = flows[s.branch.direction]
+        prev_flow = f[prev.flow_index] if s.position >= 2 else f[s.flow_index]
+        feat_n2 = prop[b, s.second_order_frame_index] if s.second_order_frame_index is not None else zero
+        bodies[b].step_dev(spatial[s.frame_index], f[s.flow_index], prev_flow, prop[b, prev.frame_index], feat_n2,
+                           flow2, prop[b, s.frame_index], has_second_order=s.position >= 2, prefix=prefix)
+    torch.cuda.synchronize()
+    ref = host(prop).copy()
+    for body in bodies:
+        body.free()
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    assert np.all(np.isfinite(got.astype(np.float32)))
+
+
+def test_clip_steps_match_oracle_teacher_forced(gpu_ctx, dcn, torch):
+    frames, h, w, blocks = 4, 12, 20, 1
+    weights, wd, x, xd = _clip_case(torch, frames, h, w, blocks, 5)
+    log("case: clip teacher-forced oracle", frames, h, w)
+    got = _run_clip(torch, gpu_ctx, wd, xd, frames, h, w, blocks)
+    plane = h * w
+    spatial = x["spatial"].reshape(frames, 64 * plane)
+    flows = {"backward": x["bflows"].reshape(-1, 2 * plane), "forward": x["fflows"].reshape(-1, 2 * plane)}
+    schedule = dcn.TemporalSchedule(frames)
+    worst = 0.0
+    for s in schedule.steps:
+        b = s.branch.branch_index
+        prefix = [got[i, s.frame_index] for i in range(b)]
+        out = got[b, s.frame_index].astype(np.float64)
+        if s.position == 0:
+            ref = br.body_initial_step(weights[b], spatial[s.frame_index], prefix, h, w, blocks).astype(np.float64)
+            e = np.abs(out - ref)
+            assert e.max() <= 2e-2 and e.mean() <= 1e-3, (s, e.max(), e.mean())
+            continue
+        steps = [t for t in schedule.steps if t.branch == s.branch]
+        prev = steps[s.position - 1]
+        f = flows[s.branch.direction]
+        step_in = {
+            "feat_current": spatial[s.frame_index],
+            "flow1": f[s.flow_index],
+            "prev_flow": f[prev.flow_index] if s.position >= 2 else f[s.flow_index],
+            "feat_prop": got[b, prev.frame_index],
+            "feat_n2": got[b, s.second_order_frame_index] if s.second_order_frame_index is not None
+            else np.zeros(64 * plane, np.float16),
+            "prefix": prefix,
+        }
+        _, ref, _ = br.body_step(weights[b], step_in, h, w, blocks, s.position >= 2)
+        e = np.abs(out - ref.astype(np.float64))
+        worst = max(worst, e.max())
+        assert e.max() <= 2e-2 and e.mean() <= 1e-3, (s, e.max(), e.mean())
+    log(f"  worst step max err {worst:.3e}")
+
+
+def test_clip_graph_replays_match_eager(gpu_ctx, torch):
+    frames, h, w, blocks = 5, 16, 16, 1
+    weights, wd, x, xd = _clip_case(torch, frames, h, w, blocks, 7)
+    log("case: clip graph replay", frames, h, w)
+    eager = _run_clip(torch, gpu_ctx, wd, xd, frames, h, w, blocks)
+    clip = gpu_ctx.clip(h, w, frames, wd, blocks=blocks)
+    prop = torch.zeros(4 * frames * 64 * h * w, dtype=torch.int16, device="cuda")
+    graph = clip.capture(xd["spatial"], xd["bflows"], xd["fflows"], prop)
+    scratch = torch.zeros_like(prop)
+    for i in range(3):
+        prop.zero_()
+        torch.cuda.synchronize()
+        graph.launch()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(prop).view(np.uint16), eager.reshape(-1).view(np.uint16)), i
+        clip.run_dev(xd["spatial"], xd["bflows"], xd["fflows"], scratch)  # eager work between replays
+        torch.cuda.synchronize()
+    graph.free()
+    clip.free()
+
+
+def test_clip_chunks_equal_independent_clips(gpu_ctx, dcn, torch):
+    frames, h, w, blocks = 7, 12, 16, 1
+    weights, wd, x, xd = _clip_case(torch, frames, h, w, blocks, 9)
+    log("case: chunked clip", frames, h, w)
+    got = _run_clip(torch, gpu_ctx, wd, xd, frames, h, w, blocks, chunk=3)
+    plane = h * w
+    ranges = dcn.temporal_chunk_ranges(frames, 3)
+    assert ranges == [range(0, 4), range(4, 7)]
+    for r in ranges:
+        n = len(r)
+        sub = {
+            "spatial": dev(torch, x["spatial"].reshape(frames, -1)[r.start:r.stop]),
+            "bflows": dev(torch, x["bflows"].reshape(frames - 1, -1)[r.start:r.stop - 1]),
+            "fflows": dev(torch, x["fflows"].reshape(frames - 1, -1)[r.start:r.stop - 1]),
+        }
+        ref = _run_clip(torch, gpu_ctx, wd, sub, n, h, w, blocks)
+        assert np.array_equal(got[:, r.start:r.stop].view(np.uint16), ref.view(np.uint16)), r
+    assert got.shape == (4, frames, 64 * plane)
+
+
+def test_clip_nonfinite_is_detected_and_ladder_gives_up(gpu_ctx, dcn, torch):
+    frames, h, w, blocks = 6, 8, 8, 1
+    weights, wd, x, xd = _clip_case(torch, frames, h, w, blocks, 11)
+    spatial = x["spatial"].copy()
+    spatial[5] = np.float16(np.inf)
+    xd["spatial"] = dev(torch, spatial)
+    log("case: clip non-finite + fallback ladder")
+    clip = gpu_ctx.clip(h, w, frames, wd, blocks=blocks)
+    prop = torch.zeros(4 * frames * 64 * h * w, dtype=torch.int16, device="cuda")
+    tried = []
+
+    def run(chunk):
+        tried.append(chunk)
+        clip.run_dev(xd["spatial"], xd["bflows"], xd["fflows"], prop, chunk)
+        gpu_ctx.check_nonfinite_f16_dev(prop, prop.numel())
+
+    with pytest.raises(dcn.DeformConvError) as e:
+        dcn.propagate_with_fallback(run, frames)
+    assert e.value.status == dcn.COMMAND_FAILED
+    assert tried == [0, 5, 3]
+    clip.free()
