@@ -9,6 +9,8 @@
 //                          runFloat16, prepacked weights, benchmarkJasnaShape
 //   DeformConvWeightSet    DeformConvWeights.swift:4-46
 //   BenchmarkStatistics    BenchmarkStatistics.swift:3-44
+//   TemporalSchedule       TemporalSchedule.swift:3-101
+//   temporalChunkRanges    SideBySideRestoration.swift:1213-1230
 //
 // Link with -ldcn (and the HIP runtime for benchmarkJasnaShape's device buffers).
 #pragma once
@@ -160,6 +162,66 @@ inline std::vector<DeformConvWeightSet> loadDeformConvWeightSets(const std::stri
     for (const char* d : {"backward_1", "forward_1", "backward_2", "forward_2"})
         sets.emplace_back(d, directory + "/" + d + ".dcnfp16");
     return sets;
+}
+
+// PropagationBranch / PropagationStep / TemporalSchedule (TemporalSchedule.swift:3-101).
+struct PropagationBranch {
+    std::string name;
+    bool backward;
+    int pass;
+    int branchIndex;
+    int backboneInputChannels() const { return (2 + branchIndex) * 64; }
+};
+
+struct PropagationStep {
+    int branch;                                // index into TemporalSchedule::branches
+    int position;
+    int frameIndex;
+    std::optional<int> flowIndex;              // nil at position 0
+    std::optional<int> secondOrderFrameIndex;  // nil below position 2
+};
+
+struct TemporalSchedule {
+    int frameCount;
+    std::vector<PropagationBranch> branches;
+    std::vector<PropagationStep> steps;
+
+    explicit TemporalSchedule(int frames) : frameCount(frames) {
+        if (frames <= 0) throw DeformConvError::invalidShape();
+        branches = {{"backward_1", true, 1, 0}, {"forward_1", false, 1, 1},
+                    {"backward_2", true, 2, 2}, {"forward_2", false, 2, 3}};
+        std::vector<dcn_schedule_step> raw(4 * (size_t)frames);
+        size_t n = 0;
+        if (dcn_temporal_schedule(frames, raw.data(), raw.size(), &n) != DCN_OK)
+            throw DeformConvError::commandFailed("invalid propagation schedule size");
+        for (size_t i = 0; i < n; ++i) {
+            const dcn_schedule_step& r = raw[i];
+            PropagationStep st{r.branch, r.position, r.frame, std::nullopt, std::nullopt};
+            if (r.flow_index >= 0) st.flowIndex = r.flow_index;
+            if (r.second_order_frame >= 0) st.secondOrderFrameIndex = r.second_order_frame;
+            steps.push_back(st);
+        }
+    }
+    int flowCountPerDirection() const { return std::max(frameCount - 1, 0); }
+    size_t persistentTensorBytes() const { return dcn_schedule_persistent_bytes(frameCount); }
+    std::vector<PropagationStep> stepsOf(const std::string& name) const {
+        std::vector<PropagationStep> out;
+        for (const auto& st : steps)
+            if (branches[(size_t)st.branch].name == name) out.push_back(st);
+        return out;
+    }
+};
+
+// Half-open frame ranges [first, second).
+inline std::vector<std::pair<int, int>> temporalChunkRanges(int frameCount, int maximumFramesPerChunk) {
+    std::vector<int> starts((size_t)std::max(frameCount, 1)), sizes(starts.size());
+    size_t n = 0;
+    if (dcn_temporal_chunk_ranges(frameCount, maximumFramesPerChunk, starts.data(), sizes.data(), starts.size(),
+                                  &n) != DCN_OK)
+        throw DeformConvError::invalidShape();
+    std::vector<std::pair<int, int>> out;
+    for (size_t i = 0; i < n; ++i) out.emplace_back(starts[i], starts[i] + sizes[i]);
+    return out;
 }
 
 class PackedWeights {

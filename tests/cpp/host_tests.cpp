@@ -4,6 +4,8 @@
 //   BenchmarkStatisticsTests.swift:5-20      (summary of [4,1,3,2]; nil for [] and [1, inf])
 //   MetalNonFiniteFlagTests.swift:5-55       (flag_non_finite_fp16 on finite / inf / nan)
 //   JasnaCLI.swift:68-110                    (correctnessTest: seeded 1x2x5x5 -> 3, 2e-5 gate)
+//   TemporalScheduleTests.swift:4-40         (traversal, widths, second order, 30 frames)
+//   RestorationResumeTests.swift:51-72       (temporalChunkRanges)
 // plus the weight-set loader and benchmarkJasnaShape. The CPU oracle (oracle/liboracle.so)
 // stands in for DeformConvCPU as the checker; the library under test never calls it.
 //
@@ -195,6 +197,70 @@ TEST(cpu, weightSetChecksumIsTheStride257Sum) {
     const jasna::DeformConvWeightSet set("backward_1", tempFile(bytes, "backward_1.dcnfp16"));
     EXPECT(set.checksum() == 288.0);
     EXPECT(dcn_dcnfp16_bytes() == (size_t)jasna::DeformConvWeightSet::expectedBytes);
+}
+
+std::vector<int> frames(const std::vector<jasna::PropagationStep>& v) {
+    std::vector<int> out;
+    for (const auto& s : v) out.push_back(s.frameIndex);
+    return out;
+}
+std::vector<int> flows(const std::vector<jasna::PropagationStep>& v) {  // -1 for nil
+    std::vector<int> out;
+    for (const auto& s : v) out.push_back(s.flowIndex.value_or(-1));
+    return out;
+}
+std::vector<int> secondOrder(const std::vector<jasna::PropagationStep>& v) {
+    std::vector<int> out;
+    for (const auto& s : v) out.push_back(s.secondOrderFrameIndex.value_or(-1));
+    return out;
+}
+
+TEST(cpu, temporalScheduleMatchesBasicVSRTraversal) {
+    const jasna::TemporalSchedule schedule(4);
+    const auto backward = schedule.stepsOf("backward_1"), forward = schedule.stepsOf("forward_1");
+    EXPECT((frames(backward) == std::vector<int>{3, 2, 1, 0}));
+    EXPECT((flows(backward) == std::vector<int>{-1, 2, 1, 0}));
+    EXPECT((frames(forward) == std::vector<int>{0, 1, 2, 3}));
+    EXPECT((flows(forward) == std::vector<int>{-1, 0, 1, 2}));
+    EXPECT(backward[2].secondOrderFrameIndex == 3);
+    EXPECT(forward[2].secondOrderFrameIndex == 0);
+}
+
+TEST(cpu, temporalScheduleUsesExpectedBackboneWidths) {
+    const jasna::TemporalSchedule schedule(3);
+    std::vector<int> widths;
+    for (const auto& b : schedule.branches) widths.push_back(b.backboneInputChannels());
+    EXPECT((widths == std::vector<int>{128, 192, 256, 320}));
+    EXPECT(schedule.steps.size() == 12);
+    EXPECT(schedule.flowCountPerDirection() == 2);
+}
+
+TEST(cpu, fiveFrameScheduleCarriesRollingSecondOrderHistory) {
+    const jasna::TemporalSchedule schedule(5);
+    const auto backward = schedule.stepsOf("backward_1"), forward = schedule.stepsOf("forward_1");
+    EXPECT((frames(backward) == std::vector<int>{4, 3, 2, 1, 0}));
+    EXPECT((flows(backward) == std::vector<int>{-1, 3, 2, 1, 0}));
+    EXPECT((secondOrder(backward) == std::vector<int>{-1, -1, 4, 3, 2}));
+    EXPECT((frames(forward) == std::vector<int>{0, 1, 2, 3, 4}));
+    EXPECT((flows(forward) == std::vector<int>{-1, 0, 1, 2, 3}));
+    EXPECT((secondOrder(forward) == std::vector<int>{-1, -1, 0, 1, 2}));
+}
+
+TEST(cpu, thirtyFrameScheduleHasProductionLengthResources) {
+    const jasna::TemporalSchedule schedule(30);
+    EXPECT(schedule.flowCountPerDirection() == 29);
+    EXPECT(schedule.steps.size() == 120);
+    EXPECT(schedule.persistentTensorBytes() == 91389952u);
+    EXPECT(expectThrows([] { jasna::TemporalSchedule(0); }).kind() == DeformConvError::Kind::invalidShape);
+}
+
+TEST(cpu, temporalChunkRangesMatchTheReference) {
+    using R = std::vector<std::pair<int, int>>;
+    EXPECT((jasna::temporalChunkRanges(30, 10) == R{{0, 10}, {10, 20}, {20, 30}}));
+    EXPECT((jasna::temporalChunkRanges(29, 10) == R{{0, 10}, {10, 20}, {20, 29}}));
+    EXPECT((jasna::temporalChunkRanges(11, 5) == R{{0, 4}, {4, 8}, {8, 11}}));
+    EXPECT((jasna::temporalChunkRanges(5, 3) == R{{0, 5}}));
+    EXPECT(expectThrows([] { jasna::temporalChunkRanges(2, 10); }).kind() == DeformConvError::Kind::invalidShape);
 }
 
 // ---- GPU group ---------------------------------------------------------------------
