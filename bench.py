@@ -143,6 +143,11 @@ def bench_body(args) -> int:
     out = props.cpu().numpy().view(np.float16)
     flops = dc.body_flops(H, W, 0, blocks)
     tflops = flops / (step_ms * 1e-3) / 1e12
+    for g in graphs:
+        g.free()
+    body.free()
+    clip_line = bench_clip(args, ctx, dc, clip, dev)
+    cpu = None if args.no_cpu_baseline else cpu_baseline_body(clip)
     line = {
         "metric": "BasicVSR++ propagation body us/frame (C4: offset convs + DCNv2 + 5-block backbone, hipGraph per frame)",
         "value": round(step_ms * 1e3, 3),
@@ -165,14 +170,92 @@ def bench_body(args) -> int:
                      "kernel": "whole body graph (conv3x3 x15, DCN, glue)", "flops_per_step": flops},
         "wall_ms_timed_region": wall_ms,
         "output_finite": bool(np.all(np.isfinite(out.astype(np.float32)))),
-        "cpu_baseline": None,
+        "clip": clip_line,
+        "cpu_baseline": cpu,
     }
-    for g in graphs:
-        g.free()
-    body.free()
     ctx.close()
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_clip(args, ctx, dc, clip, dev) -> dict:
+    """All four branches over the 30-frame clip captured as ONE hipGraph (the whole-clip
+    command buffer of the reference): 4 x 30 body steps, backbone inputs 128..320
+    channels. Reported beside the per-frame line; one replay is one clip."""
+    import numpy as np
+    import torch
+
+    H, W, frames, blocks = clip["height"], clip["width"], clip["frames"], clip["blocks"]
+    plane = H * W
+    weights = [clip["weights"]] + [dc.generate_body_inputs(H, W, 1, branch=b, blocks=blocks,
+                                                           seed=args.seed + b)["weights"] for b in (1, 2, 3)]
+    wd = [{k: dev(v) for k, v in w.items()} for w in weights]
+    pc = ctx.clip(H, W, frames, wd, blocks=blocks)
+    spatial = dev(clip["feats"])
+    flows = dev(clip["flows"]).view(frames, 2 * plane)
+    backward, forward = flows[: frames - 1].contiguous(), flows[1:].contiguous()
+    prop = torch.zeros(4 * frames * 64 * plane, dtype=torch.int16, device="cuda")
+    graph = pc.capture(spatial, backward, forward, prop)
+    stream = torch.cuda.Stream()
+    graph.launch(stream)
+    torch.cuda.synchronize()
+    reps = 3
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(reps):
+            graph.launch(stream)
+        end.record(stream)
+    torch.cuda.synchronize()
+    clip_ms = start.elapsed_time(end) / reps
+    out = prop.cpu().numpy().view(np.float16)
+    flops = dc.clip_flops(H, W, frames, blocks)
+    graph.free()
+    pc.free()
+    return {"workload": f"4 branches x {frames} frames (backward_1, forward_1, backward_2, forward_2), one hipGraph",
+            "ms_per_clip": clip_ms, "body_steps": 4 * frames, "us_per_body_step": clip_ms * 1e3 / (4 * frames),
+            "tflops": flops / (clip_ms * 1e-3) / 1e12, "flops_per_clip": flops, "replays_timed": reps,
+            "output_finite": bool(np.all(np.isfinite(out.astype(np.float32))))}
+
+
+def cpu_baseline_body(clip) -> dict:
+    """One C4 body step (branch 0) on the host through the C oracle: temporal preparation,
+    the four offset convs, the offset transform, the FP32 DCN and the backbone, FP16 between
+    layers; the convs run on all host cores (OpenMP), the DCN on the same threads."""
+    import os
+
+    import numpy as np
+
+    import oracle
+
+    oracle.load()
+    H, W, blocks = clip["height"], clip["width"], clip["blocks"]
+    w = clip["weights"]
+    feats, flows = clip["feats"], clip["flows"].reshape(clip["frames"], -1)
+    threads = os.cpu_count() or 1
+    f16 = lambda a: np.asarray(a, np.float32).astype(np.float16)  # noqa: E731
+    t0 = time.perf_counter()
+    flow2, cond, dinp = oracle.temporal_prepare_f16(W, H, True, feats[1], feats[2], feats[0], flows[2], flows[1])
+    h = cond
+    for i, (ci, co) in enumerate([(196, 64), (64, 64), (64, 64)]):
+        h = oracle.conv3x3_f16(ci, co, H, W, h, w[f"offset_w{i}"], w[f"offset_b{i}"], 1, 0.1)
+    raw = oracle.conv3x3_f16(64, 432, H, W, h, w["offset_w3"], w["offset_b3"], 0, 0.1)
+    off, msk = oracle.offset_transform_f16(H * W, raw, flows[2], flow2)
+    shape = oracle.OracleShape(1, 128, H, W, 64, H, W, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    aligned = f16(oracle.forward_f32_threads(shape, dinp.astype(np.float32), off.astype(np.float32),
+                                             msk.astype(np.float32), w["dcn_w"].astype(np.float32),
+                                             w["dcn_b"].astype(np.float32), threads))
+    bb = np.concatenate([feats[2], aligned])
+    feat = oracle.conv3x3_f16(128, 64, H, W, bb, w["backbone_w0"], w["backbone_b0"], 1, 0.1)
+    for i in range(blocks):
+        t = oracle.conv3x3_f16(64, 64, H, W, feat, w[f"backbone_w{1 + 2 * i}"], w[f"backbone_b{1 + 2 * i}"], 2, 0.1)
+        feat = oracle.conv3x3_f16(64, 64, H, W, t, w[f"backbone_w{2 + 2 * i}"], w[f"backbone_b{2 + 2 * i}"], 0,
+                                  0.1, feat)
+    out = f16(aligned.astype(np.float32) + feat.astype(np.float32))
+    seconds = time.perf_counter() - t0
+    return {"value": seconds * 1e6, "unit": "us/frame", "cores": threads, "kind": "port",
+            "sample": "one full body step (branch 0, 64x64, 5 blocks) through the C oracle, "
+                      f"output finite: {bool(np.all(np.isfinite(out.astype(np.float32))))}"}
 
 
 def main() -> int:

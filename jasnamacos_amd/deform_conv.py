@@ -843,6 +843,17 @@ def body_flops(height: int, width: int, branch: int = 0, blocks: int = 5) -> int
     return sum(2 * plane * 9 * ci * co for ci, co in convs) + 2 * plane * 9 * 128 * 64
 
 
+def clip_flops(height: int, width: int, frames: int, blocks: int = 5) -> int:
+    """GEMM-equivalent flops of a four-branch clip: per branch one first step (backbone
+    only) and frames - 1 full bodies."""
+    plane = height * width
+    total = 0
+    for b in range(4):
+        backbone = sum(2 * plane * 9 * ci * co for ci, co in [(64 * (b + 2), 64)] + [(64, 64)] * (2 * blocks))
+        total += backbone + (frames - 1) * body_flops(height, width, b, blocks)
+    return total
+
+
 def pack_ic_k_oc(weight_oihw: np.ndarray, shape: DeformConvShape) -> np.ndarray:
     """OIHW -> [ic][k][oc] (MetalRunner.swift:235-243; tools/export_deform_weights.py:47)."""
     w = np.asarray(weight_oihw).reshape(shape.output_channels, shape.input_channels, shape.kernel_area)
