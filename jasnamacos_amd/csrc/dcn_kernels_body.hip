@@ -40,11 +40,17 @@ __device__ __forceinline__ float sample_zero(const uint16_t* plane, int H, int W
     const int x0 = (int)fminf(fmaxf(fx, -4.0f), (float)W + 4.0f);
     const int y1 = y0 + 1, x1 = x0 + 1;
     const float ly = y - fy, lx = x - fx;
-    auto v = [&](int yy, int xx) -> float {
-        return (yy >= 0 && yy < H && xx >= 0 && xx < W) ? h2f(plane[(size_t)yy * W + xx]) : 0.0f;
-    };
-    return v(y0, x0) * (1.0f - ly) * (1.0f - lx) + v(y0, x1) * (1.0f - ly) * lx +
-           v(y1, x0) * ly * (1.0f - lx) + v(y1, x1) * ly * lx;
+    // Every corner is loaded from an index clamped into the plane and zeroed afterwards
+    // when it lies outside: unconditional loads, all in flight together.
+    const int yc0 = min(max(y0, 0), H - 1), yc1 = min(max(y1, 0), H - 1);
+    const int xc0 = min(max(x0, 0), W - 1), xc1 = min(max(x1, 0), W - 1);
+    const float t00 = h2f(plane[(size_t)yc0 * W + xc0]), t01 = h2f(plane[(size_t)yc0 * W + xc1]);
+    const float t10 = h2f(plane[(size_t)yc1 * W + xc0]), t11 = h2f(plane[(size_t)yc1 * W + xc1]);
+    const bool r0 = y0 >= 0 && y0 < H, r1 = y1 >= 0 && y1 < H;
+    const bool c0 = x0 >= 0 && x0 < W, c1 = x1 >= 0 && x1 < W;
+    const float v00 = (r0 && c0) ? t00 : 0.0f, v01 = (r0 && c1) ? t01 : 0.0f;
+    const float v10 = (r1 && c0) ? t10 : 0.0f, v11 = (r1 && c1) ? t11 : 0.0f;
+    return v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx + v10 * ly * (1.0f - lx) + v11 * ly * lx;
 }
 
 // accumulate_second_order_flow_fp16 (MetalShader.swift:738-763):
@@ -194,13 +200,27 @@ __device__ __forceinline__ void sample8_zero(const uint16_t* planes, size_t plan
     const float ly = y - fy, lx = x - fx;
     const bool r0 = y0 >= 0 && y0 < H, r1 = y1 >= 0 && y1 < H;
     const bool c0 = x0 >= 0 && x0 < W, c1 = x1 >= 0 && x1 < W;
+    // Unconditional loads from clamped indices (32 in flight), out-of-plane corners
+    // zeroed afterwards: the same values as loading only the valid corners.
+    const size_t i00 = (size_t)min(max(y0, 0), H - 1) * W + min(max(x0, 0), W - 1);
+    const size_t i01 = (size_t)min(max(y0, 0), H - 1) * W + min(max(x1, 0), W - 1);
+    const size_t i10 = (size_t)min(max(y1, 0), H - 1) * W + min(max(x0, 0), W - 1);
+    const size_t i11 = (size_t)min(max(y1, 0), H - 1) * W + min(max(x1, 0), W - 1);
+    uint16_t t[8][4];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const uint16_t* p = planes + (size_t)c * plane;
-        const float v00 = (r0 && c0) ? h2f(p[(size_t)y0 * W + x0]) : 0.0f;
-        const float v01 = (r0 && c1) ? h2f(p[(size_t)y0 * W + x1]) : 0.0f;
-        const float v10 = (r1 && c0) ? h2f(p[(size_t)y1 * W + x0]) : 0.0f;
-        const float v11 = (r1 && c1) ? h2f(p[(size_t)y1 * W + x1]) : 0.0f;
+        t[c][0] = p[i00];
+        t[c][1] = p[i01];
+        t[c][2] = p[i10];
+        t[c][3] = p[i11];
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const float v00 = (r0 && c0) ? h2f(t[c][0]) : 0.0f;
+        const float v01 = (r0 && c1) ? h2f(t[c][1]) : 0.0f;
+        const float v10 = (r1 && c0) ? h2f(t[c][2]) : 0.0f;
+        const float v11 = (r1 && c1) ? h2f(t[c][3]) : 0.0f;
         v[c] = v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx + v10 * ly * (1.0f - lx) +
                v11 * ly * lx;
     }
