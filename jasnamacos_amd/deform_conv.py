@@ -370,7 +370,7 @@ class HipDeformConv:
             packed_w, bias = _weights.unpack_weight_set(_weights.read_weight_set(weight_set))
             w16 = np.ascontiguousarray(np.transpose(packed_w, (2, 0, 1))).reshape(-1).astype(np.float16)
             b16 = np.asarray(bias, np.float16)
-        dev = lambda a: torch.from_numpy(np.ascontiguousarray(np.asarray(a, np.float16)).view(np.int16)).cuda()  # noqa: E731
+        dev = lambda a: torch.from_numpy(np.array(a, np.float16).view(np.int16)).cuda()  # noqa: E731 (a writable copy)
         x, off, msk, w, b = (dev(a) for a in (d["input"], d["offset"], d["mask"], w16, b16))
         base_out = torch.empty(shape.output_count, dtype=torch.int16, device="cuda")
         fused_out = torch.empty_like(base_out)
