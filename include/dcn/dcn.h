@@ -390,6 +390,18 @@ dcn_status dcn_conv3x3_f16_dev(dcn_context* ctx, const dcn_conv* conv, const voi
                                dcn_tensor_layout res2_layout, void* d_out,
                                dcn_tensor_layout out_layout, void* stream);
 
+/* Two chained 64 -> 64 convs of one plane in one launch: t = half(act1(conv1(x) + b1)),
+ * out = half(r2 + half(r1 + act2(conv2(t) + b2))). The residual block of the backbone
+ * (conv-ReLU-conv + skip) and two LeakyReLU layers of conv_offset
+ * (tools/convert_basicvsrpp.py:181-197); t never leaves the chip, and the result equals
+ * two dcn_conv3x3_f16_dev calls bit for bit. DCN_INVALID_SHAPE unless both convs are
+ * 64 -> 64 over the same plane. */
+dcn_status dcn_conv3x3_pair_f16_dev(dcn_context* ctx, const dcn_conv* conv1, const dcn_conv* conv2,
+                                    const void* d_x_cb8, int activation1, int activation2, float slope,
+                                    const void* d_res1, dcn_tensor_layout res1_layout,
+                                    const void* d_res2, dcn_tensor_layout res2_layout, void* d_out,
+                                    dcn_tensor_layout out_layout, void* stream);
+
 /* One propagation body: conv_offset (196->64->64->64->432, LeakyReLU 0.1 between), the
  * offset transform, the 128->64 DCN (16 deformable groups, 3x3), the backbone
  * ([feat_current, extra prefix features..., aligned] -> 64 conv + LeakyReLU 0.1, then

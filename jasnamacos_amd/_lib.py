@@ -146,6 +146,8 @@ SIGNATURES: dict[str, tuple] = {
     "dcn_conv3x3_free": (None, [c_void]),
     "dcn_conv3x3_f16_dev": (C.c_int, [CtxP, c_void, c_void, C.c_int, C.c_float, c_void, C.c_int, c_void,
                                       C.c_int, c_void, C.c_int, c_void]),
+    "dcn_conv3x3_pair_f16_dev": (C.c_int, [CtxP, c_void, c_void, c_void, C.c_int, C.c_int, C.c_float, c_void,
+                                           C.c_int, c_void, C.c_int, c_void, C.c_int, c_void]),
     "dcn_body_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(DcnBodyWeights),
                                   c_void, C.POINTER(c_void)]),
     "dcn_body_destroy": (None, [c_void]),

@@ -49,7 +49,7 @@ struct dcn_body {
     uint16_t* offset = nullptr;      // 288 NCHW
     uint16_t* mask = nullptr;        // 144 NCHW
     uint16_t* bb_in = nullptr;       // backbone input [feat_current, prefix..., aligned] CB8
-    uint16_t* feat[3] = {};          // backbone features, 64 channels CB8
+    uint16_t* feat[2] = {};          // backbone features, 64 channels CB8
     hipStream_t capture_stream = nullptr;
 };
 
@@ -309,6 +309,29 @@ dcn_status dcn_conv3x3_f16_dev(dcn_context* ctx, const dcn_conv* conv, const voi
     return DCN_OK;
 }
 
+dcn_status dcn_conv3x3_pair_f16_dev(dcn_context* ctx, const dcn_conv* conv1, const dcn_conv* conv2,
+                                    const void* d_x_cb8, int activation1, int activation2, float slope,
+                                    const void* d_res1, dcn_tensor_layout res1_layout, const void* d_res2,
+                                    dcn_tensor_layout res2_layout, void* d_out, dcn_tensor_layout out_layout,
+                                    void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    if (!conv1 || !conv2 || !d_x_cb8 || !d_out) return fail(ctx, DCN_INVALID_ARGUMENT, "null conv or pointer");
+    for (int act : {activation1, activation2})
+        if (act < 0 || act > 2) return fail(ctx, DCN_INVALID_ARGUMENT, "unknown activation");
+    for (int l : {(int)res1_layout, (int)res2_layout, (int)out_layout})
+        if (l != DCN_TENSOR_NCHW && l != DCN_TENSOR_CB8)
+            return fail(ctx, DCN_INVALID_ARGUMENT, "unknown tensor layout");
+    if (conv1->g.cin != 64 || conv1->g.cout != 64 || conv2->g.cin != 64 || conv2->g.cout != 64 ||
+        conv1->g.h != conv2->g.h || conv1->g.w != conv2->g.w)
+        return fail(ctx, DCN_INVALID_SHAPE, "a conv pair needs two 64 -> 64 convs of one plane");
+    DeviceGuard guard(ctx->device);
+    DCN_HIP(ctx, dcn::launch_conv3x3_pair(conv1->g, conv2->g, d_x_cb8, conv1->wpk, conv1->bias, activation1,
+                                          conv2->wpk, conv2->bias, activation2, slope,
+                                          (const uint16_t*)d_res1, res1_layout, (const uint16_t*)d_res2,
+                                          res2_layout, (uint16_t*)d_out, out_layout, (hipStream_t)stream));
+    return DCN_OK;
+}
+
 void dcn_body_destroy(dcn_body* body) {
     if (!body) return;
     DeviceGuard guard(body->ctx ? body->ctx->device : 0);
@@ -377,7 +400,7 @@ dcn_status dcn_body_create(dcn_context* ctx, int height, int width, int branch, 
     // CB8 borders and padding channels are zero once and never written again, so a
     // step (and its captured graph) holds no memset.
     for (uint16_t* p : {b->cond_cb8, b->deform_cb8, b->off_a, b->off_b, b->bb_in, b->feat[0],
-                        b->feat[1], b->feat[2]}) {
+                        b->feat[1]}) {
         size_t elems = 0;
         if (p == b->cond_cb8) elems = dcn::cb8_tensor_elems(196, height, width);
         else if (p == b->deform_cb8) elems = dcn::cb8_tensor_elems(128, height, width);
@@ -408,17 +431,18 @@ dcn_status run_backbone(dcn_body* body, void* d_feat_prop_out, hipStream_t s) {
     const int aligned_c = 64 * (body->branch + 1);
     DCN_TRY(run_conv(ctx, body->backbone[0], body->bb_in, 1, nullptr, NCHW, nullptr, NCHW,
                      body->feat[0], CB8, s));
+    // Each block's two convs run as one launch (t = ReLU(conv(x)) stays in LDS).
     int x = 0;
     for (int i = 0; i < body->blocks; ++i) {
-        const int t = (x + 1) % 3, y = (x + 2) % 3;
-        DCN_TRY(run_conv(ctx, body->backbone[1 + 2 * i], body->feat[x], 2, nullptr, NCHW, nullptr,
-                         NCHW, body->feat[t], CB8, s));
+        const int y = x ^ 1;
         const bool last = i + 1 == body->blocks;
-        const dcn_conv* c = body->backbone[2 + 2 * i];
-        DCN_HIP(ctx, dcn::launch_conv3x3(c->g, body->feat[t], c->wpk, c->bias, 0, 0.1f, body->feat[x], CB8,
-                                         last ? body->bb_in : nullptr, CB8,
-                                         last ? (uint16_t*)d_feat_prop_out : body->feat[y],
-                                         last ? NCHW : CB8, s, aligned_c));
+        const dcn_conv* c1 = body->backbone[1 + 2 * i];
+        const dcn_conv* c2 = body->backbone[2 + 2 * i];
+        DCN_HIP(ctx, dcn::launch_conv3x3_pair(c1->g, c2->g, body->feat[x], c1->wpk, c1->bias, 2, c2->wpk,
+                                              c2->bias, 0, 0.1f, body->feat[x], CB8,
+                                              last ? body->bb_in : nullptr, CB8,
+                                              last ? (uint16_t*)d_feat_prop_out : body->feat[y],
+                                              last ? NCHW : CB8, s, aligned_c));
         x = y;
     }
     return DCN_OK;
@@ -458,12 +482,12 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
     // output into offsets and masks in its epilogue.
     DCN_TRY(run_conv(ctx, body->offset_conv[0], body->cond_cb8, 1, nullptr, NCHW, nullptr, NCHW,
                      body->off_a, CB8, s));
-    DCN_TRY(run_conv(ctx, body->offset_conv[1], body->off_a, 1, nullptr, NCHW, nullptr, NCHW,
-                     body->off_b, CB8, s));
-    DCN_TRY(run_conv(ctx, body->offset_conv[2], body->off_b, 1, nullptr, NCHW, nullptr, NCHW,
-                     body->off_a, CB8, s));
+    const dcn_conv* c1 = body->offset_conv[1];
+    const dcn_conv* c2 = body->offset_conv[2];
+    DCN_HIP(ctx, dcn::launch_conv3x3_pair(c1->g, c2->g, body->off_a, c1->wpk, c1->bias, 1, c2->wpk, c2->bias,
+                                          1, 0.1f, nullptr, NCHW, nullptr, NCHW, body->off_b, CB8, s));
     const dcn_conv* c3 = body->offset_conv[3];
-    DCN_HIP(ctx, dcn::launch_conv3x3_offsets(c3->g, body->off_a, c3->wpk, c3->bias,
+    DCN_HIP(ctx, dcn::launch_conv3x3_offsets(c3->g, body->off_b, c3->wpk, c3->bias,
                                              (const uint16_t*)d_flow1, (const uint16_t*)d_flow2_out,
                                              body->offset, body->mask, s));
     // The DCN writes the aligned feature into the backbone input (CB8, after the prefix).

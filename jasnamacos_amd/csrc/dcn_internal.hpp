@@ -147,6 +147,13 @@ hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* 
                           const float* bias, int act, float slope, const uint16_t* res1,
                           int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,
                           int out_layout, hipStream_t stream, int res2_coff = 0);
+// Two chained 64 -> 64 convs in one launch: t = half(act1(conv1(x) + b1)) held in LDS,
+// then conv2 over t with launch_conv3x3's epilogue; bit-identical to two launches.
+hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, const void* x_cb8,
+                               const void* wpk1, const float* bias1, int act1, const void* wpk2,
+                               const float* bias2, int act2, float slope, const uint16_t* res1,
+                               int res1_layout, const uint16_t* res2, int res2_layout,
+                               uint16_t* out, int out_layout, hipStream_t stream, int res2_coff = 0);
 // The last conv_offset layer (cout 432) with prepare_dcn_offsets_fp16 in its epilogue:
 // raw = half(conv + bias), offsets = half(10 tanh(raw) + flow), masks = half(sigmoid(raw)).
 hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, const void* wpk,

@@ -513,6 +513,16 @@ class Conv3x3:
                                                           int(res2_layout), _ptr(out), int(out_layout),
                                                           _stream(stream)))
 
+    def run_pair_dev(self, second: "Conv3x3", x_cb8, out, out_layout=TENSOR_NCHW, activation1=2,
+                     activation2=0, slope=0.1, res1=None, res1_layout=TENSOR_NCHW, res2=None,
+                     res2_layout=TENSOR_NCHW, stream=None) -> None:
+        """This conv then `second` in one launch (both 64 -> 64): the intermediate
+        half(act1(conv(x) + b)) stays on chip; equal to two run_dev calls bit for bit."""
+        self.ctx._check(self.ctx._lib.dcn_conv3x3_pair_f16_dev(
+            self.ctx.ctx, self.handle, second.handle, _ptr(x_cb8), int(activation1), int(activation2),
+            float(slope), _ptr(res1), int(res1_layout), _ptr(res2), int(res2_layout), _ptr(out),
+            int(out_layout), _stream(stream)))
+
     def free(self) -> None:
         if self.handle:
             self.ctx._lib.dcn_conv3x3_free(self.handle)

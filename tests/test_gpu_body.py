@@ -8,6 +8,8 @@ Bars:
     the host's), and inside the reference's own 5e-3 gate (JasnaCLI.swift:177-211);
   * conv3x3: within 2 FP16 ulp + 1e-4 of the oracle (only the FP32 summation order
     differs);
+  * the one-launch conv pair: bit-identical to two conv3x3 launches (same K split and
+    summation order), including the zero padding of the intermediate at the map edge;
   * one whole body step: max |err| <= 2e-2, mean |err| <= 1e-3 against the oracle chain
     (north-star FP16 tolerances), second-order flow bit-identical;
   * a captured body graph replays bit-identically to the eager step.
@@ -178,6 +180,63 @@ def test_conv3x3_matches_oracle(gpu_ctx, dcn, oracle, torch, cin, cout, act, res
     ok = ulp_close(got, ref, ulps=2, atol=1e-4)
     assert np.all(ok), float(np.abs(got.astype(np.float64) - ref).max())
     conv.free()
+
+
+PAIR_CASES = [
+    # h, w, act1, act2, res1 layout (None = none), res2 layout, out layout
+    (13, 21, 2, 0, 1, None, 1),   # residual block, partial 2 x 8 tiles on both edges
+    (16, 24, 1, 1, None, None, 1),  # two LeakyReLU conv_offset layers
+    (64, 64, 2, 0, 1, 1, 0),      # the last block: skip + aligned feature, NCHW out
+    (7, 9, 2, 0, 0, 0, 0),        # a few partial tiles, NCHW residuals
+    (5, 3, 0, 2, None, 0, 1),
+]
+
+
+@pytest.mark.parametrize("h,w,act1,act2,r1l,r2l,out_layout", PAIR_CASES)
+def test_conv_pair_equals_two_convs(gpu_ctx, dcn, torch, h, w, act1, act2, r1l, r2l, out_layout):
+    rng = np.random.default_rng(h * 31 + w + act1)
+    x = br.f16(rng.standard_normal(64 * h * w))
+    w1 = br.f16(rng.normal(0, 0.05, (64, 64, 3, 3)))
+    w2 = br.f16(rng.normal(0, 0.05, (64, 64, 3, 3)))
+    b1 = br.f16(rng.normal(0, 0.05, 64))
+    b2 = br.f16(rng.normal(0, 0.05, 64))
+    log("case: conv pair", h, w, act1, act2, r1l, r2l, out_layout)
+    c1 = gpu_ctx.conv3x3(64, 64, h, w, dev(torch, w1), dev(torch, b1))
+    c2 = gpu_ctx.conv3x3(64, 64, h, w, dev(torch, w2), dev(torch, b2))
+    xd = dev(torch, br.to_cb8(x, 64, h, w))
+
+    def residual(layout, seed):
+        if layout is None:
+            return None
+        r = br.f16(np.random.default_rng(seed).standard_normal(64 * h * w))
+        return dev(torch, br.to_cb8(r, 64, h, w) if layout == 1 else r)
+
+    r1 = xd if r1l == 1 else residual(r1l, 5)
+    r2 = residual(r2l, 6)
+    n = dcn.cb8_tensor_count(64, h, w) if out_layout else 64 * h * w
+    t = torch.zeros(dcn.cb8_tensor_count(64, h, w), dtype=torch.int16, device="cuda")
+    ref = torch.zeros(n, dtype=torch.int16, device="cuda")
+    got = torch.zeros(n, dtype=torch.int16, device="cuda")
+    c1.run_dev(xd, t, dcn.TENSOR_CB8, act1, 0.1)
+    c2.run_dev(t, ref, out_layout, act2, 0.1, r1, r1l or 0, r2, r2l or 0)
+    c1.run_pair_dev(c2, xd, got, out_layout, act1, act2, 0.1, r1, r1l or 0, r2, r2l or 0)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(got).view(np.uint16), host(ref).view(np.uint16))
+    c1.free()
+    c2.free()
+
+
+def test_conv_pair_rejects_other_widths(gpu_ctx, dcn, torch):
+    h, w = 8, 8
+    c1 = gpu_ctx.conv3x3(64, 64, h, w, dev(torch, np.zeros((64, 64, 3, 3))), dev(torch, np.zeros(64)))
+    c2 = gpu_ctx.conv3x3(64, 32, h, w, dev(torch, np.zeros((32, 64, 3, 3))), dev(torch, np.zeros(32)))
+    x = torch.zeros(dcn.cb8_tensor_count(64, h, w), dtype=torch.int16, device="cuda")
+    out = torch.zeros(32 * h * w, dtype=torch.int16, device="cuda")
+    with pytest.raises(dcn.DeformConvError) as e:
+        c1.run_pair_dev(c2, x, out)
+    assert e.value.status == dcn.INVALID_SHAPE
+    c1.free()
+    c2.free()
 
 
 def _body_case(torch, gpu_ctx, h, w, branch, blocks, seed):
