@@ -390,6 +390,16 @@ dcn_status dcn_conv3x3_f16_dev(dcn_context* ctx, const dcn_conv* conv, const voi
                                dcn_tensor_layout res2_layout, void* d_out,
                                dcn_tensor_layout out_layout, void* stream);
 
+/* The last conv_offset layer (cin -> 432) fused with prepare_dcn_offsets_fp16
+ * (MetalShader.swift:815-839; runDCNOffsetTransform, MetalRunner.swift:469-508): raw =
+ * half(conv(x) + b), offset [288][plane] = half(10 tanh(raw) + flow), mask [144][plane] =
+ * half(sigmoid(raw)); flows [2][plane] (x, y), flow1 for the first 144 offset channels and
+ * flow2 for the rest. Equals dcn_conv3x3_f16_dev (NCHW) followed by
+ * dcn_offset_transform_f16_dev bit for bit. DCN_INVALID_SHAPE unless cout is 432. */
+dcn_status dcn_conv3x3_offsets_f16_dev(dcn_context* ctx, const dcn_conv* conv, const void* d_x_cb8,
+                                       const void* d_flow1, const void* d_flow2, void* d_offset,
+                                       void* d_mask, void* stream);
+
 /* Two chained 64 -> 64 convs of one plane in one launch: t = half(act1(conv1(x) + b1)),
  * out = half(r2 + half(r1 + act2(conv2(t) + b2))). The residual block of the backbone
  * (conv-ReLU-conv + skip) and two LeakyReLU layers of conv_offset

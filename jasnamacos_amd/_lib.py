@@ -146,6 +146,7 @@ SIGNATURES: dict[str, tuple] = {
     "dcn_conv3x3_free": (None, [c_void]),
     "dcn_conv3x3_f16_dev": (C.c_int, [CtxP, c_void, c_void, C.c_int, C.c_float, c_void, C.c_int, c_void,
                                       C.c_int, c_void, C.c_int, c_void]),
+    "dcn_conv3x3_offsets_f16_dev": (C.c_int, [CtxP, c_void, c_void, c_void, c_void, c_void, c_void, c_void]),
     "dcn_conv3x3_pair_f16_dev": (C.c_int, [CtxP, c_void, c_void, c_void, C.c_int, C.c_int, C.c_float, c_void,
                                            C.c_int, c_void, C.c_int, c_void, C.c_int, c_void]),
     "dcn_body_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(DcnBodyWeights),

@@ -309,6 +309,20 @@ dcn_status dcn_conv3x3_f16_dev(dcn_context* ctx, const dcn_conv* conv, const voi
     return DCN_OK;
 }
 
+dcn_status dcn_conv3x3_offsets_f16_dev(dcn_context* ctx, const dcn_conv* conv, const void* d_x_cb8,
+                                       const void* d_flow1, const void* d_flow2, void* d_offset,
+                                       void* d_mask, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    if (!conv || !d_x_cb8 || !d_flow1 || !d_flow2 || !d_offset || !d_mask)
+        return fail(ctx, DCN_INVALID_ARGUMENT, "null conv or pointer");
+    if (conv->g.cout != 432) return fail(ctx, DCN_INVALID_SHAPE, "the offset conv has 432 output channels");
+    DeviceGuard guard(ctx->device);
+    DCN_HIP(ctx, dcn::launch_conv3x3_offsets(conv->g, d_x_cb8, conv->wpk, conv->bias, (const uint16_t*)d_flow1,
+                                             (const uint16_t*)d_flow2, (uint16_t*)d_offset, (uint16_t*)d_mask,
+                                             (hipStream_t)stream));
+    return DCN_OK;
+}
+
 dcn_status dcn_conv3x3_pair_f16_dev(dcn_context* ctx, const dcn_conv* conv1, const dcn_conv* conv2,
                                     const void* d_x_cb8, int activation1, int activation2, float slope,
                                     const void* d_res1, dcn_tensor_layout res1_layout, const void* d_res2,

@@ -13,7 +13,7 @@
 // pixels; chunks split Cout (432 -> 7 chunks, the last one partly padded with zero
 // weights). Epilogue: + bias, activation (none / LeakyReLU(slope) / ReLU), optional
 // residual r1 and second residual r2, each add rounded to FP16 as a separate FP16 op:
-// out = half(r2 + half(r1 + act(acc))). Output NCHW or CB8. A second epilogue (the
+// out = half(r2 + half(r1 + act(acc))). Output NCHW or CB8. conv_offsets_kernel (the
 // body's last conv_offset layer) turns the FP16 conv output into DCN offsets and masks.
 #include <hip/hip_runtime.h>
 
@@ -42,7 +42,7 @@ struct ConvArgs {
     uint32_t xin_bytes, wpk_bytes;
     int res1_layout, res2_layout, out_layout;
     int res2_coff;          // channel offset of the second residual inside its tensor
-    // Offsets epilogue (cout 432): out unused; offsets and masks from half(conv + bias).
+    // conv_offsets_kernel (cout 432): offsets and masks from half(conv + bias).
     int offsets;
     const uint16_t* flow1;  // [2][H][W] (x, y)
     const uint16_t* flow2;
@@ -145,23 +145,6 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a) {
         const int yy = pp / a.W;
         const int xx = pp - yy * a.W;
         float r = sum + a.bias[oc];
-        if (a.offsets) {
-            // prepare_dcn_offsets_fp16 (MetalShader.swift:815-839) on the FP16 conv output.
-            const float raw = (float)round_f16(r);
-            const size_t px = (size_t)yy * a.W + xx;
-            const size_t plane = (size_t)M;
-            if (oc < 288) {
-                const uint16_t* flow = oc < 144 ? a.flow1 : a.flow2;
-                const int flow_channel = ((oc % 144) & 1) == 0 ? 1 : 0;  // even = dy = flow y
-                const float residue = 10.0f * tanhf(raw);
-                const float f = (float)__builtin_bit_cast(_Float16, flow[flow_channel * plane + px]);
-                a.offset[(size_t)oc * plane + px] = __builtin_bit_cast(uint16_t, round_f16(residue + f));
-            } else {
-                a.mask[(size_t)(oc - 288) * plane + px] =
-                    __builtin_bit_cast(uint16_t, round_f16(1.0f / (1.0f + expf(-raw))));
-            }
-            continue;
-        }
         if (a.act == 1 && r < 0.0f) r = r * a.slope;
         if (a.act == 2 && r < 0.0f) r = 0.0f;
         if (a.res1 != nullptr) {
@@ -177,6 +160,135 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a) {
         }
         a.out[conv_index(a.out_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)] =
             __builtin_bit_cast(uint16_t, round_f16(r));
+    }
+}
+
+// The last conv_offset layer (64 -> 432) with prepare_dcn_offsets_fp16 in its epilogue.
+// Its 1,792 workgroups (256 tiles x 7 chunks of 64 channels) queue on the CUs, so
+// occupancy sets its time: conv3x3_kernel<8, 4> holds four K-steps of weight fragments
+// (108 VGPRs, two workgroups per CU, four rounds). This kernel keeps U K-steps in flight
+// under a MINW waves-per-SIMD bound; the launcher uses U = 2, MINW = 6 (65 VGPRs, three
+// workgroups per CU). Measured per body frame against conv3x3_kernel: 95.3 -> 91.5 us.
+// Wider tiles (RT row tiles x 16 NB channels: 2 x 144 and 1 x 144) cut the weight
+// traffic but measured slower (96.0 and 96.5 us: fewer, longer workgroups per CU).
+// Same K split and summation order as conv3x3_kernel<NW, U>: the results are the same
+// bits.
+template <int NW, int U, int NB, int RT, int MINW>
+__global__ __launch_bounds__(64 * NW, MINW) void conv_offsets_kernel(ConvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) f32x4 red4[];  // [NW][RT][NB][64] partial sums
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int quarter = lane >> 4;
+
+    const int per_xcd = (a.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+    const int chunk = blockIdx.y;
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+
+    const int M = a.H * a.W;
+    uint32_t base[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int pc = min((tile * RT + rt) * 16 + (lane & 15), M - 1);
+        const int y = pc / a.W;
+        const int x = pc - y * a.W;
+        base[rt] = (uint32_t)(y + kPad - 1) * a.Wp + x + kPad - 1;
+    }
+
+    f32x4 acc[RT][NB];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[rt][nb] = f32x4{};
+
+    const int s0 = wave * a.ksteps / NW;
+    const int s1 = (wave + 1) * a.ksteps / NW;
+    for (int sb = s0; sb < s1; sb += U) {
+        h8 Bf[U][NB];
+        u32x4 q[U][RT];
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int s = sb + i < s1 ? sb + i : s1 - 1;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                Bf[i][nb] = __builtin_bit_cast(
+                    h8, load16(wr, (uint32_t)((s * a.NBT + chunk * NB + nb) * 64 + lane) * 16u));
+            const int kb = 4 * s + quarter;
+            const int kbc = kb < a.KB ? kb : a.KB - 1;
+            const int tap = fast_div(kbc, a.magic_cb);
+            const int cb = kbc - tap * a.CB;
+            const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
+            const int kx = tap - ky * 3;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                q[i][rt] = load16(xr, (base[rt] + (uint32_t)(cb * a.Hp + ky) * a.Wp + kx) * 16u);
+        }
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            if (sb + i < s1) {  // uniform across the wave
+                const int kb = 4 * (sb + i) + quarter;
+                const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const h8 A = __builtin_bit_cast(h8, kb < a.KB ? q[i][rt] : z);
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc[rt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[rt][nb], 0, 0, 0);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) red4[((wave * RT + rt) * NB + nb) * 64 + lane] = acc[rt][nb];
+    __syncthreads();
+
+    // Thread (rt, nb, l, h) sums the 8-byte half h of rows (w, rt, nb, l) over the waves in
+    // wave order (consecutive threads read consecutive 8 bytes: no bank conflicts), giving
+    // pixels (tile * RT + rt) * 16 + 4 (l / 16) + 2 h + j (j = 0, 1) of channel
+    // chunk * 16 NB + 16 nb + l % 16. Two outputs per thread keep every wave busy in the
+    // transcendental epilogue.
+    const size_t plane = (size_t)M;
+    const float2* red2 = reinterpret_cast<const float2*>(red4);
+    for (int g = tid; g < RT * NB * 128; g += 64 * NW) {
+        const int h = g & 1;
+        const int row = g >> 1;  // (rt, nb, l)
+        const int l = row & 63;
+        const int nb = (row >> 6) % NB;
+        const int rt = row / (NB * 64);
+        float2 sum = {0.0f, 0.0f};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float2 t = red2[(((w * RT + rt) * NB + nb) * 64 + l) * 2 + h];
+            sum.x += t.x;
+            sum.y += t.y;
+        }
+        const int oc = chunk * 16 * NB + nb * 16 + (l & 15);
+        if (oc >= a.Cout) continue;
+        const float bias = a.bias[oc];
+        const int p0 = (tile * RT + rt) * 16 + 4 * (l >> 4) + 2 * h;
+        // prepare_dcn_offsets_fp16 (MetalShader.swift:815-839) on the FP16 conv output.
+        const uint16_t* flow = oc < 144 ? a.flow1 : a.flow2;
+        const int flow_channel = ((oc % 144) & 1) == 0 ? 1 : 0;  // even = dy = flow y
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int px = p0 + j;
+            if (px >= M) continue;
+            const float raw = (float)round_f16((j ? sum.y : sum.x) + bias);
+            if (oc < 288) {
+                const float residue = 10.0f * tanhf(raw);
+                const float f = (float)__builtin_bit_cast(_Float16, flow[flow_channel * plane + px]);
+                a.offset[(size_t)oc * plane + px] = __builtin_bit_cast(uint16_t, round_f16(residue + f));
+            } else {
+                a.mask[(size_t)(oc - 288) * plane + px] =
+                    __builtin_bit_cast(uint16_t, round_f16(1.0f / (1.0f + expf(-raw))));
+            }
+        }
     }
 }
 
@@ -496,6 +608,7 @@ hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, cons
                                   const float* bias, const uint16_t* flow1, const uint16_t* flow2,
                                   uint16_t* offset, uint16_t* mask, hipStream_t stream) {
     if (g.cout != 432) return hipErrorInvalidValue;
+    constexpr int NW = 8, U = 2, NB = 4, RT = 1, MINW = 6;
     ConvArgs a{};
     a.xin = x_cb8;
     a.wpk = wpk;
@@ -505,7 +618,27 @@ hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, cons
     a.flow2 = flow2;
     a.offset = offset;
     a.mask = mask;
-    return run_conv(g, a, stream);
+    a.H = g.h;
+    a.W = g.w;
+    a.Hp = g.h + 2 * kPad;
+    a.Wp = g.w + 2 * kPad;
+    a.xin_bytes = (uint32_t)((size_t)g.cb * a.Hp * a.Wp * 16);
+    a.wpk_bytes = (uint32_t)conv_packed_bytes(g);
+    a.CB = g.cb;
+    a.KB = g.kb;
+    a.ksteps = g.ksteps;
+    a.NBT = g.nbt;
+    a.Cout = g.cout;
+    a.tiles = (g.h * g.w + 16 * RT - 1) / (16 * RT);
+    a.magic_cb = magic_for(g.cb);
+    constexpr size_t lds = (size_t)NW * RT * NB * 64 * sizeof(f32x4);
+    auto kernel = &conv_offsets_kernel<NW, U, NB, RT, MINW>;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)((g.cout + 16 * NB - 1) / (16 * NB)));
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * NW), lds, stream, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,

@@ -513,6 +513,13 @@ class Conv3x3:
                                                           int(res2_layout), _ptr(out), int(out_layout),
                                                           _stream(stream)))
 
+    def run_offsets_dev(self, x_cb8, flow1, flow2, offset, mask, stream=None) -> None:
+        """The 432-channel conv_offset layer with the DCN offset transform in its epilogue:
+        offset = half(10 tanh(half(conv + b)) + flow), mask = half(sigmoid(half(conv + b)))."""
+        self.ctx._check(self.ctx._lib.dcn_conv3x3_offsets_f16_dev(
+            self.ctx.ctx, self.handle, _ptr(x_cb8), _ptr(flow1), _ptr(flow2), _ptr(offset), _ptr(mask),
+            _stream(stream)))
+
     def run_pair_dev(self, second: "Conv3x3", x_cb8, out, out_layout=TENSOR_NCHW, activation1=2,
                      activation2=0, slope=0.1, res1=None, res1_layout=TENSOR_NCHW, res2=None,
                      res2_layout=TENSOR_NCHW, stream=None) -> None:

@@ -10,6 +10,7 @@ Bars:
     differs);
   * the one-launch conv pair: bit-identical to two conv3x3 launches (same K split and
     summation order), including the zero padding of the intermediate at the map edge;
+  * the fused 432-channel offsets conv: bit-identical to conv3x3 + the offset transform;
   * one whole body step: max |err| <= 2e-2, mean |err| <= 1e-3 against the oracle chain
     (north-star FP16 tolerances), second-order flow bit-identical;
   * a captured body graph replays bit-identically to the eager step.
@@ -224,6 +225,30 @@ def test_conv_pair_equals_two_convs(gpu_ctx, dcn, torch, h, w, act1, act2, r1l, 
     assert np.array_equal(host(got).view(np.uint16), host(ref).view(np.uint16))
     c1.free()
     c2.free()
+
+
+@pytest.mark.parametrize("h,w", [(64, 64), (13, 21), (5, 3)])
+def test_offsets_conv_equals_conv_then_transform(gpu_ctx, dcn, torch, h, w):
+    """The fused 432-channel layer == conv3x3 (NCHW) + offset transform, bit for bit."""
+    rng = np.random.default_rng(h * 7 + w)
+    plane = h * w
+    x = br.f16(rng.standard_normal(64 * plane))
+    wt = br.f16(rng.normal(0, 0.05, (432, 64, 3, 3)))
+    b = br.f16(rng.normal(0, 0.05, 432))
+    f1 = br.f16(rng.uniform(-6, 6, 2 * plane))
+    f2 = br.f16(rng.uniform(-6, 6, 2 * plane))
+    log("case: offsets conv", h, w)
+    conv = gpu_ctx.conv3x3(64, 432, h, w, dev(torch, wt), dev(torch, b))
+    xd, f1d, f2d = dev(torch, br.to_cb8(x, 64, h, w)), dev(torch, f1), dev(torch, f2)
+    raw = torch.zeros(432 * plane, dtype=torch.int16, device="cuda")
+    outs = [torch.zeros(n * plane, dtype=torch.int16, device="cuda") for n in (288, 144, 288, 144)]
+    conv.run_dev(xd, raw, dcn.TENSOR_NCHW, 0, 0.1)
+    gpu_ctx.offset_transform_f16_dev(plane, raw, f1d, f2d, outs[0], outs[1])
+    conv.run_offsets_dev(xd, f1d, f2d, outs[2], outs[3])
+    torch.cuda.synchronize()
+    assert np.array_equal(host(outs[2]).view(np.uint16), host(outs[0]).view(np.uint16))
+    assert np.array_equal(host(outs[3]).view(np.uint16), host(outs[1]).view(np.uint16))
+    conv.free()
 
 
 def test_conv_pair_rejects_other_widths(gpu_ctx, dcn, torch):
