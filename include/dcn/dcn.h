@@ -412,6 +412,38 @@ dcn_status dcn_conv3x3_pair_f16_dev(dcn_context* ctx, const dcn_conv* conv1, con
                                     const void* d_res2, dcn_tensor_layout res2_layout, void* d_out,
                                     dcn_tensor_layout out_layout, void* stream);
 
+/* ---- SPyNet flow estimation: the producer of the first-order flows ---- */
+
+/* jasna_bicubic_downsample_quarter_fp16 (MetalShader.swift:488-521): out [c][h/4][w/4] =
+ * torch interpolate(scale_factor=0.25, mode="bicubic", a = -0.75) of in [c][h][w], FP32
+ * sums in the reference's order, one FP16 rounding. h and w multiples of 4 (the 256 x 256
+ * LQ tile -> the 64 x 64 SPyNet input). */
+dcn_status dcn_bicubic_quarter_f16_dev(dcn_context* ctx, int channels, int height, int width,
+                                       const void* d_in, void* d_out, void* stream);
+
+/* SPyNet: six levels (h/32 .. h), each [reference, support warped by the upsampled flow
+ * (border padding), flow] -> 7x7 convs 8->32->64->32->16->2 (ReLU between) -> flow +=
+ * residual (spynet_build_pyramid_pair_fp16, spynet_prepare_fp16, spynet_add_flow_fp16,
+ * MetalShader.swift:523-649; level order of tools/convert_basicvsrpp.py:82-100; the
+ * bidirectional pair of verifySPyNetPair, SPyNetPairProbe.swift:47-449). Weights OIHW
+ * FP16 device pointers, level 0 = the coarsest; packed at creation. */
+#define DCN_SPYNET_LEVELS 6
+#define DCN_SPYNET_LAYERS 5
+typedef struct dcn_spynet_weights {
+    const void* weight[DCN_SPYNET_LEVELS][DCN_SPYNET_LAYERS];
+    const void* bias[DCN_SPYNET_LEVELS][DCN_SPYNET_LAYERS];
+} dcn_spynet_weights;
+typedef struct dcn_spynet dcn_spynet;
+/* height and width multiples of 32 (the reference's 64 x 64). */
+dcn_status dcn_spynet_create(dcn_context* ctx, int height, int width, const dcn_spynet_weights* weights,
+                             void* stream, dcn_spynet** out);
+void dcn_spynet_destroy(dcn_spynet* spynet);
+/* reference, support: RGB [3][h][w] FP16 in [0, 1]. d_flow [1 + both][2][h][w] (x, y):
+ * image 0 = spynet(reference, support), image 1 (both_directions) = spynet(support,
+ * reference). Stream-ordered, no allocation, no memset: graph-capturable. */
+dcn_status dcn_spynet_flow_dev(dcn_spynet* spynet, const void* d_reference, const void* d_support,
+                               int both_directions, void* d_flow, void* stream);
+
 /* One propagation body: conv_offset (196->64->64->64->432, LeakyReLU 0.1 between), the
  * offset transform, the 128->64 DCN (16 deformable groups, 3x3), the backbone
  * ([feat_current, extra prefix features..., aligned] -> 64 conv + LeakyReLU 0.1, then

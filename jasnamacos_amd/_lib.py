@@ -56,6 +56,19 @@ class DcnScheduleStep(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("branch", "position", "frame", "flow_index", "second_order_frame")]
 
 
+SPYNET_LEVELS = 6
+SPYNET_LAYERS = 5
+
+
+class DcnSpynetWeights(C.Structure):
+    """dcn_spynet_weights: OIHW FP16 device pointers, [level][layer], level 0 coarsest."""
+
+    _fields_ = [
+        ("weight", (C.c_void_p * SPYNET_LAYERS) * SPYNET_LEVELS),
+        ("bias", (C.c_void_p * SPYNET_LAYERS) * SPYNET_LEVELS),
+    ]
+
+
 class DcnBodyWeights(C.Structure):
     """dcn_body_weights: OIHW FP16 device pointers of one propagation body."""
 
@@ -146,6 +159,11 @@ SIGNATURES: dict[str, tuple] = {
     "dcn_conv3x3_free": (None, [c_void]),
     "dcn_conv3x3_f16_dev": (C.c_int, [CtxP, c_void, c_void, C.c_int, C.c_float, c_void, C.c_int, c_void,
                                       C.c_int, c_void, C.c_int, c_void]),
+    "dcn_bicubic_quarter_f16_dev": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, c_void, c_void, c_void]),
+    "dcn_spynet_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.POINTER(DcnSpynetWeights), c_void,
+                                    C.POINTER(c_void)]),
+    "dcn_spynet_destroy": (None, [c_void]),
+    "dcn_spynet_flow_dev": (C.c_int, [c_void, c_void, c_void, C.c_int, c_void, c_void]),
     "dcn_conv3x3_offsets_f16_dev": (C.c_int, [CtxP, c_void, c_void, c_void, c_void, c_void, c_void, c_void]),
     "dcn_conv3x3_pair_f16_dev": (C.c_int, [CtxP, c_void, c_void, c_void, C.c_int, C.c_int, C.c_float, c_void,
                                            C.c_int, c_void, C.c_int, c_void, C.c_int, c_void]),

@@ -154,6 +154,38 @@ hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, c
                                const float* bias2, int act2, float slope, const uint16_t* res1,
                                int res1_layout, const uint16_t* res2, int res2_layout,
                                uint16_t* out, int out_layout, hipStream_t stream, int res2_coff = 0);
+// SPyNet (dcn_kernels_spynet.hip).
+constexpr int kSpynetMaxLevels = DCN_SPYNET_LEVELS;
+struct ConvKGeometry {
+    int ks, cin, cout, h, w;
+    int cb;      // ceil(cin / 8)
+    int kb;      // K-blocks = ks * ks * cb
+    int ksteps;  // K-steps of 4 K-blocks
+    int nb;      // 16-column blocks per workgroup (1, 2 or 4)
+    int chunks;  // workgroup columns
+    int nbt;     // 16-column blocks over all chunks
+};
+ConvKGeometry convk_geometry(int ks, int cin, int cout, int height, int width);
+size_t convk_packed_bytes(const ConvKGeometry& g);
+hipError_t launch_convk_prepack(const ConvKGeometry& g, const uint16_t* w, const uint16_t* bias, void* wpk,
+                                float* bpk, hipStream_t stream);
+// k x k conv over `batch` CB8 images with a `pad`-pixel zero border (pad >= ks / 2);
+// act 2 = ReLU; base (optional, NCHW) makes out = half(base + half(acc)); out NCHW or CB8
+// with the same border.
+hipError_t launch_convk(const ConvKGeometry& g, int batch, int pad, const void* x_cb8, const void* wpk,
+                        const float* bias, int act, const uint16_t* base, uint16_t* out, int out_cb8,
+                        hipStream_t stream);
+hipError_t launch_bicubic_quarter(const uint16_t* in, uint16_t* out, int channels, int height, int width,
+                                  hipStream_t stream);
+// Pyramids of `count` (1, 2) RGB frames: levels[f][l] = [3][h >> (n-1-l)][w >> (n-1-l)].
+hipError_t launch_spynet_pyramid(const uint16_t* const* frames, int count,
+                                 uint16_t* (*levels)[kSpynetMaxLevels], int nlevels, int height,
+                                 int width, hipStream_t stream);
+hipError_t launch_spynet_prepare(int batch, const uint16_t* const* reference, const uint16_t* const* support,
+                                 const uint16_t* source_flow, int source_height, int source_width,
+                                 int first_level, uint16_t* features, int pad, uint16_t* base_flow,
+                                 int height, int width, hipStream_t stream);
+
 // The last conv_offset layer (cout 432) with prepare_dcn_offsets_fp16 in its epilogue:
 // raw = half(conv + bias), offsets = half(10 tanh(raw) + flow), masks = half(sigmoid(raw)).
 hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, const void* wpk,

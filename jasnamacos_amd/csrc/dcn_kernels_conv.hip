@@ -367,7 +367,6 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     f32x4* red4 = reinterpret_cast<f32x4*>(lds);  // [NW][RT][NB][64] partial sums
     u32x4* tt = reinterpret_cast<u32x4*>(lds + (size_t)NW * kPairRT1 * NB * 64 * 16);
-    float* redf = reinterpret_cast<float*>(lds);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;

@@ -1,0 +1,452 @@
+// SPyNet flow estimation for the propagation body's flows (gfx950): the quarter-scale
+// bicubic input, the normalised image pyramid, the per-level block input (flow upsample +
+// border warp + concatenation) and the basic module's 7 x 7 convolutions.
+//
+// The elementwise kernels evaluate the reference's FP32 expressions in the same order
+// (jasna_bicubic_downsample_quarter_fp16, spynet_build_pyramid_pair_fp16,
+// spynet_prepare_fp16: MetalShader.swift:473-639), so they are bit-identical to the CPU
+// oracle. The convolutions are implicit GEMMs on v_mfma_f32_16x16x32_f16 like
+// conv3x3_kernel, generalised to k x k taps, a batch of images and a configurable zero
+// border of the CB8 activations (SPyNet's are padded by 3 for the 7 x 7 taps).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "dcn_device.hpp"
+#include "dcn_internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace dcn {
+namespace {
+
+using namespace dev;
+
+__device__ __forceinline__ float h2f(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
+__device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, round_f16(v)); }
+
+unsigned blocks_for(long n) { return (unsigned)((n + 255) / 256); }
+
+// cubic_weight (MetalShader.swift:473-483), a = -0.75.
+__device__ __forceinline__ float cubic_weight(float distance) {
+    const float a = -0.75f;
+    const float x = fabsf(distance);
+    if (x <= 1.0f) return (a + 2.0f) * x * x * x - (a + 3.0f) * x * x + 1.0f;
+    if (x < 2.0f) return a * x * x * x - 5.0f * a * x * x + 8.0f * a * x - 4.0f * a;
+    return 0.0f;
+}
+
+// jasna_bicubic_downsample_quarter_fp16 (MetalShader.swift:488-521), any C x H x W with
+// H, W multiples of 4 (every 4 x 4 footprint is then inside the image).
+__global__ __launch_bounds__(256) void bicubic_quarter_kernel(const uint16_t* __restrict__ in,
+                                                              uint16_t* __restrict__ out, int C, int H,
+                                                              int W) {
+    const int oh = H >> 2, ow = W >> 2;
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= (long)C * oh * ow) return;
+    const int c = (int)(gid / ((long)oh * ow));
+    const int sp = (int)(gid - (long)c * oh * ow);
+    const int oy = sp / ow;
+    const int ox = sp - oy * ow;
+    const float sy = ((float)oy + 0.5f) * 4.0f - 0.5f;
+    const float sx = ((float)ox + 0.5f) * 4.0f - 0.5f;
+    const int by = (int)floorf(sy);
+    const int bx = (int)floorf(sx);
+    float value = 0.0f;
+#pragma unroll
+    for (int yy = -1; yy <= 2; ++yy) {
+        const float wy = cubic_weight(sy - (float)(by + yy));
+        const uint16_t* row = in + ((size_t)c * H + (by + yy)) * W;
+#pragma unroll
+        for (int xx = -1; xx <= 2; ++xx) {
+            const float wx = cubic_weight(sx - (float)(bx + xx));
+            value += h2f(row[bx + xx]) * wy * wx;
+        }
+    }
+    out[gid] = f2h(value);
+}
+
+// spynet_build_pyramid_pair_fp16 (MetalShader.swift:523-570): level l (coarsest first) of
+// frame f is the direct box average over factor x factor pixels, normalised with the
+// ImageNet mean/std (:560-563). One thread per output value of every level and frame.
+struct PyramidArgs {
+    const uint16_t* frame[2];
+    uint16_t* level[2][kSpynetMaxLevels];
+    long offset[kSpynetMaxLevels + 1];  // first output index of each level (per frame)
+    int frames, levels, H, W;
+};
+
+__global__ __launch_bounds__(256) void spynet_pyramid_kernel(PyramidArgs a) {
+    const long per_frame = a.offset[a.levels];
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= per_frame * a.frames) return;
+    const int f = (int)(gid / per_frame);
+    const long r = gid - (long)f * per_frame;
+    int l = 0;
+    while (r >= a.offset[l + 1]) ++l;
+    const int shift = a.levels - 1 - l;
+    const int lh = a.H >> shift, lw = a.W >> shift;
+    const long e = r - a.offset[l];
+    const int c = (int)(e / ((long)lh * lw));
+    const int sp = (int)(e - (long)c * lh * lw);
+    const int y = sp / lw;
+    const int x = sp - y * lw;
+    const int factor = 1 << shift;
+    const float mean = c == 0 ? 0.485f : (c == 1 ? 0.456f : 0.406f);
+    const float stddev = c == 0 ? 0.229f : (c == 1 ? 0.224f : 0.225f);
+    float sum = 0.0f;
+    const uint16_t* src = a.frame[f] + ((size_t)c * a.H + (size_t)y * factor) * a.W + (size_t)x * factor;
+    for (int yy = 0; yy < factor; ++yy)
+        for (int xx = 0; xx < factor; ++xx) sum += h2f(src[(size_t)yy * a.W + xx]);
+    const float inverse_area = 1.0f / (float)(factor * factor);
+    a.level[f][l][e] = f2h((sum * inverse_area - mean) / stddev);
+}
+
+// sample_border_fp16 (MetalShader.swift:572-599).
+__device__ __forceinline__ float sample_border(const uint16_t* plane, int H, int W, float y, float x) {
+    y = fminf(fmaxf(y, 0.0f), (float)(H - 1));
+    x = fminf(fmaxf(x, 0.0f), (float)(W - 1));
+    const int y0 = (int)floorf(y);
+    const int x0 = (int)floorf(x);
+    const int y1 = min(y0 + 1, H - 1);
+    const int x1 = min(x0 + 1, W - 1);
+    const float ly = y - (float)y0;
+    const float lx = x - (float)x0;
+    const float v00 = h2f(plane[(size_t)y0 * W + x0]);
+    const float v01 = h2f(plane[(size_t)y0 * W + x1]);
+    const float v10 = h2f(plane[(size_t)y1 * W + x0]);
+    const float v11 = h2f(plane[(size_t)y1 * W + x1]);
+    return v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx + v10 * ly * (1.0f - lx) +
+           v11 * ly * lx;
+}
+
+// spynet_prepare_fp16 (MetalShader.swift:601-639) for a batch of (reference, support)
+// pairs: base flow [b][2][H][W] = half(2 * align-corners upsample of the previous level's
+// flow) (zero on the first level) and the 8-channel block input written as one 16-byte
+// CB8 unit per pixel ([b][1][H + 2 pad][W + 2 pad][8]).
+struct PrepareArgs {
+    const uint16_t* reference[2];
+    const uint16_t* support[2];
+    const uint16_t* source_flow;  // [b][2][SH][SW], unused on the first level
+    uint16_t* features;           // CB8, one block per image
+    uint16_t* base_flow;          // [b][2][H][W]
+    int batch, H, W, SH, SW, first_level, pad;
+};
+
+__global__ __launch_bounds__(256) void spynet_prepare_kernel(PrepareArgs a) {
+    const int plane = a.H * a.W;
+    const int gid = blockIdx.x * 256 + threadIdx.x;
+    if (gid >= a.batch * plane) return;
+    const int b = gid / plane;
+    const int sp = gid - b * plane;
+    const int y = sp / a.W;
+    const int x = sp - y * a.W;
+    float flow_x = 0.0f, flow_y = 0.0f;
+    if (!a.first_level) {
+        const float sx = a.W > 1 ? (float)x * (float)(a.SW - 1) / (float)(a.W - 1) : 0.0f;
+        const float sy = a.H > 1 ? (float)y * (float)(a.SH - 1) / (float)(a.H - 1) : 0.0f;
+        const uint16_t* src = a.source_flow + (size_t)b * 2 * a.SH * a.SW;
+        flow_x = 2.0f * sample_border(src, a.SH, a.SW, sy, sx);
+        flow_y = 2.0f * sample_border(src + (size_t)a.SH * a.SW, a.SH, a.SW, sy, sx);
+    }
+    uint16_t* base = a.base_flow + (size_t)b * 2 * plane;
+    base[sp] = f2h(flow_x);
+    base[plane + sp] = f2h(flow_y);
+    const uint16_t* ref = a.reference[b];
+    const uint16_t* sup = a.support[b];
+    uint16_t v[8];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        v[c] = ref[(size_t)c * plane + sp];
+        v[c + 3] = f2h(sample_border(sup + (size_t)c * plane, a.H, a.W, (float)y + flow_y, (float)x + flow_x));
+    }
+    v[6] = f2h(flow_x);
+    v[7] = f2h(flow_y);
+    const int Hp = a.H + 2 * a.pad, Wp = a.W + 2 * a.pad;
+    u32x4 unit;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) unit[i] = (uint32_t)v[2 * i] | ((uint32_t)v[2 * i + 1] << 16);
+    *reinterpret_cast<u32x4*>(a.features + (((size_t)b * Hp + y + a.pad) * Wp + x + a.pad) * 8) = unit;
+}
+
+// k x k convolution, stride 1, pad k/2, on CB8 activations with a zero border of `pad`
+// >= k/2 pixels ([B][CB][H + 2 pad][W + 2 pad][8]). conv3x3_kernel's scheme: 16-pixel
+// tiles (pixels of the whole batch in order), NB 16-column blocks of output channels per
+// workgroup, K-block kb = tap * CB + cb split over NW waves, cross-wave sum in LDS.
+// Epilogue: + bias, ReLU (act 2), optionally out = half(base + half(acc)) (the level's
+// residual flow added to its base flow, spynet_add_flow_fp16 MetalShader.swift:641-649),
+// NCHW or CB8 output.
+struct ConvKArgs {
+    const void* xin;
+    const void* wpk;      // [ksteps][NBT][64][8]
+    const float* bias;
+    const uint16_t* base; // optional [B][Cout][H][W]
+    uint16_t* out;
+    uint32_t xin_bytes, wpk_bytes;
+    int B, H, W, Hp, Wp, pad, CB, KB, ksteps, NBT, Cout, tiles, act, out_cb8;
+    uint32_t magic_cb;
+};
+
+template <int KS, int NW, int U, int NB>
+__global__ __launch_bounds__(64 * NW) void convk_kernel(ConvKArgs a) {
+    extern __shared__ float red[];  // [NW][NB][4][65]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int quarter = lane >> 4;
+
+    const int per_xcd = (a.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+    const int chunk = blockIdx.y;
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+
+    const int plane = a.H * a.W;
+    const int M = a.B * plane;
+    const int p = tile * 16 + (lane & 15);
+    const int pc = p < M ? p : M - 1;
+    const int b = pc / plane;
+    const int sp = pc - b * plane;
+    const int y = sp / a.W;
+    const int x = sp - y * a.W;
+    // 16-byte unit of (image b, cb 0, tap (0, 0)) in the padded planes.
+    const uint32_t base = ((uint32_t)(b * a.CB * a.Hp) + y + a.pad - KS / 2) * a.Wp + x + a.pad - KS / 2;
+
+    f32x4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{};
+
+    const int s0 = wave * a.ksteps / NW;
+    const int s1 = (wave + 1) * a.ksteps / NW;
+    for (int sb = s0; sb < s1; sb += U) {
+        h8 Bf[U][NB];
+        u32x4 q[U];
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            const int s = sb + i < s1 ? sb + i : s1 - 1;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                Bf[i][nb] = __builtin_bit_cast(
+                    h8, load16(wr, (uint32_t)((s * a.NBT + chunk * NB + nb) * 64 + lane) * 16u));
+            const int kb = 4 * s + quarter;
+            const int kbc = kb < a.KB ? kb : a.KB - 1;
+            const int tap = fast_div(kbc, a.magic_cb);
+            const int cb = kbc - tap * a.CB;
+            const int ky = tap / KS;
+            const int kx = tap - ky * KS;
+            q[i] = load16(xr, (base + (uint32_t)(cb * a.Hp + ky) * a.Wp + kx) * 16u);
+        }
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+            if (sb + i < s1) {  // uniform across the wave
+                const int kb = 4 * (sb + i) + quarter;
+                const u32x4 z = {0u, 0u, 0u, 0u};
+                const h8 A = __builtin_bit_cast(h8, kb < a.KB ? q[i] : z);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+    __syncthreads();
+
+    for (int idx = tid; idx < 16 * NB * 16; idx += 64 * NW) {
+        const int pl = idx & 15;
+        const int ocl = idx >> 4;
+        const int nb = ocl >> 4;
+        const int src = ((pl >> 2) << 4) + (ocl & 15);
+        const int v = pl & 3;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
+        const int oc = chunk * NB * 16 + ocl;
+        const int pp = tile * 16 + pl;
+        if (pp >= M || oc >= a.Cout) continue;
+        const int bb = pp / plane;
+        const int ss = pp - bb * plane;
+        float r = sum + a.bias[oc];
+        if (a.act == 2 && r < 0.0f) r = 0.0f;
+        if (a.base != nullptr) r = h2f(a.base[((size_t)bb * a.Cout + oc) * plane + ss]) + (float)round_f16(r);
+        size_t dst;
+        if (a.out_cb8) {
+            const int yy = ss / a.W;
+            const int xx = ss - yy * a.W;
+            dst = ((((size_t)bb * ((a.Cout + 7) >> 3) + (oc >> 3)) * a.Hp + yy + a.pad) * a.Wp + xx + a.pad) * 8 +
+                  (oc & 7);
+        } else {
+            dst = ((size_t)bb * a.Cout + oc) * plane + ss;
+        }
+        a.out[dst] = f2h(r);
+    }
+}
+
+// OIHW [Cout][Cin][KS][KS] -> [ksteps][NBT][64][8]: lane l of K-step s holds output channel
+// nb * 16 + l % 16 and K-block 4 s + l / 16 = tap * CB + cb (zero past Cin, Cout, KB).
+__global__ __launch_bounds__(256) void convk_prepack_kernel(const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ bias,
+                                                            uint16_t* __restrict__ wpk,
+                                                            float* __restrict__ bpk, int KS, int Cin,
+                                                            int Cout, int CB, int KB, int NBT,
+                                                            long total) {
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid < Cout) bpk[gid] = h2f(bias[gid]);
+    if (gid >= total) return;
+    const int e = (int)(gid & 7);
+    const int lane = (int)((gid >> 3) & 63);
+    const long q = gid >> 9;
+    const int nb = (int)(q % NBT);
+    const int s = (int)(q / NBT);
+    const int kb = 4 * s + (lane >> 4);
+    const int oc = nb * 16 + (lane & 15);
+    uint16_t v = 0;
+    if (kb < KB && oc < Cout) {
+        const int tap = kb / CB;
+        const int ic = (kb - tap * CB) * 8 + e;
+        if (ic < Cin) v = w[((size_t)oc * Cin + ic) * KS * KS + tap];
+    }
+    wpk[gid] = v;
+}
+
+}  // namespace
+
+ConvKGeometry convk_geometry(int ks, int cin, int cout, int height, int width) {
+    ConvKGeometry g;
+    g.ks = ks;
+    g.cin = cin;
+    g.cout = cout;
+    g.h = height;
+    g.w = width;
+    g.cb = (cin + 7) / 8;
+    g.kb = ks * ks * g.cb;
+    g.ksteps = (g.kb + 3) / 4;
+    g.nb = std::min(4, (cout + 15) / 16);
+    g.chunks = (cout + 16 * g.nb - 1) / (16 * g.nb);
+    g.nbt = g.chunks * g.nb;
+    return g;
+}
+
+size_t convk_packed_bytes(const ConvKGeometry& g) { return (size_t)g.ksteps * g.nbt * 64 * 8 * 2; }
+
+hipError_t launch_convk_prepack(const ConvKGeometry& g, const uint16_t* w, const uint16_t* bias, void* wpk,
+                                float* bpk, hipStream_t stream) {
+    const long total = (long)g.ksteps * g.nbt * 64 * 8;
+    hipLaunchKernelGGL(convk_prepack_kernel, dim3(blocks_for(std::max<long>(total, g.cout))), dim3(256), 0,
+                       stream, w, bias, (uint16_t*)wpk, bpk, g.ks, g.cin, g.cout, g.cb, g.kb, g.nbt, total);
+    return hipGetLastError();
+}
+
+namespace {
+
+template <int NB>
+hipError_t launch_convk_nb(const ConvKGeometry& g, ConvKArgs& a, hipStream_t stream) {
+    constexpr int NW = 8, U = 4;
+    const size_t lds = (size_t)NW * NB * 4 * 65 * sizeof(float);
+    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)g.chunks);
+    if (g.ks == 7) {
+        hipLaunchKernelGGL((convk_kernel<7, NW, U, NB>), grid, dim3(64 * NW), lds, stream, a);
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_convk(const ConvKGeometry& g, int batch, int pad, const void* x_cb8, const void* wpk,
+                        const float* bias, int act, const uint16_t* base, uint16_t* out, int out_cb8,
+                        hipStream_t stream) {
+    if (pad < g.ks / 2) return hipErrorInvalidValue;
+    ConvKArgs a{};
+    a.xin = x_cb8;
+    a.wpk = wpk;
+    a.bias = bias;
+    a.base = base;
+    a.out = out;
+    a.B = batch;
+    a.H = g.h;
+    a.W = g.w;
+    a.pad = pad;
+    a.Hp = g.h + 2 * pad;
+    a.Wp = g.w + 2 * pad;
+    a.CB = g.cb;
+    a.KB = g.kb;
+    a.ksteps = g.ksteps;
+    a.NBT = g.nbt;
+    a.Cout = g.cout;
+    a.act = act;
+    a.out_cb8 = out_cb8;
+    a.xin_bytes = (uint32_t)((size_t)batch * g.cb * a.Hp * a.Wp * 16);
+    a.wpk_bytes = (uint32_t)convk_packed_bytes(g);
+    a.tiles = (batch * g.h * g.w + 15) / 16;
+    a.magic_cb = magic_for(g.cb);
+    switch (g.nb) {
+        case 1: return launch_convk_nb<1>(g, a, stream);
+        case 2: return launch_convk_nb<2>(g, a, stream);
+        case 4: return launch_convk_nb<4>(g, a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_bicubic_quarter(const uint16_t* in, uint16_t* out, int channels, int height, int width,
+                                  hipStream_t stream) {
+    const long n = (long)channels * (height / 4) * (width / 4);
+    hipLaunchKernelGGL(bicubic_quarter_kernel, dim3(blocks_for(n)), dim3(256), 0, stream, in, out, channels,
+                       height, width);
+    return hipGetLastError();
+}
+
+hipError_t launch_spynet_pyramid(const uint16_t* const* frames, int count, uint16_t* (*levels)[kSpynetMaxLevels],
+                                 int nlevels, int height, int width, hipStream_t stream) {
+    if (count < 1 || count > 2 || nlevels < 1 || nlevels > kSpynetMaxLevels) return hipErrorInvalidValue;
+    PyramidArgs a{};
+    a.frames = count;
+    a.levels = nlevels;
+    a.H = height;
+    a.W = width;
+    long off = 0;
+    for (int l = 0; l < nlevels; ++l) {
+        a.offset[l] = off;
+        const int shift = nlevels - 1 - l;
+        off += 3L * (height >> shift) * (width >> shift);
+    }
+    a.offset[nlevels] = off;
+    for (int f = 0; f < count; ++f) {
+        a.frame[f] = frames[f];
+        for (int l = 0; l < nlevels; ++l) a.level[f][l] = levels[f][l];
+    }
+    hipLaunchKernelGGL(spynet_pyramid_kernel, dim3(blocks_for(off * count)), dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_spynet_prepare(int batch, const uint16_t* const* reference, const uint16_t* const* support,
+                                 const uint16_t* source_flow, int source_height, int source_width,
+                                 int first_level, uint16_t* features, int pad, uint16_t* base_flow,
+                                 int height, int width, hipStream_t stream) {
+    if (batch < 1 || batch > 2) return hipErrorInvalidValue;
+    PrepareArgs a{};
+    for (int b = 0; b < batch; ++b) {
+        a.reference[b] = reference[b];
+        a.support[b] = support[b];
+    }
+    a.source_flow = source_flow;
+    a.features = features;
+    a.base_flow = base_flow;
+    a.batch = batch;
+    a.H = height;
+    a.W = width;
+    a.SH = source_height;
+    a.SW = source_width;
+    a.first_level = first_level;
+    a.pad = pad;
+    hipLaunchKernelGGL(spynet_prepare_kernel, dim3(blocks_for((long)batch * height * width)), dim3(256), 0,
+                       stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace dcn

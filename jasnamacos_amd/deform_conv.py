@@ -479,6 +479,24 @@ class HipDeformConv:
                                               C.byref(w), _stream(stream), C.byref(handle)))
         return PropagationBody(self, handle.value, height, width, branch, blocks)
 
+    def bicubic_quarter_f16_dev(self, channels, height, width, src, out, stream=None) -> None:
+        """jasna_bicubic_downsample_quarter_fp16: [c][h][w] -> [c][h/4][w/4] (h, w multiples of 4)."""
+        self._check(self._lib.dcn_bicubic_quarter_f16_dev(self.ctx, int(channels), int(height), int(width),
+                                                          _ptr(src), _ptr(out), _stream(stream)))
+
+    def spynet(self, height, width, weights, stream=None) -> "SpyNet":
+        """weights: device tensors "w{level}_{layer}" and "b{level}_{layer}" (OIHW FP16),
+        level 0..5 coarsest first, layer 0..4 (8->32->64->32->16->2, 7x7)."""
+        w = _lib.DcnSpynetWeights()
+        for level in range(_lib.SPYNET_LEVELS):
+            for layer in range(_lib.SPYNET_LAYERS):
+                w.weight[level][layer] = _ptr(weights[f"w{level}_{layer}"])
+                w.bias[level][layer] = _ptr(weights[f"b{level}_{layer}"])
+        handle = C.c_void_p()
+        self._check(self._lib.dcn_spynet_create(self.ctx, int(height), int(width), C.byref(w), _stream(stream),
+                                                C.byref(handle)))
+        return SpyNet(self, handle.value, height, width)
+
     def clip(self, height, width, frames, weights, blocks: int = 5, stream=None) -> "PropagationClip":
         """The four propagation branches over `frames` frames; weights: four body weight dicts
         (backward_1, forward_1, backward_2, forward_2), as for body()."""
@@ -623,6 +641,32 @@ def _body_weights(weights: dict, blocks: int) -> "_lib.DcnBodyWeights":
         w.backbone_weight[i] = _ptr(weights[f"backbone_w{i}"])
         w.backbone_bias[i] = _ptr(weights[f"backbone_b{i}"])
     return w
+
+
+class SpyNet:
+    """SPyNet flow estimation (dcn_spynet): RGB frames [3][H][W] in, flows [n][2][H][W] out."""
+
+    def __init__(self, ctx: HipDeformConv, handle: int, height, width):
+        self.ctx, self.handle = ctx, C.c_void_p(handle)
+        self.height, self.width = height, width
+
+    def flow_dev(self, reference, support, flow, both_directions: bool = True, stream=None) -> None:
+        """flow[0] = spynet(reference, support); flow[1] = spynet(support, reference) when
+        both_directions (verifySPyNetPair's backward and forward, SPyNetPairProbe.swift)."""
+        self.ctx._check(self.ctx._lib.dcn_spynet_flow_dev(self.handle, _ptr(reference), _ptr(support),
+                                                          int(bool(both_directions)), _ptr(flow),
+                                                          _stream(stream)))
+
+    def free(self) -> None:
+        if self.handle:
+            self.ctx._lib.dcn_spynet_destroy(self.handle)
+            self.handle = C.c_void_p(None)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class PropagationClip:

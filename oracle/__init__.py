@@ -47,6 +47,13 @@ _SIG = {
     "oracle_temporal_prepare_f16": (None, [C.c_int, C.c_int, C.c_int, _h, _h, _h, _h, _h, _h, _h, _h]),
     "oracle_conv3x3_f16": (None, [C.c_int, C.c_int, C.c_int, C.c_int, _h, _h, _h, C.c_int, C.c_float,
                                   _h, _h]),
+    "oracle_bicubic_quarter_f16": (None, [C.c_int, C.c_int, C.c_int, _h, _h]),
+    "oracle_spynet_pyramid_f16": (None, [C.c_int, C.c_int, C.c_int, _h, C.POINTER(_h)]),
+    "oracle_sample_border_f16": (C.c_float, [_h, C.c_size_t, C.c_int, C.c_int, C.c_float, C.c_float]),
+    "oracle_spynet_prepare_f16": (None, [C.c_int, C.c_int, C.c_int, _h, _h, _h, C.c_int, C.c_int, _h, _h]),
+    "oracle_add_f16": (None, [C.c_size_t, _h, _h, _h]),
+    "oracle_convk_f16": (None, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _h, _h, _h, C.c_int, C.c_float,
+                                _h]),
 }
 
 _LIB = None
@@ -203,4 +210,54 @@ def conv3x3_f16(cin, cout, height, width, input, weight, bias, activation=0, slo
     out = np.empty(cout * height * width, dtype=np.uint16)
     load().oracle_conv3x3_f16(cin, cout, height, width, *[p for _, p in keep], int(activation), float(slope),
                               res[1], out.ctypes.data_as(_h))
+    return out.view(np.float16)
+
+
+def bicubic_quarter_f16(channels, height, width, input):
+    """jasna_bicubic_downsample_quarter_fp16 (MetalShader.swift:488-521)."""
+    i, p = _u16(input)
+    out = np.empty(channels * (height // 4) * (width // 4), dtype=np.uint16)
+    load().oracle_bicubic_quarter_f16(channels, height, width, p, out.ctypes.data_as(_h))
+    return out.view(np.float16)
+
+
+def spynet_pyramid_f16(height, width, levels, frame):
+    """spynet_build_pyramid_pair_fp16 (MetalShader.swift:523-570), one frame: a list of
+    `levels` [3][h_l][w_l] arrays, coarsest first."""
+    f, p = _u16(frame)
+    outs = [np.empty(3 * (height >> (levels - 1 - l)) * (width >> (levels - 1 - l)), dtype=np.uint16)
+            for l in range(levels)]
+    ptrs = (_h * levels)(*[o.ctypes.data_as(_h) for o in outs])
+    load().oracle_spynet_pyramid_f16(height, width, levels, p, ptrs)
+    return [o.view(np.float16) for o in outs]
+
+
+def spynet_prepare_f16(width, height, first_level, reference, support, source_flow, source_width,
+                       source_height):
+    """spynet_prepare_fp16 (MetalShader.swift:601-639): (features [8][h][w], base_flow [2][h][w])."""
+    keep = [_u16(a) for a in (reference, support)]
+    src = _u16(source_flow if source_flow is not None else np.zeros(2, np.float16))
+    plane = width * height
+    feat = np.empty(8 * plane, dtype=np.uint16)
+    base = np.empty(2 * plane, dtype=np.uint16)
+    load().oracle_spynet_prepare_f16(width, height, int(bool(first_level)), *[p for _, p in keep], src[1],
+                                     source_width, source_height, feat.ctypes.data_as(_h),
+                                     base.ctypes.data_as(_h))
+    return feat.view(np.float16), base.view(np.float16)
+
+
+def add_f16(base, residual):
+    """spynet_add_flow_fp16 (MetalShader.swift:641-649)."""
+    b, pb = _u16(base)
+    r, pr = _u16(residual)
+    out = np.empty(b.size, dtype=np.uint16)
+    load().oracle_add_f16(b.size, pb, pr, out.ctypes.data_as(_h))
+    return out.view(np.float16)
+
+
+def convk_f16(k, cin, cout, height, width, input, weight, bias, activation=0, slope=0.1):
+    keep = [_u16(a) for a in (input, weight, bias)]
+    out = np.empty(cout * height * width, dtype=np.uint16)
+    load().oracle_convk_f16(k, cin, cout, height, width, *[p for _, p in keep], int(activation), float(slope),
+                            out.ctypes.data_as(_h))
     return out.view(np.float16)

@@ -455,3 +455,155 @@ void oracle_conv3x3_f16(int cin, int cout, int height, int width, const uint16_t
         }
     }
 }
+
+/* ---- SPyNet flow estimation ---- */
+
+/* cubic_weight (MetalShader.swift:473-483), a = -0.75. */
+static float cubic_weight(float distance) {
+    const float a = -0.75f;
+    const float x = fabsf(distance);
+    if (x <= 1.0f) return (a + 2.0f) * x * x * x - (a + 3.0f) * x * x + 1.0f;
+    if (x < 2.0f) return a * x * x * x - 5.0f * a * x * x + 8.0f * a * x - 4.0f * a;
+    return 0.0f;
+}
+
+void oracle_bicubic_quarter_f16(int channels, int height, int width, const uint16_t* input,
+                                uint16_t* output) {
+    /* jasna_bicubic_downsample_quarter_fp16 (MetalShader.swift:488-521). */
+    const int oh = height / 4, ow = width / 4;
+    for (int c = 0; c < channels; ++c) {
+        for (int oy = 0; oy < oh; ++oy) {
+            for (int ox = 0; ox < ow; ++ox) {
+                const float sy = ((float)oy + 0.5f) * 4.0f - 0.5f;
+                const float sx = ((float)ox + 0.5f) * 4.0f - 0.5f;
+                const int by = (int)floorf(sy);
+                const int bx = (int)floorf(sx);
+                float value = 0.0f;
+                for (int yy = -1; yy <= 2; ++yy) {
+                    const float wy = cubic_weight(sy - (float)(by + yy));
+                    for (int xx = -1; xx <= 2; ++xx) {
+                        const float wx = cubic_weight(sx - (float)(bx + xx));
+                        const size_t src = ((size_t)c * height + (size_t)(by + yy)) * width + (size_t)(bx + xx);
+                        value += oracle_f16_to_f32(input[src]) * wy * wx;
+                    }
+                }
+                output[((size_t)c * oh + oy) * ow + ox] = oracle_f32_to_f16(value);
+            }
+        }
+    }
+}
+
+void oracle_spynet_pyramid_f16(int height, int width, int levels, const uint16_t* frame,
+                               uint16_t* const* out) {
+    /* spynet_build_pyramid_pair_fp16 (MetalShader.swift:523-570): direct box averages,
+     * ImageNet normalisation (:560-563). */
+    static const float mean[3] = {0.485f, 0.456f, 0.406f};
+    static const float stddev[3] = {0.229f, 0.224f, 0.225f};
+    for (int l = 0; l < levels; ++l) {
+        const int shift = levels - 1 - l;
+        const int lh = height >> shift, lw = width >> shift;
+        const int factor = 1 << shift;
+        const float inverse_area = 1.0f / (float)(factor * factor);
+        for (int c = 0; c < 3; ++c) {
+            for (int y = 0; y < lh; ++y) {
+                for (int x = 0; x < lw; ++x) {
+                    float sum = 0.0f;
+                    for (int yy = 0; yy < factor; ++yy)
+                        for (int xx = 0; xx < factor; ++xx)
+                            sum += oracle_f16_to_f32(
+                                frame[((size_t)c * height + (size_t)(y * factor + yy)) * width + x * factor + xx]);
+                    out[l][((size_t)c * lh + y) * lw + x] =
+                        oracle_f32_to_f16((sum * inverse_area - mean[c]) / stddev[c]);
+                }
+            }
+        }
+    }
+}
+
+float oracle_sample_border_f16(const uint16_t* values, size_t base, int height, int width,
+                               float y, float x) {
+    /* sample_border_fp16 (MetalShader.swift:572-599). */
+    y = fminf(fmaxf(y, 0.0f), (float)(height - 1));
+    x = fminf(fmaxf(x, 0.0f), (float)(width - 1));
+    const int y0 = (int)floorf(y);
+    const int x0 = (int)floorf(x);
+    const int y1 = y0 + 1 < height - 1 ? y0 + 1 : height - 1;
+    const int x1 = x0 + 1 < width - 1 ? x0 + 1 : width - 1;
+    const float ly = y - (float)y0;
+    const float lx = x - (float)x0;
+    const float v00 = oracle_f16_to_f32(values[base + (size_t)y0 * width + x0]);
+    const float v01 = oracle_f16_to_f32(values[base + (size_t)y0 * width + x1]);
+    const float v10 = oracle_f16_to_f32(values[base + (size_t)y1 * width + x0]);
+    const float v11 = oracle_f16_to_f32(values[base + (size_t)y1 * width + x1]);
+    return v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx + v10 * ly * (1.0f - lx) +
+           v11 * ly * lx;
+}
+
+void oracle_spynet_prepare_f16(int width, int height, int first_level, const uint16_t* reference,
+                               const uint16_t* support, const uint16_t* source_flow,
+                               int source_width, int source_height, uint16_t* features,
+                               uint16_t* base_flow) {
+    /* spynet_prepare_fp16 (MetalShader.swift:601-639). */
+    const size_t plane = (size_t)width * height;
+    const size_t source_plane = (size_t)source_width * source_height;
+    for (int y = 0; y < height; ++y) {
+        for (int x = 0; x < width; ++x) {
+            const size_t gid = (size_t)y * width + x;
+            float flow_x = 0.0f, flow_y = 0.0f;
+            if (!first_level) {
+                const float sx = width > 1 ? (float)x * (float)(source_width - 1) / (float)(width - 1) : 0.0f;
+                const float sy = height > 1 ? (float)y * (float)(source_height - 1) / (float)(height - 1) : 0.0f;
+                flow_x = 2.0f * oracle_sample_border_f16(source_flow, 0, source_height, source_width, sy, sx);
+                flow_y = 2.0f * oracle_sample_border_f16(source_flow, source_plane, source_height, source_width,
+                                                         sy, sx);
+            }
+            base_flow[gid] = oracle_f32_to_f16(flow_x);
+            base_flow[plane + gid] = oracle_f32_to_f16(flow_y);
+            for (int c = 0; c < 3; ++c) {
+                features[(size_t)c * plane + gid] = reference[(size_t)c * plane + gid];
+                const float warped = oracle_sample_border_f16(support, (size_t)c * plane, height, width,
+                                                              (float)y + flow_y, (float)x + flow_x);
+                features[(size_t)(c + 3) * plane + gid] = oracle_f32_to_f16(warped);
+            }
+            features[6 * plane + gid] = oracle_f32_to_f16(flow_x);
+            features[7 * plane + gid] = oracle_f32_to_f16(flow_y);
+        }
+    }
+}
+
+void oracle_add_f16(size_t count, const uint16_t* base, const uint16_t* residual, uint16_t* out) {
+    /* spynet_add_flow_fp16 (MetalShader.swift:641-649): a half + half add is the exact
+     * sum rounded once. */
+    for (size_t i = 0; i < count; ++i)
+        out[i] = oracle_f32_to_f16(oracle_f16_to_f32(base[i]) + oracle_f16_to_f32(residual[i]));
+}
+
+void oracle_convk_f16(int k, int cin, int cout, int height, int width, const uint16_t* input,
+                      const uint16_t* weight, const uint16_t* bias, int activation, float slope,
+                      uint16_t* output) {
+    const size_t plane = (size_t)width * height;
+    const int pad = k / 2;
+#pragma omp parallel for schedule(static)
+    for (int oc = 0; oc < cout; ++oc) {
+        for (int oy = 0; oy < height; ++oy) {
+            for (int ox = 0; ox < width; ++ox) {
+                float acc = oracle_f16_to_f32(bias[oc]);
+                for (int ic = 0; ic < cin; ++ic) {
+                    for (int ky = 0; ky < k; ++ky) {
+                        const int iy = oy + ky - pad;
+                        if (iy < 0 || iy >= height) continue;
+                        for (int kx = 0; kx < k; ++kx) {
+                            const int ix = ox + kx - pad;
+                            if (ix < 0 || ix >= width) continue;
+                            acc += oracle_f16_to_f32(input[(size_t)ic * plane + (size_t)iy * width + ix]) *
+                                   oracle_f16_to_f32(weight[(((size_t)oc * cin + ic) * k + ky) * k + kx]);
+                        }
+                    }
+                }
+                if (activation == 1 && acc < 0.0f) acc = acc * slope;
+                if (activation == 2 && acc < 0.0f) acc = 0.0f;
+                output[(size_t)oc * plane + (size_t)oy * width + ox] = oracle_f32_to_f16(acc);
+            }
+        }
+    }
+}

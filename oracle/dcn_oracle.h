@@ -109,6 +109,46 @@ void oracle_conv3x3_f16(int cin, int cout, int height, int width, const uint16_t
                         const uint16_t* weight, const uint16_t* bias, int activation,
                         float slope, const uint16_t* residual, uint16_t* output);
 
+/* ---- SPyNet flow estimation (the producer of the flows that feed the offsets) ---- */
+
+/* jasna_bicubic_downsample_quarter_fp16 (MetalShader.swift:488-521) with cubic_weight
+ * (:473-483, a = -0.75): out [c][h/4][w/4] = half(sum_{yy,xx in -1..2} in * wy * wx) at
+ * the half-pixel source position 4 o + 1.5; every 4x4 footprint is inside the image when
+ * h and w are multiples of 4 (torch interpolate(scale_factor=0.25, mode="bicubic")). */
+void oracle_bicubic_quarter_f16(int channels, int height, int width, const uint16_t* input,
+                                uint16_t* output);
+
+/* spynet_build_pyramid_pair_fp16 (MetalShader.swift:523-570) for one frame: level l of
+ * `levels` has size (h >> (levels - 1 - l)) x (w >> ...); each value is the direct box
+ * average of the RGB frame over the level's factor x factor footprint, normalised by the
+ * ImageNet mean/std and rounded once to FP16. out[l] = [3][h_l][w_l]. */
+void oracle_spynet_pyramid_f16(int height, int width, int levels, const uint16_t* frame,
+                               uint16_t* const* out);
+
+/* sample_border_fp16 (MetalShader.swift:572-599): bilinear sample of plane `base` with
+ * coordinates clamped into the image (grid_sample border padding, align_corners). */
+float oracle_sample_border_f16(const uint16_t* values, size_t base, int height, int width,
+                               float y, float x);
+
+/* spynet_prepare_fp16 (MetalShader.swift:601-639): base flow [2][h][w] = half(2 *
+ * align-corners upsample of source_flow [2][sh][sw]) (zero on the first level), and the
+ * 8-channel block input [reference (3), support warped by the FP32 base flow with border
+ * padding (3), base flow (2)]. */
+void oracle_spynet_prepare_f16(int width, int height, int first_level, const uint16_t* reference,
+                               const uint16_t* support, const uint16_t* source_flow,
+                               int source_width, int source_height, uint16_t* features,
+                               uint16_t* base_flow);
+
+/* spynet_add_flow_fp16 (MetalShader.swift:641-649): out = half(base + residual), FP16 add. */
+void oracle_add_f16(size_t count, const uint16_t* base, const uint16_t* residual, uint16_t* out);
+
+/* k x k convolution (odd k), stride 1, pad k/2, otherwise as oracle_conv3x3_f16: FP32
+ * accumulation in (ic, ky, kx) order from the bias, activation, output rounded to FP16.
+ * SPyNet's basic-module layers are 7 x 7. */
+void oracle_convk_f16(int k, int cin, int cout, int height, int width, const uint16_t* input,
+                      const uint16_t* weight, const uint16_t* bias, int activation, float slope,
+                      uint16_t* output);
+
 #ifdef __cplusplus
 }
 #endif
