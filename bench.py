@@ -167,7 +167,8 @@ def bench_body(args) -> int:
         "tflops": tflops,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None,
-                     "kernel": "whole body graph (conv3x3 x15, DCN, glue)", "flops_per_step": flops},
+                     "kernel": "whole body graph (temporal, 2 conv3x3, 6 conv pairs, offsets conv, DCN)",
+                     "flops_per_step": flops},
         "wall_ms_timed_region": wall_ms,
         "output_finite": bool(np.all(np.isfinite(out.astype(np.float32)))),
         "clip": clip_line,
@@ -176,6 +177,110 @@ def bench_body(args) -> int:
     ctx.close()
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_spynet(args) -> int:
+    """SPyNet flow of a frame pair, both directions, from two 256 x 256 RGB LQ tiles: the
+    quarter bicubic downsample of each tile, then the six-level network on the 64 x 64
+    copies, all in one hipGraph; a step is one replay (one bidirectional pair)."""
+    import numpy as np
+    import torch
+
+    from jasnamacos_amd import deform_conv as dc
+
+    d = dc.generate_spynet_inputs(seed=args.seed)
+    tile = d["tile"]
+    H = W = tile // 4
+    dev = lambda a: torch.from_numpy(np.array(a, np.float16).view(np.int16)).cuda()  # noqa: E731
+    ctx = dc.HipDeformConv(0)
+    spy = ctx.spynet(H, W, {k: dev(v) for k, v in d["weights"].items()})
+    lq = [dev(d["reference"]), dev(d["support"])]
+    small = [torch.zeros(3 * H * W, dtype=torch.int16, device="cuda") for _ in range(2)]
+    flow = torch.zeros(2 * 2 * H * W, dtype=torch.int16, device="cuda")
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        cur = torch.cuda.current_stream()
+        for i in range(2):
+            ctx.bicubic_quarter_f16_dev(3, tile, tile, lq[i], small[i], stream=cur)
+        spy.flow_dev(small[0], small[1], flow, both_directions=True, stream=cur)
+    for _ in range(max(args.warmup, 1)):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    step_ms = start.elapsed_time(end) / args.steps
+    out = flow.cpu().numpy().view(np.float16).astype(np.float32)
+    flops = 2 * dc.spynet_flops(H, W)
+    tflops = flops / (step_ms * 1e-3) / 1e12
+    del graph
+    spy.free()
+    cpu = None if args.no_cpu_baseline else cpu_baseline_spynet(d)
+    line = {
+        "metric": "SPyNet bidirectional flow pair us (two 256x256 RGB tiles -> bicubic 1/4 -> six-level net at 64x64)",
+        "value": round(step_ms * 1e3, 3),
+        "unit": "us/pair",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (numpy PCG64: sinusoid RGB tiles, He-normal random SPyNet weights)",
+        "config": {"workload": "SPyNet pair: 2 x bicubic quarter downsample + spynet(ref, sup) and "
+                               "spynet(sup, ref), 6 levels 2..64, one hipGraph", "height": H, "width": W},
+        "tflops": tflops,
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": tflops / MFMA_F16_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "whole pair graph (2 bicubic, pyramid, 6 x (prepare + 5 convk))",
+                     "flops_per_step": flops},
+        "wall_ms_timed_region": wall_ms,
+        "flow_abs_max": float(np.abs(out).max()),
+        "output_finite": bool(np.all(np.isfinite(out))),
+        "cpu_baseline": cpu,
+    }
+    ctx.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_spynet(d) -> dict:
+    """The same pair through the C oracle on the host: two bicubic downsamples, both
+    pyramids, both directions' six levels (7x7 convs on all host cores, OpenMP)."""
+    import os
+
+    import numpy as np
+
+    import oracle
+
+    oracle.load()
+    tile = d["tile"]
+    H = W = tile // 4
+    w = d["weights"]
+    t0 = time.perf_counter()
+    small = [oracle.bicubic_quarter_f16(3, tile, tile, d[k]) for k in ("reference", "support")]
+    pyr = [oracle.spynet_pyramid_f16(H, W, 6, s) for s in small]
+    for a, b in ((0, 1), (1, 0)):
+        flow, fh, fw = None, 1, 1
+        for level in range(6):
+            h, ww = H >> (5 - level), W >> (5 - level)
+            x, base = oracle.spynet_prepare_f16(ww, h, level == 0, pyr[a][level], pyr[b][level], flow, fw, fh)
+            for i, (ci, co) in enumerate([(8, 32), (32, 64), (64, 32), (32, 16), (16, 2)]):
+                x = oracle.convk_f16(7, ci, co, h, ww, x, w[f"w{level}_{i}"], w[f"b{level}_{i}"], 2 if i < 4 else 0)
+            flow, fh, fw = oracle.add_f16(base, x), h, ww
+    seconds = time.perf_counter() - t0
+    return {"value": seconds * 1e6, "unit": "us/pair", "cores": os.cpu_count() or 1, "kind": "port",
+            "sample": "one bidirectional pair (64x64, six levels) through the C oracle, "
+                      f"flow finite: {bool(np.all(np.isfinite(flow.astype(np.float32))))}"}
 
 
 def bench_clip(args, ctx, dc, clip, dev) -> dict:
@@ -266,6 +371,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=sorted(WORKLOADS))
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--spynet", action="store_true",
+                    help="measure the SPyNet flow pair (the producer of the body's flows) instead of a config")
     ap.add_argument("--kernel-reps", type=int, default=5, help="repetitions of the fused-only timing")
     ap.add_argument("--cold-calls", type=int, default=20,
                     help="single calls timed after flushing the caches with a 512 MB write (0: skip)")
@@ -288,6 +395,8 @@ def main() -> int:
     from jasnamacos_amd import deform_conv as dc
 
     torch.cuda.set_device(0)
+    if args.spynet:
+        return bench_spynet(args)
     if args.config == 4:
         return bench_body(args)
     d = dc.generate_config_inputs(args.config, args.seed)

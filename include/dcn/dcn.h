@@ -438,6 +438,11 @@ typedef struct dcn_spynet dcn_spynet;
 dcn_status dcn_spynet_create(dcn_context* ctx, int height, int width, const dcn_spynet_weights* weights,
                              void* stream, dcn_spynet** out);
 void dcn_spynet_destroy(dcn_spynet* spynet);
+/* spynet_build_pyramid_pair_fp16 (MetalShader.swift:523-570) for one RGB frame [3][h][w]:
+ * out = the DCN_SPYNET_LEVELS normalised levels [3][h >> (5 - l)][w >> (5 - l)],
+ * coarsest first, one after the other (the pyramid dcn_spynet_flow_dev builds inside). */
+dcn_status dcn_spynet_pyramid_f16_dev(dcn_context* ctx, int height, int width, const void* d_frame,
+                                      void* d_out, void* stream);
 /* reference, support: RGB [3][h][w] FP16 in [0, 1]. d_flow [1 + both][2][h][w] (x, y):
  * image 0 = spynet(reference, support), image 1 (both_directions) = spynet(support,
  * reference). Stream-ordered, no allocation, no memset: graph-capturable. */

@@ -163,6 +163,7 @@ SIGNATURES: dict[str, tuple] = {
     "dcn_spynet_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.POINTER(DcnSpynetWeights), c_void,
                                     C.POINTER(c_void)]),
     "dcn_spynet_destroy": (None, [c_void]),
+    "dcn_spynet_pyramid_f16_dev": (C.c_int, [CtxP, C.c_int, C.c_int, c_void, c_void, c_void]),
     "dcn_spynet_flow_dev": (C.c_int, [c_void, c_void, c_void, C.c_int, c_void, c_void]),
     "dcn_conv3x3_offsets_f16_dev": (C.c_int, [CtxP, c_void, c_void, c_void, c_void, c_void, c_void, c_void]),
     "dcn_conv3x3_pair_f16_dev": (C.c_int, [CtxP, c_void, c_void, c_void, C.c_int, C.c_int, C.c_float, c_void,

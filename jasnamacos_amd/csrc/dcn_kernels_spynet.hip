@@ -74,6 +74,7 @@ struct PyramidArgs {
     uint16_t* level[2][kSpynetMaxLevels];
     long offset[kSpynetMaxLevels + 1];  // first output index of each level (per frame)
     int frames, levels, H, W;
+    int aligned;  // frames 16-byte aligned and W a multiple of 8: rows of 8 pixels load as 16 bytes
 };
 
 __global__ __launch_bounds__(256) void spynet_pyramid_kernel(PyramidArgs a) {
@@ -96,8 +97,22 @@ __global__ __launch_bounds__(256) void spynet_pyramid_kernel(PyramidArgs a) {
     const float stddev = c == 0 ? 0.229f : (c == 1 ? 0.224f : 0.225f);
     float sum = 0.0f;
     const uint16_t* src = a.frame[f] + ((size_t)c * a.H + (size_t)y * factor) * a.W + (size_t)x * factor;
-    for (int yy = 0; yy < factor; ++yy)
-        for (int xx = 0; xx < factor; ++xx) sum += h2f(src[(size_t)yy * a.W + xx]);
+    if (a.aligned && factor >= 8) {
+        // Same row-major order of FP32 adds; the row segments come in 16-byte loads, several
+        // rows in flight (a coarse level sums up to (h / 2)^2 values per output).
+#pragma unroll 4
+        for (int yy = 0; yy < factor; ++yy) {
+            const uint16_t* row = src + (size_t)yy * a.W;
+            for (int xb = 0; xb < factor; xb += 8) {
+                const h8 v = __builtin_bit_cast(h8, *reinterpret_cast<const u32x4*>(row + xb));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sum += (float)v[j];
+            }
+        }
+    } else {
+        for (int yy = 0; yy < factor; ++yy)
+            for (int xx = 0; xx < factor; ++xx) sum += h2f(src[(size_t)yy * a.W + xx]);
+    }
     const float inverse_area = 1.0f / (float)(factor * factor);
     a.level[f][l][e] = f2h((sum * inverse_area - mean) / stddev);
 }
@@ -416,7 +431,9 @@ hipError_t launch_spynet_pyramid(const uint16_t* const* frames, int count, uint1
         off += 3L * (height >> shift) * (width >> shift);
     }
     a.offset[nlevels] = off;
+    a.aligned = width % 8 == 0;
     for (int f = 0; f < count; ++f) {
+        if (reinterpret_cast<uintptr_t>(frames[f]) % 16 != 0) a.aligned = 0;
         a.frame[f] = frames[f];
         for (int l = 0; l < nlevels; ++l) a.level[f][l] = levels[f][l];
     }

@@ -163,6 +163,27 @@ dcn_status dcn_spynet_flow_dev(dcn_spynet* s, const void* d_reference, const voi
     return DCN_OK;
 }
 
+dcn_status dcn_spynet_pyramid_f16_dev(dcn_context* ctx, int height, int width, const void* d_frame, void* d_out,
+                                      void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    constexpr int kCoarsest = 1 << (DCN_SPYNET_LEVELS - 1);
+    if (height < kCoarsest || width < kCoarsest || height % kCoarsest || width % kCoarsest || height > 4096 ||
+        width > 4096)
+        return fail(ctx, DCN_INVALID_SHAPE, "SPyNet needs a plane whose sides are multiples of 32");
+    if (!d_frame || !d_out) return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    DeviceGuard guard(ctx->device);
+    uint16_t* levels[1][dcn::kSpynetMaxLevels] = {};
+    size_t off = 0;
+    for (int l = 0; l < DCN_SPYNET_LEVELS; ++l) {
+        levels[0][l] = (uint16_t*)d_out + off;
+        off += (size_t)3 * (height >> (DCN_SPYNET_LEVELS - 1 - l)) * (width >> (DCN_SPYNET_LEVELS - 1 - l));
+    }
+    const uint16_t* frames[1] = {(const uint16_t*)d_frame};
+    DCN_HIP(ctx, dcn::launch_spynet_pyramid(frames, 1, levels, DCN_SPYNET_LEVELS, height, width,
+                                            (hipStream_t)stream));
+    return DCN_OK;
+}
+
 dcn_status dcn_bicubic_quarter_f16_dev(dcn_context* ctx, int channels, int height, int width,
                                        const void* d_in, void* d_out, void* stream) {
     if (!ctx) return DCN_INVALID_ARGUMENT;

@@ -484,6 +484,11 @@ class HipDeformConv:
         self._check(self._lib.dcn_bicubic_quarter_f16_dev(self.ctx, int(channels), int(height), int(width),
                                                           _ptr(src), _ptr(out), _stream(stream)))
 
+    def spynet_pyramid_f16_dev(self, height, width, frame, out, stream=None) -> None:
+        """The six normalised SPyNet levels of one RGB frame, coarsest first, concatenated."""
+        self._check(self._lib.dcn_spynet_pyramid_f16_dev(self.ctx, int(height), int(width), _ptr(frame), _ptr(out),
+                                                         _stream(stream)))
+
     def spynet(self, height, width, weights, stream=None) -> "SpyNet":
         """weights: device tensors "w{level}_{layer}" and "b{level}_{layer}" (OIHW FP16),
         level 0..5 coarsest first, layer 0..4 (8->32->64->32->16->2, 7x7)."""
@@ -912,6 +917,45 @@ def clip_flops(height: int, width: int, frames: int, blocks: int = 5) -> int:
     for b in range(4):
         backbone = sum(2 * plane * 9 * ci * co for ci, co in [(64 * (b + 2), 64)] + [(64, 64)] * (2 * blocks))
         total += backbone + (frames - 1) * body_flops(height, width, b, blocks)
+    return total
+
+
+SPYNET_LAYERS = [(8, 32), (32, 64), (64, 32), (32, 16), (16, 2)]
+
+
+def generate_spynet_inputs(tile: int = 256, seed: int = 6, flow_std: float = 0.04) -> dict:
+    """Synthetic SPyNet workload: two RGB LQ tiles [3][tile][tile] in [0, 1] (random
+    sinusoids, the second shifted by (1.5, -2.0) px) and random-init basic modules
+    (He-normal 7x7 weights for the ReLU layers, N(0, flow_std) for the flow layer, biases
+    N(0, 0.01); OIHW FP16 "w{level}_{layer}" / "b{level}_{layer}"), numpy PCG64."""
+    rng = np.random.default_rng(seed)
+    f16 = lambda a: np.asarray(a, np.float32).astype(np.float16)  # noqa: E731
+    w = {}
+    for level in range(_lib.SPYNET_LEVELS):
+        for i, (ci, co) in enumerate(SPYNET_LAYERS):
+            std = flow_std if i == len(SPYNET_LAYERS) - 1 else np.sqrt(2.0 / (ci * 49))
+            w[f"w{level}_{i}"] = f16(rng.normal(0, std, (co, ci, 7, 7)))
+            w[f"b{level}_{i}"] = f16(rng.normal(0, 0.01, co))
+    waves = [(rng.uniform(-0.08, 0.08, 2), rng.uniform(0.2, 1.0), rng.uniform(0, 2 * np.pi))
+             for _ in range(12)]
+
+    def frame(dy, dx):
+        y, x = np.meshgrid(np.arange(tile) + dy, np.arange(tile) + dx, indexing="ij")
+        out = np.empty((3, tile, tile))
+        for c in range(3):
+            acc = sum(a * np.sin(f[0] * y + f[1] * x + ph) for f, a, ph in waves[4 * c:4 * c + 4])
+            out[c] = 0.5 + 0.12 * acc
+        return f16(np.clip(out, 0, 1).ravel())
+
+    return {"tile": tile, "weights": w, "reference": frame(0.0, 0.0), "support": frame(1.5, -2.0)}
+
+
+def spynet_flops(height: int, width: int) -> int:
+    """GEMM-equivalent flops of one SPyNet direction (the 7x7 convs of six levels)."""
+    total = 0
+    for level in range(_lib.SPYNET_LEVELS):
+        plane = (height >> (_lib.SPYNET_LEVELS - 1 - level)) * (width >> (_lib.SPYNET_LEVELS - 1 - level))
+        total += sum(2 * plane * 49 * ci * co for ci, co in SPYNET_LAYERS)
     return total
 
 

@@ -1,7 +1,8 @@
 """GPU parity of SPyNet flow estimation against the CPU oracle chain.
 
 Bars:
-  * bicubic quarter downsample: bit-identical to the oracle (same FP32 expression order);
+  * bicubic quarter downsample and the pyramid: bit-identical to the oracle (same FP32
+    expression order);
   * the six-level flow: within 2e-2 * max(1, |flow|max) max and 1e-3 * max(1, |flow|max)
     mean of the oracle's FP16 chain (the conv sums are ordered differently and each of the
     30 layers rounds to FP16);
@@ -57,6 +58,19 @@ def test_bicubic_rejects_bad_sizes(gpu_ctx, dcn, torch):
     with pytest.raises(dcn.DeformConvError) as e:
         gpu_ctx.bicubic_quarter_f16_dev(1, 6, 8, buf, buf)
     assert e.value.status == dcn.INVALID_SHAPE
+
+
+@pytest.mark.parametrize("h,w,offset", [(64, 64, 0), (32, 96, 0), (64, 64, 3)])
+def test_pyramid_bit_exact(gpu_ctx, oracle, torch, h, w, offset):
+    """Both load paths (16-byte rows; scalar for a frame that is not 16-byte aligned)."""
+    frame = sr.smooth_frame(np.random.default_rng(h + offset), h, w)
+    log("case: pyramid", h, w, offset)
+    buf = dev(torch, np.concatenate([np.zeros(offset, np.float16), frame]))
+    want = np.concatenate(oracle.spynet_pyramid_f16(h, w, 6, frame))
+    out = torch.zeros(want.size, dtype=torch.int16, device="cuda")
+    gpu_ctx.spynet_pyramid_f16_dev(h, w, buf[offset:], out)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out).view(np.uint16), want.view(np.uint16))
 
 
 def _spynet(torch, gpu_ctx, h, w, seed):
