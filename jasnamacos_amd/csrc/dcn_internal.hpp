@@ -181,6 +181,13 @@ hipError_t launch_bicubic_quarter(const uint16_t* in, uint16_t* out, int channel
 hipError_t launch_spynet_pyramid(const uint16_t* const* frames, int count,
                                  uint16_t* (*levels)[kSpynetMaxLevels], int nlevels, int height,
                                  int width, hipStream_t stream);
+// The leading levels with at most 16 pixels per image in one launch (one workgroup per
+// image, activations in LDS); writes the last fused level's flow [b][2][h][w].
+size_t spynet_small_lds_bytes(int units);
+hipError_t launch_spynet_small(int batch, int levels, const int* heights, const int* widths,
+                               const uint16_t* const (*reference)[2], const uint16_t* const (*support)[2],
+                               const void* const (*wpk)[5], const float* const (*bias)[5],
+                               const uint32_t (*wpk_bytes)[5], uint16_t* flow_out, hipStream_t stream);
 hipError_t launch_spynet_prepare(int batch, const uint16_t* const* reference, const uint16_t* const* support,
                                  const uint16_t* source_flow, int source_height, int source_width,
                                  int first_level, uint16_t* features, int pad, uint16_t* base_flow,

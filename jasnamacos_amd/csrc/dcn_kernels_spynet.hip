@@ -73,33 +73,83 @@ struct PyramidArgs {
     const uint16_t* frame[2];
     uint16_t* level[2][kSpynetMaxLevels];
     long offset[kSpynetMaxLevels + 1];  // first output index of each level (per frame)
+    long coarse;  // outputs per frame (the first ones) summed by a whole wave
     int frames, levels, H, W;
     int aligned;  // frames 16-byte aligned and W a multiple of 8: rows of 8 pixels load as 16 bytes
 };
 
-__global__ __launch_bounds__(256) void spynet_pyramid_kernel(PyramidArgs a) {
-    const long per_frame = a.offset[a.levels];
-    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
-    if (gid >= per_frame * a.frames) return;
-    const int f = (int)(gid / per_frame);
-    const long r = gid - (long)f * per_frame;
-    int l = 0;
-    while (r >= a.offset[l + 1]) ++l;
-    const int shift = a.levels - 1 - l;
+constexpr int kPyramidWaveFactor = 16;  // levels with factor >= 16 (and <= 64): one wave per output
+constexpr int kPyramidMaxFactor = 64;
+
+// One output of the pyramid: level, channel and position of output r of a frame.
+struct PyramidOut {
+    int l, c, y, x, factor;
+    long e;
+};
+__device__ __forceinline__ PyramidOut pyramid_out(const PyramidArgs& a, long r) {
+    PyramidOut o;
+    o.l = 0;
+    while (r >= a.offset[o.l + 1]) ++o.l;
+    const int shift = a.levels - 1 - o.l;
     const int lh = a.H >> shift, lw = a.W >> shift;
-    const long e = r - a.offset[l];
-    const int c = (int)(e / ((long)lh * lw));
-    const int sp = (int)(e - (long)c * lh * lw);
-    const int y = sp / lw;
-    const int x = sp - y * lw;
-    const int factor = 1 << shift;
+    o.e = r - a.offset[o.l];
+    o.c = (int)(o.e / ((long)lh * lw));
+    const int sp = (int)(o.e - (long)o.c * lh * lw);
+    o.y = sp / lw;
+    o.x = sp - o.y * lw;
+    o.factor = 1 << shift;
+    return o;
+}
+
+__device__ __forceinline__ uint16_t pyramid_value(float sum, int c, int factor) {
     const float mean = c == 0 ? 0.485f : (c == 1 ? 0.456f : 0.406f);
     const float stddev = c == 0 ? 0.229f : (c == 1 ? 0.224f : 0.225f);
+    const float inverse_area = 1.0f / (float)(factor * factor);
+    return f2h((sum * inverse_area - mean) / stddev);
+}
+
+// 64-thread blocks. The first coarse * frames blocks each sum one coarse output: the wave
+// copies the factor x factor box into LDS with 16-byte loads, then one lane adds it in
+// the reference's row-major order (a coarse level sums up to 4,096 values per output).
+// The remaining blocks give one thread per output.
+__global__ __launch_bounds__(64) void spynet_pyramid_kernel(PyramidArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t box[kPyramidMaxFactor * kPyramidMaxFactor];
+    const long per_frame = a.offset[a.levels];
+    const int lane = threadIdx.x;
+    if ((long)blockIdx.x < a.coarse * a.frames) {
+        const int f = (int)(blockIdx.x / a.coarse);
+        const PyramidOut o = pyramid_out(a, (long)blockIdx.x - (long)f * a.coarse);
+        const int F = o.factor;
+        const uint16_t* src = a.frame[f] + ((size_t)o.c * a.H + (size_t)o.y * F) * a.W + (size_t)o.x * F;
+        const int row_chunks = F / 8;
+        for (int ch = lane; ch < F * row_chunks; ch += 64) {
+            const int yy = ch / row_chunks;
+            const int xb = (ch - yy * row_chunks) * 8;
+            *reinterpret_cast<u32x4*>(box + yy * F + xb) =
+                *reinterpret_cast<const u32x4*>(src + (size_t)yy * a.W + xb);
+        }
+        __syncthreads();
+        if (lane == 0) {
+            float sum = 0.0f;
+            for (int i = 0; i < F * F; i += 8) {
+                const h8 v = __builtin_bit_cast(h8, *reinterpret_cast<const u32x4*>(box + i));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sum += (float)v[j];
+            }
+            a.level[f][o.l][o.e] = pyramid_value(sum, o.c, F);
+        }
+        return;
+    }
+    const long fine = per_frame - a.coarse;
+    const long gid = ((long)blockIdx.x - a.coarse * a.frames) * 64 + lane;
+    if (gid >= fine * a.frames) return;
+    const int f = (int)(gid / fine);
+    const PyramidOut o = pyramid_out(a, a.coarse + (gid - (long)f * fine));
+    const int factor = o.factor;
     float sum = 0.0f;
-    const uint16_t* src = a.frame[f] + ((size_t)c * a.H + (size_t)y * factor) * a.W + (size_t)x * factor;
+    const uint16_t* src = a.frame[f] + ((size_t)o.c * a.H + (size_t)o.y * factor) * a.W + (size_t)o.x * factor;
     if (a.aligned && factor >= 8) {
-        // Same row-major order of FP32 adds; the row segments come in 16-byte loads, several
-        // rows in flight (a coarse level sums up to (h / 2)^2 values per output).
+        // Same row-major order of FP32 adds; the row segments come in 16-byte loads.
 #pragma unroll 4
         for (int yy = 0; yy < factor; ++yy) {
             const uint16_t* row = src + (size_t)yy * a.W;
@@ -113,8 +163,7 @@ __global__ __launch_bounds__(256) void spynet_pyramid_kernel(PyramidArgs a) {
         for (int yy = 0; yy < factor; ++yy)
             for (int xx = 0; xx < factor; ++xx) sum += h2f(src[(size_t)yy * a.W + xx]);
     }
-    const float inverse_area = 1.0f / (float)(factor * factor);
-    a.level[f][l][e] = f2h((sum * inverse_area - mean) / stddev);
+    a.level[f][o.l][o.e] = pyramid_value(sum, o.c, factor);
 }
 
 // sample_border_fp16 (MetalShader.swift:572-599).
@@ -302,6 +351,166 @@ __global__ __launch_bounds__(64 * NW) void convk_kernel(ConvKArgs a) {
     }
 }
 
+// The small levels of SPyNet (at most kSmallMaxPx pixels per image) in one launch: one
+// workgroup per image runs prepare + the five 7x7 convs + the flow add of every such
+// level back to back, the activations held in LDS as CB8 tiles with a 3-pixel zero border
+// (the per-layer launches cost 2.3-6 us each on these 4..16-pixel maps, mostly launch and
+// latency). Each conv is an implicit GEMM on v_mfma_f32_16x16x32_f16: one 16-pixel row
+// tile, every 16-channel column block, the K range split over the NW waves (each wave
+// streams only its slice of the weights), partial sums added in wave order in LDS.
+constexpr int kSmallMaxPx = 16;
+constexpr int kSmallMaxNb = 4;
+constexpr int kSmallLayerIn[5] = {8, 32, 64, 32, 16};
+constexpr int kSmallLayerOut[5] = {32, 64, 32, 16, 2};
+
+struct SmallLevel {
+    const uint16_t* ref[2];
+    const uint16_t* sup[2];
+    const void* wpk[5];
+    const float* bias[5];
+    uint32_t wpk_bytes[5];
+    int h, w;
+};
+
+struct SmallArgs {
+    SmallLevel level[kSpynetMaxLevels];
+    uint16_t* flow_out;  // [b][2][h][w] of the last fused level
+    int levels, units;   // fused levels; LDS units per activation block
+};
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void spynet_small_kernel(SmallArgs a) {
+    constexpr int U = 8;  // K-steps of loads in flight
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int units = a.units;
+    u32x4* tiles = reinterpret_cast<u32x4*>(lds);  // [2][8 blocks][units]
+    f32x4* red = reinterpret_cast<f32x4*>(lds + (size_t)2 * 8 * units * 16);  // [NW][kSmallMaxNb][64]
+    uint16_t* fprev = reinterpret_cast<uint16_t*>(red + NW * kSmallMaxNb * 64);  // [2][kSmallMaxPx]
+    uint16_t* fbase = fprev + 2 * kSmallMaxPx;                                     // [2][kSmallMaxPx]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int quarter = lane >> 4;
+    const int b = blockIdx.x;
+
+    for (int l = 0; l < a.levels; ++l) {
+        const SmallLevel& L = a.level[l];
+        const int h = L.h, w = L.w, npx = h * w, hp = h + 6, wp = w + 6;
+        // This level's tile geometry: every border unit must read zero.
+        for (int i = tid; i < 2 * 8 * units; i += 64 * NW) tiles[i] = u32x4{0u, 0u, 0u, 0u};
+        __syncthreads();
+        // spynet_prepare_fp16 (MetalShader.swift:601-639) for this image's pixels.
+        if (tid < npx) {
+            const int y = tid / w;
+            const int x = tid - y * w;
+            float flow_x = 0.0f, flow_y = 0.0f;
+            if (l > 0) {
+                const int sh = a.level[l - 1].h, sw = a.level[l - 1].w;
+                const float sx = w > 1 ? (float)x * (float)(sw - 1) / (float)(w - 1) : 0.0f;
+                const float sy = h > 1 ? (float)y * (float)(sh - 1) / (float)(h - 1) : 0.0f;
+                flow_x = 2.0f * sample_border(fprev, sh, sw, sy, sx);
+                flow_y = 2.0f * sample_border(fprev + kSmallMaxPx, sh, sw, sy, sx);
+            }
+            fbase[tid] = f2h(flow_x);
+            fbase[kSmallMaxPx + tid] = f2h(flow_y);
+            uint16_t v[8];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                v[c] = L.ref[b][c * npx + tid];
+                v[c + 3] = f2h(sample_border(L.sup[b] + c * npx, h, w, (float)y + flow_y, (float)x + flow_x));
+            }
+            v[6] = f2h(flow_x);
+            v[7] = f2h(flow_y);
+            u32x4 unit;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) unit[i] = (uint32_t)v[2 * i] | ((uint32_t)v[2 * i + 1] << 16);
+            tiles[(y + 3) * wp + x + 3] = unit;
+        }
+        __syncthreads();
+
+        // A rows: pixel lane % 16 of the single row tile (the tail repeats the last pixel).
+        const int p = min(lane & 15, npx - 1);
+        const int py = p / w;
+        const int px = p - py * w;
+        int cur = 0;
+        for (int li = 0; li < 5; ++li) {
+            const int CB = kSmallLayerIn[li] / 8;
+            const int cout = kSmallLayerOut[li];
+            const int KB = 49 * CB;
+            const int ksteps = (KB + 3) / 4;
+            const int nnb = (cout + 15) / 16;  // = the packed layout's column blocks
+            const u32x4* in = tiles + (size_t)cur * 8 * units;
+            const __amdgpu_buffer_rsrc_t wr = make_rsrc(L.wpk[li], L.wpk_bytes[li]);
+            f32x4 acc[kSmallMaxNb];
+#pragma unroll
+            for (int nb = 0; nb < kSmallMaxNb; ++nb) acc[nb] = f32x4{};
+            const int s0 = wave * ksteps / NW;
+            const int s1 = (wave + 1) * ksteps / NW;
+            for (int sb = s0; sb < s1; sb += U) {
+                h8 Bf[U][kSmallMaxNb];
+                u32x4 q[U];
+#pragma unroll
+                for (int i = 0; i < U; ++i) {
+                    const int s = sb + i < s1 ? sb + i : s1 - 1;
+#pragma unroll
+                    for (int nb = 0; nb < kSmallMaxNb; ++nb)
+                        if (nb < nnb)
+                            Bf[i][nb] = __builtin_bit_cast(
+                                h8, load16(wr, (uint32_t)((s * nnb + nb) * 64 + lane) * 16u));
+                    const int kb = min(4 * s + quarter, KB - 1);
+                    const int tap = kb / CB;
+                    const int cb = kb - tap * CB;
+                    const int ky = tap / 7;
+                    const int kx = tap - ky * 7;
+                    q[i] = in[(cb * hp + py + ky) * wp + px + kx];
+                }
+#pragma unroll
+                for (int i = 0; i < U; ++i) {
+                    if (sb + i < s1) {  // uniform across the wave
+                        const u32x4 z = {0u, 0u, 0u, 0u};
+                        const h8 A = __builtin_bit_cast(h8, 4 * (sb + i) + quarter < KB ? q[i] : z);
+#pragma unroll
+                        for (int nb = 0; nb < kSmallMaxNb; ++nb)
+                            if (nb < nnb)
+                                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int nb = 0; nb < kSmallMaxNb; ++nb) red[(wave * kSmallMaxNb + nb) * 64 + lane] = acc[nb];
+            __syncthreads();
+            const float* redf = reinterpret_cast<const float*>(red);
+            uint16_t* outh = reinterpret_cast<uint16_t*>(tiles + (size_t)(cur ^ 1) * 8 * units);
+            for (int e = tid; e < nnb * 256; e += 64 * NW) {
+                const int nb = e >> 8;
+                const int r = (e >> 4) & 15;
+                const int c = e & 15;
+                const int oc = nb * 16 + c;
+                if (r >= npx || oc >= cout) continue;
+                const int src = ((r >> 2) << 4) + c;
+                float sum = 0.0f;
+#pragma unroll
+                for (int k = 0; k < NW; ++k) sum += redf[((k * kSmallMaxNb + nb) * 64 + src) * 4 + (r & 3)];
+                float v = sum + L.bias[li][oc];
+                if (li < 4) {
+                    if (v < 0.0f) v = 0.0f;
+                    const int ry = r / w;
+                    const int rx = r - ry * w;
+                    outh[((size_t)((oc >> 3) * hp + ry + 3) * wp + rx + 3) * 8 + (oc & 7)] = f2h(v);
+                } else {
+                    // spynet_add_flow_fp16: flow = half(base + half(residual)).
+                    fprev[oc * kSmallMaxPx + r] = f2h(h2f(fbase[oc * kSmallMaxPx + r]) + (float)round_f16(v));
+                }
+            }
+            __syncthreads();
+            cur ^= 1;
+        }
+    }
+    const int npx = a.level[a.levels - 1].h * a.level[a.levels - 1].w;
+    for (int t = tid; t < 2 * npx; t += 64 * NW)
+        a.flow_out[(size_t)b * 2 * npx + t] = fprev[(t / npx) * kSmallMaxPx + t % npx];
+}
+
 // OIHW [Cout][Cin][KS][KS] -> [ksteps][NBT][64][8]: lane l of K-step s holds output channel
 // nb * 16 + l % 16 and K-block 4 s + l / 16 = tap * CB + cb (zero past Cin, Cout, KB).
 __global__ __launch_bounds__(256) void convk_prepack_kernel(const uint16_t* __restrict__ w,
@@ -437,7 +646,17 @@ hipError_t launch_spynet_pyramid(const uint16_t* const* frames, int count, uint1
         a.frame[f] = frames[f];
         for (int l = 0; l < nlevels; ++l) a.level[f][l] = levels[f][l];
     }
-    hipLaunchKernelGGL(spynet_pyramid_kernel, dim3(blocks_for(off * count)), dim3(256), 0, stream, a);
+    // Coarse levels come first; those whose factor is in [16, 64] get a wave per output.
+    a.coarse = 0;
+    if (a.aligned)
+        for (int l = 0; l < nlevels; ++l) {
+            const int factor = 1 << (nlevels - 1 - l);
+            if (factor >= kPyramidWaveFactor && factor <= kPyramidMaxFactor) a.coarse = a.offset[l + 1];
+        }
+    for (int l = 0; l < nlevels && a.coarse > 0; ++l)  // the wave path must start at level 0
+        if ((1 << (nlevels - 1 - l)) > kPyramidMaxFactor) a.coarse = 0;
+    const long blocks = a.coarse * count + ((off - a.coarse) * count + 63) / 64;
+    hipLaunchKernelGGL(spynet_pyramid_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, a);
     return hipGetLastError();
 }
 
@@ -463,6 +682,47 @@ hipError_t launch_spynet_prepare(int batch, const uint16_t* const* reference, co
     a.pad = pad;
     hipLaunchKernelGGL(spynet_prepare_kernel, dim3(blocks_for((long)batch * height * width)), dim3(256), 0,
                        stream, a);
+    return hipGetLastError();
+}
+
+size_t spynet_small_lds_bytes(int units) {
+    return (size_t)2 * 8 * units * 16 + (size_t)8 * kSmallMaxNb * 64 * 16 + (size_t)4 * kSmallMaxPx * 2;
+}
+
+hipError_t launch_spynet_small(int batch, int levels, const int* heights, const int* widths,
+                               const uint16_t* const (*reference)[2], const uint16_t* const (*support)[2],
+                               const void* const (*wpk)[5], const float* const (*bias)[5],
+                               const uint32_t (*wpk_bytes)[5], uint16_t* flow_out, hipStream_t stream) {
+    if (batch < 1 || batch > 2 || levels < 1 || levels > kSpynetMaxLevels) return hipErrorInvalidValue;
+    constexpr int NW = 8;
+    SmallArgs a{};
+    a.levels = levels;
+    a.flow_out = flow_out;
+    int units = 0;
+    for (int l = 0; l < levels; ++l) {
+        if (heights[l] * widths[l] > kSmallMaxPx) return hipErrorInvalidValue;
+        SmallLevel& L = a.level[l];
+        L.h = heights[l];
+        L.w = widths[l];
+        for (int b = 0; b < 2; ++b) {
+            L.ref[b] = reference[l][b];
+            L.sup[b] = support[l][b];
+        }
+        for (int i = 0; i < 5; ++i) {
+            L.wpk[i] = wpk[l][i];
+            L.bias[i] = bias[l][i];
+            L.wpk_bytes[i] = wpk_bytes[l][i];
+        }
+        units = std::max(units, (L.h + 6) * (L.w + 6));
+    }
+    a.units = units;
+    const size_t lds = spynet_small_lds_bytes(units);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
+    auto kernel = &spynet_small_kernel<NW>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)batch), dim3(64 * NW), lds, stream, a);
     return hipGetLastError();
 }
 

@@ -140,7 +140,36 @@ dcn_status dcn_spynet_flow_dev(dcn_spynet* s, const void* d_reference, const voi
     // Both frames' pyramids (spynet_build_pyramid_pair_fp16), one launch.
     const uint16_t* frames[2] = {(const uint16_t*)d_reference, (const uint16_t*)d_support};
     DCN_HIP(ctx, dcn::launch_spynet_pyramid(frames, 2, s->pyramid, DCN_SPYNET_LEVELS, s->h, s->w, st));
-    for (int l = 0; l < DCN_SPYNET_LEVELS; ++l) {
+    // The leading levels of at most 16 pixels run in one launch, their activations in LDS.
+    int fused = 0, units = 0;
+    while (fused < DCN_SPYNET_LEVELS - 1 && level_h(s, fused) * level_w(s, fused) <= 16) {
+        const int u = std::max(units, (level_h(s, fused) + 6) * (level_w(s, fused) + 6));
+        if (dcn::spynet_small_lds_bytes(u) > 160 * 1024) break;
+        units = u;
+        ++fused;
+    }
+    if (fused > 0) {
+        int hs[DCN_SPYNET_LEVELS], ws[DCN_SPYNET_LEVELS];
+        const uint16_t* refs[DCN_SPYNET_LEVELS][2];
+        const uint16_t* sups[DCN_SPYNET_LEVELS][2];
+        const void* wpk[DCN_SPYNET_LEVELS][DCN_SPYNET_LAYERS];
+        const float* bias[DCN_SPYNET_LEVELS][DCN_SPYNET_LAYERS];
+        uint32_t wbytes[DCN_SPYNET_LEVELS][DCN_SPYNET_LAYERS];
+        for (int l = 0; l < fused; ++l) {
+            hs[l] = level_h(s, l);
+            ws[l] = level_w(s, l);
+            refs[l][0] = sups[l][1] = s->pyramid[0][l];
+            refs[l][1] = sups[l][0] = s->pyramid[1][l];
+            for (int i = 0; i < DCN_SPYNET_LAYERS; ++i) {
+                wpk[l][i] = s->layer[l][i].wpk;
+                bias[l][i] = s->layer[l][i].bias;
+                wbytes[l][i] = (uint32_t)dcn::convk_packed_bytes(s->layer[l][i].g);
+            }
+        }
+        DCN_HIP(ctx, dcn::launch_spynet_small(batch, fused, hs, ws, refs, sups, wpk, bias, wbytes,
+                                              s->flow[fused - 1], st));
+    }
+    for (int l = fused; l < DCN_SPYNET_LEVELS; ++l) {
         const int lh = level_h(s, l), lw = level_w(s, l);
         // Image 0 estimates spynet(reference, support); image 1 the reverse direction.
         const uint16_t* refs[2] = {s->pyramid[0][l], s->pyramid[1][l]};
