@@ -222,6 +222,7 @@ def bench_spynet(args) -> int:
     tflops = flops / (step_ms * 1e-3) / 1e12
     del graph
     spy.free()
+    clip_line = bench_spynet_clip(args, ctx, dc, d, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_spynet(d)
     line = {
         "metric": "SPyNet bidirectional flow pair us (two 256x256 RGB tiles -> bicubic 1/4 -> six-level net at 64x64)",
@@ -246,11 +247,58 @@ def bench_spynet(args) -> int:
         "wall_ms_timed_region": wall_ms,
         "flow_abs_max": float(np.abs(out).max()),
         "output_finite": bool(np.all(np.isfinite(out))),
+        "clip": clip_line,
         "cpu_baseline": cpu,
     }
     ctx.close()
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_spynet_clip(args, ctx, dc, d, dev, frames: int = 30) -> dict:
+    """All flows of a 30-frame clip (both directions of the 29 adjacent pairs) from 256 x 256
+    tiles: one bicubic launch over every frame, then dcn_spynet_clip_flows_dev, which runs
+    each level once over the batch of 58 images; one hipGraph, a step is one clip."""
+    import numpy as np
+    import torch
+
+    tile = d["tile"]
+    H = W = tile // 4
+    rng = np.random.default_rng(args.seed + 1)
+    shifts = np.cumsum(rng.uniform(-2, 2, (frames, 2)), axis=0)
+    lq = [dc.generate_spynet_inputs(tile, seed=args.seed)["reference"]]
+    base = np.asarray(lq[0], np.float16).reshape(3, tile, tile)
+    for t in range(1, frames):  # the first tile moved by a random walk of whole pixels
+        lq.append(np.roll(base, (int(round(shifts[t, 0])), int(round(shifts[t, 1]))), axis=(1, 2)).ravel())
+    spy = ctx.spynet(H, W, {k: dev(v) for k, v in d["weights"].items()}, max_frames=frames)
+    lq_t = dev(np.concatenate(lq))
+    small = torch.zeros(frames * 3 * H * W, dtype=torch.int16, device="cuda")
+    flows = torch.zeros(2 * (frames - 1) * 2 * H * W, dtype=torch.int16, device="cuda")
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        cur = torch.cuda.current_stream()
+        ctx.bicubic_quarter_f16_dev(3 * frames, tile, tile, lq_t, small, stream=cur)
+        spy.clip_flows_dev(small, frames, flows, stream=cur)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = 10
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    clip_ms = start.elapsed_time(end) / reps
+    out = flows.cpu().numpy().view(np.float16).astype(np.float32)
+    flops = 2 * (frames - 1) * dc.spynet_flops(H, W)
+    del graph
+    spy.free()
+    return {"workload": f"{frames} frames: bicubic 1/4 of every tile + both directions of the {frames - 1} pairs",
+            "ms_per_clip": clip_ms, "pairs": frames - 1, "us_per_pair": clip_ms * 1e3 / (frames - 1),
+            "tflops": flops / (clip_ms * 1e-3) / 1e12, "replays_timed": reps,
+            "output_finite": bool(np.all(np.isfinite(out)))}
 
 
 def cpu_baseline_spynet(d) -> dict:

@@ -434,9 +434,10 @@ typedef struct dcn_spynet_weights {
     const void* bias[DCN_SPYNET_LEVELS][DCN_SPYNET_LAYERS];
 } dcn_spynet_weights;
 typedef struct dcn_spynet dcn_spynet;
-/* height and width multiples of 32 (the reference's 64 x 64). */
-dcn_status dcn_spynet_create(dcn_context* ctx, int height, int width, const dcn_spynet_weights* weights,
-                             void* stream, dcn_spynet** out);
+/* height and width multiples of 32 (the reference's 64 x 64); max_frames (>= 2) sizes the
+ * clip entry point (2 for pairs only). */
+dcn_status dcn_spynet_create(dcn_context* ctx, int height, int width, int max_frames,
+                             const dcn_spynet_weights* weights, void* stream, dcn_spynet** out);
 void dcn_spynet_destroy(dcn_spynet* spynet);
 /* spynet_build_pyramid_pair_fp16 (MetalShader.swift:523-570) for one RGB frame [3][h][w]:
  * out = the DCN_SPYNET_LEVELS normalised levels [3][h >> (5 - l)][w >> (5 - l)],
@@ -448,6 +449,13 @@ dcn_status dcn_spynet_pyramid_f16_dev(dcn_context* ctx, int height, int width, c
  * reference). Stream-ordered, no allocation, no memset: graph-capturable. */
 dcn_status dcn_spynet_flow_dev(dcn_spynet* spynet, const void* d_reference, const void* d_support,
                                int both_directions, void* d_flow, void* stream);
+/* All flows of a clip in one pass (FusedSPyNetClipGraph.swift:29-315, compute_flow):
+ * d_frames [frames][3][h][w] (the 64 x 64 copies), d_flows [2][frames - 1][2][h][w]:
+ * [0][t] = spynet(frame t, frame t + 1) (the backward flows), [1][t] = spynet(frame t + 1,
+ * frame t) (the forward flows), as dcn_clip_run_dev takes them. Every level runs once over
+ * the batch of 2 (frames - 1) images. frames <= max_frames. */
+dcn_status dcn_spynet_clip_flows_dev(dcn_spynet* spynet, const void* d_frames, int frames, void* d_flows,
+                                     void* stream);
 
 /* One propagation body: conv_offset (196->64->64->64->432, LeakyReLU 0.1 between), the
  * offset transform, the 128->64 DCN (16 deformable groups, 3x3), the backbone

@@ -160,8 +160,9 @@ SIGNATURES: dict[str, tuple] = {
     "dcn_conv3x3_f16_dev": (C.c_int, [CtxP, c_void, c_void, C.c_int, C.c_float, c_void, C.c_int, c_void,
                                       C.c_int, c_void, C.c_int, c_void]),
     "dcn_bicubic_quarter_f16_dev": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, c_void, c_void, c_void]),
-    "dcn_spynet_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.POINTER(DcnSpynetWeights), c_void,
+    "dcn_spynet_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.POINTER(DcnSpynetWeights), c_void,
                                     C.POINTER(c_void)]),
+    "dcn_spynet_clip_flows_dev": (C.c_int, [c_void, c_void, C.c_int, c_void, c_void]),
     "dcn_spynet_destroy": (None, [c_void]),
     "dcn_spynet_pyramid_f16_dev": (C.c_int, [CtxP, C.c_int, C.c_int, c_void, c_void, c_void]),
     "dcn_spynet_flow_dev": (C.c_int, [c_void, c_void, c_void, C.c_int, c_void, c_void]),

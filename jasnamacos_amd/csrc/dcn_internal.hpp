@@ -177,21 +177,22 @@ hipError_t launch_convk(const ConvKGeometry& g, int batch, int pad, const void* 
                         hipStream_t stream);
 hipError_t launch_bicubic_quarter(const uint16_t* in, uint16_t* out, int channels, int height, int width,
                                   hipStream_t stream);
-// Pyramids of `count` (1, 2) RGB frames: levels[f][l] = [3][h >> (n-1-l)][w >> (n-1-l)].
-hipError_t launch_spynet_pyramid(const uint16_t* const* frames, int count,
-                                 uint16_t* (*levels)[kSpynetMaxLevels], int nlevels, int height,
-                                 int width, hipStream_t stream);
+// Pyramids of `count` RGB frames (frame 0, frame 1, frame f >= 2 at frame0 + f * stride):
+// level l of frame f at levels[l] + f * 3 * h_l * w_l, h_l = h >> (n - 1 - l).
+hipError_t launch_spynet_pyramid(const uint16_t* frame0, const uint16_t* frame1, long frame_stride, int count,
+                                 uint16_t* const* levels, int nlevels, int height, int width, hipStream_t stream);
+// Images b < batch over `pairs` frame pairs: b < pairs is spynet(frame b, frame b + 1), the
+// rest the reverse direction of pair b - pairs.
+hipError_t launch_spynet_prepare(int batch, int pairs, const uint16_t* pyramid_level, const uint16_t* source_flow,
+                                 int source_height, int source_width, int first_level, uint16_t* features, int pad,
+                                 uint16_t* base_flow, int height, int width, hipStream_t stream);
 // The leading levels with at most 16 pixels per image in one launch (one workgroup per
 // image, activations in LDS); writes the last fused level's flow [b][2][h][w].
 size_t spynet_small_lds_bytes(int units);
-hipError_t launch_spynet_small(int batch, int levels, const int* heights, const int* widths,
-                               const uint16_t* const (*reference)[2], const uint16_t* const (*support)[2],
-                               const void* const (*wpk)[5], const float* const (*bias)[5],
-                               const uint32_t (*wpk_bytes)[5], uint16_t* flow_out, hipStream_t stream);
-hipError_t launch_spynet_prepare(int batch, const uint16_t* const* reference, const uint16_t* const* support,
-                                 const uint16_t* source_flow, int source_height, int source_width,
-                                 int first_level, uint16_t* features, int pad, uint16_t* base_flow,
-                                 int height, int width, hipStream_t stream);
+hipError_t launch_spynet_small(int batch, int pairs, int levels, const int* heights, const int* widths,
+                               const uint16_t* const* pyramid, const void* const (*wpk)[5],
+                               const float* const (*bias)[5], const uint32_t (*wpk_bytes)[5], uint16_t* flow_out,
+                               hipStream_t stream);
 
 // The last conv_offset layer (cout 432) with prepare_dcn_offsets_fp16 in its epilogue:
 // raw = half(conv + bias), offsets = half(10 tanh(raw) + flow), masks = half(sigmoid(raw)).

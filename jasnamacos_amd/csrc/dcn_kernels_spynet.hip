@@ -70,8 +70,9 @@ __global__ __launch_bounds__(256) void bicubic_quarter_kernel(const uint16_t* __
 // frame f is the direct box average over factor x factor pixels, normalised with the
 // ImageNet mean/std (:560-563). One thread per output value of every level and frame.
 struct PyramidArgs {
-    const uint16_t* frame[2];
-    uint16_t* level[2][kSpynetMaxLevels];
+    const uint16_t* frame[2];  // frames 0 and 1; frame f >= 2 at frame[0] + f * frame_stride
+    long frame_stride;
+    uint16_t* level[kSpynetMaxLevels];  // level l of frame f at level[l] + f * 3 * h_l * w_l
     long offset[kSpynetMaxLevels + 1];  // first output index of each level (per frame)
     long coarse;  // outputs per frame (the first ones) summed by a whole wave
     int frames, levels, H, W;
@@ -101,6 +102,13 @@ __device__ __forceinline__ PyramidOut pyramid_out(const PyramidArgs& a, long r) 
     return o;
 }
 
+__device__ __forceinline__ const uint16_t* pyramid_frame(const PyramidArgs& a, int f) {
+    return f < 2 ? a.frame[f] : a.frame[0] + (size_t)f * a.frame_stride;
+}
+__device__ __forceinline__ uint16_t* pyramid_dst(const PyramidArgs& a, int f, const PyramidOut& o) {
+    return a.level[o.l] + (size_t)f * (a.offset[o.l + 1] - a.offset[o.l]) + o.e;
+}
+
 __device__ __forceinline__ uint16_t pyramid_value(float sum, int c, int factor) {
     const float mean = c == 0 ? 0.485f : (c == 1 ? 0.456f : 0.406f);
     const float stddev = c == 0 ? 0.229f : (c == 1 ? 0.224f : 0.225f);
@@ -120,7 +128,7 @@ __global__ __launch_bounds__(64) void spynet_pyramid_kernel(PyramidArgs a) {
         const int f = (int)(blockIdx.x / a.coarse);
         const PyramidOut o = pyramid_out(a, (long)blockIdx.x - (long)f * a.coarse);
         const int F = o.factor;
-        const uint16_t* src = a.frame[f] + ((size_t)o.c * a.H + (size_t)o.y * F) * a.W + (size_t)o.x * F;
+        const uint16_t* src = pyramid_frame(a, f) + ((size_t)o.c * a.H + (size_t)o.y * F) * a.W + (size_t)o.x * F;
         const int row_chunks = F / 8;
         for (int ch = lane; ch < F * row_chunks; ch += 64) {
             const int yy = ch / row_chunks;
@@ -136,7 +144,7 @@ __global__ __launch_bounds__(64) void spynet_pyramid_kernel(PyramidArgs a) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) sum += (float)v[j];
             }
-            a.level[f][o.l][o.e] = pyramid_value(sum, o.c, F);
+            *pyramid_dst(a, f, o) = pyramid_value(sum, o.c, F);
         }
         return;
     }
@@ -147,7 +155,7 @@ __global__ __launch_bounds__(64) void spynet_pyramid_kernel(PyramidArgs a) {
     const PyramidOut o = pyramid_out(a, a.coarse + (gid - (long)f * fine));
     const int factor = o.factor;
     float sum = 0.0f;
-    const uint16_t* src = a.frame[f] + ((size_t)o.c * a.H + (size_t)o.y * factor) * a.W + (size_t)o.x * factor;
+    const uint16_t* src = pyramid_frame(a, f) + ((size_t)o.c * a.H + (size_t)o.y * factor) * a.W + (size_t)o.x * factor;
     if (a.aligned && factor >= 8) {
         // Same row-major order of FP32 adds; the row segments come in 16-byte loads.
 #pragma unroll 4
@@ -163,7 +171,7 @@ __global__ __launch_bounds__(64) void spynet_pyramid_kernel(PyramidArgs a) {
         for (int yy = 0; yy < factor; ++yy)
             for (int xx = 0; xx < factor; ++xx) sum += h2f(src[(size_t)yy * a.W + xx]);
     }
-    a.level[f][o.l][o.e] = pyramid_value(sum, o.c, factor);
+    *pyramid_dst(a, f, o) = pyramid_value(sum, o.c, factor);
 }
 
 // sample_border_fp16 (MetalShader.swift:572-599).
@@ -188,9 +196,17 @@ __device__ __forceinline__ float sample_border(const uint16_t* plane, int H, int
 // pairs: base flow [b][2][H][W] = half(2 * align-corners upsample of the previous level's
 // flow) (zero on the first level) and the 8-channel block input written as one 16-byte
 // CB8 unit per pixel ([b][1][H + 2 pad][W + 2 pad][8]).
+// Image b of a batch over P frame pairs: b < P estimates spynet(frame b, frame b + 1), b >= P
+// the reverse direction spynet(frame b - P + 1, frame b - P) (the backward and forward
+// flows of compute_flow; P = 1 is one pair in both directions).
+__device__ __forceinline__ void pair_frames(int b, int pairs, int& ref, int& sup) {
+    ref = b < pairs ? b : b - pairs + 1;
+    sup = b < pairs ? b + 1 : b - pairs;
+}
+
 struct PrepareArgs {
-    const uint16_t* reference[2];
-    const uint16_t* support[2];
+    const uint16_t* level;  // pyramid level [frame][3][H][W]
+    int pairs;
     const uint16_t* source_flow;  // [b][2][SH][SW], unused on the first level
     uint16_t* features;           // CB8, one block per image
     uint16_t* base_flow;          // [b][2][H][W]
@@ -216,8 +232,10 @@ __global__ __launch_bounds__(256) void spynet_prepare_kernel(PrepareArgs a) {
     uint16_t* base = a.base_flow + (size_t)b * 2 * plane;
     base[sp] = f2h(flow_x);
     base[plane + sp] = f2h(flow_y);
-    const uint16_t* ref = a.reference[b];
-    const uint16_t* sup = a.support[b];
+    int rf, sf;
+    pair_frames(b, a.pairs, rf, sf);
+    const uint16_t* ref = a.level + (size_t)rf * 3 * plane;
+    const uint16_t* sup = a.level + (size_t)sf * 3 * plane;
     uint16_t v[8];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
@@ -364,8 +382,7 @@ constexpr int kSmallLayerIn[5] = {8, 32, 64, 32, 16};
 constexpr int kSmallLayerOut[5] = {32, 64, 32, 16, 2};
 
 struct SmallLevel {
-    const uint16_t* ref[2];
-    const uint16_t* sup[2];
+    const uint16_t* pyr;  // pyramid level [frame][3][h][w]
     const void* wpk[5];
     const float* bias[5];
     uint32_t wpk_bytes[5];
@@ -376,6 +393,7 @@ struct SmallArgs {
     SmallLevel level[kSpynetMaxLevels];
     uint16_t* flow_out;  // [b][2][h][w] of the last fused level
     int levels, units;   // fused levels; LDS units per activation block
+    int pairs;
 };
 
 template <int NW>
@@ -392,10 +410,14 @@ __global__ __launch_bounds__(64 * NW) void spynet_small_kernel(SmallArgs a) {
     const int wave = tid >> 6;
     const int quarter = lane >> 4;
     const int b = blockIdx.x;
+    int rf, sf;
+    pair_frames(b, a.pairs, rf, sf);
 
     for (int l = 0; l < a.levels; ++l) {
         const SmallLevel& L = a.level[l];
         const int h = L.h, w = L.w, npx = h * w, hp = h + 6, wp = w + 6;
+        const uint16_t* ref = L.pyr + (size_t)rf * 3 * npx;
+        const uint16_t* sup = L.pyr + (size_t)sf * 3 * npx;
         // This level's tile geometry: every border unit must read zero.
         for (int i = tid; i < 2 * 8 * units; i += 64 * NW) tiles[i] = u32x4{0u, 0u, 0u, 0u};
         __syncthreads();
@@ -416,8 +438,8 @@ __global__ __launch_bounds__(64 * NW) void spynet_small_kernel(SmallArgs a) {
             uint16_t v[8];
 #pragma unroll
             for (int c = 0; c < 3; ++c) {
-                v[c] = L.ref[b][c * npx + tid];
-                v[c + 3] = f2h(sample_border(L.sup[b] + c * npx, h, w, (float)y + flow_y, (float)x + flow_x));
+                v[c] = ref[c * npx + tid];
+                v[c + 3] = f2h(sample_border(sup + c * npx, h, w, (float)y + flow_y, (float)x + flow_x));
             }
             v[6] = f2h(flow_x);
             v[7] = f2h(flow_y);
@@ -625,9 +647,9 @@ hipError_t launch_bicubic_quarter(const uint16_t* in, uint16_t* out, int channel
     return hipGetLastError();
 }
 
-hipError_t launch_spynet_pyramid(const uint16_t* const* frames, int count, uint16_t* (*levels)[kSpynetMaxLevels],
-                                 int nlevels, int height, int width, hipStream_t stream) {
-    if (count < 1 || count > 2 || nlevels < 1 || nlevels > kSpynetMaxLevels) return hipErrorInvalidValue;
+hipError_t launch_spynet_pyramid(const uint16_t* frame0, const uint16_t* frame1, long frame_stride, int count,
+                                 uint16_t* const* levels, int nlevels, int height, int width, hipStream_t stream) {
+    if (count < 1 || nlevels < 1 || nlevels > kSpynetMaxLevels) return hipErrorInvalidValue;
     PyramidArgs a{};
     a.frames = count;
     a.levels = nlevels;
@@ -638,14 +660,14 @@ hipError_t launch_spynet_pyramid(const uint16_t* const* frames, int count, uint1
         a.offset[l] = off;
         const int shift = nlevels - 1 - l;
         off += 3L * (height >> shift) * (width >> shift);
+        a.level[l] = levels[l];
     }
     a.offset[nlevels] = off;
-    a.aligned = width % 8 == 0;
-    for (int f = 0; f < count; ++f) {
-        if (reinterpret_cast<uintptr_t>(frames[f]) % 16 != 0) a.aligned = 0;
-        a.frame[f] = frames[f];
-        for (int l = 0; l < nlevels; ++l) a.level[f][l] = levels[f][l];
-    }
+    a.frame[0] = frame0;
+    a.frame[1] = count > 1 ? frame1 : frame0;
+    a.frame_stride = frame_stride;
+    a.aligned = width % 8 == 0 && reinterpret_cast<uintptr_t>(frame0) % 16 == 0 &&
+                reinterpret_cast<uintptr_t>(a.frame[1]) % 16 == 0 && (count <= 2 || frame_stride % 8 == 0);
     // Coarse levels come first; those whose factor is in [16, 64] get a wave per output.
     a.coarse = 0;
     if (a.aligned)
@@ -660,16 +682,13 @@ hipError_t launch_spynet_pyramid(const uint16_t* const* frames, int count, uint1
     return hipGetLastError();
 }
 
-hipError_t launch_spynet_prepare(int batch, const uint16_t* const* reference, const uint16_t* const* support,
-                                 const uint16_t* source_flow, int source_height, int source_width,
-                                 int first_level, uint16_t* features, int pad, uint16_t* base_flow,
-                                 int height, int width, hipStream_t stream) {
-    if (batch < 1 || batch > 2) return hipErrorInvalidValue;
+hipError_t launch_spynet_prepare(int batch, int pairs, const uint16_t* pyramid_level, const uint16_t* source_flow,
+                                 int source_height, int source_width, int first_level, uint16_t* features, int pad,
+                                 uint16_t* base_flow, int height, int width, hipStream_t stream) {
+    if (batch < 1 || pairs < 1 || batch > 2 * pairs) return hipErrorInvalidValue;
     PrepareArgs a{};
-    for (int b = 0; b < batch; ++b) {
-        a.reference[b] = reference[b];
-        a.support[b] = support[b];
-    }
+    a.level = pyramid_level;
+    a.pairs = pairs;
     a.source_flow = source_flow;
     a.features = features;
     a.base_flow = base_flow;
@@ -689,14 +708,16 @@ size_t spynet_small_lds_bytes(int units) {
     return (size_t)2 * 8 * units * 16 + (size_t)8 * kSmallMaxNb * 64 * 16 + (size_t)4 * kSmallMaxPx * 2;
 }
 
-hipError_t launch_spynet_small(int batch, int levels, const int* heights, const int* widths,
-                               const uint16_t* const (*reference)[2], const uint16_t* const (*support)[2],
-                               const void* const (*wpk)[5], const float* const (*bias)[5],
-                               const uint32_t (*wpk_bytes)[5], uint16_t* flow_out, hipStream_t stream) {
-    if (batch < 1 || batch > 2 || levels < 1 || levels > kSpynetMaxLevels) return hipErrorInvalidValue;
+hipError_t launch_spynet_small(int batch, int pairs, int levels, const int* heights, const int* widths,
+                               const uint16_t* const* pyramid, const void* const (*wpk)[5],
+                               const float* const (*bias)[5], const uint32_t (*wpk_bytes)[5], uint16_t* flow_out,
+                               hipStream_t stream) {
+    if (batch < 1 || pairs < 1 || batch > 2 * pairs || levels < 1 || levels > kSpynetMaxLevels)
+        return hipErrorInvalidValue;
     constexpr int NW = 8;
     SmallArgs a{};
     a.levels = levels;
+    a.pairs = pairs;
     a.flow_out = flow_out;
     int units = 0;
     for (int l = 0; l < levels; ++l) {
@@ -704,10 +725,7 @@ hipError_t launch_spynet_small(int batch, int levels, const int* heights, const 
         SmallLevel& L = a.level[l];
         L.h = heights[l];
         L.w = widths[l];
-        for (int b = 0; b < 2; ++b) {
-            L.ref[b] = reference[l][b];
-            L.sup[b] = support[l][b];
-        }
+        L.pyr = pyramid[l];
         for (int i = 0; i < 5; ++i) {
             L.wpk[i] = wpk[l][i];
             L.bias[i] = bias[l][i];

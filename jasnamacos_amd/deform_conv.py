@@ -489,18 +489,19 @@ class HipDeformConv:
         self._check(self._lib.dcn_spynet_pyramid_f16_dev(self.ctx, int(height), int(width), _ptr(frame), _ptr(out),
                                                          _stream(stream)))
 
-    def spynet(self, height, width, weights, stream=None) -> "SpyNet":
+    def spynet(self, height, width, weights, max_frames: int = 2, stream=None) -> "SpyNet":
         """weights: device tensors "w{level}_{layer}" and "b{level}_{layer}" (OIHW FP16),
-        level 0..5 coarsest first, layer 0..4 (8->32->64->32->16->2, 7x7)."""
+        level 0..5 coarsest first, layer 0..4 (8->32->64->32->16->2, 7x7); max_frames sizes
+        clip_flows_dev (2: pairs only)."""
         w = _lib.DcnSpynetWeights()
         for level in range(_lib.SPYNET_LEVELS):
             for layer in range(_lib.SPYNET_LAYERS):
                 w.weight[level][layer] = _ptr(weights[f"w{level}_{layer}"])
                 w.bias[level][layer] = _ptr(weights[f"b{level}_{layer}"])
         handle = C.c_void_p()
-        self._check(self._lib.dcn_spynet_create(self.ctx, int(height), int(width), C.byref(w), _stream(stream),
-                                                C.byref(handle)))
-        return SpyNet(self, handle.value, height, width)
+        self._check(self._lib.dcn_spynet_create(self.ctx, int(height), int(width), int(max_frames), C.byref(w),
+                                                _stream(stream), C.byref(handle)))
+        return SpyNet(self, handle.value, height, width, max_frames)
 
     def clip(self, height, width, frames, weights, blocks: int = 5, stream=None) -> "PropagationClip":
         """The four propagation branches over `frames` frames; weights: four body weight dicts
@@ -651,9 +652,9 @@ def _body_weights(weights: dict, blocks: int) -> "_lib.DcnBodyWeights":
 class SpyNet:
     """SPyNet flow estimation (dcn_spynet): RGB frames [3][H][W] in, flows [n][2][H][W] out."""
 
-    def __init__(self, ctx: HipDeformConv, handle: int, height, width):
+    def __init__(self, ctx: HipDeformConv, handle: int, height, width, max_frames=2):
         self.ctx, self.handle = ctx, C.c_void_p(handle)
-        self.height, self.width = height, width
+        self.height, self.width, self.max_frames = height, width, max_frames
 
     def flow_dev(self, reference, support, flow, both_directions: bool = True, stream=None) -> None:
         """flow[0] = spynet(reference, support); flow[1] = spynet(support, reference) when
@@ -661,6 +662,12 @@ class SpyNet:
         self.ctx._check(self.ctx._lib.dcn_spynet_flow_dev(self.handle, _ptr(reference), _ptr(support),
                                                           int(bool(both_directions)), _ptr(flow),
                                                           _stream(stream)))
+
+    def clip_flows_dev(self, frames, count: int, flows, stream=None) -> None:
+        """frames [count][3][H][W] -> flows [2][count-1][2][H][W]: [0][t] = spynet(t, t+1)
+        (backward), [1][t] = spynet(t+1, t) (forward) (FusedSPyNetClipGraph.swift)."""
+        self.ctx._check(self.ctx._lib.dcn_spynet_clip_flows_dev(self.handle, _ptr(frames), int(count), _ptr(flows),
+                                                                _stream(stream)))
 
     def free(self) -> None:
         if self.handle:

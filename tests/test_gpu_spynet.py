@@ -116,6 +116,32 @@ def test_spynet_directions_bit_consistent(gpu_ctx, torch):
     spy.free()
 
 
+def test_clip_flows_equal_pair_calls(gpu_ctx, torch):
+    """All pairs of a 5-frame clip in one pass == one pair call per adjacent pair, bit for
+    bit (each image of the batch is computed independently of the others)."""
+    h = w = 64
+    frames = 5
+    rng = np.random.default_rng(51)
+    weights = sr.spynet_weights(rng)
+    spy = gpu_ctx.spynet(h, w, {k: dev(torch, v) for k, v in weights.items()}, max_frames=frames)
+    clip = [sr.smooth_frame(rng, h, w, shift=(0.7 * t, -1.1 * t)) for t in range(frames)]
+    fr = dev(torch, np.concatenate(clip))
+    log("case: spynet clip flows", frames)
+    flows = torch.zeros(2 * (frames - 1) * 2 * h * w, dtype=torch.int16, device="cuda")
+    spy.clip_flows_dev(fr, frames, flows)
+    pair = torch.zeros(4 * h * w, dtype=torch.int16, device="cuda")
+    plane = 3 * h * w
+    f2 = 2 * h * w
+    for t in range(frames - 1):
+        spy.flow_dev(fr[t * plane:(t + 1) * plane], fr[(t + 1) * plane:(t + 2) * plane], pair)
+        torch.cuda.synchronize()
+        assert torch.equal(flows[t * f2:(t + 1) * f2], pair[:f2]), t
+        assert torch.equal(flows[(frames - 1 + t) * f2:(frames + t) * f2], pair[f2:]), t
+    with pytest.raises(Exception):
+        spy.clip_flows_dev(fr, frames + 1, flows)
+    spy.free()
+
+
 def test_spynet_graph_replays_match_eager(gpu_ctx, torch):
     h = w = 64
     _, spy, ref, sup = _spynet(torch, gpu_ctx, h, w, 41)
