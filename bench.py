@@ -364,11 +364,46 @@ def bench_clip(args, ctx, dc, clip, dev) -> dict:
     out = prop.cpu().numpy().view(np.float16)
     flops = dc.clip_flops(H, W, frames, blocks)
     graph.free()
+    # The same clip fed by learned flows: the 256 x 256 LQ tiles downsampled, SPyNet over
+    # every adjacent pair (dcn_spynet_clip_flows_dev) and the four branches, one stream.
+    sd = dc.generate_spynet_inputs(4 * H, seed=args.seed)
+    spy = ctx.spynet(H, W, {k: dev(v) for k, v in sd["weights"].items()}, max_frames=frames)
+    base_tile = np.asarray(sd["reference"], np.float16).reshape(3, 4 * H, 4 * W)
+    lq = dev(np.concatenate([np.roll(base_tile, (t, -t), axis=(1, 2)).ravel() for t in range(frames)]))
+    small = torch.zeros(frames * 3 * plane, dtype=torch.int16, device="cuda")
+    learned = torch.zeros(2 * (frames - 1) * 2 * plane, dtype=torch.int16, device="cuda")
+    half = (frames - 1) * 2 * plane
+
+    def learned_clip(cur):
+        ctx.bicubic_quarter_f16_dev(3 * frames, 4 * H, 4 * W, lq, small, stream=cur)
+        spy.clip_flows_dev(small, frames, learned, stream=cur)
+        pc.run_dev(spatial, learned[:half], learned[half:], prop, 0, stream=cur)
+
+    lgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(lgraph, stream=stream):
+        learned_clip(torch.cuda.current_stream())
+    lgraph.replay()
+    torch.cuda.synchronize()
+    start2, end2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start2.record(stream)
+        for _ in range(reps):
+            lgraph.replay()
+        end2.record(stream)
+    torch.cuda.synchronize()
+    learned_ms = start2.elapsed_time(end2) / reps
+    learned_out = prop.cpu().numpy().view(np.float16)
+    del lgraph
+    spy.free()
     pc.free()
     return {"workload": f"4 branches x {frames} frames (backward_1, forward_1, backward_2, forward_2), one hipGraph",
             "ms_per_clip": clip_ms, "body_steps": 4 * frames, "us_per_body_step": clip_ms * 1e3 / (4 * frames),
             "tflops": flops / (clip_ms * 1e-3) / 1e12, "flops_per_clip": flops, "replays_timed": reps,
-            "output_finite": bool(np.all(np.isfinite(out.astype(np.float32))))}
+            "output_finite": bool(np.all(np.isfinite(out.astype(np.float32)))),
+            "with_spynet_flows": {"ms_per_clip": learned_ms,
+                                  "workload": "bicubic 1/4 of 30 LQ tiles + SPyNet clip flows + the four branches, "
+                                              "one hipGraph",
+                                  "output_finite": bool(np.all(np.isfinite(learned_out.astype(np.float32))))}}
 
 
 def cpu_baseline_body(clip) -> dict:
