@@ -11,6 +11,8 @@
 //   BenchmarkStatistics    BenchmarkStatistics.swift:3-44
 //   TemporalSchedule       TemporalSchedule.swift:3-101
 //   temporalChunkRanges    SideBySideRestoration.swift:1213-1230
+//   SPyNetPairResult,      SPyNetPairProbe.swift:4-18, :47-449
+//   verifySPyNetPair       (the deterministic inputs of tools/export_spynet_oracle.py:14-19)
 //
 // Link with -ldcn (and the HIP runtime for benchmarkJasnaShape's device buffers).
 #pragma once
@@ -21,8 +23,10 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <cstring>
 #include <fstream>
 #include <iterator>
+#include <memory>
 #include <optional>
 #include <stdexcept>
 #include <string>
@@ -253,6 +257,46 @@ struct BenchmarkResult {  // BenchmarkResult (MetalRunner.swift:67-90), this bui
 };
 
 // MetalDeformConv's role on a HIP device.
+// SPyNetPairResult (SPyNetPairProbe.swift:4-18): timing of the bidirectional pair over 7
+// samples, per-direction maxima and stride-257 checksums, repeat and oracle errors, flows.
+struct SPyNetPairResult {
+    double medianMilliseconds = 0, minimumMilliseconds = 0, maximumMilliseconds = 0;
+    int iterations = 0;
+    int elementCount = 0;
+    float backwardMaximum = 0, forwardMaximum = 0, repeatMaximumError = 0, oracleMaximumError = 0;
+    double backwardChecksum = 0, forwardChecksum = 0;
+    std::vector<uint16_t> backwardFlow, forwardFlow;
+};
+
+// The six basic modules of SPyNet, OIHW FP16 bit patterns, level 0 the coarsest; layer i
+// of every level is kSPyNetLayers[i] = {cin, cout}, 7 x 7.
+struct SPyNetWeights {
+    static constexpr int layers[DCN_SPYNET_LAYERS][2] = {{8, 32}, {32, 64}, {64, 32}, {32, 16}, {16, 2}};
+    std::vector<uint16_t> weight[DCN_SPYNET_LEVELS][DCN_SPYNET_LAYERS];
+    std::vector<uint16_t> bias[DCN_SPYNET_LEVELS][DCN_SPYNET_LAYERS];
+    void validate() const {
+        for (int l = 0; l < DCN_SPYNET_LEVELS; ++l)
+            for (int i = 0; i < DCN_SPYNET_LAYERS; ++i) {
+                const size_t expected = (size_t)layers[i][0] * layers[i][1] * 49;
+                if (weight[l][i].size() != expected)
+                    throw DeformConvError::invalidArrayCount("spynet.weight", (long)expected, (long)weight[l][i].size());
+                if (bias[l][i].size() != (size_t)layers[i][1])
+                    throw DeformConvError::invalidArrayCount("spynet.bias", layers[i][1], (long)bias[l][i].size());
+            }
+    }
+};
+
+// deterministic_frame of tools/export_spynet_oracle.py:14-19: RGB 3 x 64 x 64 values
+// ((i * multiplier + addend) % modulus) / divisor rounded to FP16.
+inline std::vector<uint16_t> deterministicSPyNetFrame(long multiplier, long addend, long modulus, long divisor,
+                                                     int size = 64) {
+    std::vector<float> v((size_t)3 * size * size);
+    for (size_t i = 0; i < v.size(); ++i) v[i] = (float)(((long)i * multiplier + addend) % modulus) / (float)divisor;
+    std::vector<uint16_t> h(v.size());
+    dcn_f32_to_f16_array(v.data(), h.data(), v.size());
+    return h;
+}
+
 class HipDeformConv {
 public:
     explicit HipDeformConv(int device = 0) {
@@ -391,6 +435,104 @@ public:
                                                  std::to_string(r.maxDifferenceFromBaseline));
         r.checksum = dcn_checksum_f16(f.data(), f.size());
         r.iterations = std::max(iterations, 1);
+        return r;
+    }
+
+    // jasna_bicubic_downsample_quarter_fp16 (MetalShader.swift:488-521) on host arrays.
+    std::vector<uint16_t> bicubicQuarter(int channels, int height, int width, const std::vector<uint16_t>& input) {
+        if (input.size() != (size_t)channels * height * width)
+            throw DeformConvError::invalidArrayCount("input", (long)channels * height * width, (long)input.size());
+        DeviceBuffer in(input), out((size_t)channels * (height / 4) * (width / 4));
+        check(dcn_bicubic_quarter_f16_dev(ctx_, channels, height, width, in.p, out.p, nullptr));
+        return out.download();
+    }
+
+    // verifySPyNetPair (SPyNetPairProbe.swift:47-449): the bidirectional pair on 64 x 64
+    // frames (default: the deterministic frames of tools/export_spynet_oracle.py), 2 warm-ups
+    // and 7 timed runs, then the reference's gates: both maxima > 0.001, repeat error <=
+    // 0.001 and, when an oracle directory with backward.f16 / forward.f16 is given, oracle
+    // error <= 0.05. Throws commandFailed when a gate fails or a flow is non-finite.
+    SPyNetPairResult verifySPyNetPair(const SPyNetWeights& weights, const std::vector<uint16_t>* reference = nullptr,
+                                      const std::vector<uint16_t>* support = nullptr,
+                                      const std::string& oracleDirectory = "") {
+        constexpr int size = 64, plane = size * size;
+        weights.validate();
+        const std::vector<uint16_t> ref = reference ? *reference : deterministicSPyNetFrame(29, 17, 1021, 1020);
+        const std::vector<uint16_t> sup = support ? *support : deterministicSPyNetFrame(43, 31, 1019, 1018);
+        if (ref.size() != (size_t)3 * plane) throw DeformConvError::invalidArrayCount("reference", 3 * plane, (long)ref.size());
+        if (sup.size() != (size_t)3 * plane) throw DeformConvError::invalidArrayCount("support", 3 * plane, (long)sup.size());
+        std::vector<std::unique_ptr<DeviceBuffer>> wbuf;
+        dcn_spynet_weights w{};
+        for (int l = 0; l < DCN_SPYNET_LEVELS; ++l)
+            for (int i = 0; i < DCN_SPYNET_LAYERS; ++i) {
+                wbuf.emplace_back(new DeviceBuffer(weights.weight[l][i]));
+                w.weight[l][i] = wbuf.back()->p;
+                wbuf.emplace_back(new DeviceBuffer(weights.bias[l][i]));
+                w.bias[l][i] = wbuf.back()->p;
+            }
+        dcn_spynet* raw = nullptr;
+        check(dcn_spynet_create(ctx_, size, size, 2, &w, nullptr, &raw));
+        std::unique_ptr<dcn_spynet, void (*)(dcn_spynet*)> net(raw, dcn_spynet_destroy);
+        DeviceBuffer dref(ref), dsup(sup), flow((size_t)4 * plane);
+        Event e0, e1;
+        auto execute = [&](std::vector<uint16_t>* out) {
+            hip(hipEventRecord(e0.e, nullptr));
+            check(dcn_spynet_flow_dev(net.get(), dref.p, dsup.p, 1, flow.p, nullptr));
+            hip(hipEventRecord(e1.e, nullptr));
+            hip(hipEventSynchronize(e1.e));
+            float t = 0;
+            hip(hipEventElapsedTime(&t, e0.e, e1.e));
+            if (out) *out = flow.download();
+            return (double)t;
+        };
+        execute(nullptr);
+        execute(nullptr);
+        std::vector<uint16_t> first, last;
+        std::vector<double> samples{execute(&first)};
+        for (int i = 1; i < 7; ++i) samples.push_back(execute(&last));
+        std::sort(samples.begin(), samples.end());
+        std::vector<uint16_t> oracle[2];
+        if (!oracleDirectory.empty()) {
+            const char* names[2] = {"backward.f16", "forward.f16"};
+            for (int d = 0; d < 2; ++d) {
+                std::ifstream f(oracleDirectory + "/" + names[d], std::ios::binary);
+                std::vector<char> bytes((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+                if (!f.good() && !f.eof()) throw DeformConvError::commandFailed("cannot read the SPyNet oracle");
+                if (bytes.size() != (size_t)2 * plane * 2) throw DeformConvError::commandFailed("invalid SPyNet oracle size");
+                oracle[d].resize((size_t)2 * plane);
+                std::memcpy(oracle[d].data(), bytes.data(), bytes.size());
+            }
+        }
+        SPyNetPairResult r;
+        float maxima[2] = {0, 0};
+        double checksums[2] = {0, 0};
+        for (int d = 0; d < 2; ++d)
+            for (size_t i = 0; i < (size_t)2 * plane; ++i) {
+                const size_t k = (size_t)d * 2 * plane + i;
+                const float v = dcn_f16_to_f32(last[k]);
+                if (!std::isfinite(v)) throw DeformConvError::commandFailed("SPyNet produced a non-finite flow");
+                maxima[d] = std::max(maxima[d], std::fabs(v));
+                r.repeatMaximumError = std::max(r.repeatMaximumError, std::fabs(dcn_f16_to_f32(first[k]) - v));
+                if (!oracle[d].empty())
+                    r.oracleMaximumError = std::max(r.oracleMaximumError, std::fabs(dcn_f16_to_f32(oracle[d][i]) - v));
+                if (i % 257 == 0) checksums[d] += (double)v;
+            }
+        if (!(maxima[0] > 0.001f && maxima[1] > 0.001f) || r.repeatMaximumError > 0.001f || r.oracleMaximumError > 0.05f)
+            throw DeformConvError::commandFailed("SPyNet validation failed (maxima=[" + std::to_string(maxima[0]) + ", " +
+                                                 std::to_string(maxima[1]) + "], repeat=" +
+                                                 std::to_string(r.repeatMaximumError) + ", oracle=" +
+                                                 std::to_string(r.oracleMaximumError) + ")");
+        r.medianMilliseconds = samples[samples.size() / 2];
+        r.minimumMilliseconds = samples.front();
+        r.maximumMilliseconds = samples.back();
+        r.iterations = (int)samples.size();
+        r.elementCount = 2 * 2 * plane;
+        r.backwardMaximum = maxima[0];
+        r.forwardMaximum = maxima[1];
+        r.backwardChecksum = checksums[0];
+        r.forwardChecksum = checksums[1];
+        r.backwardFlow.assign(last.begin(), last.begin() + 2 * plane);
+        r.forwardFlow.assign(last.begin() + 2 * plane, last.end());
         return r;
     }
 

@@ -6,6 +6,7 @@
 //   JasnaCLI.swift:68-110                    (correctnessTest: seeded 1x2x5x5 -> 3, 2e-5 gate)
 //   TemporalScheduleTests.swift:4-40         (traversal, widths, second order, 30 frames)
 //   RestorationResumeTests.swift:51-72       (temporalChunkRanges)
+//   SPyNetPairProbe.swift:47-449             (verifySPyNetPair: gates, oracle files)
 // plus the weight-set loader and benchmarkJasnaShape. The CPU oracle (oracle/liboracle.so)
 // stands in for DeformConvCPU as the checker; the library under test never calls it.
 //
@@ -376,6 +377,75 @@ TEST(gpu, benchmarkJasnaShapeReportsGatedStatistics) {
     EXPECT(r.maxDifferenceFromBaseline <= 2e-3f);
     std::printf("  jasna shape: baseline median %.4f ms, gather %.4f ms, fused %.4f ms, checksum %.6f\n",
                 r.baseline.median, r.gather.median, r.fused.median, r.checksum);
+}
+
+// Random SPyNet basic modules: He-uniform 7x7 weights for the ReLU layers, small ones for
+// the flow layer (no checkpoint in this tree).
+jasna::SPyNetWeights randomSPyNetWeights(uint64_t seed) {
+    jasna::SeededGenerator rng(seed);
+    jasna::SPyNetWeights w;
+    auto half = [](const std::vector<float>& v) {
+        std::vector<uint16_t> h(v.size());
+        dcn_f32_to_f16_array(v.data(), h.data(), v.size());
+        return h;
+    };
+    for (int l = 0; l < DCN_SPYNET_LEVELS; ++l)
+        for (int i = 0; i < DCN_SPYNET_LAYERS; ++i) {
+            const int cin = jasna::SPyNetWeights::layers[i][0], cout = jasna::SPyNetWeights::layers[i][1];
+            const float bound = i + 1 < DCN_SPYNET_LAYERS ? std::sqrt(6.0f / (cin * 49.0f)) : 0.07f;
+            w.weight[l][i] = half(rng.floats((size_t)cout * cin * 49, -bound, bound));
+            w.bias[l][i] = half(rng.floats((size_t)cout, -0.01f, 0.01f));
+        }
+    return w;
+}
+
+TEST(gpu, verifySPyNetPairPassesItsGatesAndChecksAnOracle) {
+    jasna::HipDeformConv runner;
+    const auto weights = randomSPyNetWeights(0x5350594E4554ull);
+    const auto r = runner.verifySPyNetPair(weights);
+    EXPECT(r.iterations == 7 && r.elementCount == 2 * 2 * 4096);
+    EXPECT(r.backwardMaximum > 0.001f && r.forwardMaximum > 0.001f);
+    EXPECT(r.repeatMaximumError == 0.0f && r.oracleMaximumError == 0.0f);
+    EXPECT(r.minimumMilliseconds <= r.medianMilliseconds && r.medianMilliseconds <= r.maximumMilliseconds);
+    EXPECT(r.backwardFlow.size() == 2 * 4096 && r.forwardFlow.size() == 2 * 4096);
+    EXPECT(std::isfinite(r.backwardChecksum) && std::isfinite(r.forwardChecksum));
+    std::printf("  spynet pair: median %.4f ms, maxima %.3f / %.3f, checksums %.6f / %.6f\n", r.medianMilliseconds,
+                r.backwardMaximum, r.forwardMaximum, r.backwardChecksum, r.forwardChecksum);
+    // Oracle files in the reference's format (raw FP16 [2][64][64] per direction): this run's
+    // own flows pass with error 0; one value moved by 0.25 px fails the 0.05 gate.
+    char dir[] = "/tmp/spynet_oracle_XXXXXX";
+    EXPECT(mkdtemp(dir) != nullptr);
+    auto write = [&](const char* name, const std::vector<uint16_t>& v) {
+        std::FILE* f = std::fopen((std::string(dir) + "/" + name).c_str(), "wb");
+        EXPECT(f != nullptr);
+        std::fwrite(v.data(), 2, v.size(), f);
+        std::fclose(f);
+    };
+    write("backward.f16", r.backwardFlow);
+    write("forward.f16", r.forwardFlow);
+    const auto again = runner.verifySPyNetPair(weights, nullptr, nullptr, dir);
+    EXPECT(again.oracleMaximumError == 0.0f && again.backwardChecksum == r.backwardChecksum);
+    auto moved = r.forwardFlow;
+    moved[100] = dcn_f32_to_f16(dcn_f16_to_f32(moved[100]) + 0.25f);
+    write("forward.f16", moved);
+    bool threw = false;
+    try {
+        runner.verifySPyNetPair(weights, nullptr, nullptr, dir);
+    } catch (const jasna::DeformConvError& e) {
+        threw = e.kind() == jasna::DeformConvError::Kind::commandFailed;
+    }
+    EXPECT(threw);
+    std::remove((std::string(dir) + "/backward.f16").c_str());
+    std::remove((std::string(dir) + "/forward.f16").c_str());
+    rmdir(dir);
+}
+
+TEST(gpu, bicubicQuarterKeepsAConstantImageConstant) {
+    jasna::HipDeformConv runner;
+    const std::vector<uint16_t> in((size_t)3 * 256 * 256, dcn_f32_to_f16(0.375f));
+    const auto out = runner.bicubicQuarter(3, 256, 256, in);
+    EXPECT(out.size() == (size_t)3 * 64 * 64);
+    for (uint16_t v : out) EXPECT(v == dcn_f32_to_f16(0.375f));
 }
 
 }  // namespace
