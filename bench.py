@@ -147,6 +147,7 @@ def bench_body(args) -> int:
         g.free()
     body.free()
     clip_line = bench_clip(args, ctx, dc, clip, dev)
+    tiles_line = bench_body_tiles(args, ctx, dc, clip, dev)
     cpu = None if args.no_cpu_baseline else cpu_baseline_body(clip)
     line = {
         "metric": "BasicVSR++ propagation body us/frame (C4: offset convs + DCNv2 + 5-block backbone, hipGraph per frame)",
@@ -172,11 +173,53 @@ def bench_body(args) -> int:
         "wall_ms_timed_region": wall_ms,
         "output_finite": bool(np.all(np.isfinite(out.astype(np.float32)))),
         "clip": clip_line,
+        "tiles": tiles_line,
         "cpu_baseline": cpu,
     }
     ctx.close()
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_body_tiles(args, ctx, dc, clip, dev, tiles: int = 16) -> dict:
+    """The same body step over 16 tiles at once (dcn_body_create_tiles: every kernel runs
+    once over the batch), one captured graph replayed; the production pipeline runs many
+    tiles of a frame (README.md:589-591). Reported beside the one-tile frame time."""
+    import numpy as np
+    import torch
+
+    H, W, blocks = clip["height"], clip["width"], clip["blocks"]
+    plane = H * W
+    wd = {k: dev(v) for k, v in clip["weights"].items()}
+    body = ctx.body(H, W, wd, branch=0, blocks=blocks, tiles=tiles)
+    rng = np.random.default_rng(args.seed + 7)
+    f16 = lambda a: np.asarray(a, np.float32).astype(np.float16)  # noqa: E731
+    feats = [dev(f16(rng.standard_normal(tiles * 64 * plane))) for _ in range(3)]
+    flows = [dev(f16(rng.uniform(-4, 4, tiles * 2 * plane))) for _ in range(2)]
+    flow2 = torch.zeros(tiles * 2 * plane, dtype=torch.int16, device="cuda")
+    out = torch.zeros(tiles * 64 * plane, dtype=torch.int16, device="cuda")
+    graph = body.capture(feats[0], flows[0], flows[1], feats[1], feats[2], flow2, out, has_second_order=True)
+    stream = torch.cuda.Stream()
+    for _ in range(10):
+        graph.launch(stream)
+    torch.cuda.synchronize()
+    reps = 50
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(reps):
+            graph.launch(stream)
+        end.record(stream)
+    torch.cuda.synchronize()
+    step_ms = start.elapsed_time(end) / reps
+    result = out.cpu().numpy().view(np.float16).astype(np.float32)
+    flops = tiles * dc.body_flops(H, W, 0, blocks)
+    graph.free()
+    body.free()
+    return {"workload": f"one body step (branch 0, {blocks} blocks) over {tiles} 64x64 tiles, one hipGraph",
+            "tiles": tiles, "us_per_step": step_ms * 1e3, "us_per_tile": step_ms * 1e3 / tiles,
+            "tflops": flops / (step_ms * 1e-3) / 1e12, "replays_timed": reps,
+            "output_finite": bool(np.all(np.isfinite(result)))}
 
 
 def bench_spynet(args) -> int:

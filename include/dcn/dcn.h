@@ -478,6 +478,11 @@ typedef struct dcn_body_weights {
 typedef struct dcn_body dcn_body;
 dcn_status dcn_body_create(dcn_context* ctx, int height, int width, int branch, int blocks,
                            const dcn_body_weights* weights, void* stream, dcn_body** out);
+/* dcn_body_create for `tiles` independent tiles per step (1..1024; the production
+ * pipeline runs many tiles of a frame, README.md:589-591): every tensor of a step then
+ * holds all tiles, [tiles][C][H][W], and each kernel runs once over the batch. */
+dcn_status dcn_body_create_tiles(dcn_context* ctx, int height, int width, int branch, int blocks, int tiles,
+                                 const dcn_body_weights* weights, void* stream, dcn_body** out);
 void dcn_body_destroy(dcn_body* body);
 /* One step, stream-ordered. feat_current, feat_prop, feat_n2, feat_prop_out: NCHW
  * [64][H][W]; flow1, prev_flow, flow2_out: [2][H][W]; d_prefix: `branch` further
@@ -539,6 +544,10 @@ dcn_status dcn_temporal_chunk_ranges(int frame_count, int max_frames_per_chunk, 
 typedef struct dcn_clip dcn_clip;
 dcn_status dcn_clip_create(dcn_context* ctx, int height, int width, int frames, int blocks,
                            const dcn_body_weights* weights, void* stream, dcn_clip** out);
+/* dcn_clip_create for `tiles` tiles: spatial [T][tiles][64][H][W], flows
+ * [T-1][tiles][2][H][W], propagated [4][T][tiles][64][H][W]. */
+dcn_status dcn_clip_create_tiles(dcn_context* ctx, int height, int width, int frames, int blocks, int tiles,
+                                 const dcn_body_weights* weights, void* stream, dcn_clip** out);
 void dcn_clip_destroy(dcn_clip* clip);
 /* The whole clip in schedule order, stream-ordered: spatial [frames][64][H][W];
  * backward_flows / forward_flows [frames-1][2][H][W] indexed by the schedule's

@@ -171,6 +171,8 @@ SIGNATURES: dict[str, tuple] = {
                                            C.c_int, c_void, C.c_int, c_void, C.c_int, c_void]),
     "dcn_body_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(DcnBodyWeights),
                                   c_void, C.POINTER(c_void)]),
+    "dcn_body_create_tiles": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.POINTER(DcnBodyWeights), c_void, C.POINTER(c_void)]),
     "dcn_body_destroy": (None, [c_void]),
     "dcn_body_step_dev": (C.c_int, [c_void, c_void, c_void, c_void, c_void, c_void, C.POINTER(c_void),
                                     C.c_int, c_void, c_void, c_void]),
@@ -186,6 +188,8 @@ SIGNATURES: dict[str, tuple] = {
                                             C.POINTER(c_size)]),
     "dcn_clip_create": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(DcnBodyWeights), c_void,
                                   C.POINTER(c_void)]),
+    "dcn_clip_create_tiles": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.POINTER(DcnBodyWeights), c_void, C.POINTER(c_void)]),
     "dcn_clip_destroy": (None, [c_void]),
     "dcn_clip_run_dev": (C.c_int, [c_void, c_void, c_void, c_void, c_void, C.c_int, c_void]),
     "dcn_clip_capture": (C.c_int, [c_void, c_void, c_void, c_void, c_void, C.c_int, C.POINTER(c_void)]),

@@ -27,7 +27,7 @@ struct dcn_graph {
 
 struct dcn_clip {
     dcn_context* ctx = nullptr;
-    int h = 0, w = 0, frames = 0, blocks = 0;
+    int h = 0, w = 0, frames = 0, blocks = 0, tiles = 1;
     dcn_body* body[4] = {};
     uint16_t* zero_feat = nullptr;  // 64 x plane zeros: the feat_n2 of positions 0 and 1
     uint16_t* flow2 = nullptr;      // 2 x plane second-order flow scratch
@@ -37,7 +37,7 @@ struct dcn_clip {
 
 struct dcn_body {
     dcn_context* ctx = nullptr;
-    int h = 0, w = 0, branch = 0, blocks = 0;
+    int h = 0, w = 0, branch = 0, blocks = 0, tiles = 1;  // tiles: images per step
     dcn_conv* offset_conv[4] = {};
     dcn_conv* backbone[1 + 2 * DCN_BODY_MAX_BLOCKS] = {};
     dcn_packed* dcn = nullptr;
@@ -79,11 +79,16 @@ dcn_status alloc(dcn_context* ctx, std::vector<void*>& owned, T** p, size_t elem
 
 dcn_status run_conv(dcn_context* ctx, const dcn_conv* c, const void* x, int act, const void* r1,
                     int r1_layout, const void* r2, int r2_layout, void* out, int out_layout,
-                    hipStream_t stream) {
+                    hipStream_t stream, const dcn::ConvBatch& batch = dcn::ConvBatch{}) {
     DCN_HIP(ctx, dcn::launch_conv3x3(c->g, x, c->wpk, c->bias, act, 0.1f, (const uint16_t*)r1,
                                      r1_layout, (const uint16_t*)r2, r2_layout, (uint16_t*)out,
-                                     out_layout, stream));
+                                     out_layout, stream, 0, batch));
     return DCN_OK;
+}
+
+// Elements per image of a CB8 tensor of `blocks` 8-channel blocks.
+long cb8_image(const dcn_body* b, int blocks) {
+    return (long)blocks * (b->h + 2 * DCN_CB8_PAD) * (b->w + 2 * DCN_CB8_PAD) * 8;
 }
 
 dcn_shape body_dcn_shape(int h, int w) {
@@ -359,11 +364,18 @@ void dcn_body_destroy(dcn_body* body) {
 
 dcn_status dcn_body_create(dcn_context* ctx, int height, int width, int branch, int blocks,
                            const dcn_body_weights* weights, void* stream, dcn_body** out) {
+    return dcn_body_create_tiles(ctx, height, width, branch, blocks, 1, weights, stream, out);
+}
+
+dcn_status dcn_body_create_tiles(dcn_context* ctx, int height, int width, int branch, int blocks, int tiles,
+                                 const dcn_body_weights* weights, void* stream, dcn_body** out) {
     if (!ctx || !out) return DCN_INVALID_ARGUMENT;
     *out = nullptr;
     DCN_TRY(check_plane(ctx, width, height));
     if (branch < 0 || branch > 3 || blocks < 1 || blocks > DCN_BODY_MAX_BLOCKS || !weights)
         return fail(ctx, DCN_INVALID_ARGUMENT, "body needs branch 0..3, 1..8 blocks and weights");
+    if (tiles < 1 || tiles > 1024 || (long long)tiles * width * height * 432 >= (1LL << 30))
+        return fail(ctx, DCN_INVALID_SHAPE, "a body batches 1..1024 tiles");
     DeviceGuard guard(ctx->device);
     auto* b = new dcn_body();
     b->ctx = ctx;
@@ -371,6 +383,7 @@ dcn_status dcn_body_create(dcn_context* ctx, int height, int width, int branch, 
     b->w = width;
     b->branch = branch;
     b->blocks = blocks;
+    b->tiles = tiles;
     const hipStream_t s = (hipStream_t)stream;
     auto bail = [&](dcn_status st) {
         dcn_body_destroy(b);
@@ -398,28 +411,29 @@ dcn_status dcn_body_create(dcn_context* ctx, int height, int width, int branch, 
         if (st != DCN_OK) return bail(st);
     }
     const size_t plane = (size_t)width * height;
+    const size_t T = (size_t)tiles;
     dcn_status st = DCN_OK;
     auto a16 = [&](uint16_t** p, size_t elems) {
         if (st == DCN_OK) st = alloc(ctx, b->buffers, p, elems);
     };
-    a16(&b->cond_cb8, dcn::cb8_tensor_elems(196, height, width));
-    a16(&b->deform_cb8, dcn::cb8_tensor_elems(128, height, width));
-    a16(&b->off_a, dcn::cb8_tensor_elems(64, height, width));
-    a16(&b->off_b, dcn::cb8_tensor_elems(64, height, width));
-    a16(&b->offset, 288 * plane);
-    a16(&b->mask, 144 * plane);
-    a16(&b->bb_in, dcn::cb8_tensor_elems(bb_in, height, width));
-    for (auto& f : b->feat) a16(&f, dcn::cb8_tensor_elems(64, height, width));
+    a16(&b->cond_cb8, T * dcn::cb8_tensor_elems(196, height, width));
+    a16(&b->deform_cb8, T * dcn::cb8_tensor_elems(128, height, width));
+    a16(&b->off_a, T * dcn::cb8_tensor_elems(64, height, width));
+    a16(&b->off_b, T * dcn::cb8_tensor_elems(64, height, width));
+    a16(&b->offset, T * 288 * plane);
+    a16(&b->mask, T * 144 * plane);
+    a16(&b->bb_in, T * dcn::cb8_tensor_elems(bb_in, height, width));
+    for (auto& f : b->feat) a16(&f, T * dcn::cb8_tensor_elems(64, height, width));
     if (st != DCN_OK) return bail(st);
     // CB8 borders and padding channels are zero once and never written again, so a
     // step (and its captured graph) holds no memset.
     for (uint16_t* p : {b->cond_cb8, b->deform_cb8, b->off_a, b->off_b, b->bb_in, b->feat[0],
                         b->feat[1]}) {
         size_t elems = 0;
-        if (p == b->cond_cb8) elems = dcn::cb8_tensor_elems(196, height, width);
-        else if (p == b->deform_cb8) elems = dcn::cb8_tensor_elems(128, height, width);
-        else if (p == b->bb_in) elems = dcn::cb8_tensor_elems(bb_in, height, width);
-        else elems = dcn::cb8_tensor_elems(64, height, width);
+        if (p == b->cond_cb8) elems = T * dcn::cb8_tensor_elems(196, height, width);
+        else if (p == b->deform_cb8) elems = T * dcn::cb8_tensor_elems(128, height, width);
+        else if (p == b->bb_in) elems = T * dcn::cb8_tensor_elems(bb_in, height, width);
+        else elems = T * dcn::cb8_tensor_elems(64, height, width);
         if (hipMemsetAsync(p, 0, elems * 2, s) != hipSuccess)
             return bail(fail(ctx, DCN_COMMAND_FAILED, "clearing body buffers failed"));
     }
@@ -443,8 +457,14 @@ dcn_status run_backbone(dcn_body* body, void* d_feat_prop_out, hipStream_t s) {
     dcn_context* ctx = body->ctx;
     const int NCHW = DCN_TENSOR_NCHW, CB8 = DCN_TENSOR_CB8;
     const int aligned_c = 64 * (body->branch + 1);
+    const long feat_ts = cb8_image(body, 8), bb_ts = cb8_image(body, 8 * (body->branch + 2));
+    const long out_ts = 64L * body->h * body->w;
+    dcn::ConvBatch in_conv;
+    in_conv.images = body->tiles;
+    in_conv.x = bb_ts;
+    in_conv.out = feat_ts;
     DCN_TRY(run_conv(ctx, body->backbone[0], body->bb_in, 1, nullptr, NCHW, nullptr, NCHW,
-                     body->feat[0], CB8, s));
+                     body->feat[0], CB8, s, in_conv));
     // Each block's two convs run as one launch (t = ReLU(conv(x)) stays in LDS).
     int x = 0;
     for (int i = 0; i < body->blocks; ++i) {
@@ -452,11 +472,17 @@ dcn_status run_backbone(dcn_body* body, void* d_feat_prop_out, hipStream_t s) {
         const bool last = i + 1 == body->blocks;
         const dcn_conv* c1 = body->backbone[1 + 2 * i];
         const dcn_conv* c2 = body->backbone[2 + 2 * i];
+        dcn::ConvBatch pb;
+        pb.images = body->tiles;
+        pb.x = feat_ts;
+        pb.res1 = feat_ts;
+        pb.res2 = last ? bb_ts : 0;
+        pb.out = last ? out_ts : feat_ts;
         DCN_HIP(ctx, dcn::launch_conv3x3_pair(c1->g, c2->g, body->feat[x], c1->wpk, c1->bias, 2, c2->wpk,
                                               c2->bias, 0, 0.1f, body->feat[x], CB8,
                                               last ? body->bb_in : nullptr, CB8,
                                               last ? (uint16_t*)d_feat_prop_out : body->feat[y],
-                                              last ? NCHW : CB8, s, aligned_c));
+                                              last ? NCHW : CB8, s, aligned_c, pb));
         x = y;
     }
     return DCN_OK;
@@ -491,21 +517,31 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
                                            (const uint16_t*)d_feat_n2, (const uint16_t*)d_flow1,
                                            (const uint16_t*)d_prev_flow, has_second_order ? 1 : 0,
                                            prefix, body->branch, (uint16_t*)d_flow2_out, body->cond_cb8,
-                                           body->deform_cb8, body->bb_in, H, W, s));
+                                           body->deform_cb8, body->bb_in, H, W, s, body->tiles));
+    const long off_ts = cb8_image(body, 8);
     // conv_offset: 196 -> 64 -> 64 -> 64 (LeakyReLU 0.1) -> 432, the last one turning its
     // output into offsets and masks in its epilogue.
+    dcn::ConvBatch cond_conv;
+    cond_conv.images = body->tiles;
+    cond_conv.x = cb8_image(body, 25);
+    cond_conv.out = off_ts;
     DCN_TRY(run_conv(ctx, body->offset_conv[0], body->cond_cb8, 1, nullptr, NCHW, nullptr, NCHW,
-                     body->off_a, CB8, s));
+                     body->off_a, CB8, s, cond_conv));
     const dcn_conv* c1 = body->offset_conv[1];
     const dcn_conv* c2 = body->offset_conv[2];
+    dcn::ConvBatch off_pair;
+    off_pair.images = body->tiles;
+    off_pair.x = off_ts;
+    off_pair.out = off_ts;
     DCN_HIP(ctx, dcn::launch_conv3x3_pair(c1->g, c2->g, body->off_a, c1->wpk, c1->bias, 1, c2->wpk, c2->bias,
-                                          1, 0.1f, nullptr, NCHW, nullptr, NCHW, body->off_b, CB8, s));
+                                          1, 0.1f, nullptr, NCHW, nullptr, NCHW, body->off_b, CB8, s, 0, off_pair));
     const dcn_conv* c3 = body->offset_conv[3];
     DCN_HIP(ctx, dcn::launch_conv3x3_offsets(c3->g, body->off_b, c3->wpk, c3->bias,
                                              (const uint16_t*)d_flow1, (const uint16_t*)d_flow2_out,
-                                             body->offset, body->mask, s));
+                                             body->offset, body->mask, s, body->tiles));
     // The DCN writes the aligned feature into the backbone input (CB8, after the prefix).
-    const dcn_shape ds = body_dcn_shape(H, W);
+    dcn_shape ds = body_dcn_shape(H, W);
+    ds.batch = body->tiles;
     dcn::FusedGeometry g;
     dcn::fused_geometry(ds, &g);
     const dcn::FusedConfig cfg{dcn::kVariantNarrow, 1, 12, dcn::kSamplerFast};
@@ -535,7 +571,7 @@ dcn_status dcn_body_initial_step_dev(dcn_body* body, const void* d_feat_current,
         prefix[i] = (const uint16_t*)d_prefix[i];
     }
     DCN_HIP(ctx, dcn::launch_body_initial((const uint16_t*)d_feat_current, prefix, body->branch, body->bb_in,
-                                          body->h, body->w, s));
+                                          body->h, body->w, s, body->tiles));
     return run_backbone(body, d_feat_prop_out, s);
 }
 
@@ -599,6 +635,11 @@ void dcn_clip_destroy(dcn_clip* clip) {
 
 dcn_status dcn_clip_create(dcn_context* ctx, int height, int width, int frames, int blocks,
                            const dcn_body_weights* weights, void* stream, dcn_clip** out) {
+    return dcn_clip_create_tiles(ctx, height, width, frames, blocks, 1, weights, stream, out);
+}
+
+dcn_status dcn_clip_create_tiles(dcn_context* ctx, int height, int width, int frames, int blocks, int tiles,
+                                 const dcn_body_weights* weights, void* stream, dcn_clip** out) {
     if (!ctx || !out) return DCN_INVALID_ARGUMENT;
     *out = nullptr;
     if (frames <= 0) return fail(ctx, DCN_INVALID_SHAPE, "a clip needs at least one frame");
@@ -611,15 +652,17 @@ dcn_status dcn_clip_create(dcn_context* ctx, int height, int width, int frames, 
     c->w = width;
     c->frames = frames;
     c->blocks = blocks;
+    c->tiles = tiles;
     auto bail = [&](dcn_status st) {
         dcn_clip_destroy(c);
         return st;
     };
     for (int b = 0; b < 4; ++b) {
-        const dcn_status st = dcn_body_create(ctx, height, width, b, blocks, &weights[b], stream, &c->body[b]);
+        const dcn_status st =
+            dcn_body_create_tiles(ctx, height, width, b, blocks, tiles, &weights[b], stream, &c->body[b]);
         if (st != DCN_OK) return bail(st);
     }
-    const size_t plane = (size_t)width * height;
+    const size_t plane = (size_t)width * height * tiles;
     dcn_status st = alloc(ctx, c->buffers, &c->zero_feat, 64 * plane);
     if (st == DCN_OK) st = alloc(ctx, c->buffers, &c->flow2, 2 * plane);
     if (st != DCN_OK) return bail(st);
@@ -653,7 +696,8 @@ dcn_status dcn_clip_run_dev(dcn_clip* clip, const void* d_spatial, const void* d
         sizes.resize(n);
     }
     DeviceGuard guard(ctx->device);
-    const size_t plane = (size_t)clip->w * clip->h;
+    // Every per-frame tensor holds all tiles: [tiles][C][H][W].
+    const size_t plane = (size_t)clip->w * clip->h * clip->tiles;
     const uint16_t* spatial = (const uint16_t*)d_spatial;
     const uint16_t* bflows = (const uint16_t*)d_backward_flows;
     const uint16_t* fflows = (const uint16_t*)d_forward_flows;

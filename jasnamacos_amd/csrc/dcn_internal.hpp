@@ -143,17 +143,25 @@ ConvGeometry conv_geometry(int cin, int cout, int height, int width);
 size_t conv_packed_bytes(const ConvGeometry& g);
 hipError_t launch_conv_prepack(const ConvGeometry& g, const uint16_t* w, const uint16_t* bias,
                                void* wpk, float* bpk, hipStream_t stream);
+// A batch of `images` independent images in one launch (grid z): each tensor argument
+// advances by its per-image stride in elements (zero for a tensor shared by the batch).
+struct ConvBatch {
+    int images = 1;
+    long x = 0, res1 = 0, res2 = 0, out = 0;
+};
 hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                           const float* bias, int act, float slope, const uint16_t* res1,
                           int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,
-                          int out_layout, hipStream_t stream, int res2_coff = 0);
+                          int out_layout, hipStream_t stream, int res2_coff = 0,
+                          const ConvBatch& batch = ConvBatch{});
 // Two chained 64 -> 64 convs in one launch: t = half(act1(conv1(x) + b1)) held in LDS,
 // then conv2 over t with launch_conv3x3's epilogue; bit-identical to two launches.
 hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, const void* x_cb8,
                                const void* wpk1, const float* bias1, int act1, const void* wpk2,
                                const float* bias2, int act2, float slope, const uint16_t* res1,
                                int res1_layout, const uint16_t* res2, int res2_layout,
-                               uint16_t* out, int out_layout, hipStream_t stream, int res2_coff = 0);
+                               uint16_t* out, int out_layout, hipStream_t stream, int res2_coff = 0,
+                               const ConvBatch& batch = ConvBatch{});
 // SPyNet (dcn_kernels_spynet.hip).
 constexpr int kSpynetMaxLevels = DCN_SPYNET_LEVELS;
 struct ConvKGeometry {
@@ -196,21 +204,22 @@ hipError_t launch_spynet_small(int batch, int pairs, int levels, const int* heig
 
 // The last conv_offset layer (cout 432) with prepare_dcn_offsets_fp16 in its epilogue:
 // raw = half(conv + bias), offsets = half(10 tanh(raw) + flow), masks = half(sigmoid(raw)).
+// `images` images: CB8 inputs, flows [2][plane], offsets and masks at their own strides.
 hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                                   const float* bias, const uint16_t* flow1, const uint16_t* flow2,
-                                  uint16_t* offset, uint16_t* mask, hipStream_t stream);
+                                  uint16_t* offset, uint16_t* mask, hipStream_t stream, int images = 1);
 // One kernel for the body's temporal inputs: second-order flow (NCHW), conditions and
 // the DCN input in CB8, and the backbone input's leading [feat_current, prefix...] in CB8.
 // Backbone input of a branch's first step: [feat_current, prefix...] and a zero aligned
 // slot, CB8 with 64 * (nprefix + 2) channels.
 hipError_t launch_body_initial(const uint16_t* feat_current, const uint16_t* const* prefix, int nprefix,
-                               uint16_t* bb_cb8, int H, int W, hipStream_t stream);
+                               uint16_t* bb_cb8, int H, int W, hipStream_t stream, int images = 1);
 hipError_t launch_body_temporal(const uint16_t* feat_prop, const uint16_t* feat_current,
                                 const uint16_t* feat_n2, const uint16_t* flow1,
                                 const uint16_t* prev_flow, int has_second_order,
                                 const uint16_t* const* prefix, int nprefix, uint16_t* flow2,
                                 uint16_t* cond_cb8, uint16_t* deform_cb8, uint16_t* bb_cb8, int H,
-                                int W, hipStream_t stream);
+                                int W, hipStream_t stream, int images = 1);
 hipError_t launch_second_order_flow(const uint16_t* flow1, const uint16_t* prev, uint16_t* flow2,
                                     int H, int W, int has_second_order, hipStream_t stream);
 hipError_t launch_temporal_assemble(const uint16_t* feat_prop, const uint16_t* feat_current,

@@ -233,6 +233,41 @@ struct BodyTemporalArgs {
     uint16_t *flow2, *cond, *deform, *bb;
 };
 
+// The arguments of image blockIdx.z of a batch of tiles: features [64][H][W] and flows
+// [2][H][W] per image; CB8 conditions (25 blocks), DCN input (16) and backbone input
+// (8 (nprefix + 2)) per image. Plain fields, no array and no member function: either
+// would keep the local struct in scratch memory (measured: 7.4 -> 18 us).
+struct BodyImage {
+    const uint16_t *feat_prop, *feat_current, *feat_n2, *flow1, *prev_flow, *p0, *p1, *p2;
+    uint16_t *flow2, *cond, *deform, *bb;
+    int nprefix, has_second_order, H, W;
+};
+
+__device__ __forceinline__ BodyImage temporal_image(const BodyTemporalArgs& a0) {
+    BodyImage a;
+    const long z = blockIdx.z;
+    const long fs = z * 64 * a0.H * a0.W;  // per-image offset of a feature, then of a flow
+    const long ls = z * 2 * a0.H * a0.W;
+    const long unit = (long)(a0.H + 2 * kPad) * (a0.W + 2 * kPad) * 8;
+    a.feat_prop = a0.feat_prop + fs;
+    a.feat_current = a0.feat_current + fs;
+    a.feat_n2 = a0.feat_n2 + fs;
+    a.flow1 = a0.flow1 + ls;
+    a.prev_flow = a0.prev_flow + ls;
+    a.p0 = a0.prefix[0] + fs;
+    a.p1 = a0.prefix[1] + fs;
+    a.p2 = a0.prefix[2] + fs;
+    a.flow2 = a0.flow2 + ls;
+    a.cond = a0.cond + z * 25 * unit;
+    a.deform = a0.deform + z * 16 * unit;
+    a.bb = a0.bb + z * 8 * (a0.nprefix + 2) * unit;
+    a.nprefix = a0.nprefix;
+    a.has_second_order = a0.has_second_order;
+    a.H = a0.H;
+    a.W = a0.W;
+    return a;
+}
+
 // The body's temporal inputs in one pass. Workgroup row blockIdx.y selects an 8-channel
 // output block: 0-24 the conditions [warp(feat_prop, flow1), feat_current,
 // warp(feat_n2, flow2), flow1, flow2, 4 zero channels], 25-40 the DCN input
@@ -240,7 +275,8 @@ struct BodyTemporalArgs {
 // per pixel writes the block's 16 bytes of CB8. The second-order flow of a pixel is
 // recomputed by each thread that needs it (same arithmetic, same bits) and stored by
 // the flow block's thread.
-__global__ __launch_bounds__(256) void body_temporal_kernel(BodyTemporalArgs a) {
+__global__ __launch_bounds__(256) void body_temporal_kernel(BodyTemporalArgs a0) {
+    const BodyImage a = temporal_image(a0);
     const int plane = a.H * a.W;
     const int p = blockIdx.x * 256 + threadIdx.x;
     if (p >= plane) return;
@@ -286,7 +322,7 @@ __global__ __launch_bounds__(256) void body_temporal_kernel(BodyTemporalArgs a) 
         dst = a.bb;
         dblock = kind - 41;
         const int src = dblock >> 3;
-        const uint16_t* base = src == 0 ? a.feat_current : a.prefix[src - 1];
+        const uint16_t* base = src == 0 ? a.feat_current : (src == 1 ? a.p0 : (src == 2 ? a.p1 : a.p2));
         copy_src = base + (size_t)(dblock & 7) * 8 * pl;
     }
     u32x4 out;
@@ -312,7 +348,8 @@ __global__ __launch_bounds__(256) void body_temporal_kernel(BodyTemporalArgs a) 
 // The backbone input of a branch's first step: [feat_current, prefix...] copied into CB8
 // and the aligned slot (the last 64 channels) written as zeros. Workgroup row blockIdx.y
 // is the 8-channel output block.
-__global__ __launch_bounds__(256) void body_initial_kernel(BodyTemporalArgs a) {
+__global__ __launch_bounds__(256) void body_initial_kernel(BodyTemporalArgs a0) {
+    const BodyImage a = temporal_image(a0);
     const int plane = a.H * a.W;
     const int p = blockIdx.x * 256 + threadIdx.x;
     if (p >= plane) return;
@@ -323,7 +360,7 @@ __global__ __launch_bounds__(256) void body_initial_kernel(BodyTemporalArgs a) {
     const int src = dblock >> 3;
     u32x4 out = {0u, 0u, 0u, 0u};
     if (src <= a.nprefix) {
-        const uint16_t* base = src == 0 ? a.feat_current : a.prefix[src - 1];
+        const uint16_t* base = src == 0 ? a.feat_current : (src == 1 ? a.p0 : (src == 2 ? a.p1 : a.p2));
         const uint16_t* copy_src = base + (size_t)(dblock & 7) * 8 * pl;
         uint16_t h[8];
 #pragma unroll
@@ -362,8 +399,8 @@ hipError_t launch_body_temporal(const uint16_t* feat_prop, const uint16_t* feat_
                                 const uint16_t* prev_flow, int has_second_order,
                                 const uint16_t* const* prefix, int nprefix, uint16_t* flow2,
                                 uint16_t* cond_cb8, uint16_t* deform_cb8, uint16_t* bb_cb8, int H,
-                                int W, hipStream_t stream) {
-    if (nprefix < 0 || nprefix > 3) return hipErrorInvalidValue;
+                                int W, hipStream_t stream, int images) {
+    if (nprefix < 0 || nprefix > 3 || images < 1) return hipErrorInvalidValue;
     BodyTemporalArgs a{};
     a.feat_prop = feat_prop;
     a.feat_current = feat_current;
@@ -379,14 +416,14 @@ hipError_t launch_body_temporal(const uint16_t* feat_prop, const uint16_t* feat_
     a.cond = cond_cb8;
     a.deform = deform_cb8;
     a.bb = bb_cb8;
-    const dim3 grid(blocks_for((long)H * W), (unsigned)(41 + 8 * (1 + nprefix)));
+    const dim3 grid(blocks_for((long)H * W), (unsigned)(41 + 8 * (1 + nprefix)), (unsigned)images);
     hipLaunchKernelGGL(body_temporal_kernel, grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 
 hipError_t launch_body_initial(const uint16_t* feat_current, const uint16_t* const* prefix, int nprefix,
-                               uint16_t* bb_cb8, int H, int W, hipStream_t stream) {
-    if (nprefix < 0 || nprefix > 3) return hipErrorInvalidValue;
+                               uint16_t* bb_cb8, int H, int W, hipStream_t stream, int images) {
+    if (nprefix < 0 || nprefix > 3 || images < 1) return hipErrorInvalidValue;
     BodyTemporalArgs a{};
     a.feat_current = feat_current;
     for (int i = 0; i < 3; ++i) a.prefix[i] = i < nprefix ? prefix[i] : feat_current;
@@ -394,7 +431,7 @@ hipError_t launch_body_initial(const uint16_t* feat_current, const uint16_t* con
     a.H = H;
     a.W = W;
     a.bb = bb_cb8;
-    const dim3 grid(blocks_for((long)H * W), (unsigned)(8 * (2 + nprefix)));
+    const dim3 grid(blocks_for((long)H * W), (unsigned)(8 * (2 + nprefix)), (unsigned)images);
     hipLaunchKernelGGL(body_initial_kernel, grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }

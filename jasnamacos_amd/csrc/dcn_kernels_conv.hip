@@ -51,7 +51,24 @@ struct ConvArgs {
     int H, W, Hp, Wp, CB, KB, ksteps, NBT, Cout, tiles, act;
     float slope;
     uint32_t magic_cb;
+    // Image blockIdx.z of a batch: every tensor advances by its per-image stride (elements).
+    long xin_ts, res1_ts, res2_ts, out_ts, flow_ts, offset_ts, mask_ts;
 };
+
+// The arguments of image blockIdx.z of a batch of images.
+__device__ __forceinline__ ConvArgs conv_image(const ConvArgs& a0) {
+    ConvArgs a = a0;
+    const long z = blockIdx.z;
+    a.xin = static_cast<const uint16_t*>(a0.xin) + z * a0.xin_ts;
+    if (a.res1) a.res1 += z * a0.res1_ts;
+    if (a.res2) a.res2 += z * a0.res2_ts;
+    if (a.out) a.out += z * a0.out_ts;
+    if (a.flow1) a.flow1 += z * a0.flow_ts;
+    if (a.flow2) a.flow2 += z * a0.flow_ts;
+    if (a.offset) a.offset += z * a0.offset_ts;
+    if (a.mask) a.mask += z * a0.mask_ts;
+    return a;
+}
 
 __device__ __forceinline__ size_t conv_index(int layout, int c, int y, int x, int H, int W, int Hp,
                                              int Wp) {
@@ -60,7 +77,8 @@ __device__ __forceinline__ size_t conv_index(int layout, int c, int y, int x, in
 }
 
 template <int NW, int U>
-__global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a) {
+__global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a0) {
+    const ConvArgs a = conv_image(a0);
     constexpr int NB = kConvNbc;
     extern __shared__ float red[];  // [NW][NB][4][65]
     const int tid = threadIdx.x;
@@ -174,7 +192,8 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a) {
 // Same K split and summation order as conv3x3_kernel<NW, U>: the results are the same
 // bits.
 template <int NW, int U, int NB, int RT, int MINW>
-__global__ __launch_bounds__(64 * NW, MINW) void conv_offsets_kernel(ConvArgs a) {
+__global__ __launch_bounds__(64 * NW, MINW) void conv_offsets_kernel(ConvArgs a0) {
+    const ConvArgs a = conv_image(a0);
     extern __shared__ __attribute__((aligned(16))) f32x4 red4[];  // [NW][RT][NB][64] partial sums
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -354,6 +373,7 @@ struct PairArgs {
     float slope;
     int res1_layout, res2_layout, out_layout, res2_coff;
     int H, W, Hp, Wp, tiles_x, tiles;
+    long xin_ts, res1_ts, res2_ts, out_ts;  // per-image strides of a batch (blockIdx.z)
 };
 
 __host__ __device__ constexpr size_t pair_lds_bytes(int nw) {
@@ -361,7 +381,15 @@ __host__ __device__ constexpr size_t pair_lds_bytes(int nw) {
 }
 
 template <int NW>
-__global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
+__global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a0) {
+    PairArgs a = a0;
+    {
+        const long z = blockIdx.z;
+        a.xin = static_cast<const uint16_t*>(a0.xin) + z * a0.xin_ts;
+        if (a.res1) a.res1 += z * a0.res1_ts;
+        if (a.res2) a.res2 += z * a0.res2_ts;
+        a.out += z * a0.out_ts;
+    }
     constexpr int NB = kConvNbc;
     constexpr int KMAX = (kPairKsteps + NW - 1) / NW;  // K-steps of the busiest wave
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -580,8 +608,13 @@ hipError_t launch_conv_prepack(const ConvGeometry& g, const uint16_t* w, const u
 
 namespace {
 
-hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, hipStream_t stream) {
+hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, const ConvBatch& batch, hipStream_t stream) {
     constexpr int NW = 8, U = 4;
+    if (batch.images < 1) return hipErrorInvalidValue;
+    a.xin_ts = batch.x;
+    a.res1_ts = batch.res1;
+    a.res2_ts = batch.res2;
+    a.out_ts = batch.out;
     a.H = g.h;
     a.W = g.w;
     a.Hp = g.h + 2 * kPad;
@@ -596,7 +629,7 @@ hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, hipStream_t stream) {
     a.tiles = (g.h * g.w + 15) / 16;
     a.magic_cb = magic_for(g.cb);
     const size_t lds = (size_t)NW * kConvNbc * 4 * 65 * sizeof(float);
-    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)g.chunks);
+    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)g.chunks, (unsigned)batch.images);
     hipLaunchKernelGGL((conv3x3_kernel<NW, U>), grid, dim3(64 * NW), lds, stream, a);
     return hipGetLastError();
 }
@@ -605,8 +638,8 @@ hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, hipStream_t stream) {
 
 hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                                   const float* bias, const uint16_t* flow1, const uint16_t* flow2,
-                                  uint16_t* offset, uint16_t* mask, hipStream_t stream) {
-    if (g.cout != 432) return hipErrorInvalidValue;
+                                  uint16_t* offset, uint16_t* mask, hipStream_t stream, int images) {
+    if (g.cout != 432 || images < 1) return hipErrorInvalidValue;
     constexpr int NW = 8, U = 2, NB = 4, RT = 1, MINW = 6;
     ConvArgs a{};
     a.xin = x_cb8;
@@ -630,12 +663,18 @@ hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, cons
     a.Cout = g.cout;
     a.tiles = (g.h * g.w + 16 * RT - 1) / (16 * RT);
     a.magic_cb = magic_for(g.cb);
+    const long plane = (long)g.h * g.w;
+    a.xin_ts = (long)g.cb * a.Hp * a.Wp * 8;
+    a.flow_ts = 2 * plane;
+    a.offset_ts = 288 * plane;
+    a.mask_ts = 144 * plane;
     constexpr size_t lds = (size_t)NW * RT * NB * 64 * sizeof(f32x4);
     auto kernel = &conv_offsets_kernel<NW, U, NB, RT, MINW>;
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)((g.cout + 16 * NB - 1) / (16 * NB)));
+    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)((g.cout + 16 * NB - 1) / (16 * NB)),
+                    (unsigned)images);
     hipLaunchKernelGGL(kernel, grid, dim3(64 * NW), lds, stream, a);
     return hipGetLastError();
 }
@@ -643,7 +682,7 @@ hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, cons
 hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                           const float* bias, int act, float slope, const uint16_t* res1,
                           int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,
-                          int out_layout, hipStream_t stream, int res2_coff) {
+                          int out_layout, hipStream_t stream, int res2_coff, const ConvBatch& batch) {
     ConvArgs a{};
     a.res2_coff = res2_coff;
     a.xin = x_cb8;
@@ -657,16 +696,17 @@ hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* 
     a.out_layout = out_layout;
     a.act = act;
     a.slope = slope;
-    return run_conv(g, a, stream);
+    return run_conv(g, a, batch, stream);
 }
 
 hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, const void* x_cb8,
                                const void* wpk1, const float* bias1, int act1, const void* wpk2,
                                const float* bias2, int act2, float slope, const uint16_t* res1,
                                int res1_layout, const uint16_t* res2, int res2_layout,
-                               uint16_t* out, int out_layout, hipStream_t stream, int res2_coff) {
+                               uint16_t* out, int out_layout, hipStream_t stream, int res2_coff,
+                               const ConvBatch& batch) {
     if (g1.cin != 64 || g1.cout != 64 || g2.cin != 64 || g2.cout != 64 || g1.h != g2.h ||
-        g1.w != g2.w || g1.ksteps != kPairKsteps || g1.nbt != kConvNbc)
+        g1.w != g2.w || g1.ksteps != kPairKsteps || g1.nbt != kConvNbc || batch.images < 1)
         return hipErrorInvalidValue;
     constexpr int NW = 8;
     PairArgs a{};
@@ -685,6 +725,10 @@ hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, c
     a.res2_layout = res2_layout;
     a.out_layout = out_layout;
     a.res2_coff = res2_coff;
+    a.xin_ts = batch.x;
+    a.res1_ts = batch.res1;
+    a.res2_ts = batch.res2;
+    a.out_ts = batch.out;
     a.H = g1.h;
     a.W = g1.w;
     a.Hp = g1.h + 2 * kPad;
@@ -698,7 +742,8 @@ hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, c
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)((a.tiles + 7) / 8 * 8)), dim3(64 * NW), lds, stream, a);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((a.tiles + 7) / 8 * 8), 1, (unsigned)batch.images), dim3(64 * NW),
+                       lds, stream, a);
     return hipGetLastError();
 }
 

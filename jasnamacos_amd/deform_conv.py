@@ -470,13 +470,15 @@ class HipDeformConv:
                                                      _ptr(weight), _ptr(bias), _stream(stream), C.byref(handle)))
         return Conv3x3(self, handle.value, cin, cout, height, width)
 
-    def body(self, height, width, weights: dict, branch: int = 0, blocks: int = 5, stream=None) -> "PropagationBody":
+    def body(self, height, width, weights: dict, branch: int = 0, blocks: int = 5, stream=None,
+             tiles: int = 1) -> "PropagationBody":
         """weights: device tensors "offset_w{0..3}", "offset_b{0..3}", "dcn_w", "dcn_b",
-        "backbone_w{0..2*blocks}", "backbone_b{0..2*blocks}" (OIHW FP16)."""
+        "backbone_w{0..2*blocks}", "backbone_b{0..2*blocks}" (OIHW FP16). tiles > 1: every
+        step tensor holds that many independent tiles, [tiles][C][H][W]."""
         w = _body_weights(weights, blocks)
         handle = C.c_void_p()
-        self._check(self._lib.dcn_body_create(self.ctx, int(height), int(width), int(branch), int(blocks),
-                                              C.byref(w), _stream(stream), C.byref(handle)))
+        self._check(self._lib.dcn_body_create_tiles(self.ctx, int(height), int(width), int(branch), int(blocks),
+                                                    int(tiles), C.byref(w), _stream(stream), C.byref(handle)))
         return PropagationBody(self, handle.value, height, width, branch, blocks)
 
     def bicubic_quarter_f16_dev(self, channels, height, width, src, out, stream=None) -> None:
@@ -503,15 +505,16 @@ class HipDeformConv:
                                                 _stream(stream), C.byref(handle)))
         return SpyNet(self, handle.value, height, width, max_frames)
 
-    def clip(self, height, width, frames, weights, blocks: int = 5, stream=None) -> "PropagationClip":
+    def clip(self, height, width, frames, weights, blocks: int = 5, stream=None, tiles: int = 1) -> "PropagationClip":
         """The four propagation branches over `frames` frames; weights: four body weight dicts
-        (backward_1, forward_1, backward_2, forward_2), as for body()."""
+        (backward_1, forward_1, backward_2, forward_2), as for body(). tiles > 1: spatial
+        [T][tiles][64][H][W], flows [T-1][tiles][2][H][W], propagated [4][T][tiles][64][H][W]."""
         if len(weights) != 4:
             raise DeformConvError(INVALID_ARGUMENT, "a clip needs four branch weight sets")
         ws = (_lib.DcnBodyWeights * 4)(*[_body_weights(w, blocks) for w in weights])
         handle = C.c_void_p()
-        self._check(self._lib.dcn_clip_create(self.ctx, int(height), int(width), int(frames), int(blocks), ws,
-                                              _stream(stream), C.byref(handle)))
+        self._check(self._lib.dcn_clip_create_tiles(self.ctx, int(height), int(width), int(frames), int(blocks),
+                                                    int(tiles), ws, _stream(stream), C.byref(handle)))
         return PropagationClip(self, handle.value, height, width, frames, blocks)
 
 

@@ -294,6 +294,44 @@ def test_body_step_matches_oracle_chain(gpu_ctx, torch, h, w, branch, blocks):
     body.free()
 
 
+@pytest.mark.parametrize("h,w,branch,tiles", [(16, 24, 1, 3), (13, 21, 0, 2)])
+def test_body_tiles_equal_single_tiles(gpu_ctx, torch, h, w, branch, tiles):
+    """A body over `tiles` tiles per step == one single-tile body per tile, bit for bit
+    (full step and a branch's first step); 13 x 21 puts DCN pixel tiles across tiles."""
+    blocks = 2
+    rng = np.random.default_rng(70 + h + tiles)
+    weights = br.body_weights(rng, branch, blocks)
+    wd = {k: dev(torch, v) for k, v in weights.items()}
+    xs = [br.body_inputs(rng, h, w, branch) for _ in range(tiles)]
+    cat = lambda k: dev(torch, np.concatenate([x[k] for x in xs]))  # noqa: E731
+    log("case: body tiles", h, w, "branch", branch, "tiles", tiles)
+    big = gpu_ctx.body(h, w, wd, branch=branch, blocks=blocks, tiles=tiles)
+    plane = h * w
+    flow2 = torch.zeros(tiles * 2 * plane, dtype=torch.int16, device="cuda")
+    out = torch.zeros(tiles * 64 * plane, dtype=torch.int16, device="cuda")
+    first = torch.zeros_like(out)
+    prefix = [dev(torch, np.concatenate([x["prefix"][i] for x in xs])) for i in range(branch)]
+    big.step_dev(cat("feat_current"), cat("flow1"), cat("prev_flow"), cat("feat_prop"), cat("feat_n2"), flow2, out,
+                 True, prefix or None)
+    big.initial_step_dev(cat("feat_current"), first, prefix or None)
+    one = gpu_ctx.body(h, w, wd, branch=branch, blocks=blocks)
+    f2 = torch.zeros(2 * plane, dtype=torch.int16, device="cuda")
+    o1 = torch.zeros(64 * plane, dtype=torch.int16, device="cuda")
+    i1 = torch.zeros_like(o1)
+    for t, x in enumerate(xs):
+        xd = {k: dev(torch, x[k]) for k in ("feat_current", "flow1", "prev_flow", "feat_prop", "feat_n2")}
+        pre = [dev(torch, p) for p in x["prefix"]]
+        one.step_dev(xd["feat_current"], xd["flow1"], xd["prev_flow"], xd["feat_prop"], xd["feat_n2"], f2, o1, True,
+                     pre or None)
+        one.initial_step_dev(xd["feat_current"], i1, pre or None)
+        torch.cuda.synchronize()
+        assert torch.equal(flow2[t * 2 * plane:(t + 1) * 2 * plane], f2), t
+        assert torch.equal(out[t * 64 * plane:(t + 1) * 64 * plane], o1), t
+        assert torch.equal(first[t * 64 * plane:(t + 1) * 64 * plane], i1), t
+    big.free()
+    one.free()
+
+
 def test_body_graph_replays_match_eager(gpu_ctx, torch):
     h, w, blocks = 32, 32, 3
     weights, x, wd, body, xd = _body_case(torch, gpu_ctx, h, w, 0, blocks, 77)

@@ -179,6 +179,32 @@ def test_clip_chunks_equal_independent_clips(gpu_ctx, dcn, torch):
     assert got.shape == (4, frames, 64 * plane)
 
 
+def test_clip_tiles_equal_single_tile_clips(gpu_ctx, torch):
+    """A clip over 2 tiles ([T][tiles][...] tensors) == one clip per tile, bit for bit."""
+    frames, h, w, blocks, tiles = 4, 16, 24, 2, 2
+    cases = [_clip_case(torch, frames, h, w, blocks, 90 + t) for t in range(tiles)]
+    wd = cases[0][1]
+    plane = h * w
+    log("case: clip tiles", frames, h, w, tiles)
+
+    def interleave(key, per_frame):
+        arrs = [c[2][key].reshape(-1, per_frame) for c in cases]
+        return dev(torch, np.stack(arrs, axis=1).ravel())
+
+    spatial = interleave("spatial", 64 * plane)
+    bflows = interleave("bflows", 2 * plane)
+    fflows = interleave("fflows", 2 * plane)
+    clip = gpu_ctx.clip(h, w, frames, wd, blocks=blocks, tiles=tiles)
+    prop = torch.zeros(4 * frames * tiles * 64 * plane, dtype=torch.int16, device="cuda")
+    clip.run_dev(spatial, bflows, fflows, prop)
+    torch.cuda.synchronize()
+    got = host(prop).reshape(4, frames, tiles, 64 * plane)
+    clip.free()
+    for t, c in enumerate(cases):
+        want = _run_clip(torch, gpu_ctx, wd, c[3], frames, h, w, blocks)
+        assert np.array_equal(got[:, :, t].view(np.uint16), want.view(np.uint16)), t
+
+
 def test_clip_nonfinite_is_detected_and_ladder_gives_up(gpu_ctx, dcn, torch):
     frames, h, w, blocks = 6, 8, 8, 1
     weights, wd, x, xd = _clip_case(torch, frames, h, w, blocks, 11)
