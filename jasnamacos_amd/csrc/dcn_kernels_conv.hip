@@ -55,10 +55,9 @@ struct ConvArgs {
     long xin_ts, res1_ts, res2_ts, out_ts, flow_ts, offset_ts, mask_ts;
 };
 
-// The arguments of image blockIdx.z of a batch of images.
-__device__ __forceinline__ ConvArgs conv_image(const ConvArgs& a0) {
+// The arguments of image z of a batch of images.
+__device__ __forceinline__ ConvArgs conv_image_at(const ConvArgs& a0, long z) {
     ConvArgs a = a0;
-    const long z = blockIdx.z;
     a.xin = static_cast<const uint16_t*>(a0.xin) + z * a0.xin_ts;
     if (a.res1) a.res1 += z * a0.res1_ts;
     if (a.res2) a.res2 += z * a0.res2_ts;
@@ -69,6 +68,7 @@ __device__ __forceinline__ ConvArgs conv_image(const ConvArgs& a0) {
     if (a.mask) a.mask += z * a0.mask_ts;
     return a;
 }
+__device__ __forceinline__ ConvArgs conv_image(const ConvArgs& a0) { return conv_image_at(a0, blockIdx.z); }
 
 __device__ __forceinline__ size_t conv_index(int layout, int c, int y, int x, int H, int W, int Hp,
                                              int Wp) {
@@ -178,6 +178,132 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a0) {
         }
         a.out[conv_index(a.out_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)] =
             __builtin_bit_cast(uint16_t, round_f16(r));
+    }
+}
+
+// conv3x3_kernel<NW, U> for a batch of images (the body over many tiles): workgroup
+// (tile, chunk, z) runs images z * zpw .. z * zpw + zpw - 1 one after another. Each wave
+// keeps the weight fragments of its K range (at most KMAX K-steps) in registers for all of
+// them and requests the next image's rows before the current one is reduced. Same K split
+// and summation order as conv3x3_kernel: every image's results are the same bits.
+template <int NW, int KMAX>
+__global__ __launch_bounds__(64 * NW) void conv3x3_images_kernel(ConvArgs a0, int images, int zpw) {
+    constexpr int NB = kConvNbc;
+    constexpr int kItems = 16 * kConvChunk;
+    constexpr int kIters = (kItems + 64 * NW - 1) / (64 * NW);
+    extern __shared__ float red[];  // [NW][NB][4][65]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int quarter = lane >> 4;
+
+    const int per_xcd = (a0.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a0.tiles) return;  // whole workgroup, before any barrier
+    const int chunk = blockIdx.y;
+    const int z0 = blockIdx.z * zpw;
+    const int z1 = min(z0 + zpw, images);
+
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a0.wpk, a0.wpk_bytes);
+    const int M = a0.H * a0.W;
+    const int pc = min(tile * 16 + (lane & 15), M - 1);
+    const int y = pc / a0.W;
+    const uint32_t base = (uint32_t)(y + kPad - 1) * a0.Wp + (pc - y * a0.W) + kPad - 1;
+
+    const int s0 = wave * a0.ksteps / NW;
+    const int s1 = (wave + 1) * a0.ksteps / NW;
+    h8 Bf[KMAX][NB];
+    uint32_t koff[KMAX];
+    bool kin[KMAX];
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+        const int s = s0 + i < s1 ? s0 + i : s1 - 1;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            Bf[i][nb] = __builtin_bit_cast(
+                h8, load16(wr, (uint32_t)((s * a0.NBT + chunk * NB + nb) * 64 + lane) * 16u));
+        const int kb = 4 * s + quarter;
+        kin[i] = kb < a0.KB;
+        const int kbc = kin[i] ? kb : a0.KB - 1;
+        const int tap = fast_div(kbc, a0.magic_cb);
+        const int cb = kbc - tap * a0.CB;
+        const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
+        const int kx = tap - ky * 3;
+        koff[i] = (uint32_t)(cb * a0.Hp + ky) * a0.Wp + kx;
+    }
+    u32x4 q[KMAX];
+    auto load_rows = [&](int z) {
+        const __amdgpu_buffer_rsrc_t xr =
+            make_rsrc(static_cast<const uint16_t*>(a0.xin) + (long)z * a0.xin_ts, a0.xin_bytes);
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) q[i] = load16(xr, (base + koff[i]) * 16u);
+    };
+    load_rows(z0);
+    float biasv[kIters];
+#pragma unroll
+    for (int j = 0; j < kIters; ++j) {
+        const int oc = chunk * kConvChunk + ((tid + j * 64 * NW) >> 4);
+        biasv[j] = oc < a0.Cout ? a0.bias[oc] : 0.0f;
+    }
+
+    for (int z = z0; z < z1; ++z) {
+        const ConvArgs a = conv_image_at(a0, z);
+        f32x4 acc[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{};
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) {
+            if (s0 + i < s1) {  // uniform across the wave
+                const u32x4 zero = {0u, 0u, 0u, 0u};
+                // Padding K-blocks multiply zero weights; zero A keeps a non-finite
+                // input from turning 0 * inf into NaN there.
+                const h8 A = __builtin_bit_cast(h8, kin[i] ? q[i] : zero);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+            }
+        }
+        if (z + 1 < z1) load_rows(z + 1);  // in flight through the reduction and epilogue
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+        __syncthreads();
+
+#pragma unroll
+        for (int j = 0; j < kIters; ++j) {
+            const int idx = tid + j * 64 * NW;
+            const int pl = idx & 15;
+            const int ocl = idx >> 4;
+            const int nb = ocl >> 4;
+            const int src = ((pl >> 2) << 4) + (ocl & 15);
+            const int v = pl & 3;
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
+            const int oc = chunk * kConvChunk + ocl;
+            const int pp = tile * 16 + pl;
+            if (pp >= M || oc >= a.Cout) continue;
+            const int yy = pp / a.W;
+            const int xx = pp - yy * a.W;
+            float r = sum + biasv[j];
+            if (a.act == 1 && r < 0.0f) r = r * a.slope;
+            if (a.act == 2 && r < 0.0f) r = 0.0f;
+            if (a.res1 != nullptr) {
+                const float id = (float)__builtin_bit_cast(
+                    _Float16, a.res1[conv_index(a.res1_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)]);
+                r = id + r;
+            }
+            if (a.res2 != nullptr) {
+                const float r1 = (float)round_f16(r);
+                const float id = (float)__builtin_bit_cast(
+                    _Float16, a.res2[conv_index(a.res2_layout, a.res2_coff + oc, yy, xx, a.H, a.W, a.Hp, a.Wp)]);
+                r = id + r1;
+            }
+            a.out[conv_index(a.out_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)] =
+                __builtin_bit_cast(uint16_t, round_f16(r));
+        }
+        if (z + 1 < z1) __syncthreads();  // sums read before the next image's partials
     }
 }
 
@@ -311,6 +437,132 @@ __global__ __launch_bounds__(64 * NW, MINW) void conv_offsets_kernel(ConvArgs a0
     }
 }
 
+// conv_offsets_kernel for a batch of images (the body over many tiles): workgroup
+// (tile, chunk, z) runs images z * zpw .. z * zpw + zpw - 1 one after another, each wave
+// keeping the weight fragments of its K range (three K-steps of 64 channels) in registers
+// for all of them and requesting the next image's rows before the current one is
+// reduced. 64 input channels only (18 K-steps, no padded K-blocks). Same K split and
+// summation order as conv_offsets_kernel: every image's results are the same bits.
+template <int NW, int NB, int MINW>
+__global__ __launch_bounds__(64 * NW, MINW) void conv_offsets_images_kernel(ConvArgs a0, int images,
+                                                                            int zpw) {
+    constexpr int KS = 18;
+    constexpr int KMAX = (KS + NW - 1) / NW;
+    static_assert(NB * 128 == 64 * NW, "one epilogue item (two pixels) per thread");
+    extern __shared__ __attribute__((aligned(16))) f32x4 red4[];  // [NW][NB][64] partial sums
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int quarter = lane >> 4;
+
+    const int per_xcd = (a0.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a0.tiles) return;  // whole workgroup, before any barrier
+    const int chunk = blockIdx.y;
+    const int z0 = blockIdx.z * zpw;
+    const int z1 = min(z0 + zpw, images);
+
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a0.wpk, a0.wpk_bytes);
+    const int M = a0.H * a0.W;
+    uint32_t base;
+    {
+        const int pc = min(tile * 16 + (lane & 15), M - 1);
+        const int y = pc / a0.W;
+        base = (uint32_t)(y + kPad - 1) * a0.Wp + (pc - y * a0.W) + kPad - 1;
+    }
+    const int s0 = wave * KS / NW;
+    const int s1 = (wave + 1) * KS / NW;
+    h8 Bf[KMAX][NB];
+    uint32_t koff[KMAX];
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+        const int s = s0 + i < s1 ? s0 + i : s1 - 1;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            Bf[i][nb] = __builtin_bit_cast(
+                h8, load16(wr, (uint32_t)((s * a0.NBT + chunk * NB + nb) * 64 + lane) * 16u));
+        const int kb = 4 * s + quarter;
+        const int tap = kb >> 3;
+        const int cb = kb & 7;
+        const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
+        const int kx = tap - ky * 3;
+        koff[i] = (uint32_t)(cb * a0.Hp + ky) * a0.Wp + kx;
+    }
+    u32x4 q[KMAX];
+    auto load_rows = [&](int z) {
+        const __amdgpu_buffer_rsrc_t xr =
+            make_rsrc(static_cast<const uint16_t*>(a0.xin) + (long)z * a0.xin_ts, a0.xin_bytes);
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) q[i] = load16(xr, (base + koff[i]) * 16u);
+    };
+    load_rows(z0);
+
+    // Epilogue item of this thread: the 8-byte half h of row (nb, l), i.e. pixels
+    // tile * 16 + 4 (l / 16) + 2 h + j (j = 0, 1) of channel chunk * 16 NB + 16 nb + l % 16.
+    const int h = tid & 1;
+    const int l = (tid >> 1) & 63;
+    const int nb_e = ((tid >> 1) >> 6) % NB;
+    const int oc = chunk * 16 * NB + nb_e * 16 + (l & 15);
+    const bool oc_ok = oc < a0.Cout;
+    const float bias = oc_ok ? a0.bias[oc] : 0.0f;
+    const int p0 = tile * 16 + 4 * (l >> 4) + 2 * h;
+    const int flow_channel = ((oc % 144) & 1) == 0 ? 1 : 0;  // even = dy = flow y
+    const float2* red2 = reinterpret_cast<const float2*>(red4);
+
+    for (int z = z0; z < z1; ++z) {
+        const ConvArgs a = conv_image_at(a0, z);
+        // The flow under this thread's offsets, requested before the convolution.
+        uint16_t fv[2] = {0, 0};
+        const uint16_t* flow = oc < 144 ? a.flow1 : a.flow2;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (oc_ok && oc < 288 && p0 + j < M) fv[j] = flow[flow_channel * (size_t)M + p0 + j];
+
+        f32x4 acc[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{};
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) {
+            if (s0 + i < s1) {  // uniform across the wave
+                const h8 A = __builtin_bit_cast(h8, q[i]);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+            }
+        }
+        if (z + 1 < z1) load_rows(z + 1);  // in flight through the reduction and epilogue
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) red4[(wave * NB + nb) * 64 + lane] = acc[nb];
+        __syncthreads();
+
+        float2 sum = {0.0f, 0.0f};
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float2 t = red2[((w * NB + nb_e) * 64 + l) * 2 + h];
+            sum.x += t.x;
+            sum.y += t.y;
+        }
+        if (oc_ok) {
+            // prepare_dcn_offsets_fp16 (MetalShader.swift:815-839) on the FP16 conv output.
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int px = p0 + j;
+                if (px >= M) continue;
+                const float raw = (float)round_f16((j ? sum.y : sum.x) + bias);
+                if (oc < 288) {
+                    const float residue = 10.0f * tanhf(raw);
+                    const float f = (float)__builtin_bit_cast(_Float16, fv[j]);
+                    a.offset[(size_t)oc * M + px] = __builtin_bit_cast(uint16_t, round_f16(residue + f));
+                } else {
+                    a.mask[(size_t)(oc - 288) * M + px] =
+                        __builtin_bit_cast(uint16_t, round_f16(1.0f / (1.0f + expf(-raw))));
+                }
+            }
+        }
+        if (z + 1 < z1) __syncthreads();  // sums read before the next image's partials
+    }
+}
+
 // Conv weights OIHW FP16 [Cout][Cin][3][3] -> B fragments [ksteps][NBT][64][8]:
 // lane l of K-step s holds output channel nb*16 + l%16 and K-block 4s + l/16 =
 // tap * CB + cb, channels 8 cb .. 8 cb + 7 (zero past Cin, past Cout and past KB).
@@ -351,6 +603,12 @@ __global__ __launch_bounds__(256) void conv_prepack_kernel(const uint16_t* __res
 // Both convs split K over the NW waves exactly as conv3x3_kernel<NW, U> does (wave w owns
 // K-steps [w * 18 / NW, (w + 1) * 18 / NW), MFMA chains in K-step order, partial sums added
 // in wave order from 0), so every value equals the two-launch result bit for bit.
+//
+// Batches: workgroup (tile, z) runs the same tile of images z * zpw .. z * zpw + zpw - 1 one
+// after another. Each wave keeps its weight fragments of both convs in registers for all of
+// them (the 144 KB of B fragments are fetched once per workgroup instead of once per image)
+// and requests the next image's conv1 rows while the current one is reduced and runs conv2.
+// The arithmetic of every image is the single-image arithmetic.
 constexpr int kPairTH = 2, kPairTW = 8;                 // output tile
 constexpr int kPairHH = kPairTH + 2, kPairHW = kPairTW + 2;
 constexpr int kPairHalo = kPairHH * kPairHW;            // halo pixels
@@ -373,7 +631,8 @@ struct PairArgs {
     float slope;
     int res1_layout, res2_layout, out_layout, res2_coff;
     int H, W, Hp, Wp, tiles_x, tiles;
-    long xin_ts, res1_ts, res2_ts, out_ts;  // per-image strides of a batch (blockIdx.z)
+    int images, zpw;                        // batch size, images per workgroup
+    long xin_ts, res1_ts, res2_ts, out_ts;  // per-image strides of a batch
 };
 
 __host__ __device__ constexpr size_t pair_lds_bytes(int nw) {
@@ -381,15 +640,7 @@ __host__ __device__ constexpr size_t pair_lds_bytes(int nw) {
 }
 
 template <int NW>
-__global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a0) {
-    PairArgs a = a0;
-    {
-        const long z = blockIdx.z;
-        a.xin = static_cast<const uint16_t*>(a0.xin) + z * a0.xin_ts;
-        if (a.res1) a.res1 += z * a0.res1_ts;
-        if (a.res2) a.res2 += z * a0.res2_ts;
-        a.out += z * a0.out_ts;
-    }
+__global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
     constexpr int NB = kConvNbc;
     constexpr int KMAX = (kPairKsteps + NW - 1) / NW;  // K-steps of the busiest wave
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -407,7 +658,8 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a0) {
     const int oy0 = ty * kPairTH;
     const int ox0 = (tile - ty * a.tiles_x) * kPairTW;
 
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const int z0 = blockIdx.z * a.zpw;
+    const int z1 = min(z0 + a.zpw, a.images);
     const __amdgpu_buffer_rsrc_t w1 = make_rsrc(a.wpk1, a.wpk_bytes);
     const __amdgpu_buffer_rsrc_t w2 = make_rsrc(a.wpk2, a.wpk_bytes);
 
@@ -426,23 +678,36 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a0) {
 
     const int s0 = wave * kPairKsteps / NW;
     const int s1 = (wave + 1) * kPairKsteps / NW;
+    // Offset of K-step slot i's K-block (tap, channel block) in the padded CB8 input.
+    uint32_t koff[KMAX];
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+        const int s = s0 + i < s1 ? s0 + i : s1 - 1;
+        const int kb = 4 * s + quarter;
+        const int tap = kb >> 3;
+        const int cb = kb & 7;
+        const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
+        const int kx = tap - ky * 3;
+        koff[i] = (uint32_t)(cb * a.Hp + ky) * a.Wp + kx;
+    }
     h8 B1[KMAX][NB], B2[KMAX][NB];
     u32x4 q[KMAX][kPairRT1];
+    auto load_rows = [&](int z) {
+        const __amdgpu_buffer_rsrc_t xr =
+            make_rsrc(static_cast<const uint16_t*>(a.xin) + (long)z * a.xin_ts, a.xin_bytes);
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i)
+#pragma unroll
+            for (int rt = 0; rt < kPairRT1; ++rt) q[i][rt] = load16(xr, (base1[rt] + koff[i]) * 16u);
+    };
 #pragma unroll
     for (int i = 0; i < KMAX; ++i) {
         const int s = s0 + i < s1 ? s0 + i : s1 - 1;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
             B1[i][nb] = __builtin_bit_cast(h8, load16(w1, (uint32_t)((s * NB + nb) * 64 + lane) * 16u));
-        const int kb = 4 * s + quarter;
-        const int tap = kb >> 3;
-        const int cb = kb & 7;
-        const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
-        const int kx = tap - ky * 3;
-#pragma unroll
-        for (int rt = 0; rt < kPairRT1; ++rt)
-            q[i][rt] = load16(xr, (base1[rt] + (uint32_t)(cb * a.Hp + ky) * a.Wp + kx) * 16u);
     }
+    load_rows(z0);
 #pragma unroll
     for (int i = 0; i < KMAX; ++i) {
         const int s = s0 + i < s1 ? s0 + i : s1 - 1;
@@ -451,131 +716,164 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a0) {
             B2[i][nb] = __builtin_bit_cast(h8, load16(w2, (uint32_t)((s * NB + nb) * 64 + lane) * 16u));
     }
 
-    f32x4 acc1[kPairRT1][NB];
+    // Per-thread constants of the two reductions, the same for every image: the biases,
+    // and the epilogue's output positions (thread tid < 256 owns output pixels
+    // 4 (l / 16) + v of channel 16 nb + l % 16, l = tid % 64, nb = tid / 64).
+    constexpr int kSums1 = kPairRT1 * NB * 64;
+    constexpr int kIters1 = (kSums1 + 64 * NW - 1) / (64 * NW);
+    constexpr int kSums2 = kPairRT2 * NB * 64;
+    static_assert(kPairRT2 == 1 && kSums2 <= 64 * NW, "one epilogue item per thread");
+    float bias1v[kIters1];
 #pragma unroll
-    for (int rt = 0; rt < kPairRT1; ++rt)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc1[rt][nb] = f32x4{};
-#pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-        if (s0 + i < s1) {  // uniform across the wave
-#pragma unroll
-            for (int rt = 0; rt < kPairRT1; ++rt) {
-                const h8 A = __builtin_bit_cast(h8, q[i][rt]);
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    acc1[rt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B1[i][nb], acc1[rt][nb], 0, 0, 0);
-            }
-        }
+    for (int j = 0; j < kIters1; ++j) {
+        const int g = tid + j * 64 * NW;
+        bias1v[j] = g < kSums1 ? a.bias1[((g >> 6) % NB) * 16 + (g & 15)] : 0.0f;
     }
+    const bool epi = tid < kSums2;
+    const int epi_oc = ((tid >> 6) % NB) * 16 + (tid & 15);
+    const float bias2v = epi ? a.bias2[epi_oc] : 0.0f;
+    bool epi_in[4];
+    uint32_t epi_out[4], epi_r1[4], epi_r2[4];
 #pragma unroll
-    for (int rt = 0; rt < kPairRT1; ++rt)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) red4[((wave * kPairRT1 + rt) * NB + nb) * 64 + lane] = acc1[rt][nb];
-    __syncthreads();
+    for (int v = 0; v < 4; ++v) {
+        const int op = 4 * ((tid & 63) >> 4) + v;
+        const int yy = oy0 + (op >> 3);
+        const int xx = ox0 + (op & 7);
+        epi_in[v] = epi && yy < a.H && xx < a.W;
+        epi_out[v] = (uint32_t)conv_index(a.out_layout, epi_oc, yy, xx, a.H, a.W, a.Hp, a.Wp);
+        epi_r1[v] = (uint32_t)conv_index(a.res1_layout, epi_oc, yy, xx, a.H, a.W, a.Hp, a.Wp);
+        epi_r2[v] = (uint32_t)conv_index(a.res2_layout, a.res2_coff + epi_oc, yy, xx, a.H, a.W, a.Hp, a.Wp);
+    }
 
-    // t tile: thread (rt, nb, l) sums the 16-byte partial rows (w, rt, nb, l) over the
-    // waves (consecutive lanes read consecutive rows: no bank conflicts), giving the four
-    // halo pixels rt * 16 + 4 (l / 16) + v of channel 16 nb + l % 16.
-    for (int g = tid; g < kPairRT1 * NB * 64; g += 64 * NW) {
-        const int l = g & 63;
-        const int nb = (g >> 6) % NB;
-        const int rt = g / (NB * 64);
-        f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const f32x4 t = red4[((w * kPairRT1 + rt) * NB + nb) * 64 + l];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) sum[v] += t[v];
-        }
-        const int oc = nb * 16 + (l & 15);
-        const float bias = a.bias1[oc];
-        _Float16* th = reinterpret_cast<_Float16*>(tt + (oc >> 3) * kPairTStride);
+    for (int z = z0; z < z1; ++z) {
+        const uint16_t* res1 = a.res1 ? a.res1 + (long)z * a.res1_ts : nullptr;
+        const uint16_t* res2 = a.res2 ? a.res2 + (long)z * a.res2_ts : nullptr;
+        uint16_t* out = a.out + (long)z * a.out_ts;
+        // The epilogue's residual inputs, requested now so that they arrive during the convs.
+        uint16_t r1v[4] = {0, 0, 0, 0}, r2v[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int px = rt * 16 + 4 * (l >> 4) + v;
-            const int hy = min(px, kPairHalo - 1) / kPairHW;
-            const int iy = oy0 - 1 + hy;
-            const int ix = ox0 - 1 + px - hy * kPairHW;
-            const bool inside = px < kPairHalo && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
-            float val = sum[v] + bias;
-            if (a.act1 == 1 && val < 0.0f) val = val * a.slope;
-            if (a.act1 == 2 && val < 0.0f) val = 0.0f;
-            th[px * 8 + (oc & 7)] = inside ? round_f16(val) : (_Float16)0.0f;
+            if (epi_in[v] && res1 != nullptr) r1v[v] = res1[epi_r1[v]];
+            if (epi_in[v] && res2 != nullptr) r2v[v] = res2[epi_r2[v]];
         }
-    }
-    __syncthreads();
+        f32x4 acc1[kPairRT1][NB];
+#pragma unroll
+        for (int rt = 0; rt < kPairRT1; ++rt)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) acc1[rt][nb] = f32x4{};
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) {
+            if (s0 + i < s1) {  // uniform across the wave
+#pragma unroll
+                for (int rt = 0; rt < kPairRT1; ++rt) {
+                    const h8 A = __builtin_bit_cast(h8, q[i][rt]);
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc1[rt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B1[i][nb], acc1[rt][nb], 0, 0, 0);
+                }
+            }
+        }
+        if (z + 1 < z1) load_rows(z + 1);  // in flight through the reductions and conv2
+#pragma unroll
+        for (int rt = 0; rt < kPairRT1; ++rt)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) red4[((wave * kPairRT1 + rt) * NB + nb) * 64 + lane] = acc1[rt][nb];
+        __syncthreads();
 
-    // conv2 on the output tile, A fragments from the t tile.
-    f32x4 acc2[kPairRT2][NB];
+        // t tile: thread (rt, nb, l) sums the 16-byte partial rows (w, rt, nb, l) over the
+        // waves (consecutive lanes read consecutive rows: no bank conflicts), giving the four
+        // halo pixels rt * 16 + 4 (l / 16) + v of channel 16 nb + l % 16.
 #pragma unroll
-    for (int rt = 0; rt < kPairRT2; ++rt)
+        for (int j = 0; j < kIters1; ++j) {
+            const int g = tid + j * 64 * NW;
+            if (g >= kSums1) break;
+            const int l = g & 63;
+            const int nb = (g >> 6) % NB;
+            const int rt = g / (NB * 64);
+            f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc2[rt][nb] = f32x4{};
+            for (int w = 0; w < NW; ++w) {
+                const f32x4 t = red4[((w * kPairRT1 + rt) * NB + nb) * 64 + l];
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-        if (s0 + i < s1) {
-            const int kb = 4 * (s0 + i) + quarter;
-            const int tap = kb >> 3;
-            const int cb = kb & 7;
-            const int ky = (tap * 11) >> 5;
-            const int kx = tap - ky * 3;
+                for (int v = 0; v < 4; ++v) sum[v] += t[v];
+            }
+            const int oc = nb * 16 + (l & 15);
+            const float bias = bias1v[j];
+            _Float16* th = reinterpret_cast<_Float16*>(tt + (oc >> 3) * kPairTStride);
 #pragma unroll
-            for (int rt = 0; rt < kPairRT2; ++rt) {
-                const int op = rt * 16 + (lane & 15);
-                const int hpx = ((op >> 3) + ky) * kPairHW + (op & 7) + kx;
-                const h8 A = __builtin_bit_cast(h8, tt[cb * kPairTStride + hpx]);
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    acc2[rt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B2[i][nb], acc2[rt][nb], 0, 0, 0);
+            for (int v = 0; v < 4; ++v) {
+                const int px = rt * 16 + 4 * (l >> 4) + v;
+                const int hy = min(px, kPairHalo - 1) / kPairHW;
+                const int iy = oy0 - 1 + hy;
+                const int ix = ox0 - 1 + px - hy * kPairHW;
+                const bool inside = px < kPairHalo && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W;
+                float val = sum[v] + bias;
+                if (a.act1 == 1 && val < 0.0f) val = val * a.slope;
+                if (a.act1 == 2 && val < 0.0f) val = 0.0f;
+                th[px * 8 + (oc & 7)] = inside ? round_f16(val) : (_Float16)0.0f;
             }
         }
-    }
-    // conv1's partial sums were all read before the last barrier: reuse their LDS.
-#pragma unroll
-    for (int rt = 0; rt < kPairRT2; ++rt)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) red4[((wave * kPairRT2 + rt) * NB + nb) * 64 + lane] = acc2[rt][nb];
-    __syncthreads();
+        __syncthreads();
 
-    // Thread (rt, nb, l) sums rows (w, rt, nb, l) as for the t tile: output pixels
-    // rt * 16 + 4 (l / 16) + v of channel 16 nb + l % 16.
-    for (int g = tid; g < kPairRT2 * NB * 64; g += 64 * NW) {
-        const int l = g & 63;
-        const int nb = (g >> 6) % NB;
-        const int rt = g / (NB * 64);
-        f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+        // conv2 on the output tile, A fragments from the t tile.
+        f32x4 acc2[kPairRT2][NB];
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const f32x4 t = red4[((w * kPairRT2 + rt) * NB + nb) * 64 + l];
+        for (int rt = 0; rt < kPairRT2; ++rt)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) sum[v] += t[v];
-        }
-        const int oc = nb * 16 + (l & 15);
-        const float bias = a.bias2[oc];
+            for (int nb = 0; nb < NB; ++nb) acc2[rt][nb] = f32x4{};
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int op = rt * 16 + 4 * (l >> 4) + v;
-            const int yy = oy0 + (op >> 3);
-            const int xx = ox0 + (op & 7);
-            if (yy >= a.H || xx >= a.W) continue;
-            float val = sum[v] + bias;
-            if (a.act2 == 1 && val < 0.0f) val = val * a.slope;
-            if (a.act2 == 2 && val < 0.0f) val = 0.0f;
-            if (a.res1 != nullptr) {
-                const float id = (float)__builtin_bit_cast(
-                    _Float16, a.res1[conv_index(a.res1_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)]);
-                val = id + val;
+        for (int i = 0; i < KMAX; ++i) {
+            if (s0 + i < s1) {
+                const int kb = 4 * (s0 + i) + quarter;
+                const int tap = kb >> 3;
+                const int cb = kb & 7;
+                const int ky = (tap * 11) >> 5;
+                const int kx = tap - ky * 3;
+#pragma unroll
+                for (int rt = 0; rt < kPairRT2; ++rt) {
+                    const int op = rt * 16 + (lane & 15);
+                    const int hpx = ((op >> 3) + ky) * kPairHW + (op & 7) + kx;
+                    const h8 A = __builtin_bit_cast(h8, tt[cb * kPairTStride + hpx]);
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc2[rt][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B2[i][nb], acc2[rt][nb], 0, 0, 0);
+                }
             }
-            if (a.res2 != nullptr) {
-                const float r1 = (float)round_f16(val);
-                const float id = (float)__builtin_bit_cast(
-                    _Float16, a.res2[conv_index(a.res2_layout, a.res2_coff + oc, yy, xx, a.H, a.W, a.Hp, a.Wp)]);
-                val = id + r1;
-            }
-            a.out[conv_index(a.out_layout, oc, yy, xx, a.H, a.W, a.Hp, a.Wp)] =
-                __builtin_bit_cast(uint16_t, round_f16(val));
         }
+        // conv1's partial sums were all read before the last barrier: reuse their LDS.
+#pragma unroll
+        for (int rt = 0; rt < kPairRT2; ++rt)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) red4[((wave * kPairRT2 + rt) * NB + nb) * 64 + lane] = acc2[rt][nb];
+        __syncthreads();
+
+        // Thread (nb, l) sums rows (w, nb, l) as for the t tile: output pixels
+        // 4 (l / 16) + v of channel 16 nb + l % 16.
+        if (epi) {
+            const int l = tid & 63;
+            const int nb = (tid >> 6) % NB;
+            f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const f32x4 t = red4[(w * NB + nb) * 64 + l];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) sum[v] += t[v];
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (!epi_in[v]) continue;
+                float val = sum[v] + bias2v;
+                if (a.act2 == 1 && val < 0.0f) val = val * a.slope;
+                if (a.act2 == 2 && val < 0.0f) val = 0.0f;
+                if (res1 != nullptr) val = (float)__builtin_bit_cast(_Float16, r1v[v]) + val;
+                if (res2 != nullptr) {
+                    const float r1 = (float)round_f16(val);
+                    val = (float)__builtin_bit_cast(_Float16, r2v[v]) + r1;
+                }
+                out[epi_out[v]] = __builtin_bit_cast(uint16_t, round_f16(val));
+            }
+        }
+        if (z + 1 < z1) __syncthreads();  // sums read before the next image's partials
     }
 }
 
@@ -608,6 +906,18 @@ hipError_t launch_conv_prepack(const ConvGeometry& g, const uint16_t* w, const u
 
 namespace {
 
+// Images per workgroup of a batched conv pair, conv3x3 or offsets conv: up to kMax,
+// balanced over the workgroups of a tile. Measured for a body step over 16 tiles (images
+// per workgroup -> us per step), each kernel tuned in turn: conv pair 1 -> 955,
+// 2 -> 828, 4 -> 768, 8 -> 738, 16 -> 723 (over 64 tiles 16 beat 8 by 2 %); offsets conv
+// (4 waves per SIMD; 5 measured slower) 1 -> 754, 2 -> 715, 4 -> 692, 8 -> 680,
+// 16 -> 682; conv3x3 2 -> 685, 4 -> 667, 8 -> 658, 16 -> 654.
+template <int kMax>
+static int images_per_group(int images) {
+    const int groups = (images + kMax - 1) / kMax;
+    return (images + groups - 1) / groups;
+}
+
 hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, const ConvBatch& batch, hipStream_t stream) {
     constexpr int NW = 8, U = 4;
     if (batch.images < 1) return hipErrorInvalidValue;
@@ -629,12 +939,27 @@ hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, const ConvBatch& batch, 
     a.tiles = (g.h * g.w + 15) / 16;
     a.magic_cb = magic_for(g.cb);
     const size_t lds = (size_t)NW * kConvNbc * 4 * 65 * sizeof(float);
+    const int kmax = (g.ksteps + NW - 1) / NW;  // K-steps of the busiest wave
+    if (batch.images > 1 && kmax <= 8) {
+        const int zpw = images_per_group<16>(batch.images);
+        const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)g.chunks,
+                        (unsigned)((batch.images + zpw - 1) / zpw));
+        if (kmax <= 3)
+            hipLaunchKernelGGL((conv3x3_images_kernel<NW, 3>), grid, dim3(64 * NW), lds, stream, a, batch.images, zpw);
+        else if (kmax <= 5)
+            hipLaunchKernelGGL((conv3x3_images_kernel<NW, 5>), grid, dim3(64 * NW), lds, stream, a, batch.images, zpw);
+        else
+            hipLaunchKernelGGL((conv3x3_images_kernel<NW, 8>), grid, dim3(64 * NW), lds, stream, a, batch.images, zpw);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)g.chunks, (unsigned)batch.images);
     hipLaunchKernelGGL((conv3x3_kernel<NW, U>), grid, dim3(64 * NW), lds, stream, a);
     return hipGetLastError();
 }
 
 }  // namespace
+
+constexpr int kOffsetsImagesMinWaves = 4;
 
 hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                                   const float* bias, const uint16_t* flow1, const uint16_t* flow2,
@@ -669,6 +994,17 @@ hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, cons
     a.offset_ts = 288 * plane;
     a.mask_ts = 144 * plane;
     constexpr size_t lds = (size_t)NW * RT * NB * 64 * sizeof(f32x4);
+    if (images > 1 && g.cin == 64) {
+        const int zpw = images_per_group<8>(images);
+        auto kernel = &conv_offsets_images_kernel<NW, NB, kOffsetsImagesMinWaves>;
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (attr != hipSuccess) return attr;
+        const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)((g.cout + 16 * NB - 1) / (16 * NB)),
+                        (unsigned)((images + zpw - 1) / zpw));
+        hipLaunchKernelGGL(kernel, grid, dim3(64 * NW), lds, stream, a, images, zpw);
+        return hipGetLastError();
+    }
     auto kernel = &conv_offsets_kernel<NW, U, NB, RT, MINW>;
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -729,6 +1065,8 @@ hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, c
     a.res1_ts = batch.res1;
     a.res2_ts = batch.res2;
     a.out_ts = batch.out;
+    a.images = batch.images;
+    a.zpw = images_per_group<16>(batch.images);
     a.H = g1.h;
     a.W = g1.w;
     a.Hp = g1.h + 2 * kPad;
@@ -742,8 +1080,9 @@ hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, c
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)((a.tiles + 7) / 8 * 8), 1, (unsigned)batch.images), dim3(64 * NW),
-                       lds, stream, a);
+    const unsigned groups_z = (unsigned)((batch.images + a.zpw - 1) / a.zpw);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((a.tiles + 7) / 8 * 8), 1, groups_z), dim3(64 * NW), lds,
+                       stream, a);
     return hipGetLastError();
 }
 

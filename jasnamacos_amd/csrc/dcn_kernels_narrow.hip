@@ -192,6 +192,184 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
     }
 }
 
+// narrow_kernel for a batch of images (the propagation body over many tiles): workgroup
+// (tile, z) runs the same 16 pixels of images z * zpw .. z * zpw + zpw - 1 one after
+// another (tiles never span images here). Each wave keeps the weight fragments of its K
+// range (at most KMAX K-steps) in registers for all of them, and while image z is
+// reduced the corners of image z + 1 and the offsets of image z + 2 are in flight. Same
+// K split, blend and summation order as narrow_kernel: every image's results are the
+// same bits.
+template <int NB, int NW, int KMAX, int SAMPLER>
+__global__ __launch_bounds__(64 * NW) void narrow_images_kernel(NarrowArgs a, int images, int zpw) {
+    extern __shared__ float red[];  // [NW][NB][4][65]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int quarter = lane >> 4;
+
+    const int per_xcd = (a.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+    const int z0 = blockIdx.z * zpw;
+    const int z1 = min(z0 + zpw, images);
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+
+    // Pixel of this lane within its image; lanes past the last pixel take the last one
+    // (their results are never stored).
+    const int p = tile * 16 + (lane & 15);
+    const bool pvalid = p < a.HWo;
+    const int sp = pvalid ? p : a.HWo - 1;
+    const int oy = sp / a.Wo;
+    const int ox = sp - oy * a.Wo;
+    const int base_y = oy * a.sh - a.ph;
+    const int base_x = ox * a.sw - a.pw;
+
+    const int s0 = wave * a.ksteps / NW;
+    const int s1 = (wave + 1) * a.ksteps / NW;
+    h8 Bf[KMAX][NB];
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+        const int s = s0 + i < s1 ? s0 + i : s1 - 1;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)((s * NB + nb) * 64 + lane) * 16u));
+    }
+    // K-block of slot i -> (g * KA + tap, input plane, ky, kx); recomputed per use rather
+    // than kept live across the image loop (the weight fragments take the registers).
+    auto kblock = [&](int i, int& gt, int& plane, int& ky, int& kx) {
+        const int kb = 4 * (s0 + i) + quarter;
+        const int kbc = kb < a.KB ? kb : a.KB - 1;
+        gt = fast_div(kbc, a.magic_cb);
+        const int cb = kbc - gt * a.CB;
+        const int g = fast_div(gt, a.magic_ka);
+        const int tap = gt - g * a.KA;
+        ky = fast_div(tap, a.magic_kw);
+        kx = tap - ky * a.KW;
+        plane = g * a.CB + cb;
+    };
+
+    float dy[KMAX], dx[KMAX], m[KMAX];
+    auto load_raw = [&](int b) {
+        const uint32_t offb = (uint32_t)(b * 2 * a.GKA) * a.HWo + sp;
+        const uint32_t mskb = (uint32_t)(b * a.GKA) * a.HWo + sp;
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) {
+            int gt, plane, ky, kx;
+            kblock(i, gt, plane, ky, kx);
+            dy[i] = load_half(orr, (offb + (uint32_t)(2 * gt) * a.HWo) * 2u);
+            dx[i] = load_half(orr, (offb + (uint32_t)(2 * gt + 1) * a.HWo) * 2u);
+            m[i] = load_half(mr, (mskb + (uint32_t)gt * a.HWo) * 2u);
+        }
+    };
+    u32x4 q[KMAX][4];
+    float ly[KMAX], lx[KMAX], mm[KMAX];
+    auto load_corners = [&](int b) {
+        // 16-byte units; includes the border shift so (iy, ix) may be negative down to -2.
+        const uint32_t xinb = (uint32_t)(b * a.CBLK * a.Hp + kPad) * a.Wp + kPad;
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) {
+            int gt, plane, ky, kx;
+            kblock(i, gt, plane, ky, kx);
+            const bool live = pvalid && s0 + i < s1 && 4 * (s0 + i) + quarter < a.KB;
+            // y = float(oy*sh - ph + ky*dh) + dy, as MetalShader.swift:327-332. Dead
+            // units (tile tail, K padding) sample the zero border with weight 0.
+            const float y = live ? (float)(base_y + ky * a.dh) + dy[i] : -16.0f;
+            const float x = live ? (float)(base_x + kx * a.dw) + dx[i] : -16.0f;
+            mm[i] = live ? m[i] : 0.0f;
+            const float fy = floorf(y);
+            const float fx = floorf(x);
+            ly[i] = y - fy;
+            lx[i] = x - fx;
+            const int iy = (int)fminf(fmaxf(fy, (float)-kPad), (float)a.H);
+            const int ix = (int)fminf(fmaxf(fx, (float)-kPad), (float)a.W);
+            const uint32_t u = xinb + (uint32_t)(plane * a.Hp + iy) * a.Wp + ix;
+            q[i][0] = load16(xr, u * 16u);
+            q[i][1] = load16(xr, u * 16u + 16u);
+            q[i][2] = load16(xr, (u + a.Wp) * 16u);
+            q[i][3] = load16(xr, (u + a.Wp) * 16u + 16u);
+        }
+    };
+    load_raw(z0);
+    load_corners(z0);
+    if (z0 + 1 < z1) load_raw(z0 + 1);
+
+    for (int z = z0; z < z1; ++z) {
+        f32x4 acc[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{};
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) {
+            if (s0 + i < s1) {  // uniform across the wave
+                const h8 A = blend<SAMPLER>(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], mm[i]);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+            }
+        }
+        if (z + 1 < z1) {
+            load_corners(z + 1);
+            if (z + 2 < z1) load_raw(z + 2);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+        __syncthreads();
+
+        for (int idx = tid; idx < 16 * NB * 16; idx += 64 * NW) {
+            const int pl = idx & 15;
+            const int oc = idx >> 4;
+            const int nb = oc >> 4;
+            const int src = ((pl >> 2) << 4) + (oc & 15);
+            const int v = pl & 3;
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
+            if (pvalid) {  // pl == lane % 16: this lane's pixel
+                size_t dst;
+                if (a.out_cb8) {
+                    const int c = a.out_coff + oc;
+                    dst = (((size_t)z * a.out_cblk + (c >> 3)) * (a.Ho + 2 * kPad) + oy + kPad) *
+                              (size_t)(a.Wo + 2 * kPad) * 8 + (size_t)(ox + kPad) * 8 + (c & 7);
+                } else {
+                    dst = ((size_t)z * a.Cout + oc) * a.HWo + sp;
+                }
+                a.out[dst] = __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
+            }
+        }
+        if (z + 1 < z1) __syncthreads();  // sums read before the next image's partials
+    }
+}
+
+// Images per workgroup of the batched narrow kernel: up to 16, balanced over the
+// workgroups of a tile. Measured for a body step over 16 tiles (images per workgroup ->
+// us per step): 2 -> 642, 4 -> 632, 8 -> 628, 16 -> 627 (654 with one image per
+// workgroup of narrow_kernel).
+static int narrow_images_per_group(int images) {
+    constexpr int kMax = 16;
+    const int groups = (images + kMax - 1) / kMax;
+    return (images + groups - 1) / groups;
+}
+
+template <int NB, int NW, int SAMPLER>
+hipError_t launch_narrow_images_t(NarrowArgs a, int images, hipStream_t stream) {
+    constexpr int KMAX = 3;
+    const size_t lds = (size_t)NW * NB * 4 * 65 * sizeof(float);
+    auto kernel = &narrow_images_kernel<NB, NW, KMAX, SAMPLER>;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return attr;
+    a.tiles = (a.HWo + 15) / 16;  // per image
+    const int zpw = narrow_images_per_group(images);
+    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), 1, (unsigned)((images + zpw - 1) / zpw));
+    hipLaunchKernelGGL(kernel, grid, dim3(64 * NW), lds, stream, a, images, zpw);
+    return hipGetLastError();
+}
+
 template <int NB, int NW, int SAMPLER>
 hipError_t launch_narrow_t(const NarrowArgs& a, hipStream_t stream) {
     // K-steps whose loads are in flight at once, sized to the register budget of
@@ -280,6 +458,11 @@ hipError_t launch_narrow_f16(const KShape& s, const FusedGeometry& g, const Fuse
     a.magic_cb = magic_for(g.cb);
     a.magic_ka = magic_for(g.ka);
     a.magic_kw = magic_for(s.KW);
+    // Batches of images whose K range fits three K-steps per wave (the body's 128 -> 64
+    // DCN over many tiles): weights stay in registers across the images of a workgroup.
+    if (s.B > 1 && g.nb * 2 == 4 && cfg.ks == 12 && (a.ksteps + 11) / 12 <= 3)
+        return cfg.sampler == kSamplerExact ? launch_narrow_images_t<4, 12, kSamplerExact>(a, s.B, stream)
+                                            : launch_narrow_images_t<4, 12, kSamplerFast>(a, s.B, stream);
     if (cfg.sampler == kSamplerExact) return launch_narrow_s<kSamplerExact>(a, g.nb * 2, cfg.ks, stream);
     return launch_narrow_s<kSamplerFast>(a, g.nb * 2, cfg.ks, stream);
 }
