@@ -489,6 +489,48 @@ def cpu_baseline_body(clip) -> dict:
                       f"output finite: {bool(np.all(np.isfinite(out.astype(np.float32))))}"}
 
 
+def bench_share(args, ctx, dc, d, dev, share: int = 2) -> dict:
+    """C3 at one GPU's share of an 8-GPU split: the first `share` tiles of the same inputs
+    (tiles shard with no exchange, so a rank runs exactly this), timed like the main line:
+    `steps` calls (repack + fused) in one hipGraph, HIP events around one replay."""
+    import dataclasses
+
+    import torch
+
+    s = dataclasses.replace(d["shape"], batch=share)
+    per = {k: d["shape"].counts()[k] // d["shape"].batch for k in ("input", "offset", "mask")}
+    x, off, msk = (dev[k][: per[k] * share] for k in ("input", "offset", "mask"))
+    packed = ctx.prepack_dev(s, dev["weight"], dev["bias"])
+    ctx.reserve(s)
+    cfg = ctx.get_fused_config(s)
+    out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for _ in range(max(args.warmup, 1)):
+            ctx.forward_f16_prepacked_dev(s, x, off, msk, packed, out, stream=stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        cur = torch.cuda.current_stream()
+        for _ in range(args.steps):
+            ctx.forward_f16_prepacked_dev(s, x, off, msk, packed, out, stream=cur)
+    with torch.cuda.stream(stream):
+        graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / args.steps
+    packed.free()
+    nbytes = algorithmic_bytes(s)
+    return {"workload": f"C3 per-GPU share on 8 GPUs: the first {share} of the 16 tiles", "batch": share,
+            "us_per_call": us, "tflops": s.flops / (us * 1e-6) / 1e12,
+            "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "fused_config": cfg}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -678,6 +720,8 @@ def main() -> int:
         },
         "cpu_baseline": None,
     }
+    if args.config == 3:
+        line["per_gpu_share"] = bench_share(args, ctx, dc, d, dev)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     packed.free()
