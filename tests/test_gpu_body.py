@@ -294,10 +294,11 @@ def test_body_step_matches_oracle_chain(gpu_ctx, torch, h, w, branch, blocks):
     body.free()
 
 
-@pytest.mark.parametrize("h,w,branch,tiles", [(16, 24, 1, 3), (13, 21, 0, 2)])
+@pytest.mark.parametrize("h,w,branch,tiles", [(16, 24, 1, 3), (13, 21, 0, 2), (16, 16, 0, 5)])
 def test_body_tiles_equal_single_tiles(gpu_ctx, torch, h, w, branch, tiles):
     """A body over `tiles` tiles per step == one single-tile body per tile, bit for bit
-    (full step and a branch's first step); 13 x 21 puts DCN pixel tiles across tiles."""
+    (full step and a branch's first step); 13 x 21 puts DCN pixel tiles across tiles;
+    5 tiles run the DCN with several tiles per workgroup."""
     blocks = 2
     rng = np.random.default_rng(70 + h + tiles)
     weights = br.body_weights(rng, branch, blocks)

@@ -226,7 +226,7 @@ def test_fused_configs(gpu_ctx, dcn, c2, variant, mt, ks, sampler):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
-@pytest.mark.parametrize("variant", [0, 6])
+@pytest.mark.parametrize("variant", [0, 5, 6])
 def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle, variant):
     d = dcn.generate_config_inputs(3, 3)
     s = d["shape"]
@@ -248,6 +248,35 @@ def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle, variant):
         mx, mean = errors(out[b * c["output"]:(b + 1) * c["output"]], ref)
         log(f"  tile {b}: max {mx:.3e} mean {mean:.3e}")
         assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
+@pytest.mark.parametrize("batch,h,w", [(5, 7, 9), (4, 16, 16), (16, 64, 64)])
+def test_narrow_batch_equals_single_images(gpu_ctx, dcn, batch, h, w):
+    """The narrow variant over a batch (from four images on: several images per workgroup,
+    weights kept in registers) == one call per image, bit for bit."""
+    s = dcn.DeformConvShape(batch, 128, h, w, 64, h, w, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    one = dataclasses.replace(s, batch=1)
+    rng = np.random.default_rng(batch * 100 + h)
+    c = s.counts()
+    x = rng.standard_normal(c["input"]).astype(np.float16)
+    off = (rng.standard_normal(c["offset"]) * 4).astype(np.float16)
+    msk = rng.random(c["mask"]).astype(np.float16)
+    wt = (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16)
+    b = (rng.standard_normal(64) * 0.1).astype(np.float16)
+    log("case: narrow batch", batch, h, w)
+    gpu_ctx.set_fused_config(0, 0, -1, 5)
+    try:
+        packed = gpu_ctx.prepack(s, wt, b)
+        out = gpu_ctx.run_float16_prepacked(s, x, off, msk, packed)
+        c1 = one.counts()
+        for i in range(batch):
+            o1 = gpu_ctx.run_float16_prepacked(one, x[i * c1["input"]:(i + 1) * c1["input"]],
+                                               off[i * c1["offset"]:(i + 1) * c1["offset"]],
+                                               msk[i * c1["mask"]:(i + 1) * c1["mask"]], packed)
+            assert np.array_equal(out[i * c1["output"]:(i + 1) * c1["output"]].view(np.uint16),
+                                  np.asarray(o1).view(np.uint16)), i
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
 
 
 @pytest.mark.parametrize("variant", [0, 6])
@@ -282,6 +311,7 @@ EDGE_SHAPES = [
     (3, 24, 6, 5, 32, 6, 5, 1, 3, 0, 1, 1, 1, 1, 1, 1, 3),      # 1x3 kernel, batch 3
     (2, 16, 7, 6, 32, 7, 6, 3, 1, 1, 0, 1, 1, 1, 1, 1, 2),      # 3x1 kernel (Kw 1)
     (1, 32, 5, 9, 64, 5, 9, 1, 1, 0, 0, 1, 1, 1, 1, 1, 4),      # 1x1 kernel (Kh*Kw 1)
+    (5, 128, 7, 9, 64, 7, 9, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16),    # batch 5 of 63-pixel maps
 ]
 
 
