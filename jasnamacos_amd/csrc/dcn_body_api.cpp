@@ -46,8 +46,6 @@ struct dcn_body {
     uint16_t* deform_cb8 = nullptr;  // DCN input [feat_prop, feat_n2], 128 channels
     uint16_t* off_a = nullptr;       // conv_offset intermediates, 64 channels CB8
     uint16_t* off_b = nullptr;
-    uint16_t* offset = nullptr;      // 288 NCHW
-    uint16_t* mask = nullptr;        // 144 NCHW
     uint16_t* bb_in = nullptr;       // backbone input [feat_current, prefix..., aligned] CB8
     uint16_t* feat[2] = {};          // backbone features, 64 channels CB8
     hipStream_t capture_stream = nullptr;
@@ -410,7 +408,6 @@ dcn_status dcn_body_create_tiles(dcn_context* ctx, int height, int width, int br
                                                   weights->dcn_bias, stream, &b->dcn);
         if (st != DCN_OK) return bail(st);
     }
-    const size_t plane = (size_t)width * height;
     const size_t T = (size_t)tiles;
     dcn_status st = DCN_OK;
     auto a16 = [&](uint16_t** p, size_t elems) {
@@ -420,8 +417,6 @@ dcn_status dcn_body_create_tiles(dcn_context* ctx, int height, int width, int br
     a16(&b->deform_cb8, T * dcn::cb8_tensor_elems(128, height, width));
     a16(&b->off_a, T * dcn::cb8_tensor_elems(64, height, width));
     a16(&b->off_b, T * dcn::cb8_tensor_elems(64, height, width));
-    a16(&b->offset, T * 288 * plane);
-    a16(&b->mask, T * 144 * plane);
     a16(&b->bb_in, T * dcn::cb8_tensor_elems(bb_in, height, width));
     for (auto& f : b->feat) a16(&f, T * dcn::cb8_tensor_elems(64, height, width));
     if (st != DCN_OK) return bail(st);
@@ -520,7 +515,7 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
                                            body->deform_cb8, body->bb_in, H, W, s, body->tiles));
     const long off_ts = cb8_image(body, 8);
     // conv_offset: 196 -> 64 -> 64 -> 64 (LeakyReLU 0.1) -> 432, the last one turning its
-    // output into offsets and masks in its epilogue.
+    // output into offsets and masks for the DCN of the same launch.
     dcn::ConvBatch cond_conv;
     cond_conv.images = body->tiles;
     cond_conv.x = cb8_image(body, 25);
@@ -535,24 +530,15 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
     off_pair.out = off_ts;
     DCN_HIP(ctx, dcn::launch_conv3x3_pair(c1->g, c2->g, body->off_a, c1->wpk, c1->bias, 1, c2->wpk, c2->bias,
                                           1, 0.1f, nullptr, NCHW, nullptr, NCHW, body->off_b, CB8, s, 0, off_pair));
+    // The last conv_offset layer (offsets and masks kept in LDS) and the DCN in one
+    // launch; the DCN writes the aligned feature into the backbone input (CB8, after the
+    // prefix).
     const dcn_conv* c3 = body->offset_conv[3];
-    DCN_HIP(ctx, dcn::launch_conv3x3_offsets(c3->g, body->off_b, c3->wpk, c3->bias,
-                                             (const uint16_t*)d_flow1, (const uint16_t*)d_flow2_out,
-                                             body->offset, body->mask, s, body->tiles));
-    // The DCN writes the aligned feature into the backbone input (CB8, after the prefix).
-    dcn_shape ds = body_dcn_shape(H, W);
-    ds.batch = body->tiles;
-    dcn::FusedGeometry g;
-    dcn::fused_geometry(ds, &g);
-    const dcn::FusedConfig cfg{dcn::kVariantNarrow, 1, 12, dcn::kSamplerFast};
-    const int aligned_c = 64 * (body->branch + 1);
-    dcn::OutPlacement place;
-    place.cb8 = 1;
-    place.coff = aligned_c;
-    place.cblk = 8 * (body->branch + 2);
-    DCN_HIP(ctx, dcn::launch_narrow_f16(dcn::to_kshape(ds), g, cfg, body->deform_cb8, body->offset,
-                                        body->mask, body->dcn->weights_narrow, body->dcn->bias,
-                                        body->bb_in, s, place));
+    DCN_HIP(ctx, dcn::launch_offsets_dcn(c3->g, body->off_b, c3->wpk, c3->bias, (const uint16_t*)d_flow1,
+                                         (const uint16_t*)d_flow2_out, body->deform_cb8, body->dcn->weights_narrow,
+                                         dcn::narrow_packed_bytes(body->dcn->geometry), body->dcn->bias,
+                                         body->bb_in, 64 * (body->branch + 1), 8 * (body->branch + 2),
+                                         body->tiles, s));
     return run_backbone(body, d_feat_prop_out, s);
 }
 

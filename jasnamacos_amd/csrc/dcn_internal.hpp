@@ -205,6 +205,14 @@ hipError_t launch_spynet_small(int batch, int pairs, int levels, const int* heig
 // The last conv_offset layer (cout 432) with prepare_dcn_offsets_fp16 in its epilogue:
 // raw = half(conv + bias), offsets = half(10 tanh(raw) + flow), masks = half(sigmoid(raw)).
 // `images` images: CB8 inputs, flows [2][plane], offsets and masks at their own strides.
+// The body's last conv_offset layer (64 -> 432 with the offset/mask transform) and its
+// DCN (128 -> 64, narrow_kernel arithmetic) in one launch, the offsets kept in LDS; the
+// aligned feature goes to channels out_coff.. of the CB8 backbone input (out_cblk blocks).
+hipError_t launch_offsets_dcn(const ConvGeometry& goff, const void* xoff_cb8, const void* woff,
+                              const float* boff, const uint16_t* flow1, const uint16_t* flow2,
+                              const void* xin_cb8, const void* wdcn, size_t wdcn_bytes,
+                              const float* bdcn, uint16_t* out_cb8, int out_coff, int out_cblk,
+                              int images, hipStream_t stream);
 hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                                   const float* bias, const uint16_t* flow1, const uint16_t* flow2,
                                   uint16_t* offset, uint16_t* mask, hipStream_t stream, int images = 1);

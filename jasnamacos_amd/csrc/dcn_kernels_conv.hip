@@ -437,132 +437,6 @@ __global__ __launch_bounds__(64 * NW, MINW) void conv_offsets_kernel(ConvArgs a0
     }
 }
 
-// conv_offsets_kernel for a batch of images (the body over many tiles): workgroup
-// (tile, chunk, z) runs images z * zpw .. z * zpw + zpw - 1 one after another, each wave
-// keeping the weight fragments of its K range (three K-steps of 64 channels) in registers
-// for all of them and requesting the next image's rows before the current one is
-// reduced. 64 input channels only (18 K-steps, no padded K-blocks). Same K split and
-// summation order as conv_offsets_kernel: every image's results are the same bits.
-template <int NW, int NB, int MINW>
-__global__ __launch_bounds__(64 * NW, MINW) void conv_offsets_images_kernel(ConvArgs a0, int images,
-                                                                            int zpw) {
-    constexpr int KS = 18;
-    constexpr int KMAX = (KS + NW - 1) / NW;
-    static_assert(NB * 128 == 64 * NW, "one epilogue item (two pixels) per thread");
-    extern __shared__ __attribute__((aligned(16))) f32x4 red4[];  // [NW][NB][64] partial sums
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int quarter = lane >> 4;
-
-    const int per_xcd = (a0.tiles + 7) / 8;
-    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (tile >= a0.tiles) return;  // whole workgroup, before any barrier
-    const int chunk = blockIdx.y;
-    const int z0 = blockIdx.z * zpw;
-    const int z1 = min(z0 + zpw, images);
-
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a0.wpk, a0.wpk_bytes);
-    const int M = a0.H * a0.W;
-    uint32_t base;
-    {
-        const int pc = min(tile * 16 + (lane & 15), M - 1);
-        const int y = pc / a0.W;
-        base = (uint32_t)(y + kPad - 1) * a0.Wp + (pc - y * a0.W) + kPad - 1;
-    }
-    const int s0 = wave * KS / NW;
-    const int s1 = (wave + 1) * KS / NW;
-    h8 Bf[KMAX][NB];
-    uint32_t koff[KMAX];
-#pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-        const int s = s0 + i < s1 ? s0 + i : s1 - 1;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-            Bf[i][nb] = __builtin_bit_cast(
-                h8, load16(wr, (uint32_t)((s * a0.NBT + chunk * NB + nb) * 64 + lane) * 16u));
-        const int kb = 4 * s + quarter;
-        const int tap = kb >> 3;
-        const int cb = kb & 7;
-        const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
-        const int kx = tap - ky * 3;
-        koff[i] = (uint32_t)(cb * a0.Hp + ky) * a0.Wp + kx;
-    }
-    u32x4 q[KMAX];
-    auto load_rows = [&](int z) {
-        const __amdgpu_buffer_rsrc_t xr =
-            make_rsrc(static_cast<const uint16_t*>(a0.xin) + (long)z * a0.xin_ts, a0.xin_bytes);
-#pragma unroll
-        for (int i = 0; i < KMAX; ++i) q[i] = load16(xr, (base + koff[i]) * 16u);
-    };
-    load_rows(z0);
-
-    // Epilogue item of this thread: the 8-byte half h of row (nb, l), i.e. pixels
-    // tile * 16 + 4 (l / 16) + 2 h + j (j = 0, 1) of channel chunk * 16 NB + 16 nb + l % 16.
-    const int h = tid & 1;
-    const int l = (tid >> 1) & 63;
-    const int nb_e = ((tid >> 1) >> 6) % NB;
-    const int oc = chunk * 16 * NB + nb_e * 16 + (l & 15);
-    const bool oc_ok = oc < a0.Cout;
-    const float bias = oc_ok ? a0.bias[oc] : 0.0f;
-    const int p0 = tile * 16 + 4 * (l >> 4) + 2 * h;
-    const int flow_channel = ((oc % 144) & 1) == 0 ? 1 : 0;  // even = dy = flow y
-    const float2* red2 = reinterpret_cast<const float2*>(red4);
-
-    for (int z = z0; z < z1; ++z) {
-        const ConvArgs a = conv_image_at(a0, z);
-        // The flow under this thread's offsets, requested before the convolution.
-        uint16_t fv[2] = {0, 0};
-        const uint16_t* flow = oc < 144 ? a.flow1 : a.flow2;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            if (oc_ok && oc < 288 && p0 + j < M) fv[j] = flow[flow_channel * (size_t)M + p0 + j];
-
-        f32x4 acc[NB];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{};
-#pragma unroll
-        for (int i = 0; i < KMAX; ++i) {
-            if (s0 + i < s1) {  // uniform across the wave
-                const h8 A = __builtin_bit_cast(h8, q[i]);
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
-            }
-        }
-        if (z + 1 < z1) load_rows(z + 1);  // in flight through the reduction and epilogue
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) red4[(wave * NB + nb) * 64 + lane] = acc[nb];
-        __syncthreads();
-
-        float2 sum = {0.0f, 0.0f};
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float2 t = red2[((w * NB + nb_e) * 64 + l) * 2 + h];
-            sum.x += t.x;
-            sum.y += t.y;
-        }
-        if (oc_ok) {
-            // prepare_dcn_offsets_fp16 (MetalShader.swift:815-839) on the FP16 conv output.
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int px = p0 + j;
-                if (px >= M) continue;
-                const float raw = (float)round_f16((j ? sum.y : sum.x) + bias);
-                if (oc < 288) {
-                    const float residue = 10.0f * tanhf(raw);
-                    const float f = (float)__builtin_bit_cast(_Float16, fv[j]);
-                    a.offset[(size_t)oc * M + px] = __builtin_bit_cast(uint16_t, round_f16(residue + f));
-                } else {
-                    a.mask[(size_t)(oc - 288) * M + px] =
-                        __builtin_bit_cast(uint16_t, round_f16(1.0f / (1.0f + expf(-raw))));
-                }
-            }
-        }
-        if (z + 1 < z1) __syncthreads();  // sums read before the next image's partials
-    }
-}
-
 // Conv weights OIHW FP16 [Cout][Cin][3][3] -> B fragments [ksteps][NBT][64][8]:
 // lane l of K-step s holds output channel nb*16 + l%16 and K-block 4s + l/16 =
 // tap * CB + cb, channels 8 cb .. 8 cb + 7 (zero past Cin, past Cout and past KB).
@@ -906,12 +780,11 @@ hipError_t launch_conv_prepack(const ConvGeometry& g, const uint16_t* w, const u
 
 namespace {
 
-// Images per workgroup of a batched conv pair, conv3x3 or offsets conv: up to kMax,
-// balanced over the workgroups of a tile. Measured for a body step over 16 tiles (images
-// per workgroup -> us per step), each kernel tuned in turn: conv pair 1 -> 955,
-// 2 -> 828, 4 -> 768, 8 -> 738, 16 -> 723 (over 64 tiles 16 beat 8 by 2 %); offsets conv
-// (4 waves per SIMD; 5 measured slower) 1 -> 754, 2 -> 715, 4 -> 692, 8 -> 680,
-// 16 -> 682; conv3x3 2 -> 685, 4 -> 667, 8 -> 658, 16 -> 654.
+// Images per workgroup of a batched conv pair or conv3x3: up to kMax, balanced over the
+// workgroups of a tile. Measured for a body step over 16 tiles (images per workgroup ->
+// us per step), each kernel tuned in turn: conv pair 1 -> 955, 2 -> 828, 4 -> 768,
+// 8 -> 738, 16 -> 723 (over 64 tiles 16 beat 8 by 2 %); conv3x3 2 -> 685, 4 -> 667,
+// 8 -> 658, 16 -> 654.
 template <int kMax>
 static int images_per_group(int images) {
     const int groups = (images + kMax - 1) / kMax;
@@ -959,8 +832,6 @@ hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, const ConvBatch& batch, 
 
 }  // namespace
 
-constexpr int kOffsetsImagesMinWaves = 4;
-
 hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                                   const float* bias, const uint16_t* flow1, const uint16_t* flow2,
                                   uint16_t* offset, uint16_t* mask, hipStream_t stream, int images) {
@@ -994,17 +865,6 @@ hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, cons
     a.offset_ts = 288 * plane;
     a.mask_ts = 144 * plane;
     constexpr size_t lds = (size_t)NW * RT * NB * 64 * sizeof(f32x4);
-    if (images > 1 && g.cin == 64) {
-        const int zpw = images_per_group<8>(images);
-        auto kernel = &conv_offsets_images_kernel<NW, NB, kOffsetsImagesMinWaves>;
-        static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (attr != hipSuccess) return attr;
-        const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)((g.cout + 16 * NB - 1) / (16 * NB)),
-                        (unsigned)((images + zpw - 1) / zpw));
-        hipLaunchKernelGGL(kernel, grid, dim3(64 * NW), lds, stream, a, images, zpw);
-        return hipGetLastError();
-    }
     auto kernel = &conv_offsets_kernel<NW, U, NB, RT, MINW>;
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
