@@ -114,7 +114,8 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a0) {
         u32x4 q[U];
 #pragma unroll
         for (int i = 0; i < U; ++i) {
-            const int s = sb + i < s1 ? sb + i : s1 - 1;
+            if (sb + i >= s1) continue;  // uniform across the wave; the slot stays unused
+            const int s = sb + i;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
                 Bf[i][nb] = __builtin_bit_cast(
@@ -218,10 +219,11 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_images_kernel(ConvArgs a0, in
 #pragma unroll
     for (int i = 0; i < KMAX; ++i) {
         const int s = s0 + i < s1 ? s0 + i : s1 - 1;
+        if (s0 + i < s1)  // uniform across the wave; slots past the range stay unused
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-            Bf[i][nb] = __builtin_bit_cast(
-                h8, load16(wr, (uint32_t)((s * a0.NBT + chunk * NB + nb) * 64 + lane) * 16u));
+            for (int nb = 0; nb < NB; ++nb)
+                Bf[i][nb] = __builtin_bit_cast(
+                    h8, load16(wr, (uint32_t)((s * a0.NBT + chunk * NB + nb) * 64 + lane) * 16u));
         const int kb = 4 * s + quarter;
         kin[i] = kb < a0.KB;
         const int kbc = kin[i] ? kb : a0.KB - 1;
@@ -236,7 +238,8 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_images_kernel(ConvArgs a0, in
         const __amdgpu_buffer_rsrc_t xr =
             make_rsrc(static_cast<const uint16_t*>(a0.xin) + (long)z * a0.xin_ts, a0.xin_bytes);
 #pragma unroll
-        for (int i = 0; i < KMAX; ++i) q[i] = load16(xr, (base + koff[i]) * 16u);
+        for (int i = 0; i < KMAX; ++i)
+            if (s0 + i < s1) q[i] = load16(xr, (base + koff[i]) * 16u);
     };
     load_rows(z0);
     float biasv[kIters];
@@ -357,7 +360,8 @@ __global__ __launch_bounds__(64 * NW, MINW) void conv_offsets_kernel(ConvArgs a0
         u32x4 q[U][RT];
 #pragma unroll
         for (int i = 0; i < U; ++i) {
-            const int s = sb + i < s1 ? sb + i : s1 - 1;
+            if (sb + i >= s1) continue;  // uniform across the wave; the slot stays unused
+            const int s = sb + i;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
                 Bf[i][nb] = __builtin_bit_cast(
@@ -571,24 +575,23 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
             make_rsrc(static_cast<const uint16_t*>(a.xin) + (long)z * a.xin_ts, a.xin_bytes);
 #pragma unroll
         for (int i = 0; i < KMAX; ++i)
+            if (s0 + i < s1)  // uniform across the wave; slots past the range stay unused
 #pragma unroll
-            for (int rt = 0; rt < kPairRT1; ++rt) q[i][rt] = load16(xr, (base1[rt] + koff[i]) * 16u);
+                for (int rt = 0; rt < kPairRT1; ++rt) q[i][rt] = load16(xr, (base1[rt] + koff[i]) * 16u);
     };
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-        const int s = s0 + i < s1 ? s0 + i : s1 - 1;
+    for (int i = 0; i < KMAX; ++i)
+        if (s0 + i < s1)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-            B1[i][nb] = __builtin_bit_cast(h8, load16(w1, (uint32_t)((s * NB + nb) * 64 + lane) * 16u));
-    }
+            for (int nb = 0; nb < NB; ++nb)
+                B1[i][nb] = __builtin_bit_cast(h8, load16(w1, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
     load_rows(z0);
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-        const int s = s0 + i < s1 ? s0 + i : s1 - 1;
+    for (int i = 0; i < KMAX; ++i)
+        if (s0 + i < s1)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-            B2[i][nb] = __builtin_bit_cast(h8, load16(w2, (uint32_t)((s * NB + nb) * 64 + lane) * 16u));
-    }
+            for (int nb = 0; nb < NB; ++nb)
+                B2[i][nb] = __builtin_bit_cast(h8, load16(w2, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
 
     // Per-thread constants of the two reductions, the same for every image: the biases,
     // and the epilogue's output positions (thread tid < 256 owns output pixels
