@@ -5,11 +5,30 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
+#include <set>
 #include <string>
+#include <tuple>
 
 #include "dcn/dcn.h"
 
 namespace dcn {
+
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) on the current device, once per
+// (kernel, device, size): a launch above 64 KB of dynamic LDS needs it, and a process may
+// drive more than one device.
+inline hipError_t allow_dynamic_lds(const void* kernel, size_t bytes) {
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    static std::mutex mu;
+    static std::set<std::tuple<const void*, int, size_t>> done;
+    std::lock_guard<std::mutex> lock(mu);
+    if (done.count(std::make_tuple(kernel, device, bytes))) return hipSuccess;
+    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) done.insert(std::make_tuple(kernel, device, bytes));
+    return e;
+}
 
 // Shape as seen by device code: the 17 reference fields, by value.
 struct KShape {

@@ -869,8 +869,7 @@ hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, cons
     a.mask_ts = 144 * plane;
     constexpr size_t lds = (size_t)NW * RT * NB * 64 * sizeof(f32x4);
     auto kernel = &conv_offsets_kernel<NW, U, NB, RT, MINW>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
     if (attr != hipSuccess) return attr;
     const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)((g.cout + 16 * NB - 1) / (16 * NB)),
                     (unsigned)images);
@@ -940,8 +939,7 @@ hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, c
     a.tiles = (g1.h + kPairTH - 1) / kPairTH * a.tiles_x;
     constexpr size_t lds = pair_lds_bytes(NW);
     auto kernel = &conv_pair_kernel<NW>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
     if (attr != hipSuccess) return attr;
     const unsigned groups_z = (unsigned)((batch.images + a.zpw - 1) / a.zpw);
     hipLaunchKernelGGL(kernel, dim3((unsigned)((a.tiles + 7) / 8 * 8), 1, groups_z), dim3(64 * NW), lds,

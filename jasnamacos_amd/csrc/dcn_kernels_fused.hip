@@ -474,9 +474,7 @@ __global__ __launch_bounds__(256) void nonfinite_kernel(const uint16_t* __restri
 template <int NB, int MT, int KS, int SAMPLER>
 hipError_t launch_fused_t(const FusedArgs& a, long tiles, hipStream_t stream) {
     const size_t lds = (size_t)KS * MT * NB * 16 * 65 * sizeof(float);
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&fused_kernel<NB, MT, KS, SAMPLER>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(&fused_kernel<NB, MT, KS, SAMPLER>), lds);
     if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL((fused_kernel<NB, MT, KS, SAMPLER>), dim3((unsigned)tiles), dim3(64 * KS),
                        lds, stream, a);
@@ -502,14 +500,8 @@ hipError_t launch_staged_t(const StagedArgs& sa, long tiles, size_t lds, hipStre
     constexpr int kSpw = (kRegs - MT * NB * 16) / (NB * 4);
     constexpr int SPW = kSpw < 1 ? 1 : (kSpw > (NW == 8 ? 9 : 5) ? (NW == 8 ? 9 : 5) : kSpw);
     auto kernel = &staged_kernel<NB, MT, NW, UB, SPW, SAMPLER>;
-    static hipError_t attr = hipErrorNotReady;
-    static size_t attr_bytes = 0;
-    if (attr != hipSuccess || attr_bytes < lds) {
-        attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds);
-        attr_bytes = kMaxLds;
-        if (attr != hipSuccess) return attr;
-    }
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), kMaxLds);
+    if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(kernel, dim3((unsigned)tiles), dim3(64 * NW), lds, stream, sa);
     return hipGetLastError();
 }

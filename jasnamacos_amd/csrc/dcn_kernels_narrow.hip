@@ -360,8 +360,7 @@ hipError_t launch_narrow_images_t(NarrowArgs a, int images, hipStream_t stream) 
     constexpr int KMAX = 3;
     const size_t lds = (size_t)NW * NB * 4 * 65 * sizeof(float);
     auto kernel = &narrow_images_kernel<NB, NW, KMAX, SAMPLER>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
     if (attr != hipSuccess) return attr;
     a.tiles = (a.HWo + 15) / 16;  // per image
     const int zpw = narrow_images_per_group(images);
@@ -377,8 +376,7 @@ hipError_t launch_narrow_t(const NarrowArgs& a, hipStream_t stream) {
     constexpr int U = NB >= 6 ? (NW == 12 ? 2 : 3) : (NW == 12 ? 3 : 5);
     const size_t lds = (size_t)NW * NB * 4 * 65 * sizeof(float);
     auto kernel = &narrow_kernel<NB, NW, U, SAMPLER>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
     if (attr != hipSuccess) return attr;
     const int grid = (a.tiles + 7) / 8 * 8;
     hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(64 * NW), lds, stream, a);

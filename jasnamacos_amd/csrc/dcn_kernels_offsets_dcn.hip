@@ -307,8 +307,7 @@ hipError_t launch_offsets_dcn(const ConvGeometry& goff, const void* xoff_cb8, co
     a.woff_bytes = (uint32_t)conv_packed_bytes(goff);
     a.wdcn_bytes = (uint32_t)wdcn_bytes;
     auto kernel = &offsets_dcn_kernel<kSamplerFast>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, (int)kOdLds);
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)kOdLds);
     if (attr != hipSuccess) return attr;
     const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), 1, (unsigned)images);
     hipLaunchKernelGGL(kernel, grid, dim3(kOdThreads), kOdLds, stream, a);

@@ -737,8 +737,7 @@ hipError_t launch_spynet_small(int batch, int pairs, int levels, const int* heig
     const size_t lds = spynet_small_lds_bytes(units);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     auto kernel = &spynet_small_kernel<NW>;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), 160 * 1024);
     if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(kernel, dim3((unsigned)batch), dim3(64 * NW), lds, stream, a);
     return hipGetLastError();

@@ -689,9 +689,7 @@ __global__ __launch_bounds__(64 * kAsyncNw) void window_async_kernel(WindowArgs 
 template <int NB, int SAMPLER>
 hipError_t launch_window_async_t(const WindowArgs& a, hipStream_t stream) {
     auto kernel = &window_async_kernel<NB, SAMPLER>;
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-        AsyncLayout<NB>::kBytes);
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), AsyncLayout<NB>::kBytes);
     if (attr != hipSuccess) return attr;
     const unsigned grid = (unsigned)(((a.tiles + 7) / 8) * 8);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kAsyncNw), AsyncLayout<NB>::kBytes, stream, a);
@@ -732,8 +730,7 @@ hipError_t launch_window_t(const WindowArgs& a, hipStream_t stream) {
     constexpr int NBUF = NW == 8 ? 2 : 1;
     const size_t lds = (size_t)window_lds(NBUF) + 2 * GPS * NW * 4 * sizeof(int);
     auto kernel = &window_kernel<NB, NW, TR, GPS, SAMPLER, SPLIT, NBUF>;
-    static hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
     if (attr != hipSuccess) return attr;
     const unsigned grid = (unsigned)(((a.tiles + 7) / 8) * 8);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * NW), lds, stream, a);
