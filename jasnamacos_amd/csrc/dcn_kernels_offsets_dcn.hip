@@ -6,17 +6,18 @@
 // (no HBM round trip, SURVEY's "directly in the DCN sampler from raw conv output"), and a
 // frame saves one launch and one kernel's load/reduce latency chain.
 //
-// Workgroup: 12 waves on one 16-pixel tile of one image (grid z = image).
-//  * Phase A, the offsets conv: the tile's A fragments (18 K-steps of 64 lanes) are staged
-//    in LDS once; wave w owns 16-channel column blocks w, w + 12 (and w + 24 for w < 3) of
-//    the 27 and runs every K-step for them, streaming its weight fragments. The K range is
+// Workgroup: 12 waves on one 16-pixel tile of up to three images (grid z = image group).
+//  * Phase A, the offsets conv: the tile's A fragments (18 K-steps of 64 lanes per image)
+//    are staged in LDS once; wave w owns 16-channel column blocks w, w + 12 (and w + 24 for
+//    w < 3) of the 27 and runs every K-step for them, streaming its weight fragments and
+//    applying each to every image of the group. The K range is
 //    summed in conv_offsets_kernel's order: chains over the eight ranges
 //    [r * 18 / 8, (r + 1) * 18 / 8) from zero, added to a zero sum in range order, so each
 //    raw value, and each offset and mask after prepare_dcn_offsets_fp16
 //    (MetalShader.swift:815-839), is the same bits as conv_offsets_kernel's.
-//  * Phase B, the DCN: narrow_kernel<4, 12, 3> with the offsets and masks read from LDS
-//    (same K split, blend and summation order): the aligned feature is the same bits as
-//    the two-kernel path.
+//  * Phase B, the DCN, image by image with the weight fragments held in registers:
+//    narrow_kernel<4, 12, 3> with the offsets and masks read from LDS (same K split, blend
+//    and summation order): the aligned feature is the same bits as the two-kernel path.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -42,17 +43,21 @@ constexpr int kDcnKsteps = 36;                 // 128 channels x 9 taps / 32
 constexpr int kDcnNb = 4;                      // 64 output channels
 constexpr int kDcnPerWave = kDcnKsteps / kOdWaves;
 
-constexpr size_t kStageBytes = (size_t)kOffKsteps * 64 * 16;       // A fragments
-constexpr size_t kOffsBytes = (size_t)kOffChannels * 16 * 2;        // [432][16] FP16
+constexpr size_t kStageBytes = (size_t)kOffKsteps * 64 * 16;       // A fragments of an image
+constexpr size_t kOffsBytes = (size_t)kOffChannels * 16 * 2;        // [432][16] FP16 per image
 constexpr size_t kRedBytes = (size_t)kOdWaves * kDcnNb * 4 * 65 * 4;  // narrow_kernel's sums
-constexpr size_t kOdLds = kStageBytes + kOffsBytes + kRedBytes;
-
-// True when K-step s ends one of the eight K ranges of conv_offsets_kernel.
-__host__ __device__ constexpr bool range_end(int s) {
-    for (int r = 0; r < kOffSplit; ++r)
-        if ((r + 1) * kOffKsteps / kOffSplit - 1 == s) return true;
-    return false;
+constexpr size_t kFlowBytes = 2 * 2 * 16 * 2;                      // [flow][channel][16] FP16 per image
+__host__ __device__ constexpr size_t od_lds_bytes(int images) {
+    return (size_t)images * (kStageBytes + kOffsBytes + kFlowBytes) + kRedBytes;
 }
+
+// Bit s set when K-step s ends one of the eight K ranges of conv_offsets_kernel.
+__host__ __device__ constexpr uint32_t range_ends() {
+    uint32_t m = 0;
+    for (int r = 0; r < kOffSplit; ++r) m |= 1u << ((r + 1) * kOffKsteps / kOffSplit - 1);
+    return m;
+}
+constexpr uint32_t kRangeEnds = range_ends();
 
 struct OffsetsDcnArgs {
     const void* xoff;       // CB8 offset-branch features (64 channels), per image xoff_ts
@@ -65,16 +70,20 @@ struct OffsetsDcnArgs {
     const float* bdcn;      // [64]
     uint16_t* out;          // CB8 backbone input, per image out_ts
     uint32_t xoff_bytes, woff_bytes, xin_bytes, wdcn_bytes;
-    int H, W, Hp, Wp, nbt, tiles, out_coff, out_cblk;
+    int H, W, Hp, Wp, nbt, tiles, out_coff, out_cblk, images;
     long xoff_ts, flow_ts, xin_ts, out_ts;
 };
 
-template <int SAMPLER>
+// Workgroup (tile, zg) runs images zg * Z .. zg * Z + Z - 1 (fewer in the last group):
+// phase A for all of them at once (each weight fragment applied to every image's A
+// fragment), then phase B image by image with the DCN weights held in registers.
+template <int SAMPLER, int Z>
 __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    u32x4* stage = reinterpret_cast<u32x4*>(lds);                          // [18][64]
-    uint16_t* offs = reinterpret_cast<uint16_t*>(lds + kStageBytes);      // [432][16]
-    float* red = reinterpret_cast<float*>(lds + kStageBytes + kOffsBytes);  // [12][4][4][65]
+    u32x4* stage = reinterpret_cast<u32x4*>(lds);                                 // [Z][18][64]
+    uint16_t* offs = reinterpret_cast<uint16_t*>(lds + Z * kStageBytes);         // [Z][432][16]
+    float* red = reinterpret_cast<float*>(lds + Z * (kStageBytes + kOffsBytes));  // [12][4][4][65]
+    uint16_t* flows = reinterpret_cast<uint16_t*>(lds + Z * (kStageBytes + kOffsBytes) + kRedBytes);  // [Z][2][2][16]
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -83,23 +92,22 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     const int per_xcd = (a.tiles + 7) / 8;
     const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (tile >= a.tiles) return;  // whole workgroup, before any barrier
-    const long z = blockIdx.z;
+    const long z0 = (long)blockIdx.z * Z;
+    const int nimg = (int)min((long)Z, (long)a.images - z0);  // uniform, >= 1
     const int M = a.H * a.W;
-
-    const __amdgpu_buffer_rsrc_t xor_ =
-        make_rsrc(static_cast<const uint16_t*>(a.xoff) + z * a.xoff_ts, a.xoff_bytes);
     const __amdgpu_buffer_rsrc_t wor = make_rsrc(a.woff, a.woff_bytes);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(static_cast<const uint16_t*>(a.xin) + z * a.xin_ts, a.xin_bytes);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wdcn, a.wdcn_bytes);
-    const uint16_t* flow1 = a.flow1 + z * a.flow_ts;
-    const uint16_t* flow2 = a.flow2 + z * a.flow_ts;
 
     // ---- phase A: the offsets conv on this tile ----------------------------------------
     // A fragment of K-step s, lane l: pixel l % 16 (clamped into the image), K-block
     // 4 s + l / 16 = tap * 8 + cb, as conv_offsets_kernel loads it.
-    for (int u = tid; u < kOffKsteps * 64; u += kOdThreads) {
-        const int s = u >> 6;
-        const int l = u & 63;
+    for (int u = tid; u < nimg * kOffKsteps * 64; u += kOdThreads) {
+        const int img = u / (kOffKsteps * 64);
+        const int r = u - img * (kOffKsteps * 64);
+        const int s = r >> 6;
+        const int l = r & 63;
+        const __amdgpu_buffer_rsrc_t xor_ =
+            make_rsrc(static_cast<const uint16_t*>(a.xoff) + (z0 + img) * a.xoff_ts, a.xoff_bytes);
         const int pc = min(tile * 16 + (l & 15), M - 1);
         const int y = pc / a.W;
         const uint32_t base = (uint32_t)(y + kPad - 1) * a.Wp + (pc - y * a.W) + kPad - 1;
@@ -111,21 +119,17 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
         stage[u] = load16(xor_, (base + (uint32_t)(cb * a.Hp + ky) * a.Wp + kx) * 16u);
     }
 
-    // Column blocks of this wave, and the flow under each of its outputs (pixel
-    // 4 (l / 16) + v of the tile, channel 16 nb + l % 16), requested up front.
-    const int nblocks = wave < kOffBlocks - 2 * kOdWaves ? 3 : 2;
-    uint16_t fl[3][4];
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int oc = (wave + kOdWaves * j) * 16 + (lane & 15);
-        const uint16_t* flow = oc < 144 ? flow1 : flow2;
-        const int channel = ((oc % 144) & 1) == 0 ? 1 : 0;  // even = dy = flow y
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int px = tile * 16 + 4 * quarter + v;
-            fl[j][v] = (j < nblocks && oc < 288 && px < M) ? flow[channel * (size_t)M + px] : (uint16_t)0;
-        }
+    // The tile's flows (both flows, both channels, 16 pixels per image) into LDS.
+    if (tid < nimg * 64) {
+        const int img = tid >> 6;
+        const int f = (tid >> 5) & 1;
+        const int c = (tid >> 4) & 1;
+        const int px = tile * 16 + (tid & 15);
+        const uint16_t* flow = (f == 0 ? a.flow1 : a.flow2) + (z0 + img) * a.flow_ts;
+        flows[tid] = px < M ? flow[c * (size_t)M + px] : (uint16_t)0;
     }
+    // Column blocks of this wave.
+    const int nblocks = wave < kOffBlocks - 2 * kOdWaves ? 3 : 2;
 
     h8 Bq[kOffRing][3];
     auto load_b = [&](int slot, int s) {
@@ -139,48 +143,71 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     for (int s = 0; s < kOffRing; ++s) load_b(s, s);
     __syncthreads();  // A fragments staged
 
-    f32x4 acc[3], sum[3];
+    f32x4 acc[Z][3], sum[Z][3];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        acc[j] = f32x4{};
-        sum[j] = f32x4{};
-    }
+    for (int i = 0; i < Z; ++i)
 #pragma unroll
-    for (int s = 0; s < kOffKsteps; ++s) {
-        const h8 A = __builtin_bit_cast(h8, stage[s * 64 + lane]);
-        const int slot = s % kOffRing;
+        for (int j = 0; j < 3; ++j) {
+            acc[i][j] = f32x4{};
+            sum[i][j] = f32x4{};
+        }
+    // Groups of kOffRing K-steps, one ring slot each; the group loop stays rolled so that
+    // the compiler does not hoist later groups' loads (and their registers) forward.
+    static_assert(kOffKsteps % kOffRing == 0, "whole ring groups");
+#pragma unroll 1
+    for (int sg = 0; sg < kOffKsteps; sg += kOffRing) {
 #pragma unroll
-        for (int j = 0; j < 3; ++j)
-            if (j < nblocks) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bq[slot][j], acc[j], 0, 0, 0);
-        if (s + kOffRing < kOffKsteps) load_b(slot, s + kOffRing);
-        if (range_end(s)) {
+        for (int slot = 0; slot < kOffRing; ++slot) {
+            const int s = sg + slot;
 #pragma unroll
-            for (int j = 0; j < 3; ++j) {
+            for (int i = 0; i < Z; ++i) {
+                if (i >= nimg) continue;
+                const h8 A = __builtin_bit_cast(h8, stage[(i * kOffKsteps + s) * 64 + lane]);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) sum[j][v] += acc[j][v];
-                acc[j] = f32x4{};
+                for (int j = 0; j < 3; ++j)
+                    if (j < nblocks)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bq[slot][j], acc[i][j], 0, 0, 0);
+            }
+            if (s + kOffRing < kOffKsteps) load_b(slot, s + kOffRing);
+            if ((kRangeEnds >> s) & 1) {
+#pragma unroll
+                for (int i = 0; i < Z; ++i)
+#pragma unroll
+                    for (int j = 0; j < 3; ++j) {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) sum[i][j][v] += acc[i][j][v];
+                        acc[i][j] = f32x4{};
+                    }
             }
         }
     }
     // prepare_dcn_offsets_fp16 (MetalShader.swift:815-839) on the FP16 conv output, into
-    // the LDS offsets [channel][pixel].
+    // the LDS offsets [image][channel][pixel].
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
         if (j >= nblocks) continue;
         const int oc = (wave + kOdWaves * j) * 16 + (lane & 15);
         const float bias = a.boff[oc];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int px = 4 * quarter + v;
-            const float raw = (float)round_f16(sum[j][v] + bias);
-            _Float16 r;
-            if (oc < 288) {
-                const float residue = 10.0f * tanhf(raw);
-                r = round_f16(residue + (float)__builtin_bit_cast(_Float16, fl[j][v]));
-            } else {
-                r = round_f16(1.0f / (1.0f + expf(-raw)));
+        for (int i = 0; i < Z; ++i) {
+            if (i >= nimg) continue;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int px = 4 * quarter + v;
+                const float raw = (float)round_f16(sum[i][j][v] + bias);
+                _Float16 r;
+                if (oc < 288) {
+                    // flow1 under channels < 144, flow2 above; even channels (dy) take
+                    // the flow's y component (channel 1).
+                    const float residue = 10.0f * tanhf(raw);
+                    const int fc = ((oc % 144) & 1) == 0 ? 1 : 0;
+                    const uint16_t f = flows[((i * 2 + (oc < 144 ? 0 : 1)) * 2 + fc) * 16 + px];
+                    r = round_f16(residue + (float)__builtin_bit_cast(_Float16, f));
+                } else {
+                    r = round_f16(1.0f / (1.0f + expf(-raw)));
+                }
+                offs[(i * kOffChannels + oc) * 16 + px] = __builtin_bit_cast(uint16_t, r);
             }
-            offs[oc * 16 + px] = __builtin_bit_cast(uint16_t, r);
         }
     }
     __syncthreads();  // offsets and masks of the tile complete
@@ -202,74 +229,90 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
 #pragma unroll
         for (int nb = 0; nb < kDcnNb; ++nb)
             Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)(((s0 + i) * kDcnNb + nb) * 64 + lane) * 16u));
-    u32x4 q[kDcnPerWave][4];
-    float ly[kDcnPerWave], lx[kDcnPerWave], m[kDcnPerWave];
+
+    for (int img = 0; img < nimg; ++img) {
+        const long z = z0 + img;
+        const __amdgpu_buffer_rsrc_t xr =
+            make_rsrc(static_cast<const uint16_t*>(a.xin) + z * a.xin_ts, a.xin_bytes);
+        const uint16_t* io = offs + img * kOffChannels * 16;
+        u32x4 q[kDcnPerWave][4];
+        float ly[kDcnPerWave], lx[kDcnPerWave], m[kDcnPerWave];
 #pragma unroll
-    for (int i = 0; i < kDcnPerWave; ++i) {
-        const int gt = 4 * (s0 + i) + quarter;  // K-block = g * 9 + tap (8 channels per group)
-        const int g = (gt * 57) >> 9;           // gt / 9 for gt < 144
-        const int tap = gt - g * 9;
-        const int ky = (tap * 11) >> 5;
-        const int kx = tap - ky * 3;
-        const int pl = lane & 15;
-        const float dy = (float)__builtin_bit_cast(_Float16, offs[(2 * gt) * 16 + pl]);
-        const float dx = (float)__builtin_bit_cast(_Float16, offs[(2 * gt + 1) * 16 + pl]);
-        const float mk = (float)__builtin_bit_cast(_Float16, offs[(288 + gt) * 16 + pl]);
-        // y = float(oy*sh - ph + ky*dh) + dy, as MetalShader.swift:327-332. Dead lanes
-        // (tile tail) sample the zero border with weight 0.
-        const float y = pvalid ? (float)(base_y + ky) + dy : -16.0f;
-        const float x = pvalid ? (float)(base_x + kx) + dx : -16.0f;
-        m[i] = pvalid ? mk : 0.0f;
-        const float fy = floorf(y);
-        const float fx = floorf(x);
-        ly[i] = y - fy;
-        lx[i] = x - fx;
-        const int iy = (int)fminf(fmaxf(fy, (float)-kPad), (float)a.H);
-        const int ix = (int)fminf(fmaxf(fx, (float)-kPad), (float)a.W);
-        const uint32_t uu = xinb + (uint32_t)(g * a.Hp + iy) * a.Wp + ix;
-        q[i][0] = load16(xr, uu * 16u);
-        q[i][1] = load16(xr, uu * 16u + 16u);
-        q[i][2] = load16(xr, (uu + a.Wp) * 16u);
-        q[i][3] = load16(xr, (uu + a.Wp) * 16u + 16u);
-    }
-    f32x4 dacc[kDcnNb];
+        for (int i = 0; i < kDcnPerWave; ++i) {
+            const int gt = 4 * (s0 + i) + quarter;  // K-block = g * 9 + tap (8 channels per group)
+            const int g = (gt * 57) >> 9;           // gt / 9 for gt < 144
+            const int tap = gt - g * 9;
+            const int ky = (tap * 11) >> 5;
+            const int kx = tap - ky * 3;
+            const int pl = lane & 15;
+            const float dy = (float)__builtin_bit_cast(_Float16, io[(2 * gt) * 16 + pl]);
+            const float dx = (float)__builtin_bit_cast(_Float16, io[(2 * gt + 1) * 16 + pl]);
+            const float mk = (float)__builtin_bit_cast(_Float16, io[(288 + gt) * 16 + pl]);
+            // y = float(oy*sh - ph + ky*dh) + dy, as MetalShader.swift:327-332. Dead lanes
+            // (tile tail) sample the zero border with weight 0.
+            const float y = pvalid ? (float)(base_y + ky) + dy : -16.0f;
+            const float x = pvalid ? (float)(base_x + kx) + dx : -16.0f;
+            m[i] = pvalid ? mk : 0.0f;
+            const float fy = floorf(y);
+            const float fx = floorf(x);
+            ly[i] = y - fy;
+            lx[i] = x - fx;
+            const int iy = (int)fminf(fmaxf(fy, (float)-kPad), (float)a.H);
+            const int ix = (int)fminf(fmaxf(fx, (float)-kPad), (float)a.W);
+            const uint32_t uu = xinb + (uint32_t)(g * a.Hp + iy) * a.Wp + ix;
+            q[i][0] = load16(xr, uu * 16u);
+            q[i][1] = load16(xr, uu * 16u + 16u);
+            q[i][2] = load16(xr, (uu + a.Wp) * 16u);
+            q[i][3] = load16(xr, (uu + a.Wp) * 16u + 16u);
+        }
+        f32x4 dacc[kDcnNb];
 #pragma unroll
-    for (int nb = 0; nb < kDcnNb; ++nb) dacc[nb] = f32x4{};
+        for (int nb = 0; nb < kDcnNb; ++nb) dacc[nb] = f32x4{};
 #pragma unroll
-    for (int i = 0; i < kDcnPerWave; ++i) {
-        const h8 A = blend<SAMPLER>(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], m[i]);
+        for (int i = 0; i < kDcnPerWave; ++i) {
+            const h8 A = blend<SAMPLER>(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], m[i]);
+#pragma unroll
+            for (int nb = 0; nb < kDcnNb; ++nb)
+                dacc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], dacc[nb], 0, 0, 0);
+        }
+        if (img > 0) __syncthreads();  // the previous image's sums were read
 #pragma unroll
         for (int nb = 0; nb < kDcnNb; ++nb)
-            dacc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], dacc[nb], 0, 0, 0);
-    }
 #pragma unroll
-    for (int nb = 0; nb < kDcnNb; ++nb)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) red[((wave * kDcnNb + nb) * 4 + v) * 65 + lane] = dacc[nb][v];
-    __syncthreads();
+            for (int v = 0; v < 4; ++v) red[((wave * kDcnNb + nb) * 4 + v) * 65 + lane] = dacc[nb][v];
+        __syncthreads();
 
-    uint16_t* out = a.out + z * a.out_ts;
-    for (int idx = tid; idx < 16 * kDcnNb * 16; idx += kOdThreads) {
-        const int pl = idx & 15;
-        const int oc = idx >> 4;
-        const int nb = oc >> 4;
-        const int src = ((pl >> 2) << 4) + (oc & 15);
-        const int v = pl & 3;
-        float s = 0.0f;
+        uint16_t* out = a.out + z * a.out_ts;
+        for (int idx = tid; idx < 16 * kDcnNb * 16; idx += kOdThreads) {
+            const int pl = idx & 15;
+            const int oc = idx >> 4;
+            const int nb = oc >> 4;
+            const int src = ((pl >> 2) << 4) + (oc & 15);
+            const int v = pl & 3;
+            float s = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kOdWaves; ++w) s += red[((w * kDcnNb + nb) * 4 + v) * 65 + src];
-        if (pvalid) {  // pl == lane % 16: this lane's pixel
-            const int c = a.out_coff + oc;
-            const size_t dst = ((size_t)((c >> 3) * (a.H + 2 * kPad) + oy + kPad) * (a.W + 2 * kPad) + ox + kPad) * 8 +
-                               (c & 7);
-            out[dst] = __builtin_bit_cast(uint16_t, round_f16(s + a.bdcn[oc]));
+            for (int w = 0; w < kOdWaves; ++w) s += red[((w * kDcnNb + nb) * 4 + v) * 65 + src];
+            if (pvalid) {  // pl == lane % 16: this lane's pixel
+                const int c = a.out_coff + oc;
+                const size_t dst =
+                    ((size_t)((c >> 3) * (a.H + 2 * kPad) + oy + kPad) * (a.W + 2 * kPad) + ox + kPad) * 8 + (c & 7);
+                out[dst] = __builtin_bit_cast(uint16_t, round_f16(s + a.bdcn[oc]));
+            }
         }
     }
 }
 
-}  // namespace
+template <int Z>
+hipError_t launch_od_t(const OffsetsDcnArgs& a, hipStream_t stream) {
+    auto kernel = &offsets_dcn_kernel<kSamplerFast, Z>;
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), od_lds_bytes(Z));
+    if (attr != hipSuccess) return attr;
+    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), 1, (unsigned)((a.images + Z - 1) / Z));
+    hipLaunchKernelGGL(kernel, grid, dim3(kOdThreads), od_lds_bytes(Z), stream, a);
+    return hipGetLastError();
+}
 
-size_t offsets_dcn_lds_bytes() { return kOdLds; }
+}  // namespace
 
 hipError_t launch_offsets_dcn(const ConvGeometry& goff, const void* xoff_cb8, const void* woff,
                               const float* boff, const uint16_t* flow1, const uint16_t* flow2,
@@ -306,12 +349,13 @@ hipError_t launch_offsets_dcn(const ConvGeometry& goff, const void* xoff_cb8, co
     a.xin_bytes = (uint32_t)(a.xin_ts * 2);
     a.woff_bytes = (uint32_t)conv_packed_bytes(goff);
     a.wdcn_bytes = (uint32_t)wdcn_bytes;
-    auto kernel = &offsets_dcn_kernel<kSamplerFast>;
-    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)kOdLds);
-    if (attr != hipSuccess) return attr;
-    const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), 1, (unsigned)images);
-    hipLaunchKernelGGL(kernel, grid, dim3(kOdThreads), kOdLds, stream, a);
-    return hipGetLastError();
+    a.images = images;
+    // Images per workgroup: three where there are three (LDS: 147 KB), measured for a
+    // body step over 16 tiles: 621 us (one), 580 (two), 574 (three); over 64 tiles
+    // 2478, 2294, 2258 us.
+    if (images >= 3) return launch_od_t<3>(a, stream);
+    if (images == 2) return launch_od_t<2>(a, stream);
+    return launch_od_t<1>(a, stream);
 }
 
 }  // namespace dcn
