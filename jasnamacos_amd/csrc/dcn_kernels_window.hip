@@ -69,8 +69,8 @@ __host__ __device__ constexpr int unit_tap(int u) {
     return GPS == 2 ? u - 9 * (u >= 9 ? 1 : 0) : (u < 9 ? u : 8);
 }
 
-template <int NB, int NW, int TR, int GPS, int SAMPLER, int SPLIT, int NBUF>
-__global__ __launch_bounds__(64 * NW) void window_kernel(WindowArgs a) {
+template <int NB, int NW, int TR, int GPS, int SAMPLER, int SPLIT, int NBUF, int UNI>
+__global__ __launch_bounds__(64 * NW, UNI ? 2 : 1) void window_kernel(WindowArgs a) {
     constexpr int kWindowLds = window_lds(NBUF);
     constexpr int TCB = NW / TR;              // row blocks across the tile
     constexpr int T = 64 * NW;
@@ -251,7 +251,9 @@ __global__ __launch_bounds__(64 * NW) void window_kernel(WindowArgs a) {
 
     // B fragments in a ring of kBDepth K-steps: step k's fragment is requested kBDepth
     // steps before it is used, across the stage boundary (the window copy hides it).
-    constexpr int kBDepth = 3;
+    // A slot must hold the same K-step of every stage, so the depth divides KS: 3 of the 9
+    // K-steps of two groups per stage, all 5 of one group per stage.
+    constexpr int kBDepth = KS % 3 == 0 ? 3 : KS;
     h8 Bq[kBDepth][NB];
     auto load_b = [&](int slot, int st, int k) {
 #pragma unroll
@@ -282,6 +284,35 @@ __global__ __launch_bounds__(64 * NW) void window_kernel(WindowArgs a) {
         // until make_state() rebuilds it after the multiply.
         if (more) load_raw(st + 1);
 
+        // UNI: when every window of the stage is in LDS, a K-loop with no global fallback,
+        // so no wait on outstanding vector loads before the corner reads. Its registers
+        // need the two-waves-per-SIMD bound above (otherwise one wave per SIMD).
+        bool all_lds = UNI != 0;
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) all_lds = all_lds && win[g].in_lds;
+        if (all_lds && !SPLIT) {
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                const int g0 = unit_group<GPS>(2 * k), g1 = unit_group<GPS>(2 * k + 1);
+                const int gi = (g0 == g1) ? g0 : half;
+                const Win& w = (g0 == g1) ? win[g0] : (half ? win[g1] : win[g0]);
+                const uint8_t* base = lds + (size_t)((NBUF == 2 ? buf : 0) * GPS + gi) * WIN;
+                const int idx = (iy[k] - w.y0) * w.ww + (ix[k] - w.x0);
+                const uint8_t* p = base + (size_t)idx * 16;
+                const u32x4 q00 = *reinterpret_cast<const u32x4*>(p);
+                const u32x4 q01 = *reinterpret_cast<const u32x4*>(p + 16);
+                const u32x4 q10 = *reinterpret_cast<const u32x4*>(p + (size_t)w.ww * 16);
+                const u32x4 q11 = *reinterpret_cast<const u32x4*>(p + (size_t)w.ww * 16 + 16);
+                h8 A = blend<SAMPLER>(q00, q01, q10, q11, ly[k], lx[k], mm[k]);
+                if (GPS == 1 && k == KS - 1 && half) A = h8{};  // the zero tenth unit
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bq[k % kBDepth][nb], acc[nb], 0, 0, 0);
+                if (k + kBDepth < KS) load_b(k % kBDepth, st, k + kBDepth);
+                else if (more) load_b(k % kBDepth, st + 1, k + kBDepth - KS);
+                __builtin_amdgcn_sched_barrier(0);  // keep K-steps apart (register pressure)
+            }
+        } else
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
             const int g0 = unit_group<GPS>(2 * k), g1 = unit_group<GPS>(2 * k + 1);
@@ -729,7 +760,15 @@ template <int NB, int NW, int TR, int GPS, int SAMPLER, int SPLIT>
 hipError_t launch_window_t(const WindowArgs& a, hipStream_t stream) {
     constexpr int NBUF = NW == 8 ? 2 : 1;
     const size_t lds = (size_t)window_lds(NBUF) + 2 * GPS * NW * 4 * sizeof(int);
-    auto kernel = &window_kernel<NB, NW, TR, GPS, SAMPLER, SPLIT, NBUF>;
+    // The uniform LDS K-loop for batches of small maps (C3's 16 tiles: 58.0 -> 55.1 us),
+    // where the windows of a stage almost always fit; large maps with large flows (C5:
+    // windows over its LDS budget in many stages) keep the single loop (71.1 us there,
+    // 74.1 us with the uniform loop's code beside it).
+    constexpr bool kUniOk = NW == 4 && GPS == 2 && SPLIT == 0;
+    auto kernel = &window_kernel<NB, NW, TR, GPS, SAMPLER, SPLIT, NBUF, 0>;
+    if constexpr (kUniOk) {
+        if (a.B > 1 && a.H * a.W <= 64 * 64) kernel = &window_kernel<NB, NW, TR, GPS, SAMPLER, SPLIT, NBUF, 1>;
+    }
     const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
     if (attr != hipSuccess) return attr;
     const unsigned grid = (unsigned)(((a.tiles + 7) / 8) * 8);

@@ -250,6 +250,61 @@ def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle, variant):
         assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
 
 
+@pytest.mark.parametrize("cout", [32, 128])
+@pytest.mark.parametrize("variant", [3, 4])
+def test_window_one_group_per_stage(gpu_ctx, dcn, oracle, cout, variant):
+    """An odd group count puts one offset group in each stage of the window kernel
+    (5 K-steps per stage): the weight-fragment ring must hand every stage its own K-steps.
+    Three groups, three stages, against the oracle."""
+    s = dcn.DeformConvShape(1, 24, 24, 40, cout, 24, 40, 3, 3, 1, 1, 1, 1, 1, 1, 1, 3)
+    rng = np.random.default_rng(cout + variant)
+    c = s.counts()
+    h = {"input": rng.standard_normal(c["input"]).astype(np.float16),
+         "offset": rng.uniform(-3, 3, c["offset"]).astype(np.float16),
+         "mask": rng.random(c["mask"]).astype(np.float16),
+         "weight": (rng.standard_normal(c["weight"]) * 0.05).astype(np.float16),
+         "bias": (rng.standard_normal(cout) * 0.1).astype(np.float16)}
+    log("case: window, 3 groups, cout", cout, "variant", variant)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(0, 0, -1, variant)
+    try:
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    w = widen(h)
+    ref = oracle.forward_f32_threads(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    mx, mean = errors(out, ref)
+    log(f"  max {mx:.3e} mean {mean:.3e}")
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
+@pytest.mark.parametrize("spread", [3.0, 40.0])
+def test_window_batch_uniform_and_overflow(gpu_ctx, dcn, oracle, spread):
+    """The window variant on a batch of 64 x 64 maps (the uniform LDS K-loop when every
+    window of a stage fits); offsets of +-40 px overflow the windows, so the stage falls
+    back to the general loop with global gathers. Both within the FP16 bars."""
+    s = dcn.DeformConvShape(2, 128, 64, 64, 64, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    rng = np.random.default_rng(int(spread) + 7)
+    c = s.counts()
+    h = {"input": rng.standard_normal(c["input"]).astype(np.float16),
+         "offset": rng.uniform(-spread, spread, c["offset"]).astype(np.float16),
+         "mask": rng.random(c["mask"]).astype(np.float16),
+         "weight": (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16),
+         "bias": (rng.standard_normal(64) * 0.1).astype(np.float16)}
+    log("case: window batch, offsets +-", spread)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(0, 0, -1, 3)
+    try:
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    w = widen(h)
+    ref = oracle.forward_f32_threads(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    mx, mean = errors(out, ref)
+    log(f"  max {mx:.3e} mean {mean:.3e}")
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
 @pytest.mark.parametrize("batch,h,w", [(5, 7, 9), (4, 16, 16), (16, 64, 64)])
 def test_narrow_batch_equals_single_images(gpu_ctx, dcn, batch, h, w):
     """The narrow variant over a batch (from four images on: several images per workgroup,
