@@ -1,4 +1,4 @@
-"""Benchmark of the MI355X DCNv2 hot path (BASELINE metric: DCNv2 forward us/call and
+"""Benchmark of the MI355X DCNv2 hot path (headline metric: DCNv2 forward us/call and
 TFLOP/s as a fraction of the HBM / MFMA rooflines at 1x128x64x64 -> 64, 16 groups).
 
 A step is one DCNv2 forward call at the workload shape on device-resident synthetic
@@ -696,7 +696,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic (seeded SplitMix64/Box-Muller inputs of the BASELINE distributions; random weights)",
+        "data": "synthetic (seeded SplitMix64/Box-Muller inputs of the benchmark distributions; random weights)",
         "config": {
             "workload": WORKLOADS[args.config],
             "batch": s.batch, "in_channels": s.input_channels, "height": s.input_height, "width": s.input_width,

@@ -262,7 +262,7 @@ uint64_t dcn_splitmix64_next(uint64_t* state);
  * Float.random(in: lo...hi, using:) per element, in order. */
 void dcn_seeded_floats(uint64_t* state, size_t count, float lo, float hi, float* out);
 
-/* BASELINE configurations: 1 = FP32 1x128x64x64->64, 2 = same in FP16,
+/* Benchmark configurations: 1 = FP32 1x128x64x64->64, 2 = same in FP16,
  * 3 = 16 tiles batched FP16, 5 = 1x128x180x320 FP16. (4, the propagation body,
  * has its own entry points.) */
 dcn_status dcn_config_shape(int config, dcn_shape* out);

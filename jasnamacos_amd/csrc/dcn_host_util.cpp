@@ -1,5 +1,5 @@
 // Host-side utilities of the C ABI: FP16 conversion, the seeded generator, the
-// BASELINE input generators, the benchmark checksum and statistics.
+// benchmark-configuration input generators, the benchmark checksum and statistics.
 #include <cmath>
 #include <cstring>
 #include <vector>

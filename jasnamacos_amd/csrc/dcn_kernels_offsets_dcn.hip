@@ -3,8 +3,8 @@
 //
 // Why: the two run back to back on the same 16-pixel tile, and the offsets of a tile are
 // only ever read by the DCN of that tile. Fused, the 432 offset/mask channels stay in LDS
-// (no HBM round trip, SURVEY's "directly in the DCN sampler from raw conv output"), and a
-// frame saves one launch and one kernel's load/reduce latency chain.
+// (the DCN samples straight from the conv's output, with no HBM round trip), and a frame
+// saves one launch and one kernel's load/reduce latency chain.
 //
 // Workgroup: 12 waves on one 16-pixel tile of up to three images (grid z = image group).
 //  * Phase A, the offsets conv: the tile's A fragments (18 K-steps of 64 lanes per image)

@@ -844,7 +844,7 @@ def config_shape(config: int) -> DeformConvShape:
 
 
 def generate_config_inputs(config: int, seed: int) -> dict:
-    """FP32 inputs of BASELINE config 1, 2, 3 or 5 (see dcn_generate_config_inputs)."""
+    """FP32 inputs of benchmark config 1, 2, 3 or 5 (see dcn_generate_config_inputs)."""
     shape = config_shape(config)
     c = shape.counts()
     arrays = {k: np.empty(c[k], dtype=np.float32) for k in ("input", "offset", "mask", "weight", "bias")}

@@ -1,6 +1,6 @@
 """GPU parity of libdcn against the CPU oracle, through the C ABI.
 
-Bars (BASELINE north star):
+Bars (the north-star tolerances):
   * FP32 path and the FP16 direct path: bit-identical to the oracle (the reference
     asks max relative error 1e-5; identical bits meet it with margin);
   * sampler (im2col): bit-identical to the reference gather arithmetic;

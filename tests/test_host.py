@@ -1,6 +1,6 @@
 """libdcn host-side behaviour that needs no GPU: exported symbols, shape validation,
 error taxonomy, the seeded generator, FP16 conversion, checksum, statistics and the
-BASELINE input generators."""
+benchmark-configuration input generators."""
 from __future__ import annotations
 
 import ctypes as C
@@ -62,7 +62,7 @@ def test_shape_validation(dcn, field, value):
 def test_shape_counts(dcn):
     s = dcn.JASNA_SHAPE
     c = s.counts()
-    # BASELINE sizes at 1x128x64x64 -> 64, 16 offset groups.
+    # Benchmark sizes at 1x128x64x64 -> 64, 16 offset groups.
     assert c["input"] == 524288 and c["offset"] == 1179648 and c["mask"] == 589824
     assert c["weight"] == 73728 and c["output"] == 262144 and c["bias"] == 64
     assert s.flops == 603979776
