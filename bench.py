@@ -449,6 +449,29 @@ def bench_clip(args, ctx, dc, clip, dev) -> dict:
     del lgraph
     spy.free()
     pc.free()
+    # The same clip over 16 tiles at once (dcn_clip_create_tiles): every kernel of a body
+    # step runs once over the tiles, whose inputs are the clip's shifted per tile.
+    tiles = 16
+    pt = ctx.clip(H, W, frames, wd, blocks=blocks, tiles=tiles)
+    feats = np.asarray(clip["feats"]).reshape(frames, 1, -1)
+    fl = np.asarray(clip["flows"]).reshape(frames, 1, -1)
+    t_spatial = dev(np.concatenate([np.roll(feats, t, axis=2) for t in range(tiles)], axis=1))
+    t_flows = dev(np.concatenate([np.roll(fl, t, axis=2) for t in range(tiles)], axis=1)).view(frames, -1)
+    t_prop = torch.zeros(4 * frames * tiles * 64 * plane, dtype=torch.int16, device="cuda")
+    tgraph = pt.capture(t_spatial, t_flows[: frames - 1].contiguous(), t_flows[1:].contiguous(), t_prop)
+    tgraph.launch(stream)
+    torch.cuda.synchronize()
+    start3, end3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start3.record(stream)
+        for _ in range(reps):
+            tgraph.launch(stream)
+        end3.record(stream)
+    torch.cuda.synchronize()
+    tiles_ms = start3.elapsed_time(end3) / reps
+    tiles_finite = bool(np.all(np.isfinite(t_prop.cpu().numpy().view(np.float16).astype(np.float32))))
+    tgraph.free()
+    pt.free()
     return {"workload": f"4 branches x {frames} frames (backward_1, forward_1, backward_2, forward_2), one hipGraph",
             "ms_per_clip": clip_ms, "body_steps": 4 * frames, "us_per_body_step": clip_ms * 1e3 / (4 * frames),
             "tflops": flops / (clip_ms * 1e-3) / 1e12, "flops_per_clip": flops, "replays_timed": reps,
@@ -456,7 +479,10 @@ def bench_clip(args, ctx, dc, clip, dev) -> dict:
             "with_spynet_flows": {"ms_per_clip": learned_ms,
                                   "workload": "bicubic 1/4 of 30 LQ tiles + SPyNet clip flows + the four branches, "
                                               "one hipGraph",
-                                  "output_finite": bool(np.all(np.isfinite(learned_out.astype(np.float32))))}}
+                                  "output_finite": bool(np.all(np.isfinite(learned_out.astype(np.float32))))},
+            "tiles": {"tiles": tiles, "ms_per_clip": tiles_ms, "ms_per_tile_clip": tiles_ms / tiles,
+                      "tflops": tiles * flops / (tiles_ms * 1e-3) / 1e12, "output_finite": tiles_finite,
+                      "workload": f"the clip over {tiles} 64x64 tiles at once (dcn_clip_create_tiles), one hipGraph"}}
 
 
 def cpu_baseline_body(clip) -> dict:
