@@ -695,7 +695,7 @@ def test_property_fp32_direct_bit_exact(gpu_ctx, dcn, oracle, case):
 
 @st.composite
 def _fused_cases(draw):
-    og = draw(st.sampled_from([1, 2, 4, 8, 16]))
+    og = draw(st.sampled_from([1, 2, 3, 4, 8, 16]))
     cin = og * 8 * draw(st.integers(1, 2))
     cout = 32 * draw(st.integers(1, 4))
     kh, kw = draw(st.sampled_from([(3, 3), (3, 3), (1, 3), (3, 1), (1, 1)]))
