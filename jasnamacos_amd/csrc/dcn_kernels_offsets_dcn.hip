@@ -6,7 +6,7 @@
 // (the DCN samples straight from the conv's output, with no HBM round trip), and a frame
 // saves one launch and one kernel's load/reduce latency chain.
 //
-// Workgroup: 12 waves on one 16-pixel tile of up to three images (grid z = image group).
+// Workgroup: 12 waves on one 16-pixel tile of up to four images (grid z = image group).
 //  * Phase A, the offsets conv: the tile's A fragments (18 K-steps of 64 lanes per image)
 //    are staged in LDS once; wave w owns 16-channel column blocks w, w + 12 (and w + 24 for
 //    w < 3) of the 27 and runs every K-step for them, streaming its weight fragments and
@@ -47,8 +47,10 @@ constexpr size_t kStageBytes = (size_t)kOffKsteps * 64 * 16;       // A fragment
 constexpr size_t kOffsBytes = (size_t)kOffChannels * 16 * 2;        // [432][16] FP16 per image
 constexpr size_t kRedBytes = (size_t)kOdWaves * kDcnNb * 4 * 65 * 4;  // narrow_kernel's sums
 constexpr size_t kFlowBytes = 2 * 2 * 16 * 2;                      // [flow][channel][16] FP16 per image
+// From three images on, the DCN's partial sums reuse the A-fragment stage (dead by then).
+__host__ __device__ constexpr bool od_red_in_stage(int images) { return images * kStageBytes >= kRedBytes; }
 __host__ __device__ constexpr size_t od_lds_bytes(int images) {
-    return (size_t)images * (kStageBytes + kOffsBytes + kFlowBytes) + kRedBytes;
+    return (size_t)images * (kStageBytes + kOffsBytes + kFlowBytes) + (od_red_in_stage(images) ? 0 : kRedBytes);
 }
 
 // Bit s set when K-step s ends one of the eight K ranges of conv_offsets_kernel.
@@ -82,8 +84,10 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     u32x4* stage = reinterpret_cast<u32x4*>(lds);                                 // [Z][18][64]
     uint16_t* offs = reinterpret_cast<uint16_t*>(lds + Z * kStageBytes);         // [Z][432][16]
-    float* red = reinterpret_cast<float*>(lds + Z * (kStageBytes + kOffsBytes));  // [12][4][4][65]
-    uint16_t* flows = reinterpret_cast<uint16_t*>(lds + Z * (kStageBytes + kOffsBytes) + kRedBytes);  // [Z][2][2][16]
+    constexpr bool kRedInStage = od_red_in_stage(Z);
+    float* red = reinterpret_cast<float*>(kRedInStage ? lds : lds + Z * (kStageBytes + kOffsBytes));  // [12][4][4][65]
+    uint16_t* flows = reinterpret_cast<uint16_t*>(lds + Z * (kStageBytes + kOffsBytes) +
+                                                  (kRedInStage ? 0 : kRedBytes));  // [Z][2][2][16]
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -350,9 +354,10 @@ hipError_t launch_offsets_dcn(const ConvGeometry& goff, const void* xoff_cb8, co
     a.woff_bytes = (uint32_t)conv_packed_bytes(goff);
     a.wdcn_bytes = (uint32_t)wdcn_bytes;
     a.images = images;
-    // Images per workgroup: three where there are three (LDS: 147 KB), measured for a
-    // body step over 16 tiles: 621 us (one), 580 (two), 574 (three); over 64 tiles
-    // 2478, 2294, 2258 us.
+    // Images per workgroup: up to four (LDS 130 KB, the DCN's sums in the dead stage),
+    // measured for a body step over 16 tiles: 621 us (one), 580 (two), 574 (three), 565
+    // (four); over 64 tiles 2478, 2294, 2258, 2230 us.
+    if (images >= 4) return launch_od_t<4>(a, stream);
     if (images >= 3) return launch_od_t<3>(a, stream);
     if (images == 2) return launch_od_t<2>(a, stream);
     return launch_od_t<1>(a, stream);
