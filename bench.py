@@ -41,7 +41,7 @@ WORKLOADS = {
 
 
 KERNEL_NAMES = {1: "fused_kernel", 2: "staged_kernel", 3: "window_kernel", 4: "window_kernel",
-                5: "narrow_kernel"}
+                5: "narrow_kernel", 6: "window_async_kernel", 7: "tile_kernel"}
 
 
 def algorithmic_bytes(shape, elem=2) -> int:
@@ -580,6 +580,10 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=5, help="repetitions of the fused-only timing")
     ap.add_argument("--cold-calls", type=int, default=20,
                     help="single calls timed after flushing the caches with a 512 MB write (0: skip)")
+    ap.add_argument("--variant", type=int, default=0,
+                    help="pin the fused variant (0 = the library's automatic choice)")
+    ap.add_argument("--mt", type=int, default=0, help="pin the fused config's mt (0 = automatic)")
+    ap.add_argument("--ks", type=int, default=0, help="pin the fused config's ks (0 = automatic)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run three device copies of this many MiB (the known-size "
                          "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -610,6 +614,8 @@ def main() -> int:
     ctx = dc.HipDeformConv(0)
     packed = ctx.prepack_dev(s, dev["weight"], dev["bias"])
     ctx.reserve(s)
+    if args.variant or args.mt or args.ks:
+        ctx.set_fused_config(args.mt, args.ks, -1, args.variant)
     fused_cfg = ctx.get_fused_config(s)
     out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
     cb8 = torch.empty(ctx.cb8_count(s), dtype=torch.int16, device="cuda")

@@ -222,7 +222,10 @@ dcn_status dcn_forward_f16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape* 
  * 5 = narrow 16-pixel tiles on 16x16x32 MFMA, one workgroup per CU on small maps
  * (mt = 1, ks = waves splitting K: 8 or 12), 6 = variant 3 on 8 x 32 tiles whose next
  * stage's windows and weights stream into LDS by DMA during the current stage (mt = ks
- * = 8; an even offset-group count). sampler: 0 = reference arithmetic
+ * = 8; an even offset-group count), 7 = tile windows: 8 waves on a 16 x 16 (mt = 16) or
+ * 8 x 32 (mt = 32) pixel tile, K ordered tap-major over two offset groups per stage, the
+ * next stage's windows copied by LDS DMA during the current stage (ks = 8; 3x3 kernels,
+ * 8 channels per group, an even group count, fast sampler). sampler: 0 = reference arithmetic
  * (FP32 bilinear in the reference's association, half(sampled*mask): the im2col
  * values of deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into
  * the bilinear weights, packed-FP16 blend). mt = 32-pixel row blocks per tile (1, 2),

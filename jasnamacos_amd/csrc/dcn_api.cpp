@@ -38,13 +38,22 @@ bool packed_matches(const dcn_packed* p, const dcn_shape* s) {
 }
 
 dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry& g,
-                               bool window_ok) {
-    const dcn::FusedConfig& o = ctx->fused_override;
+                               bool window_ok, bool tile_ok) {
+    dcn::FusedConfig o = ctx->fused_override;
+    // The tile variant implements the fast sampler only: with the exact one (or a shape
+    // it does not cover) the automatic choice below applies, with only the sampler pinned.
+    if (o.variant == dcn::kVariantTile) {
+        if (tile_ok && o.sampler != dcn::kSamplerExact)
+            return dcn::FusedConfig{dcn::kVariantTile, o.mt > 0 ? o.mt : 16, o.ks > 0 ? o.ks : 8,
+                                    dcn::kSamplerFast};
+        o = dcn::FusedConfig{0, 0, 0, o.sampler};
+    }
     const long long tiles32 = (g.m + 31) / 32;
     // Variant: small problems (one 64x64 map is 128 row blocks of 32 pixels) need every
     // CU busy and use 16-pixel tiles; large ones use LDS windows over 2D tiles.
-    int variant = o.variant > 0 ? o.variant
-                                : (window_ok && tiles32 > 1024 ? dcn::kVariantWindow : dcn::kVariantNarrow);
+    int variant = o.variant > 0 && o.variant != dcn::kVariantTile
+                      ? o.variant
+                      : (window_ok && tiles32 > 1024 ? dcn::kVariantWindow : dcn::kVariantNarrow);
     const bool window = variant == dcn::kVariantWindow || variant == dcn::kVariantWindowSplit ||
                         variant == dcn::kVariantWindowAsync;
     if (window && !window_ok) variant = dcn::kVariantNarrow;
@@ -82,6 +91,8 @@ dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry&
 }
 
 bool config_supported(const dcn::FusedConfig& c, const dcn::FusedGeometry& g) {
+    if (c.variant == dcn::kVariantTile)
+        return (c.mt == 16 || c.mt == 32) && c.ks == 8 && c.sampler == dcn::kSamplerFast;
     if (c.variant == dcn::kVariantWindowAsync) return c.mt == 8 && c.ks == 8;
     if (c.variant == dcn::kVariantNarrow) return c.mt == 1 && (c.ks == 8 || c.ks == 12);
     if (c.variant == dcn::kVariantWindow || c.variant == dcn::kVariantWindowSplit)
@@ -128,7 +139,8 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
         return fail(ctx, DCN_INVALID_ARGUMENT, "packed weights live on another device");
     if (dcn::cb8_bytes(*shape, g) >= ((size_t)1 << 31))
         return fail(ctx, DCN_INVALID_SHAPE, "padded input too large for 32-bit device indexing");
-    const dcn::FusedConfig cfg = choose_config(ctx, g, packed->weights_group != nullptr);
+    const dcn::FusedConfig cfg =
+        choose_config(ctx, g, packed->weights_group != nullptr, packed->weights_tile != nullptr);
     if (!config_supported(cfg, g))
         return fail(ctx, DCN_INVALID_ARGUMENT,
                     "unsupported fused config (variant " + std::to_string(cfg.variant) + ", mt " +
@@ -140,6 +152,14 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
         DCN_TRY(ensure_workspace(ctx, dcn::cb8_bytes(*shape, g), stream));
         DCN_HIP(ctx, dcn::launch_pack_cb8(ks, g, (const uint16_t*)d_input, ctx->workspace, stream));
         cb8 = ctx->workspace;
+    }
+    if (cfg.variant == dcn::kVariantTile) {
+        if (!packed->weights_tile)
+            return fail(ctx, DCN_INVALID_ARGUMENT, "the tile variant does not support this shape");
+        DCN_HIP(ctx, dcn::launch_tile_f16(ks, g, cfg, cb8, (const uint16_t*)d_offset,
+                                          (const uint16_t*)d_mask, packed->weights_tile,
+                                          packed->bias, (uint16_t*)d_output, stream));
+        return DCN_OK;
     }
     if (cfg.variant == dcn::kVariantNarrow) {
         DCN_HIP(ctx, dcn::launch_narrow_f16(ks, g, cfg, cb8, (const uint16_t*)d_offset,
@@ -291,7 +311,7 @@ dcn_status dcn_reserve(dcn_context* ctx, const dcn_shape* shape) {
 
 dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, int sampler) {
     if (!ctx) return DCN_INVALID_ARGUMENT;
-    if (variant < 0 || variant > 6 || mt < 0 || mt > 8 || ks < 0 || sampler < -1 || sampler > 1)
+    if (variant < 0 || variant > 7 || mt < 0 || mt > 32 || ks < 0 || sampler < -1 || sampler > 1)
         return fail(ctx, DCN_INVALID_ARGUMENT, "invalid fused config");
     ctx->fused_override = dcn::FusedConfig{variant, mt, ks, sampler};
     return DCN_OK;
@@ -304,7 +324,8 @@ dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* v
     DCN_TRY(validated_counts(ctx, shape, &c));
     dcn::FusedGeometry g;
     if (!dcn::fused_geometry(*shape, &g)) return fail(ctx, DCN_INVALID_SHAPE, "not a fused shape");
-    const dcn::FusedConfig cfg = choose_config(ctx, g, dcn::window_supported(*shape));
+    const dcn::FusedConfig cfg =
+        choose_config(ctx, g, dcn::window_supported(*shape), dcn::tile_supported(*shape));
     *variant = cfg.variant;
     *mt = cfg.mt;
     *ks = cfg.ks;
@@ -381,7 +402,9 @@ static dcn_status make_packed(dcn_context* ctx, const dcn_shape* shape, dcn_pack
         hipMalloc((void**)&p->bias, (size_t)shape->output_channels * sizeof(float)) != hipSuccess ||
         hipMalloc(&p->weights_narrow, dcn::narrow_packed_bytes(g)) != hipSuccess ||
         (dcn::window_supported(*shape) &&
-         hipMalloc(&p->weights_group, dcn::window_packed_bytes(*shape)) != hipSuccess)) {
+         hipMalloc(&p->weights_group, dcn::window_packed_bytes(*shape)) != hipSuccess) ||
+        (dcn::tile_supported(*shape) &&
+         hipMalloc(&p->weights_tile, dcn::tile_packed_bytes(*shape)) != hipSuccess)) {
         dcn_packed_free(p);
         return fail(ctx, DCN_COMMAND_FAILED, "hipMalloc of packed weights failed");
     }
@@ -412,6 +435,9 @@ dcn_status dcn_prepack_f16_dev(dcn_context* ctx, const dcn_shape* shape, const v
     if (e == hipSuccess && p->weights_group)
         e = dcn::launch_prepack_group(dcn::to_kshape(*shape), (const uint16_t*)d_weight, (int)layout,
                                       p->weights_group, (hipStream_t)stream);
+    if (e == hipSuccess && p->weights_tile)
+        e = dcn::launch_tile_prepack(dcn::to_kshape(*shape), (const uint16_t*)d_weight, (int)layout,
+                                     p->weights_tile, (hipStream_t)stream);
     if (e != hipSuccess) {
         dcn_packed_free(p);
         return hip_fail(ctx, e, "prepack launch");
@@ -452,6 +478,7 @@ void dcn_packed_free(dcn_packed* p) {
     if (p->bias) (void)hipFree(p->bias);
     if (p->weights_group) (void)hipFree(p->weights_group);
     if (p->weights_narrow) (void)hipFree(p->weights_narrow);
+    if (p->weights_tile) (void)hipFree(p->weights_tile);
     delete p;
 }
 

@@ -88,6 +88,11 @@ enum FusedVariant : int {
     // windows and B fragments streamed into a double buffer by LDS DMA while the current
     // stage is multiplied. Needs an even group count.
     kVariantWindowAsync = 6,
+    // Tile windows (dcn_kernels_tile.hip): 8 waves on a 16 x 16 (mt 16) or 8 x 32 (mt 32)
+    // pixel tile, per-stage windows of two offset groups copied by LDS DMA into a double
+    // buffer while the previous stage is multiplied. 3x3 kernels, 8 channels per group, an
+    // even group count, Cout 32 or 64; fast sampler only. Config: mt = tile width, ks = 8.
+    kVariantTile = 7,
 };
 
 struct FusedConfig {
@@ -107,6 +112,14 @@ hipError_t launch_window_f16(const KShape& s, const FusedGeometry& g, const Fuse
                              const void* cb8, const uint16_t* off, const uint16_t* mask,
                              const void* packed_w, const float* packed_b, uint16_t* out,
                              hipStream_t stream);
+bool tile_supported(const dcn_shape& s);
+size_t tile_packed_bytes(const dcn_shape& s);
+hipError_t launch_tile_prepack(const KShape& s, const uint16_t* w, int layout, void* wpk,
+                               hipStream_t stream);
+hipError_t launch_tile_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
+                           const void* cb8, const uint16_t* off, const uint16_t* mask,
+                           const void* packed_w, const float* packed_b, uint16_t* out,
+                           hipStream_t stream);
 
 // ---- launchers (return hipSuccess or the launch error) ---------------------------
 hipError_t launch_direct_f32(const KShape& s, const float* in, const float* off,
@@ -312,6 +325,7 @@ struct dcn_packed {
     void* weights = nullptr;    // B fragments, packed_weight_bytes(geometry)
     void* weights_group = nullptr;  // per-group B fragments of the window variant (or null)
     void* weights_narrow = nullptr; // 16-wide B fragments of the narrow variant
+    void* weights_tile = nullptr;   // tap-major B fragments of the tile variant (or null)
     float* bias = nullptr;      // Cout floats
     int device = 0;
 };

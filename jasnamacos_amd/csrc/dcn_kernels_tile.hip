@@ -1,0 +1,600 @@
+// Tile-window fused FP16 DCNv2 for gfx950 (3x3 kernels, 8 channels per offset group,
+// an even number of offset groups, Cout 32 or 64): batches of maps and large maps.
+//
+// Why this shape. Measured on MI355X, per CU, with L2-resident data:
+//   - random 16-byte gathers through the vector L1: 6.8 B/clk (every lane's corner is
+//     its own L2 request, ~2.2 cycles each);
+//   - random 16-byte LDS reads: 70 B/clk;
+//   - coalesced loads, or LDS DMA into LDS: 35-53 B/clk for the whole CU.
+// So the corners are gathered from LDS. The input reaches LDS as a window per offset
+// group: the exact bounding box of every corner the tile's samples touch, copied by LDS
+// DMA (buffer_load ... lds: no VGPRs, no LDS store instructions).
+//
+// The L2 -> CU path is then the scarce resource, and it is counted in instructions as
+// much as in bytes: 64 addresses take the texture addresser many cycles whatever their
+// size. Reading each sample's offsets and mask with 2-byte loads (27 per pixel and stage,
+// ~216 load instructions per CU and stage) saturated it and doubled the kernel's time.
+// So a stage's 54 offset and mask channels for the tile's 256 pixels (27 KB) are copied
+// to LDS by 27 DMA instructions and every lane reads its values from there. The path
+// also carries the windows (~60 KB per stage) and the weight fragments. With one 32-pixel block per
+// wave, every wave streams the whole weight set (8 x 18 KB per stage), more than the
+// windows. Here each wave holds two 32-pixel blocks (the MFMA B fragment is used for
+// both) and half the taps of a stage: waves 0-3 take taps 0-4, waves 4-7 taps 5-8 of
+// the same pixels. Each weight fragment crosses the path once per pixel block pair, and
+// the two halves of each pixel's sum meet in LDS at the end, in a fixed order.
+//
+// The sampler's VALU is the other limit. One sample (8 channels) feeds 64 output
+// channels, i.e. two v_mfma_f32_32x32x16_f16 (64 MFMA cycles), while its bilinear blend
+// alone is 16 packed FP16 FMAs (64 VALU cycles). So each sample's coordinates and FP16
+// corner weights are computed once, off the K-loop, and the K-loop does two address
+// additions and the blend.
+//
+// Layout. Workgroup = 8 waves on a 16 x 16 (TW = 16) or 8 x 32 (TW = 32) pixel tile.
+// Pixel block q (0-3) is 64 pixels: two segments of 32, each 32 / TW tile rows. A stage is
+// two offset groups; K-step k of stage s is tap k of both: lanes 0-31 give group 2s,
+// lanes 32-63 group 2s+1 (the A operand of v_mfma_f32_32x32x16_f16 is 32 pixels x 16 K,
+// 8 per lane), and the weights are prepacked in that order (tile_prepack_kernel).
+//
+// Pipeline (one workgroup per CU, two 66 KB window buffers), iteration s:
+//   - K-steps 0-1 also compute stage s+1's corner coordinates and their bounding box;
+//   - a barrier; stage s+2's offsets are requested by LDS DMA;
+//   - the remaining K-steps also request a slice of the windows of s+1 by LDS DMA into
+//     the other buffer (all waves, 64-unit chunks) and turn s+1's coordinates into LDS
+//     addresses;
+//   - a wait for the DMA and a barrier.
+// Vector-memory results return in issue order (one vmcnt counter), so a wait for a
+// weight fragment also waits for every older load: each stage's fragments are all in
+// registers before the stage starts (requested during the previous one), so the K-loop
+// never waits on memory.
+// A stage whose two windows do not fit their buffer gathers from the global CB8 input
+// instead (same arithmetic, no copy), so any offset field is handled.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <type_traits>
+
+#include "dcn_device.hpp"
+#include "dcn_internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace dcn {
+namespace {
+
+using namespace dev;
+
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+constexpr int kTileWaves = 4;                         // waves per workgroup (2 per CU)
+constexpr int kTilePix = 128;                         // pixels per tile
+constexpr int kTileBuf = 64 * 1024;                   // the window buffer (a stage)
+constexpr int kTileOffCh = 54;                        // offset + mask channels of a stage
+constexpr int kTileOff = kTileOffCh * kTilePix * 2;   // [36 dy/dx + 18 mask][128 px] FP16
+constexpr int kTileBox = 2 * kTileWaves * 2 * 4;      // [group][wave][min, max]
+constexpr int kTileLds = kTileBuf + kTileOff + kTileBox;  // 79,424 B: two workgroups per CU
+
+struct TileArgs {
+    const void* xin;      // CB8 input [B][CBLK][Hp][Wp][8]
+    const uint16_t* off;  // [B][2*G*9][HWo]
+    const uint16_t* msk;  // [B][G*9][HWo]
+    const void* wpk;      // [G/2][9][NB][64][8] FP16 (tile_prepack_kernel)
+    const float* bias;    // [Cout]
+    uint16_t* out;        // [B][Cout][HWo]
+    uint32_t xin_bytes, off_bytes, msk_bytes, wpk_bytes;
+    int H, W, Ho, Wo, HWo, ph, pw, sh, sw, dh, dw;
+    int G, CBLK, Hp, Wp, Cout;
+    int tiles_y, tiles_x, tiles;
+};
+
+// 16-byte LDS DMA: unit `voff` of the buffer to LDS lds_base + 16 * lane (lds_base uniform).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint8_t* lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds_base, 16, (int)voff, 0, 0, 0);
+}
+
+// Lane exchange within 32 lanes (ds_swizzle xor patterns stay inside each half-wave).
+template <int XOR>
+__device__ __forceinline__ uint32_t swz(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (XOR << 10));
+}
+__device__ __forceinline__ s16x2 as_s16x2(uint32_t v) { return __builtin_bit_cast(s16x2, v); }
+__device__ __forceinline__ uint32_t as_u32(s16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+template <int XOR>
+__device__ __forceinline__ void box_step(uint32_t& mn, uint32_t& mx) {
+    mn = as_u32(__builtin_elementwise_min(as_s16x2(mn), as_s16x2(swz<XOR>(mn))));
+    mx = as_u32(__builtin_elementwise_max(as_s16x2(mx), as_s16x2(swz<XOR>(mx))));
+}
+
+// Eight channels of one sample: the four FP16 corner weights w00, w01 (in w0) and w10,
+// w11 (in w1) applied as packed FP16 FMAs, the fast sampler of the other fused kernels.
+__device__ __forceinline__ h8 blend_w(const u32x4 (&q)[4], uint32_t w0, uint32_t w1) {
+    const h2 a = __builtin_bit_cast(h2, w0), c = __builtin_bit_cast(h2, w1);
+    const h8 w00 = a.x, w01 = a.y, w10 = c.x, w11 = c.y;
+    h8 r = w00 * __builtin_bit_cast(h8, q[0]);
+    r = __builtin_elementwise_fma(w01, __builtin_bit_cast(h8, q[1]), r);
+    r = __builtin_elementwise_fma(w10, __builtin_bit_cast(h8, q[2]), r);
+    r = __builtin_elementwise_fma(w11, __builtin_bit_cast(h8, q[3]), r);
+    return r;
+}
+
+template <int NB, int TW>
+__global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
+    constexpr int NW = kTileWaves;
+    constexpr int RPW = 32 / TW;  // tile rows per 32-pixel segment
+    constexpr int TH = 4 * RPW;   // 2 pixel blocks x 2 segments
+    constexpr int NS = 2;         // segments (32-pixel A operands) per wave
+    extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+    uint8_t* offs = lds + kTileBuf;  // a stage's offsets and masks [54][128] FP16
+    uint32_t* boxes = reinterpret_cast<uint32_t*>(offs + kTileOff);  // [2][NW][2]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = lane >> 5;  // the offset group of this lane within a stage
+    const int p = lane & 31;
+    const int pblk = wave & 1;   // pixel block (64 pixels)
+
+    // XCD-aware tile order: blockIdx lands on XCD blockIdx % 8.
+    const int per_xcd = (a.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+    const int tiles_img = a.tiles_y * a.tiles_x;
+    const int b = tile / tiles_img;
+    const int trem = tile - b * tiles_img;
+    const int ty = trem / a.tiles_x;
+    const int tx = trem - ty * a.tiles_x;
+
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+    const int stages = a.G / 2;
+
+    // Pixel of this lane in segment s (tile rows (2 * pblk + s) * RPW ..): lanes past the
+    // edge sample a clamped in-image pixel; their results are not stored. Per segment:
+    // integer sample base (oy*sh - ph, ox*sw - pw) and the byte offsets of the pixel's
+    // first dy (channel 18 * half) and first mask (channel 36 + 9 * half) of group
+    // 2s + half in the LDS copy of the stage's offsets.
+    int ybi[NS], xbi[NS];
+    uint32_t offs_lane[NS], mask_lane[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        const int oy = ty * TH + (2 * pblk + s) * RPW + p / TW;
+        const int ox = tx * TW + p % TW;
+        const int oyc = min(oy, a.Ho - 1), oxc = min(ox, a.Wo - 1);
+        ybi[s] = oyc * a.sh - a.ph;
+        xbi[s] = oxc * a.sw - a.pw;
+        const int lp = (oyc - ty * TH) * TW + (oxc - tx * TW);
+        offs_lane[s] = (uint32_t)((18 * half * kTilePix + lp) * 2);
+        mask_lane[s] = (uint32_t)(((36 + 9 * half) * kTilePix + lp) * 2);
+    }
+    // LDS DMA of stage st's offsets (channels 36st .. 36st+35) and masks (18st .. 18st+17)
+    // of the tile: 864 chunks of 8 pixels, chunk c -> LDS offs + 16c ([channel][128 px]).
+    // Rows past the map repeat its last row (the clamped pixels read those).
+    auto copy_offsets = [&](int st) {
+        constexpr int kChunksPerCh = kTilePix / 8;  // 16
+        constexpr int kRowChunks = TW / 8;
+        constexpr int kChunks = kTileOffCh * kChunksPerCh;  // 864
+        for (int i = wave; i * 64 < kChunks; i += NW) {
+            const int c = i * 64 + lane;
+            const bool is_off = i < 36 * kChunksPerCh / 64;  // uniform per instruction
+            const int ch = (is_off ? c : c - 36 * kChunksPerCh) / kChunksPerCh;
+            const int rem = c % kChunksPerCh;
+            const int y = min(ty * TH + rem / kRowChunks, a.Ho - 1);
+            const int x = tx * TW + (rem % kRowChunks) * 8;
+            const uint32_t plane = is_off ? (uint32_t)(b * 2 * a.G * 9 + 36 * st + ch)
+                                          : (uint32_t)(b * a.G * 9 + 18 * st + ch);
+            const uint32_t src = (plane * (uint32_t)a.HWo + (uint32_t)(y * a.Wo + x)) * 2u;
+            if (c < kChunks) dma16(is_off ? orr : mr, src, offs + i * 64 * 16);
+        }
+    };
+
+    // Window geometry of a stage (wave-uniform): origin, size in units, LDS placement.
+    struct Win {
+        int y0[2], x0[2], ww[2], hh[2], off[2];
+        bool lds;  // both windows are in LDS (else the stage gathers from global memory)
+    };
+    auto read_windows = [&]() {
+        // Lanes 0-7 read one wave's box of group lane / 4; reduce over the 4 waves.
+        uint32_t mn = as_u32(s16x2{SHRT_MAX, SHRT_MAX}), mx = as_u32(s16x2{SHRT_MIN, SHRT_MIN});
+        if (lane < 2 * NW) {
+            const uint32_t* s = boxes + lane * 2;  // [group][wave]
+            mn = s[0];
+            mx = s[1];
+        }
+        box_step<1>(mn, mx);
+        box_step<2>(mn, mx);
+        Win w;
+        int size[2];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const uint32_t lo = __builtin_amdgcn_readlane(mn, NW * g);
+            const uint32_t hi = __builtin_amdgcn_readlane(mx, NW * g);
+            w.y0[g] = (int)(short)(lo & 0xffffu);
+            w.x0[g] = (int)(short)(lo >> 16);
+            w.hh[g] = (int)(short)(hi & 0xffffu) - w.y0[g] + 2;
+            w.ww[g] = (int)(short)(hi >> 16) - w.x0[g] + 2;
+            size[g] = w.hh[g] * w.ww[g] * 16;
+        }
+        w.lds = size[0] + size[1] <= kTileBuf;
+        w.off[0] = 0;
+        w.off[1] = size[0];
+        return w;
+    };
+    // LDS DMA of the windows of stage st as chunks of 64 consecutive window units (one
+    // instruction each; unit f of window g is row f / ww, column f % ww). Chunk i of the
+    // stage (window 0's chunks, then window 1's) is issued by wave i % 4.
+    auto copy_windows = [&](int st, const Win& w) {
+        if (!w.lds) return;
+        const int n0 = (w.hh[0] * w.ww[0] + 63) >> 6;
+        const int n = n0 + ((w.hh[1] * w.ww[1] + 63) >> 6);
+        for (int i = wave; i < n; i += NW) {
+            const int g = i < n0 ? 0 : 1;
+            const int c = i - (g ? n0 : 0);
+            const int ww = g ? w.ww[1] : w.ww[0];
+            const int units = ww * (g ? w.hh[1] : w.hh[0]);
+            const int f = c * 64 + lane;
+            if (f < units) {
+                // f / ww through the FP32 reciprocal ((f + 0.5) / ww is at least 0.5 / ww
+                // from an integer: exact for narrow windows), then corrected by one either
+                // way for wide ones.
+                int r = (int)(((float)f + 0.5f) * __builtin_amdgcn_rcpf((float)ww));
+                r -= r * ww > f ? 1 : 0;
+                r += (r + 1) * ww <= f ? 1 : 0;
+                const int col = f - r * ww;
+                const uint32_t row0 = (uint32_t)(b * a.CBLK + 2 * st + g) * a.Hp +
+                                      (uint32_t)((g ? w.y0[1] : w.y0[0]) + kPad);
+                const uint32_t src =
+                    ((row0 + (uint32_t)r) * a.Wp + (uint32_t)((g ? w.x0[1] : w.x0[0]) + kPad + col)) * 16u;
+                dma16(xr, src, lds + (g ? w.off[1] : w.off[0]) + c * 1024);
+            }
+        }
+    };
+
+    f32x16 acc[NS][NB];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[s][nb] = f32x16{};
+
+    // The stage loop for waves with taps T0 .. T0 + NTW - 1 (compile-time per wave pair).
+    auto run = [&](auto t0_c, auto ntw_c) {
+        constexpr int T0 = decltype(t0_c)::value;
+        constexpr int NTW = decltype(ntw_c)::value;
+        constexpr int NSMP = NS * NTW;  // samples per lane and stage, j = kk * NS + s
+
+        // A sample's dy, dx and mask from the LDS copy of the stage's offsets.
+        typedef const __attribute__((address_space(3))) _Float16* lds_h;
+        auto offset_of = [&](int j, int which) {  // which: 0 = dy, 1 = dx, 2 = mask
+            const int kk = j / NS, s = j % NS, k = T0 + kk;
+            const uint32_t at = which == 2 ? mask_lane[s] + (uint32_t)(k * kTilePix * 2)
+                                           : offs_lane[s] + (uint32_t)((2 * k + which) * kTilePix * 2);
+            return *(lds_h)(uintptr_t)((uint32_t)(uintptr_t)offs + at);
+        };
+        // Sample state of a stage: a[] = clamped corner (iy, ix) as a 16-bit pair, then
+        // the sample's address; w0/w1 = the FP16 corner weights.
+        struct Samples {
+            uint32_t a[NSMP], w0[NSMP], w1[NSMP];
+        };
+        s16x2 bmin, bmax;
+        auto box_reset = [&]() {
+            bmin = s16x2{SHRT_MAX, SHRT_MAX};
+            bmax = s16x2{SHRT_MIN, SHRT_MIN};
+        };
+        auto coords = [&](int j, Samples& C) {
+            const int kk = j / NS, s = j % NS, k = T0 + kk;
+            // float(oy*sh - ph + ky*dh) + dy (MetalShader.swift:327-332), one rounding.
+            const float y = (float)(ybi[s] + (k / 3) * a.dh) + (float)offset_of(j, 0);
+            const float x = (float)(xbi[s] + (k % 3) * a.dw) + (float)offset_of(j, 1);
+            const float fy = floorf(y), fx = floorf(x);
+            const float ly = y - fy, lx = x - fx;
+            // Clamped so both rows/columns of the corner pair stay in the padded plane.
+            const int iy = (int)__builtin_amdgcn_fmed3f(fy, (float)-kPad, (float)a.H);
+            const int ix = (int)__builtin_amdgcn_fmed3f(fx, (float)-kPad, (float)a.W);
+            C.a[j] = __builtin_amdgcn_perm((uint32_t)ix, (uint32_t)iy, 0x05040100u);
+            bmin = __builtin_elementwise_min(bmin, as_s16x2(C.a[j]));
+            bmax = __builtin_elementwise_max(bmax, as_s16x2(C.a[j]));
+            // Mask folded into the four bilinear weights, each rounded once to FP16.
+            const float m = (float)offset_of(j, 2);
+            const float t0 = m * (1.0f - ly);
+            const float t1 = m * ly;
+            C.w0[j] = __builtin_bit_cast(uint32_t, h2{(_Float16)(t0 * (1.0f - lx)), (_Float16)(t0 * lx)});
+            C.w1[j] = __builtin_bit_cast(uint32_t, h2{(_Float16)(t1 * (1.0f - lx)), (_Float16)(t1 * lx)});
+        };
+        // This wave's box (per half = per group) to LDS.
+        auto publish_box = [&]() {
+            uint32_t mn = as_u32(bmin), mx = as_u32(bmax);
+            box_step<1>(mn, mx);
+            box_step<2>(mn, mx);
+            box_step<4>(mn, mx);
+            box_step<8>(mn, mx);
+            box_step<16>(mn, mx);
+            if (p == 0) {
+                uint32_t* d = boxes + (half * NW + wave) * 2;
+                d[0] = mn;
+                d[1] = mx;
+            }
+        };
+        // Addresses of a stage: LDS byte addresses when its windows are in LDS, else the
+        // byte offset of the corner in the CB8 input; `pitch` steps to the lower row.
+        struct Addressing {
+            int rs, c;  // address = iy * rs + ix * 16 + c
+            uint32_t pitch;
+        };
+        auto addressing = [&](int st, const Win& w) {
+            const int g = half;
+            const int y0 = g ? w.y0[1] : w.y0[0];
+            const int x0 = g ? w.x0[1] : w.x0[0];
+            const int ww = g ? w.ww[1] : w.ww[0];
+            const int off = g ? w.off[1] : w.off[0];
+            Addressing r;
+            r.rs = w.lds ? ww * 16 : a.Wp * 16;
+            r.pitch = (uint32_t)r.rs;
+            r.c = w.lds ? off - y0 * ww * 16 - x0 * 16
+                        : ((((b * a.CBLK + 2 * st + g) * a.Hp + kPad) * a.Wp) + kPad) * 16;
+            return r;
+        };
+        auto make_address = [&](int j, Samples& C, const Addressing& r) {
+            const int iy = (int)(short)(C.a[j] & 0xffffu);
+            const int ix = (int)(short)(C.a[j] >> 16);
+            C.a[j] = (uint32_t)(iy * r.rs + ix * 16 + r.c);
+        };
+        // Weight fragments of this wave's taps of one stage, one slot per tap: slot kk of
+        // stage st+1 is requested as soon as tap kk of stage st has used it.
+        h8 Bq[NTW][NB];
+        auto load_b = [&](int st, int kk) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                Bq[kk][nb] = __builtin_bit_cast(
+                    h8, load16(wr, (uint32_t)(((st * 9 + T0 + kk) * NB + nb) * 64 + lane) * 16u, 0));
+        };
+        auto corners = [&](int j, const Samples& C, const Addressing& r, bool from_lds, u32x4 (&q)[4]) {
+            const uint32_t a0 = C.a[j], a1 = C.a[j] + r.pitch;
+            if (from_lds) {
+                typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
+                q[0] = *(lds_u32x4)(uintptr_t)a0;
+                q[1] = *(lds_u32x4)(uintptr_t)(a0 + 16);
+                q[2] = *(lds_u32x4)(uintptr_t)a1;
+                q[3] = *(lds_u32x4)(uintptr_t)(a1 + 16);
+            } else {
+                q[0] = load16(xr, a0, 0);
+                q[1] = load16(xr, a0 + 16u, 0);
+                q[2] = load16(xr, a1, 0);
+                q[3] = load16(xr, a1 + 16u, 0);
+            }
+        };
+        // K-loop of one stage: per sample j (tap kk, segment s) the next sample's corners
+        // are requested before this one is blended and multiplied; after both segments of
+        // a tap the weight slot is refilled and side(kk) runs (the next stage's work).
+        auto kloop = [&](int st, const Samples& C, const Addressing& r, bool from_lds, auto&& side) {
+            u32x4 qa[4], qb[4];
+            corners(0, C, r, from_lds, qa);
+#pragma unroll
+            for (int j = 0; j < NSMP; ++j) {
+                u32x4(&cur)[4] = (j & 1) ? qb : qa;
+                u32x4(&nxt)[4] = (j & 1) ? qa : qb;
+                if (j + 1 < NSMP) corners(j + 1, C, r, from_lds, nxt);
+                const int kk = j / NS, s = j % NS;
+                const h8 A = blend_w(cur, C.w0[j], C.w1[j]);
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    acc[s][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bq[kk][nb], acc[s][nb], 0, 0, 0);
+                if (s == NS - 1) {
+                    if (st + 1 < stages) load_b(st + 1, kk);
+                    side(kk);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        // After the K-loop of stage st (or the prologue): stage st+1's box reduced, its
+        // windows and stage st+2's offsets requested, its addresses made, every DMA done.
+        Win win;
+        Addressing ad;
+        auto next_stage = [&](int st1, Samples& C) {
+            publish_box();
+            __syncthreads();  // every box; every wave past its corner and offset reads
+            win = read_windows();
+            copy_windows(st1, win);
+            if (st1 + 1 < stages) copy_offsets(st1 + 1);
+            ad = addressing(st1, win);
+#pragma unroll
+            for (int j = 0; j < NSMP; ++j) make_address(j, C, ad);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA
+            __syncthreads();                // every wave's DMA
+        };
+
+        // ---- prologue: stage 0's offsets, coordinates, windows and addresses ----
+        Samples ca, cb;
+#pragma unroll
+        for (int kk = 0; kk < NTW; ++kk) load_b(0, kk);
+        copy_offsets(0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // stage 0's offsets in LDS
+        box_reset();
+#pragma unroll
+        for (int j = 0; j < NSMP; ++j) coords(j, ca);
+        next_stage(0, ca);
+
+        // Iteration st: `cur` holds stage st's addresses; K-steps 0-1 also compute stage
+        // st+1's coordinates into `nxt` (from the offsets copied with st's windows).
+        auto iteration = [&](int st, Samples& cur, Samples& nxt) {
+            const bool more = st + 1 < stages;
+            if (more) box_reset();
+            constexpr int kPerCoord = (NSMP + 1) / 2;
+            auto side = [&](int kk) {
+                if (!more || kk >= 2) return;
+#pragma unroll
+                for (int i = 0; i < kPerCoord; ++i)
+                    if (kk * kPerCoord + i < NSMP) coords(kk * kPerCoord + i, nxt);
+            };
+            kloop(st, cur, ad, win.lds, side);
+            if (more) next_stage(st + 1, nxt);
+        };
+        for (int st = 0; st < stages; st += 2) {
+            iteration(st, ca, cb);
+            if (st + 1 < stages) iteration(st + 1, cb, ca);
+        }
+    };
+    if (wave < 2) run(std::integral_constant<int, 0>{}, std::integral_constant<int, 5>{});
+    else run(std::integral_constant<int, 5>{}, std::integral_constant<int, 4>{});
+
+    // ---- epilogue: the two tap halves summed (taps 0-4 + taps 5-8), bias, FP16, NCHW
+    // stores through LDS ----
+    __syncthreads();  // every wave is done with the windows
+    float* red = reinterpret_cast<float*>(lds);  // [2 pixel blocks][NS][NB][16][64]
+    if (wave >= 2) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) red[(((pblk * NS + s) * NB + nb) * 16 + v) * 64 + lane] = acc[s][nb][v];
+    }
+    __syncthreads();
+    if (wave >= 2) return;  // no barrier follows
+    uint16_t* stage = reinterpret_cast<uint16_t*>(lds + 2 * NS * NB * 16 * 64 * 4) + (size_t)wave * NS * 32 * NB * 32;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const int oc = nb * 32 + p;
+            const float bias = a.bias[oc];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float sum = acc[s][nb][v] + red[(((pblk * NS + s) * NB + nb) * 16 + v) * 64 + lane];
+                const int i = 8 * (v >> 2) + 4 * half + (v & 3);  // pixel within the segment
+                stage[(s * NB * 32 + oc) * 32 + i] = __builtin_bit_cast(uint16_t, round_f16(sum + bias));
+            }
+        }
+    // Each item: 4 consecutive pixels of one output channel and tile row. No barrier is
+    // needed: each wave stores only what it staged.
+    constexpr int kQ = TW / 4;
+    const int ox0 = tx * TW;
+    for (int it = lane; it < NS * NB * 32 * RPW * kQ; it += 64) {
+        const int q = it % kQ;
+        const int rr = (it / kQ) % RPW;
+        const int oc = (it / (kQ * RPW)) % (NB * 32);
+        const int s = it / (kQ * RPW * NB * 32);
+        const int y = ty * TH + (2 * pblk + s) * RPW + rr;
+        const int x = ox0 + 4 * q;
+        if (y >= a.Ho) continue;
+        const uint16_t* src = stage + (s * NB * 32 + oc) * 32 + rr * TW + 4 * q;
+        uint16_t* dst = a.out + ((size_t)b * a.Cout + oc) * a.HWo + (size_t)y * a.Wo + x;
+        if (x + 3 < a.Wo && (((uintptr_t)dst) & 7u) == 0) {
+            *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
+        } else {
+            for (int e = 0; e < 4; ++e)
+                if (x + e < a.Wo) dst[e] = src[e];
+        }
+    }
+}
+
+// Weights -> the tile kernel's B fragments [G/2][9][NB][64][8]: lane l of K-step k, stage
+// s holds output channel nb*32 + l%32 and the 8 channels of group 2s + l/32, tap k.
+// layout 0 = OIHW, 1 = [ic][k][oc] (.dcnfp16).
+__global__ __launch_bounds__(256) void tile_prepack_kernel(const uint16_t* __restrict__ w, int layout,
+                                                           uint16_t* __restrict__ wpk, int Cin,
+                                                           int Cout, int NB, long total) {
+    const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    const int e = (int)(gid & 7);
+    const int lane = (int)((gid >> 3) & 63);
+    long q = gid >> 9;
+    const int nb = (int)(q % NB);
+    q /= NB;
+    const int k = (int)(q % 9);
+    const int st = (int)(q / 9);
+    const int grp = 2 * st + (lane >> 5);
+    const int oc = nb * 32 + (lane & 31);
+    const int ic = grp * 8 + e;
+    uint16_t v = 0;
+    if (oc < Cout && ic < Cin)
+        v = layout == DCN_LAYOUT_OIHW ? w[((size_t)oc * Cin + ic) * 9 + k]
+                                      : w[((size_t)ic * 9 + k) * Cout + oc];
+    wpk[gid] = v;
+}
+
+template <int NB, int TW>
+hipError_t launch_tile_t(const TileArgs& a, hipStream_t stream) {
+    auto kernel = &tile_kernel<NB, TW>;
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), kTileLds);
+    if (attr != hipSuccess) return attr;
+    const unsigned grid = (unsigned)(((a.tiles + 7) / 8) * 8);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kTileWaves), kTileLds, stream, a);
+    return hipGetLastError();
+}
+
+template <int TW>
+hipError_t launch_tile_nb(const TileArgs& a, int nb, hipStream_t stream) {
+    switch (nb) {
+        case 1: return launch_tile_t<1, TW>(a, stream);
+        case 2: return launch_tile_t<2, TW>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool tile_supported(const dcn_shape& s) {
+    // Output rows of 8-pixel multiples: the offsets are copied as 16-byte chunks of rows.
+    return s.groups == 1 && s.kernel_height == 3 && s.kernel_width == 3 &&
+           s.input_channels == 8 * s.offset_groups && s.offset_groups % 2 == 0 &&
+           s.output_channels % 32 == 0 && s.output_channels <= 64 && s.output_width % 8 == 0;
+}
+
+size_t tile_packed_bytes(const dcn_shape& s) {
+    return (size_t)(s.offset_groups / 2) * 9 * (s.output_channels / 32) * 64 * 8 * sizeof(uint16_t);
+}
+
+hipError_t launch_tile_prepack(const KShape& s, const uint16_t* w, int layout, void* wpk,
+                               hipStream_t stream) {
+    const int nb = s.Cout / 32;
+    const long total = (long)(s.og / 2) * 9 * nb * 64 * 8;
+    const long grid = (total + 255) / 256;
+    hipLaunchKernelGGL(tile_prepack_kernel, dim3((unsigned)grid), dim3(256), 0, stream, w, layout,
+                       (uint16_t*)wpk, s.Cin, s.Cout, nb, total);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
+                           const void* cb8, const uint16_t* off, const uint16_t* mask,
+                           const void* packed_w, const float* packed_b, uint16_t* out,
+                           hipStream_t stream) {
+    TileArgs a;
+    a.xin = cb8;
+    a.off = off;
+    a.msk = mask;
+    a.wpk = packed_w;
+    a.bias = packed_b;
+    a.out = out;
+    const size_t hwo = (size_t)s.Ho * s.Wo;
+    a.xin_bytes = (uint32_t)((size_t)s.B * g.cblk * g.hp * g.wp * 16);
+    a.off_bytes = (uint32_t)((size_t)s.B * 2 * s.og * 9 * hwo * 2);
+    a.msk_bytes = (uint32_t)((size_t)s.B * s.og * 9 * hwo * 2);
+    a.wpk_bytes = (uint32_t)((size_t)(s.og / 2) * 9 * (s.Cout / 32) * 64 * 8 * 2);
+    a.H = s.H;
+    a.W = s.W;
+    a.Ho = s.Ho;
+    a.Wo = s.Wo;
+    a.HWo = (int)hwo;
+    a.ph = s.ph;
+    a.pw = s.pw;
+    a.sh = s.sh;
+    a.sw = s.sw;
+    a.dh = s.dh;
+    a.dw = s.dw;
+    a.G = s.og;
+    a.CBLK = g.cblk;
+    a.Hp = g.hp;
+    a.Wp = g.wp;
+    a.Cout = s.Cout;
+    const int tw = cfg.mt == 32 ? 32 : 16;  // for this variant, mt carries the tile width
+    const int th = 4 * 32 / tw;  // 2 pixel blocks x 2 segments of 32 pixels
+    a.tiles_y = (s.Ho + th - 1) / th;
+    a.tiles_x = (s.Wo + tw - 1) / tw;
+    a.tiles = a.tiles_y * a.tiles_x * s.B;
+    return tw == 32 ? launch_tile_nb<32>(a, g.nb, stream) : launch_tile_nb<16>(a, g.nb, stream);
+}
+
+}  // namespace dcn

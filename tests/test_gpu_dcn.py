@@ -193,7 +193,8 @@ FUSED_CONFIGS = [(1, 1, 8), (1, 1, 4), (1, 2, 4), (1, 2, 2),   # register varian
                  (3, 8, 8), (3, 4, 8), (3, 4, 4), (3, 2, 4),   # LDS windows (rows, waves)
                  (4, 8, 8), (4, 4, 4),                          # LDS windows + L1 lower rows
                  (5, 1, 8), (5, 1, 12),                         # narrow 16-pixel tiles (waves)
-                 (6, 8, 8)]                                     # LDS windows streamed by DMA
+                 (6, 8, 8),                                     # LDS windows streamed by DMA
+                 (7, 16, 8), (7, 32, 8)]                        # tile windows (tile width, waves)
 
 
 def test_unsupported_fused_config_is_rejected(gpu_ctx, dcn, c2):
@@ -226,7 +227,7 @@ def test_fused_configs(gpu_ctx, dcn, c2, variant, mt, ks, sampler):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
-@pytest.mark.parametrize("variant", [0, 5, 6])
+@pytest.mark.parametrize("variant", [0, 5, 6, 7])
 def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle, variant):
     d = dcn.generate_config_inputs(3, 3)
     s = d["shape"]
@@ -334,7 +335,7 @@ def test_narrow_batch_equals_single_images(gpu_ctx, dcn, batch, h, w):
         gpu_ctx.set_fused_config(0, 0, -1, 0)
 
 
-@pytest.mark.parametrize("variant", [0, 6])
+@pytest.mark.parametrize("variant", [0, 6, 7])
 def test_fused_c5_large_map(gpu_ctx, dcn, oracle, variant):
     d = dcn.generate_config_inputs(5, 5)
     s = d["shape"]
@@ -372,7 +373,7 @@ EDGE_SHAPES = [
 
 @pytest.mark.parametrize("dims", EDGE_SHAPES, ids=lambda t: "x".join(map(str, t)))
 @pytest.mark.parametrize("sampler", [0, 1])
-@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 6])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 6, 7])
 def test_fused_edge_shapes(gpu_ctx, dcn, oracle, dims, sampler, variant):
     s = dcn.DeformConvShape(*dims)
     assert s.fused_supported
@@ -392,7 +393,7 @@ def test_fused_edge_shapes(gpu_ctx, dcn, oracle, dims, sampler, variant):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 6])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 6, 7])
 def test_large_offsets_force_global_fallback(gpu_ctx, dcn, oracle, variant):
     # Offsets up to +-40 px on a 64x64 map: a tile's sample box spans the whole plane
     # (74 KB), larger than one LDS window, so the window variant gathers from global.
@@ -413,6 +414,38 @@ def test_large_offsets_force_global_fallback(gpu_ctx, dcn, oracle, variant):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
+@pytest.mark.parametrize("tw", [16, 32])
+def test_tile_stages_lds_and_global(gpu_ctx, dcn, oracle, tw):
+    """The tile variant with offsets of +-3 px in groups 0-7 and +-40 px in groups 8-15:
+    stages 0-3 gather from LDS windows, stages 4-7 (windows over the LDS budget) from global
+    memory, in one call over a batch of two 64 x 64 maps; within the FP16 bars."""
+    s = dcn.DeformConvShape(2, 128, 64, 64, 64, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    rng = np.random.default_rng(tw)
+    c = s.counts()
+    off = rng.uniform(-3, 3, c["offset"]).reshape(2, 16, 18, 64 * 64)
+    off[:, 8:] = rng.uniform(-40, 40, off[:, 8:].shape)
+    h = {"input": rng.standard_normal(c["input"]).astype(np.float16),
+         "offset": off.reshape(-1).astype(np.float16),
+         "mask": rng.random(c["mask"]).astype(np.float16),
+         "weight": (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16),
+         "bias": (rng.standard_normal(64) * 0.1).astype(np.float16)}
+    log("case: tile variant, LDS and global stages, width", tw)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(tw, 8, -1, 7)
+    try:
+        assert gpu_ctx.get_fused_config(s)["variant"] == 7
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+        again = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    assert np.array_equal(out.view(np.uint16), again.view(np.uint16))
+    w = widen(h)
+    ref = oracle.forward_f32_threads(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    mx, mean = errors(out, ref)
+    log(f"  max {mx:.3e} mean {mean:.3e}")
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
 def test_zero_padding_exact(gpu_ctx, dcn, c2):
     s, h, _ = c2
     log("case: zero padding")
@@ -420,7 +453,7 @@ def test_zero_padding_exact(gpu_ctx, dcn, c2):
     bias_out = np.repeat(h["bias"], s.output_height * s.output_width)
     for far in (1000.0, -1000.0, 66.0, -2.0 - 64.0):
         off = np.full_like(h["offset"], far)
-        for variant in (1, 2, 3, 4, 5, 6):
+        for variant in (1, 2, 3, 4, 5, 6, 7):
             gpu_ctx.set_fused_config(0, 0, -1, variant)
             try:
                 out = gpu_ctx.run_float16_prepacked(s, h["input"], off, h["mask"], packed)
@@ -705,7 +738,7 @@ def _fused_cases(draw):
     ho = max(1, (h + 2 * ph - dh * (kh - 1) - 1) // sh + 1)
     wo = max(1, (w + 2 * pw - dw * (kw - 1) - 1) // sw + 1)
     return (draw(st.integers(1, 3)), cin, h, w, cout, ho, wo, kh, kw, ph, pw, sh, sw, dh, dw, 1, og), \
-        draw(st.integers(0, 2**31 - 1)), draw(st.sampled_from([1, 2, 3, 5, 6])), draw(st.sampled_from([0, 1]))
+        draw(st.integers(0, 2**31 - 1)), draw(st.sampled_from([1, 2, 3, 5, 6, 7])), draw(st.sampled_from([0, 1]))
 
 
 @settings(max_examples=30, deadline=None, suppress_health_check=[HealthCheck.too_slow])
