@@ -213,6 +213,23 @@ dcn_status dcn_forward_f16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape* 
                                              const void* d_mask, const dcn_packed* packed,
                                              void* d_output, void* stream);
 
+/* Allocation-free variant of dcn_forward_f16_prepacked_dev. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The padded
+ * channel-block copy of the input goes to a device array of DCN_NOALLOC_SCRATCH_BYTES
+ * that the library holds on every device it runs on (resolved by dcn_create) instead
+ * of the context's workspace; the call allocates nothing (no hipMalloc / hipFree).
+ * A shape whose padded input (dcn_cb8_count * 2 bytes) exceeds the array fails with
+ * DCN_INVALID_SHAPE. All calls on one device share that device's array: calls that
+ * overlap in time on one device (other streams, other contexts, other threads) race and
+ * must be serialized by the caller. Each call writes every element it reads, so the
+ * array needs no clearing between calls. */
+#define DCN_NOALLOC_SCRATCH_BYTES (24u << 20)
+dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_shape* shape,
+                                                 const void* d_input, const void* d_offset,
+                                                 const void* d_mask, const dcn_packed* packed,
+                                                 void* d_output, void* stream);
+
 /* Fused-kernel tuning. variant: 1 = register sampling (each lane gathers its MFMA A
  * fragment directly), 2 = LDS-staged im2col tile (a sampler phase fills the tile for
  * the whole K range, an MFMA phase consumes it), 3 = LDS input windows (3x3 kernels:

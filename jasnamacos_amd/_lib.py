@@ -121,6 +121,8 @@ SIGNATURES: dict[str, tuple] = {
     "dcn_pack_input_cb8_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void]),
     "dcn_forward_f16_prepacked_cb8_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void,
                                                     PackedP, c_void, c_void]),
+    "dcn_forward_f16_prepacked_noalloc_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void,
+                                                        PackedP, c_void, c_void]),
     "dcn_set_fused_config": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, C.c_int]),
     "dcn_get_fused_config": (C.c_int, [CtxP, ShapeP, C.POINTER(C.c_int), C.POINTER(C.c_int),
                                        C.POINTER(C.c_int), C.POINTER(C.c_int)]),

@@ -121,9 +121,12 @@ dcn_status ensure_workspace(dcn_context* ctx, size_t bytes, hipStream_t stream) 
     return DCN_OK;
 }
 
+// `repack`: where an NCHW input's padded channel-block copy goes (null: the context's
+// workspace, grown on demand; else a buffer of `repack_bytes` that is never grown).
 dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const void* d_input,
                                bool input_is_cb8, const void* d_offset, const void* d_mask,
-                               const dcn_packed* packed, void* d_output, hipStream_t stream) {
+                               const dcn_packed* packed, void* d_output, hipStream_t stream,
+                               void* repack = nullptr, size_t repack_bytes = 0) {
     dcn_counts c;
     DCN_TRY(validated_counts(ctx, shape, &c));
     if (!packed) return fail(ctx, DCN_INVALID_ARGUMENT, "packed weights are null");
@@ -149,9 +152,19 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
     const dcn::KShape ks = dcn::to_kshape(*shape);
     const void* cb8 = d_input;
     if (!input_is_cb8) {
-        DCN_TRY(ensure_workspace(ctx, dcn::cb8_bytes(*shape, g), stream));
-        DCN_HIP(ctx, dcn::launch_pack_cb8(ks, g, (const uint16_t*)d_input, ctx->workspace, stream));
-        cb8 = ctx->workspace;
+        void* dst = repack;
+        if (dst) {
+            const size_t need = dcn::cb8_bytes(*shape, g);
+            if (need > repack_bytes)
+                return fail(ctx, DCN_INVALID_SHAPE,
+                            "padded input needs " + std::to_string(need) + " bytes; the allocation-free "
+                            "entry point holds at most " + std::to_string(repack_bytes));
+        } else {
+            DCN_TRY(ensure_workspace(ctx, dcn::cb8_bytes(*shape, g), stream));
+            dst = ctx->workspace;
+        }
+        DCN_HIP(ctx, dcn::launch_pack_cb8(ks, g, (const uint16_t*)d_input, dst, stream));
+        cb8 = dst;
     }
     if (cfg.variant == dcn::kVariantTile) {
         if (!packed->weights_tile)
@@ -281,6 +294,13 @@ dcn_status dcn_create(dcn_context** out, int device) {
     if (hipMalloc((void**)&ctx->flag, sizeof(uint32_t)) != hipSuccess) {
         delete ctx;
         return DCN_DEVICE_UNAVAILABLE;
+    }
+    // Set-up of the allocation-free entry point: the scratch array's device address on
+    // this device (once per device; the device is current here).
+    if (dcn::noalloc_scratch_init(device) != hipSuccess) {
+        (void)hipFree(ctx->flag);
+        delete ctx;
+        return DCN_KERNEL_MISSING;
     }
     *out = ctx;
     return DCN_OK;
@@ -555,6 +575,20 @@ dcn_status dcn_forward_f16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape* 
     DeviceGuard guard(ctx->device);
     return fused_prepacked_dev(ctx, shape, d_cb8, true, d_offset, d_mask, packed, d_output,
                                (hipStream_t)stream);
+}
+
+dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_shape* shape,
+                                                 const void* d_input, const void* d_offset,
+                                                 const void* d_mask, const dcn_packed* packed,
+                                                 void* d_output, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    DeviceGuard guard(ctx->device);
+    // The device address of the scratch array, resolved by dcn_create on this device.
+    void* scratch = dcn::noalloc_scratch(ctx->device);
+    if (!scratch)
+        return fail(ctx, DCN_COMMAND_FAILED, "allocation-free scratch is not resolved on this device");
+    return fused_prepacked_dev(ctx, shape, d_input, false, d_offset, d_mask, packed, d_output,
+                               (hipStream_t)stream, scratch, DCN_NOALLOC_SCRATCH_BYTES);
 }
 
 dcn_status dcn_forward_f16_prepacked(dcn_context* ctx, const dcn_shape* shape,

@@ -130,6 +130,11 @@ hipError_t launch_direct_f16(const KShape& s, const uint16_t* in, const uint16_t
                              uint16_t* out, hipStream_t stream);
 hipError_t launch_pack_cb8(const KShape& s, const FusedGeometry& g, const uint16_t* in_nchw,
                            void* cb8, hipStream_t stream);
+// Allocation-free entry point (dcn_scratch.hip): resolve the device address of the
+// file-scope scratch array for `device` (which must be current; once per device), and
+// look it up afterwards (null when it was never resolved).
+hipError_t noalloc_scratch_init(int device);
+void* noalloc_scratch(int device);
 hipError_t launch_prepack_weights(const KShape& s, const FusedGeometry& g, const uint16_t* w,
                                   int layout, const uint16_t* bias, void* packed_w,
                                   float* packed_b, hipStream_t stream);

@@ -322,6 +322,14 @@ class HipDeformConv:
                                                                 _ptr(off), _ptr(msk), packed.handle, _ptr(out),
                                                                 _stream(stream)))
 
+    def forward_f16_prepacked_noalloc_dev(self, shape, x, off, msk, packed: PackedWeights, out, stream=None) -> None:
+        """forward_f16_prepacked_dev without any device allocation: the input's padded
+        channel-block copy goes to the library's per-device scratch array (at most
+        DCN_NOALLOC_SCRATCH_BYTES), shared by every call on the device."""
+        self._check(self._lib.dcn_forward_f16_prepacked_noalloc_dev(self.ctx, C.byref(shape.to_c()), _ptr(x),
+                                                                    _ptr(off), _ptr(msk), packed.handle, _ptr(out),
+                                                                    _stream(stream)))
+
     def im2col_f16_dev(self, shape, x, off, msk, columns, stream=None) -> None:
         self._check(self._lib.dcn_im2col_f16_dev(self.ctx, C.byref(shape.to_c()), _ptr(x), _ptr(off), _ptr(msk),
                                                  _ptr(columns), _stream(stream)))
