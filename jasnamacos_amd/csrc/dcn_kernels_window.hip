@@ -405,23 +405,13 @@ __global__ __launch_bounds__(64 * NW, UNI ? 2 : 1) void window_kernel(WindowArgs
 // reads only LDS, so the copy latency that bounds window_kernel is hidden behind the
 // multiply. B fragments come from LDS once per workgroup instead of once per wave.
 
-// 64 lanes x 16 bytes from `g` (one per lane) into LDS [lds_addr, lds_addr + 1 KB) at
-// lds_addr + lane * 16. lds_addr is wave-uniform and goes through M0, which nothing else
-// in these kernels uses (checked in the generated code). The caller keeps every g inside
-// its buffer and waits with wait_dma() before reading.
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
-    asm volatile(
-        "s_mov_b32 m0, %1\n\t"
-        "global_load_lds_dwordx4 %0, off"
-        :
-        : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
-        : "memory");
+// 64 lanes x 16 bytes from `g` (one per lane) into LDS [dst, dst + 1 KB) at dst + lane * 16,
+// as one global_load_lds_dwordx4. dst is wave-uniform; the compiler sets M0 from it. The
+// caller keeps every g inside its buffer and waits with wait_dma() before reading.
+__device__ __forceinline__ void dma16(const void* g, uint8_t* dst) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
 }
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
-}
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0); }
 
 constexpr int kAsyncNw = 8;     // waves per workgroup = tile rows
 constexpr int kAsyncLds = 160 * 1024;
@@ -598,7 +588,7 @@ __global__ __launch_bounds__(64 * kAsyncNw) void window_async_kernel(WindowArgs 
             const int blocks = (count + 63) / 64;
             const uint32_t row0 = (uint32_t)(b * a.CBLK + st * GPS + g) * a.Hp + (uint32_t)(w[g].y0 + kPad);
             const float inv_ww = 1.0f / (float)w[g].ww;
-            const uint32_t dst = lds_address(win_buf(buf, g));
+            uint8_t* dst = win_buf(buf, g);
             for (int j = wave; j < blocks; j += NW) {
                 const int c = min(j * 64 + lane, count - 1);
                 int r = (int)((float)c * inv_ww);
@@ -606,13 +596,13 @@ __global__ __launch_bounds__(64 * kAsyncNw) void window_async_kernel(WindowArgs 
                 r += ((r + 1) * w[g].ww <= c) ? 1 : 0;
                 const int col = c - r * w[g].ww;
                 const uint32_t unit = (row0 + (uint32_t)r) * a.Wp + (uint32_t)(w[g].x0 + col + kPad);
-                dma16(xin + (size_t)unit * 16, dst + (uint32_t)j * 1024u);
+                dma16(xin + (size_t)unit * 16, dst + j * 1024);
             }
         }
         const uint8_t* src = wpk + (size_t)st * L::kStageB;
-        const uint32_t dst = lds_address(b_buf(buf));
+        uint8_t* dst = b_buf(buf);
         for (int j = wave; j < 9 * NB; j += NW)
-            dma16(src + (size_t)j * 1024 + (size_t)lane * 16, dst + (uint32_t)j * 1024u);
+            dma16(src + (size_t)j * 1024 + (size_t)lane * 16, dst + j * 1024);
     };
 
     f32x16 acc[NB];
