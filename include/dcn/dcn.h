@@ -585,6 +585,28 @@ dcn_status dcn_clip_capture(dcn_clip* clip, const void* d_spatial, const void* d
                             const void* d_forward_flows, void* d_propagated,
                             int max_frames_per_chunk, dcn_graph** out);
 
+/* The recoverable-error ladder of restoreTileWithFallback
+ * (SideBySideRestoration.swift:1065-1136, restoreTileFramesIndependently :1140-1172) over
+ * dcn_clip_run_dev. A rung fails recoverably when its output holds a NaN or Inf
+ * (DCN_NONFINITE_OUTPUT); any other error is returned at once. The rungs:
+ *   1. the whole clip (*recovered_with = 0);
+ *   2. recurrence chunks of at most 10, 5, 3 frames, those shorter than the clip
+ *      (*recovered_with = the chunk size);
+ *   3. independent zero-motion triplets: each frame t runs alone as the clip [t, t, t]
+ *      with zero flows and every branch keeps the middle frame's feat_prop
+ *      (*recovered_with = DCN_CLIP_RECOVERED_TRIPLETS);
+ *   4. if every spatial feature is finite, passthrough: every branch's feat_prop of
+ *      frame t is frame t's spatial feature, unchanged
+ *      (*recovered_with = DCN_CLIP_RECOVERED_PASSTHROUGH); otherwise DCN_COMMAND_FAILED.
+ * Host-synchronous (each rung's check waits for the stream). report, when not null,
+ * receives the reference's progress messages. */
+#define DCN_CLIP_RECOVERED_TRIPLETS (-1)
+#define DCN_CLIP_RECOVERED_PASSTHROUGH (-2)
+typedef void (*dcn_report_fn)(const char* message, void* user);
+dcn_status dcn_clip_run_with_fallback_dev(dcn_clip* clip, const void* d_spatial, const void* d_backward_flows,
+                                          const void* d_forward_flows, void* d_propagated, void* stream,
+                                          dcn_report_fn report, void* report_user, int* recovered_with);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,8 @@ c_f32p = C.POINTER(C.c_float)
 c_f64p = C.POINTER(C.c_double)
 c_u64p = C.POINTER(C.c_uint64)
 c_void = C.c_void_p
+# dcn_report_fn: void (*)(const char* message, void* user)
+ReportFn = C.CFUNCTYPE(None, C.c_char_p, C.c_void_p)
 
 
 class DcnShape(C.Structure):
@@ -195,6 +197,8 @@ SIGNATURES: dict[str, tuple] = {
     "dcn_clip_destroy": (None, [c_void]),
     "dcn_clip_run_dev": (C.c_int, [c_void, c_void, c_void, c_void, c_void, C.c_int, c_void]),
     "dcn_clip_capture": (C.c_int, [c_void, c_void, c_void, c_void, c_void, C.c_int, C.POINTER(c_void)]),
+    "dcn_clip_run_with_fallback_dev": (C.c_int, [c_void, c_void, c_void, c_void, c_void, c_void, ReportFn, c_void,
+                                                 C.POINTER(C.c_int)]),
 }
 
 _LIB: C.CDLL | None = None

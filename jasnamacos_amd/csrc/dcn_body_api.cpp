@@ -31,6 +31,7 @@ struct dcn_clip {
     dcn_body* body[4] = {};
     uint16_t* zero_feat = nullptr;  // 64 x plane zeros: the feat_n2 of positions 0 and 1
     uint16_t* flow2 = nullptr;      // 2 x plane second-order flow scratch
+    uint16_t* triplet_prop = nullptr;  // [4][3][64] x plane: the zero-motion triplet rung's output
     std::vector<void*> buffers;
     hipStream_t capture_stream = nullptr;
 };
@@ -663,6 +664,42 @@ dcn_status dcn_clip_create_tiles(dcn_context* ctx, int height, int width, int fr
     return DCN_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// One recurrence of all four branches over n frames (frame indices 0 .. n-1 of the
+// accessors), in schedule order. feat(i) is frame i's spatial feature, flow(backward, i)
+// the flow that frame i's step reads (backward flows are indexed by the frame, forward
+// flows by the frame before it), prop(b, i) branch b's feat_prop of frame i.
+template <class Feat, class Flow, class Prop>
+dcn_status run_recurrence(dcn_clip* clip, int n, Feat feat, Flow flow, Prop prop, void* stream) {
+    for (int b = 0; b < 4; ++b) {
+        const bool backward = b % 2 == 0;
+        auto frame_at = [&](int position) { return backward ? n - 1 - position : position; };
+        for (int p = 0; p < n; ++p) {
+            const int frame = frame_at(p);
+            const void* prefix[3] = {};
+            for (int i = 0; i < b; ++i) prefix[i] = prop(i, frame);
+            if (p == 0) {
+                DCN_TRY(dcn_body_initial_step_dev(clip->body[b], feat(frame), prefix, prop(b, frame), stream));
+                continue;
+            }
+            const int prev = frame_at(p - 1);
+            const uint16_t* flow1 = flow(backward, frame);
+            const uint16_t* prev_flow = p >= 2 ? flow(backward, prev) : flow1;
+            const uint16_t* feat_n2 = p >= 2 ? prop(b, frame_at(p - 2)) : clip->zero_feat;
+            DCN_TRY(dcn_body_step_dev(clip->body[b], feat(frame), flow1, prev_flow, prop(b, prev), feat_n2,
+                                      prefix, p >= 2 ? 1 : 0, clip->flow2, prop(b, frame), stream));
+        }
+    }
+    return DCN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 dcn_status dcn_clip_run_dev(dcn_clip* clip, const void* d_spatial, const void* d_backward_flows,
                             const void* d_forward_flows, void* d_propagated,
                             int max_frames_per_chunk, void* stream) {
@@ -687,35 +724,99 @@ dcn_status dcn_clip_run_dev(dcn_clip* clip, const void* d_spatial, const void* d
     const uint16_t* spatial = (const uint16_t*)d_spatial;
     const uint16_t* bflows = (const uint16_t*)d_backward_flows;
     const uint16_t* fflows = (const uint16_t*)d_forward_flows;
-    uint16_t* prop = (uint16_t*)d_propagated;
-    auto feat = [&](int frame) { return spatial + (size_t)frame * 64 * plane; };
-    auto propagated = [&](int branch, int frame) { return prop + ((size_t)branch * T + frame) * 64 * plane; };
+    uint16_t* propagated = (uint16_t*)d_propagated;
     for (size_t r = 0; r < starts.size(); ++r) {
-        const int c0 = starts[r], n = sizes[r];
-        for (int b = 0; b < 4; ++b) {
-            const bool backward = b % 2 == 0;
-            const uint16_t* flows = backward ? bflows : fflows;
-            auto frame_at = [&](int position) { return backward ? c0 + n - 1 - position : c0 + position; };
-            auto flow_of = [&](int frame) { return flows + (size_t)(backward ? frame : frame - 1) * 2 * plane; };
-            for (int p = 0; p < n; ++p) {
-                const int frame = frame_at(p);
-                const void* prefix[3] = {};
-                for (int i = 0; i < b; ++i) prefix[i] = propagated(i, frame);
-                if (p == 0) {
-                    DCN_TRY(dcn_body_initial_step_dev(clip->body[b], feat(frame), prefix, propagated(b, frame),
-                                                      stream));
-                    continue;
-                }
-                const int prev = frame_at(p - 1);
-                const uint16_t* flow1 = flow_of(frame);
-                const uint16_t* prev_flow = p >= 2 ? flow_of(prev) : flow1;
-                const uint16_t* feat_n2 = p >= 2 ? propagated(b, frame_at(p - 2)) : clip->zero_feat;
-                DCN_TRY(dcn_body_step_dev(clip->body[b], feat(frame), flow1, prev_flow, propagated(b, prev),
-                                          feat_n2, prefix, p >= 2 ? 1 : 0, clip->flow2, propagated(b, frame),
-                                          stream));
-            }
-        }
+        const int c0 = starts[r];
+        auto feat = [&](int i) { return spatial + (size_t)(c0 + i) * 64 * plane; };
+        auto flow = [&](bool backward, int i) {
+            const int frame = c0 + i;
+            return backward ? bflows + (size_t)frame * 2 * plane : fflows + (size_t)(frame - 1) * 2 * plane;
+        };
+        auto prop = [&](int b, int i) { return propagated + ((size_t)b * T + c0 + i) * 64 * plane; };
+        DCN_TRY(run_recurrence(clip, sizes[r], feat, flow, prop, stream));
     }
+    return DCN_OK;
+}
+
+dcn_status dcn_clip_run_with_fallback_dev(dcn_clip* clip, const void* d_spatial, const void* d_backward_flows,
+                                          const void* d_forward_flows, void* d_propagated, void* stream,
+                                          dcn_report_fn report, void* report_user, int* recovered_with) {
+    if (!clip || !recovered_with) return DCN_INVALID_ARGUMENT;
+    *recovered_with = 0;
+    dcn_context* ctx = clip->ctx;
+    const int T = clip->frames;
+    if (!d_spatial || !d_propagated || (T > 1 && (!d_backward_flows || !d_forward_flows)))
+        return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    DeviceGuard guard(ctx->device);
+    const hipStream_t s = (hipStream_t)stream;
+    const size_t plane = (size_t)clip->w * clip->h * clip->tiles;
+    const size_t feat_bytes = 64 * plane * sizeof(uint16_t);
+    const uint16_t* spatial = (const uint16_t*)d_spatial;
+    uint16_t* propagated = (uint16_t*)d_propagated;
+    auto say = [&](const std::string& msg) {
+        if (report) report(msg.c_str(), report_user);
+    };
+    // A rung fails recoverably when its output holds a NaN or Inf (the reference's
+    // recurrence throws nonFiniteOutput then); any other error ends the ladder.
+    auto attempt = [&](int chunk) -> dcn_status {
+        DCN_TRY(dcn_clip_run_dev(clip, d_spatial, d_backward_flows, d_forward_flows, d_propagated, chunk, stream));
+        return dcn_check_nonfinite_f16_dev(ctx, d_propagated, 4 * (size_t)T * 64 * plane, stream);
+    };
+    dcn_status st = attempt(0);
+    if (st == DCN_OK) return DCN_OK;
+    if (!dcn_status_is_recoverable(st)) return st;
+    std::string last = ctx->last_error;
+    say("clip failed its full temporal window (" + last + "); retrying shorter recurrence chunks");
+    for (int chunk : {10, 5, 3}) {
+        if (chunk >= T) continue;
+        st = attempt(chunk);
+        if (st == DCN_OK) {
+            say("clip recovered with at most " + std::to_string(chunk) + " frames per recurrence chunk");
+            *recovered_with = chunk;
+            return DCN_OK;
+        }
+        if (!dcn_status_is_recoverable(st)) return st;
+        last = ctx->last_error;
+        say("clip also failed with " + std::to_string(chunk) + "-frame chunks (" + last + ")");
+    }
+    // Independent zero-motion triplets: frame t alone as the clip [t, t, t] with zero
+    // flows; every branch keeps the middle frame's feat_prop.
+    if (!clip->triplet_prop) DCN_TRY(alloc(ctx, clip->buffers, &clip->triplet_prop, 12 * 64 * plane));
+    st = DCN_OK;
+    for (int t = 0; t < T && st == DCN_OK; ++t) {
+        const uint16_t* frame = spatial + (size_t)t * 64 * plane;
+        auto feat = [&](int) { return frame; };
+        auto flow = [&](bool, int) { return (const uint16_t*)clip->zero_feat; };  // >= 2 x plane zeros
+        auto prop = [&](int b, int i) { return clip->triplet_prop + (size_t)(b * 3 + i) * 64 * plane; };
+        DCN_TRY(run_recurrence(clip, 3, feat, flow, prop, stream));
+        st = dcn_check_nonfinite_f16_dev(ctx, clip->triplet_prop, 12 * 64 * plane, stream);
+        if (st != DCN_OK) break;
+        for (int b = 0; b < 4; ++b)
+            DCN_HIP(ctx, hipMemcpyAsync(propagated + ((size_t)b * T + t) * 64 * plane, prop(b, 1), feat_bytes,
+                                        hipMemcpyDeviceToDevice, s));
+    }
+    if (st == DCN_OK) {
+        DCN_HIP(ctx, hipStreamSynchronize(s));
+        say("clip recovered with independent zero-motion frame triplets");
+        *recovered_with = DCN_CLIP_RECOVERED_TRIPLETS;
+        return DCN_OK;
+    }
+    if (!dcn_status_is_recoverable(st)) return st;
+    last = ctx->last_error;
+    say("clip also failed independent frame recovery (" + last + ")");
+    // Passthrough of finite input: every branch's feat_prop of frame t is frame t's
+    // spatial feature, unchanged.
+    st = dcn_check_nonfinite_f16_dev(ctx, d_spatial, (size_t)T * 64 * plane, stream);
+    if (st == DCN_NONFINITE_OUTPUT)
+        return fail(ctx, DCN_COMMAND_FAILED, "clip has non-finite input features after model failure: " + last);
+    if (st != DCN_OK) return st;
+    for (int b = 0; b < 4; ++b)
+        DCN_HIP(ctx, hipMemcpyAsync(propagated + (size_t)b * T * 64 * plane, spatial, (size_t)T * feat_bytes,
+                                    hipMemcpyDeviceToDevice, s));
+    DCN_HIP(ctx, hipStreamSynchronize(s));
+    say("WARNING: clip is using finite input passthrough because all recurrence recovery modes failed (" +
+        last + ")");
+    *recovered_with = DCN_CLIP_RECOVERED_PASSTHROUGH;
     return DCN_OK;
 }
 

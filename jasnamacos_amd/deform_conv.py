@@ -708,6 +708,19 @@ class PropagationClip:
                                                        _ptr(forward_flows), _ptr(propagated),
                                                        int(max_frames_per_chunk), _stream(stream)))
 
+    def run_with_fallback_dev(self, spatial, backward_flows, forward_flows, propagated, stream=None,
+                              report=None) -> int:
+        """dcn_clip_run_with_fallback_dev: the whole recovery ladder (see
+        propagate_with_fallback) in the library; returns 0, the chunk size,
+        RECOVERED_TRIPLETS or RECOVERED_PASSTHROUGH. report(msg) receives the progress
+        messages."""
+        recovered = C.c_int()
+        cb = _lib.ReportFn(lambda msg, _user: report(msg.decode()) if report else None)
+        self.ctx._check(self.ctx._lib.dcn_clip_run_with_fallback_dev(
+            self.handle, _ptr(spatial), _ptr(backward_flows), _ptr(forward_flows), _ptr(propagated),
+            _stream(stream), cb, None, C.byref(recovered)))
+        return recovered.value
+
     def capture(self, spatial, backward_flows, forward_flows, propagated, max_frames_per_chunk: int = 0) -> BodyGraph:
         handle = C.c_void_p()
         self.ctx._check(self.ctx._lib.dcn_clip_capture(self.handle, _ptr(spatial), _ptr(backward_flows),
@@ -727,19 +740,36 @@ class PropagationClip:
             pass
 
 
-def propagate_with_fallback(run, frame_count: int, report=None) -> int:
+RECOVERED_TRIPLETS = -1  # DCN_CLIP_RECOVERED_TRIPLETS
+RECOVERED_PASSTHROUGH = -2  # DCN_CLIP_RECOVERED_PASSTHROUGH
+
+
+def propagate_with_fallback(run, frame_count: int, report=None, *, run_triplets, input_is_finite,
+                            pass_through) -> int:
     """The recoverable-error ladder of restoreTileWithFallback
-    (SideBySideRestoration.swift:1065-1110) for the propagation: run(0) propagates the
-    whole clip; when it fails with the recoverable nonFiniteOutput, run(n) is retried with
-    shorter recurrence chunks n = 10, 5, 3 (those below frame_count). Returns the chunk
-    size that succeeded (0 = whole clip). Any other error propagates at once; when every
-    chunk size fails the last nonFiniteOutput is re-raised as commandFailed."""
+    (SideBySideRestoration.swift:1065-1136) over caller-supplied rungs:
+
+    1. run(0) propagates the whole clip (returns 0);
+    2. on the recoverable nonFiniteOutput, run(n) for recurrence chunks n = 10, 5, 3, those
+       below frame_count (returns n);
+    3. run_triplets() runs every frame alone as the zero-motion clip [f, f, f] and keeps
+       the middle output (restoreTileFramesIndependently, :1140-1172; returns
+       RECOVERED_TRIPLETS);
+    4. if input_is_finite(), pass_through() hands the input on unchanged (returns
+       RECOVERED_PASSTHROUGH); otherwise commandFailed.
+
+    Any error other than nonFiniteOutput propagates at once. dcn_clip_run_with_fallback_dev
+    is the same ladder over the four-branch clip, in the library."""
     report = report or (lambda msg: None)
+
+    def recoverable(e: DeformConvError) -> bool:
+        return e.is_recoverable_numerical_failure
+
     try:
         run(0)
         return 0
     except DeformConvError as e:
-        if not e.is_recoverable_numerical_failure:
+        if not recoverable(e):
             raise
         last = e
         report(f"full temporal window failed ({e}); retrying shorter recurrence chunks")
@@ -751,11 +781,24 @@ def propagate_with_fallback(run, frame_count: int, report=None) -> int:
             report(f"recovered with at most {chunk} frames per recurrence chunk")
             return chunk
         except DeformConvError as e:
-            if not e.is_recoverable_numerical_failure:
+            if not recoverable(e):
                 raise
             last = e
             report(f"also failed with {chunk}-frame chunks ({e})")
-    raise DeformConvError(COMMAND_FAILED, f"every recurrence chunk size failed: {last}")
+    try:
+        run_triplets()
+        report("recovered with independent zero-motion frame triplets")
+        return RECOVERED_TRIPLETS
+    except DeformConvError as e:
+        if not recoverable(e):
+            raise
+        last = e
+        report(f"also failed independent frame recovery ({e})")
+    if not input_is_finite():
+        raise DeformConvError(COMMAND_FAILED, f"non-finite input after model failure: {last}")
+    report(f"WARNING: using finite input passthrough because all recurrence recovery modes failed ({last})")
+    pass_through()
+    return RECOVERED_PASSTHROUGH
 
 
 # ---- temporal schedule ----------------------------------------------------------------

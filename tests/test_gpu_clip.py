@@ -8,7 +8,10 @@ Bars:
     FP16 tolerance (max 2e-2, mean 1e-3), so errors do not compound over the recurrence;
   * one captured graph for the whole clip replays bit-identically to the eager run;
   * chunked recurrences equal independent clips over the chunk ranges;
-  * non-finite features are detected, and the fallback ladder ends in commandFailed.
+  * the recovery ladder (dcn_clip_run_with_fallback_dev): a finite clip runs whole; NaN
+    motion falls through to the zero-motion triplets, whose kept middle frames equal
+    3-frame clips run alone; overflowing weights end in finite-input passthrough;
+    non-finite features end in commandFailed.
 """
 from __future__ import annotations
 
@@ -205,24 +208,80 @@ def test_clip_tiles_equal_single_tile_clips(gpu_ctx, torch):
         assert np.array_equal(got[:, :, t].view(np.uint16), want.view(np.uint16)), t
 
 
-def test_clip_nonfinite_is_detected_and_ladder_gives_up(gpu_ctx, dcn, torch):
+def _ladder(torch, gpu_ctx, wd, xd, frames, h, w, blocks):
+    clip = gpu_ctx.clip(h, w, frames, wd, blocks=blocks)
+    prop = torch.zeros(4 * frames * 64 * h * w, dtype=torch.int16, device="cuda")
+    msgs = []
+    try:
+        rung = clip.run_with_fallback_dev(xd["spatial"], xd["bflows"], xd["fflows"], prop, report=msgs.append)
+        torch.cuda.synchronize()
+        return rung, host(prop).copy().reshape(4, frames, 64 * h * w), msgs
+    finally:
+        clip.free()
+
+
+def test_clip_ladder_full_window_when_finite(gpu_ctx, dcn, torch):
+    frames, h, w, blocks = 6, 8, 8, 1
+    weights, wd, x, xd = _clip_case(torch, frames, h, w, blocks, 12)
+    log("case: ladder, finite clip")
+    rung, got, msgs = _ladder(torch, gpu_ctx, wd, xd, frames, h, w, blocks)
+    assert rung == 0 and msgs == []
+    want = _run_clip(torch, gpu_ctx, wd, xd, frames, h, w, blocks)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_clip_ladder_recovers_with_zero_motion_triplets(gpu_ctx, dcn, torch):
+    """NaN motion into frame 1 (backward flow 1) poisons the whole clip and every chunking
+    (frame 1 never starts a chunk of 6 frames); each frame alone as [t, t, t] with zero
+    flows does not. Every branch keeps the triplet's middle feat_prop, bit for bit."""
+    frames, h, w, blocks = 6, 8, 8, 1
+    weights, wd, x, xd = _clip_case(torch, frames, h, w, blocks, 13)
+    plane = h * w
+    bflows = x["bflows"].copy()
+    bflows[1 * 2 * plane:2 * 2 * plane] = np.float16(np.nan)
+    xd["bflows"] = dev(torch, bflows)
+    log("case: ladder, NaN motion -> zero-motion triplets")
+    rung, got, msgs = _ladder(torch, gpu_ctx, wd, xd, frames, h, w, blocks)
+    assert rung == dcn.RECOVERED_TRIPLETS, msgs
+    assert [m.split(" (")[0] for m in msgs] == [
+        "clip failed its full temporal window", "clip also failed with 5-frame chunks",
+        "clip also failed with 3-frame chunks", "clip recovered with independent zero-motion frame triplets"]
+    zero = np.zeros(2 * 2 * plane, np.float16)
+    for t in range(frames):
+        f = x["spatial"][t * 64 * plane:(t + 1) * 64 * plane]
+        trip = {"spatial": dev(torch, np.tile(f, 3)), "bflows": dev(torch, zero), "fflows": dev(torch, zero)}
+        want = _run_clip(torch, gpu_ctx, wd, trip, 3, h, w, blocks)
+        assert np.array_equal(got[:, t].view(np.uint16), want[:, 1].view(np.uint16)), t
+
+
+def test_clip_ladder_passes_finite_input_through(gpu_ctx, dcn, torch):
+    """Weights ~N(0, 20) overflow FP16 within two convs at every rung; the features are
+    finite, so every branch's output is the spatial input, unchanged."""
+    frames, h, w, blocks = 4, 8, 8, 1
+    rng = np.random.default_rng(14)
+    weights = [br.body_weights(rng, b, blocks, std=20.0) for b in range(4)]
+    wd = [{k: dev(torch, v) for k, v in wb.items()} for wb in weights]
+    plane = h * w
+    x = {"spatial": br.f16(rng.standard_normal(frames * 64 * plane)),
+         "bflows": br.f16(rng.uniform(-2, 2, (frames - 1) * 2 * plane)),
+         "fflows": br.f16(rng.uniform(-2, 2, (frames - 1) * 2 * plane))}
+    xd = {k: dev(torch, v) for k, v in x.items()}
+    log("case: ladder, overflowing weights -> passthrough")
+    rung, got, msgs = _ladder(torch, gpu_ctx, wd, xd, frames, h, w, blocks)
+    assert rung == dcn.RECOVERED_PASSTHROUGH, msgs
+    assert msgs[-1].startswith("WARNING: clip is using finite input passthrough")
+    for b in range(4):
+        assert np.array_equal(got[b].ravel().view(np.uint16), x["spatial"].view(np.uint16)), b
+
+
+def test_clip_nonfinite_input_ends_the_ladder_in_command_failed(gpu_ctx, dcn, torch):
     frames, h, w, blocks = 6, 8, 8, 1
     weights, wd, x, xd = _clip_case(torch, frames, h, w, blocks, 11)
     spatial = x["spatial"].copy()
     spatial[5] = np.float16(np.inf)
     xd["spatial"] = dev(torch, spatial)
-    log("case: clip non-finite + fallback ladder")
-    clip = gpu_ctx.clip(h, w, frames, wd, blocks=blocks)
-    prop = torch.zeros(4 * frames * 64 * h * w, dtype=torch.int16, device="cuda")
-    tried = []
-
-    def run(chunk):
-        tried.append(chunk)
-        clip.run_dev(xd["spatial"], xd["bflows"], xd["fflows"], prop, chunk)
-        gpu_ctx.check_nonfinite_f16_dev(prop, prop.numel())
-
+    log("case: ladder, non-finite input -> commandFailed")
     with pytest.raises(dcn.DeformConvError) as e:
-        dcn.propagate_with_fallback(run, frames)
+        _ladder(torch, gpu_ctx, wd, xd, frames, h, w, blocks)
     assert e.value.status == dcn.COMMAND_FAILED
-    assert tried == [0, 5, 3]
-    clip.free()
+    assert "non-finite input features" in str(e.value)
