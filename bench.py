@@ -11,8 +11,12 @@ The dominant kernel (the fused sampler + MFMA GEMM) is also timed alone, from a 
 fused-only launches, with HIP events on the stream it runs on; roofline.achieved is the
 algorithmic bytes per launch over that duration.
 
+Config 1 is the FP32 entry point (runFloat32): one direct kernel per call, in the CPU
+oracle's summation order, priced against the FP32 matrix peak.
+
 cpu_baseline: the CPU oracle (a C restatement of the reference's DeformConvCPU.run),
-single thread, on the FP32 version of the same shape.
+single thread, on a bounded sample of the benchmarked workload with the same inputs; its
+output of that sample also checks the GPU's timed output (timed_output_check).
 """
 from __future__ import annotations
 
@@ -31,8 +35,10 @@ sys.path.insert(0, str(ROOT))
 METRIC = "DCNv2 fwd µs/call + TFLOP/s (% HBM/MFMA roofline) at 1×128×64×64→64, 16 dg"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
 
 WORKLOADS = {
+    1: "C1: DCNv2 1x128x64x64 -> 64, 3x3, 16 deformable groups, FP32 (runFloat32: direct kernel, oracle summation order)",
     2: "C2: DCNv2 1x128x64x64 -> 64, 3x3, 16 deformable groups, FP16 storage, FP32 accumulate, prepacked weights",
     3: "C3: DCNv2 16x128x64x64 -> 64, 3x3, 16 deformable groups, FP16, prepacked weights (batched 8K-eye tiles)",
     5: "C5: DCNv2 1x128x180x320 -> 64, 3x3, 16 deformable groups, FP16, prepacked weights (large map)",
@@ -40,7 +46,7 @@ WORKLOADS = {
 }
 
 
-KERNEL_NAMES = {1: "fused_kernel", 2: "staged_kernel", 3: "window_kernel", 4: "window_kernel",
+KERNEL_NAMES = {0: "direct_kernel", 1: "fused_kernel", 2: "staged_kernel", 3: "window_kernel", 4: "window_kernel",
                 5: "narrow_kernel", 6: "window_async_kernel", 7: "tile_kernel"}
 
 
@@ -59,52 +65,109 @@ def read_traffic(name: str):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(budget_s: float = 25.0) -> dict:
-    import numpy as np
+# The FP16 paths' parity bar against the FP32 oracle (the tests' tolerance).
+MAX_ABS_F16, MEAN_ABS_F16 = 2e-2, 1e-3
+# Output channels of the C5 sample: both ends of both 32-channel MFMA column blocks.
+C5_SAMPLE_OCS = (0, 1, 2, 3, 28, 29, 30, 31, 60, 61, 62, 63)
 
-    import oracle
-    from jasnamacos_amd import deform_conv as dc
 
-    d = dc.generate_config_inputs(1, 1)
-    s = d["shape"]
-    args = [d[k] for k in ("input", "offset", "mask", "weight", "bias")]
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        oracle.forward_f32(s, *args)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 3 or time.perf_counter() - t_start + times[-1] > budget_s:
-            break
-    med = statistics.median(times)
-    # The same restatement spread over the host's cores (at most 16, the box's CPU share),
-    # bit-identical results: a second baseline beside the single-threaded one.
-    threads = min(16, os.cpu_count() or 1)
-    mt = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        oracle.forward_f32_threads(s, *args, threads=threads)
-        mt.append(time.perf_counter() - t0)
-    cpu = "unknown"
+def _cpu_name() -> str:
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {
+    return "unknown"
+
+
+def cpu_baseline(config: int, s, inputs: dict, gpu_out, budget_s: float = 25.0) -> tuple[dict, dict]:
+    """The CPU oracle (C restatement of DeformConvCPU.run, DeformConv.swift:76-138) timed on
+    a bounded sample of the benchmarked workload, single thread, on the same (FP16-rounded
+    for C2/C3/C5) inputs the GPU ran; value is scaled to one whole call. Its output of the
+    sample is then the checker of the GPU's timed output: returns (baseline, check)."""
+    import dataclasses
+
+    import numpy as np
+
+    import oracle
+
+    args = [np.asarray(inputs[k], np.float32) for k in ("input", "offset", "mask", "weight", "bias")]
+    c = s.counts()
+    if config in (1, 2):
+        sample, scale = "the full call", 1.0
+
+        def run():
+            return [(slice(0, c["output"]), oracle.forward_f32(s, *args))]
+    elif config == 3:
+        tile = dataclasses.replace(s, batch=1)
+        tc = tile.counts()
+        images = (0, s.batch - 1)
+        sample, scale = f"images {images[0]} and {images[1]} of {s.batch} (x{s.batch // len(images)})", s.batch / 2
+
+        def run():
+            res = []
+            for b in images:
+                part = [args[0][b * tc["input"]:(b + 1) * tc["input"]], args[1][b * tc["offset"]:(b + 1) * tc["offset"]],
+                        args[2][b * tc["mask"]:(b + 1) * tc["mask"]], args[3], args[4]]
+                res.append((slice(b * tc["output"], (b + 1) * tc["output"]), oracle.forward_f32(tile, *part)))
+            return res
+    else:  # C5: a slice of output channels, every pixel and sample
+        plane = s.output_height * s.output_width
+        ocs = C5_SAMPLE_OCS
+        sample = f"output channels {list(ocs)} of {s.output_channels} (x{s.output_channels / len(ocs):.2f})"
+        scale = s.output_channels / len(ocs)
+
+        def run():
+            res = []
+            for oc in ocs:
+                ref = oracle.forward_f32_oc_range(s, *args, oc, oc + 1)
+                res.append((slice(oc * plane, (oc + 1) * plane), ref[oc * plane:(oc + 1) * plane]))
+            return res
+
+    times, t_start = [], time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        ref = run()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 3 or time.perf_counter() - t_start + times[-1] > budget_s:
+            break
+    med = statistics.median(times) * scale
+    baseline = {
         "value": med * 1e6,
         "unit": "us/call",
         "cores": 1,
         "kind": "port",
-        "sample": (f"full FP32 call at 1x128x64x64->64, 16 dg (config 1), {len(times)} run(s), median; "
-                   f"C restatement of DeformConvCPU.run, gcc -O2 -ffp-contract=off; host {cpu}, "
+        "sample": (f"{sample} at {s.batch}x{s.input_channels}x{s.input_height}x{s.input_width}->"
+                   f"{s.output_channels}, {s.offset_groups} dg, {len(times)} run(s), median scaled to one call; "
+                   f"C restatement of DeformConvCPU.run, gcc -O2 -ffp-contract=off; host {_cpu_name()}, "
                    f"nproc {os.cpu_count()}"),
         "tflops": s.flops / med / 1e12,
-        "all_cores": {"value": statistics.median(mt) * 1e6, "unit": "us/call", "cores": threads,
-                      "sample": "same call, output channels split over threads, median of 3"},
     }
+    # The same restatement spread over the host's cores (at most 16, the box's CPU share),
+    # bit-identical results, for the shapes where one call fits the budget.
+    if config in (1, 2):
+        threads = min(16, os.cpu_count() or 1)
+        mt = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            oracle.forward_f32_threads(s, *args, threads=threads)
+            mt.append(time.perf_counter() - t0)
+        baseline["all_cores"] = {"value": statistics.median(mt) * 1e6, "unit": "us/call", "cores": threads,
+                                 "sample": "same call, output channels split over threads, median of 3"}
+
+    got = np.concatenate([np.asarray(gpu_out[sl], np.float32) for sl, _ in ref])
+    want = np.concatenate([r for _, r in ref])
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    check = {"oracle": "FP32 DeformConvCPU.run restatement on the inputs the GPU ran", "sample": sample,
+             "values": int(want.size), "max_abs_err": float(err.max()), "mean_abs_err": float(err.mean())}
+    if config == 1:
+        check["bound"] = "bit-exact"
+        check["within"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+    else:
+        check["bound"] = {"max": MAX_ABS_F16, "mean": MEAN_ABS_F16}
+        check["within"] = bool(check["max_abs_err"] <= MAX_ABS_F16 and check["mean_abs_err"] <= MEAN_ABS_F16)
+    return baseline, check
 
 
 def bench_body(args) -> int:
@@ -609,28 +672,46 @@ def main() -> int:
         return bench_body(args)
     d = dc.generate_config_inputs(args.config, args.seed)
     s = d["shape"]
-    h = {k: np.asarray(d[k], np.float32).astype(np.float16) for k in ("input", "offset", "mask", "weight", "bias")}
-    dev = {k: torch.from_numpy(h[k].view(np.int16)).cuda() for k in ("input", "offset", "mask", "weight", "bias")}
+    f32 = args.config == 1
+    keys = ("input", "offset", "mask", "weight", "bias")
+    if f32:
+        h = {k: np.asarray(d[k], np.float32) for k in keys}
+        dev = {k: torch.from_numpy(h[k]).cuda() for k in keys}
+    else:
+        h = {k: np.asarray(d[k], np.float32).astype(np.float16) for k in keys}
+        dev = {k: torch.from_numpy(h[k].view(np.int16)).cuda() for k in keys}
     ctx = dc.HipDeformConv(0)
-    packed = ctx.prepack_dev(s, dev["weight"], dev["bias"])
-    ctx.reserve(s)
-    if args.variant or args.mt or args.ks:
-        ctx.set_fused_config(args.mt, args.ks, -1, args.variant)
-    fused_cfg = ctx.get_fused_config(s)
-    out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
-    cb8 = torch.empty(ctx.cb8_count(s), dtype=torch.int16, device="cuda")
     stream = torch.cuda.Stream()
+    packed = None
+    if f32:
+        fused_cfg = None
+        out = torch.empty(s.output_count, dtype=torch.float32, device="cuda")
 
-    def step(cur):
-        ctx.forward_f16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out, stream=cur)
+        def step(cur):
+            ctx.forward_f32_dev(s, dev["input"], dev["offset"], dev["mask"], dev["weight"], dev["bias"], out,
+                                stream=cur)
 
-    def fused_only(cur):
-        ctx.forward_f16_prepacked_cb8_dev(s, cb8, dev["offset"], dev["mask"], packed, out, stream=cur)
+        fused_only = step  # one kernel per call
+    else:
+        packed = ctx.prepack_dev(s, dev["weight"], dev["bias"])
+        ctx.reserve(s)
+        if args.variant or args.mt or args.ks:
+            ctx.set_fused_config(args.mt, args.ks, -1, args.variant)
+        fused_cfg = ctx.get_fused_config(s)
+        out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
+        cb8 = torch.empty(ctx.cb8_count(s), dtype=torch.int16, device="cuda")
+
+        def step(cur):
+            ctx.forward_f16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out, stream=cur)
+
+        def fused_only(cur):
+            ctx.forward_f16_prepacked_cb8_dev(s, cb8, dev["offset"], dev["mask"], packed, out, stream=cur)
 
     with torch.cuda.stream(stream):
         for _ in range(max(args.warmup, 1)):
             step(stream)
-        ctx.pack_input_cb8_dev(s, dev["input"], cb8, stream=stream)
+        if not f32:
+            ctx.pack_input_cb8_dev(s, dev["input"], cb8, stream=stream)
     torch.cuda.synchronize()
 
     g_step = torch.cuda.CUDAGraph()
@@ -706,16 +787,34 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    # correctness of what was timed: finite output with the expected checksum scale
-    res = out.cpu().numpy().view(np.float16)
-    finite = bool(np.all(np.isfinite(res.astype(np.float32))))
+    # What was timed: the output of the last timed call (checked against the oracle in the
+    # cpu_baseline leg below).
+    res = out.cpu().numpy() if f32 else out.cpu().numpy().view(np.float16).astype(np.float32)
+    finite = bool(np.all(np.isfinite(res)))
 
-    nbytes = algorithmic_bytes(s)
+    nbytes = algorithmic_bytes(s, elem=4 if f32 else 2)
     flops = s.flops
-    achieved = nbytes / (k_us * 1e-6) / 1e9
-    workload_name = {2: "dcn_c2_fp16", 3: "dcn_c3_fp16", 5: "dcn_c5_fp16"}[args.config]
-    kernel_name = KERNEL_NAMES.get(fused_cfg["variant"], "fused_kernel")
+    workload_name = {1: "dcn_c1_fp32", 2: "dcn_c2_fp16", 3: "dcn_c3_fp16", 5: "dcn_c5_fp16"}[args.config]
+    kernel_name = KERNEL_NAMES[0] if f32 else KERNEL_NAMES.get(fused_cfg["variant"], "fused_kernel")
     traffic = read_traffic(f"{kernel_name}_{workload_name}")
+    if f32:
+        # FP32 arithmetic: priced against the FP32 matrix peak (the HBM bytes take
+        # 10.5 MB / 8 TB/s = 1.3 us, below the 3.8 us of the FLOPs).
+        achieved = flops / (k_us * 1e-6) / 1e12
+        roofline = {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": achieved / FP32_PEAK_TFLOPS, "traffic": traffic,
+                    "kernel": kernel_name + " (FP32 direct, one thread per output)",
+                    "traffic_source": f"profiles/{kernel_name}_{workload_name}.md" if traffic else None,
+                    "algorithmic_bytes_per_launch": nbytes,
+                    "hbm_frac": nbytes / (k_us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+    else:
+        achieved = nbytes / (k_us * 1e-6) / 1e9
+        roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                    "kernel": kernel_name + " (sampler + MFMA GEMM)",
+                    "traffic_source": f"profiles/{kernel_name}_{workload_name}.md" if traffic else None,
+                    "algorithmic_bytes_per_launch": nbytes,
+                    "mfma_frac": flops / (k_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS}
     line = {
         "metric": METRIC,
         "value": round(us_per_call, 4),
@@ -727,7 +826,7 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": "f32" if f32 else "f16",
         "data": "synthetic (seeded SplitMix64/Box-Muller inputs of the benchmark distributions; random weights)",
         "config": {
             "workload": WORKLOADS[args.config],
@@ -738,7 +837,7 @@ def main() -> int:
         },
         "tflops": flops / (us_per_call * 1e-6) / 1e12,
         "step_hbm_frac": nbytes / (us_per_call * 1e-6) / 1e9 / HBM_PEAK_GBS,
-        "step_mfma_frac": flops / (us_per_call * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS,
+        "step_mfma_frac": flops / (us_per_call * 1e-6) / 1e12 / (FP32_PEAK_TFLOPS if f32 else MFMA_F16_PEAK_TFLOPS),
         "kernel_us": k_us,
         "cold_us_per_call": cold_us,
         "warm_single_us_per_call": warm_single_us,
@@ -748,25 +847,17 @@ def main() -> int:
         "kernel_tflops": flops / (k_us * 1e-6) / 1e12,
         "wall_ms_timed_region": wall_ms,
         "output_finite": finite,
-        "roofline": {
-            "bound": "hbm",
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": traffic,
-            "kernel": kernel_name + " (sampler + MFMA GEMM)",
-            "traffic_source": f"profiles/{kernel_name}_{workload_name}.md" if traffic else None,
-            "algorithmic_bytes_per_launch": nbytes,
-            "mfma_frac": flops / (k_us * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS,
-        },
+        "roofline": roofline,
         "cpu_baseline": None,
     }
     if args.config == 3:
         line["per_gpu_share"] = bench_share(args, ctx, dc, d, dev)
+    line["timed_output_check"] = None
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline()
-    packed.free()
+        line["cpu_baseline"], line["timed_output_check"] = cpu_baseline(
+            args.config, s, {k: h[k].astype(np.float32) for k in keys}, res)
+    if packed is not None:
+        packed.free()
     ctx.close()
     print(json.dumps(line), flush=True)
     return 0

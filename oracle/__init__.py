@@ -133,6 +133,34 @@ def forward_f32_oc_range(shape, input, offset, mask, weight, bias, oc_begin, oc_
     return out
 
 
+def forward_f32_ocs(shape, input, offset, mask, weight, bias, ocs, threads=None) -> np.ndarray:
+    """forward_f32's output channels `ocs` (zeros elsewhere), one channel per task over a
+    thread pool (the C call releases the GIL); each channel is the serial loop's bits."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
+    threads = threads or min(16, os.cpu_count() or 1)
+    keep = [_f32(a) for a in (input, offset, mask, weight, bias)]
+    out = np.zeros(_counts(shape)["output"], dtype=np.float32)
+    fn = load().oracle_dcn_forward_f32_oc_range
+    plane = shape.output_height * shape.output_width
+    outs = {}
+
+    def one(oc):
+        part = np.zeros_like(out)
+        rc = fn(C.byref(_shape(shape)), *[p for _, p in keep], part.ctypes.data_as(_f), int(oc), int(oc) + 1)
+        if rc:
+            raise ValueError("invalid shape")
+        outs[oc] = part
+
+    with ThreadPoolExecutor(threads) as pool:
+        list(pool.map(one, ocs))
+    view, cout = out.reshape(shape.batch, -1, plane), shape.output_channels
+    for oc, part in outs.items():
+        view[:, oc] = part.reshape(shape.batch, cout, plane)[:, oc]
+    return out
+
+
 def forward_f16_direct(shape, input, offset, mask, weight, bias) -> np.ndarray:
     """deform_conv2d_fp16 (MetalShader.swift:126-174)."""
     keep = [_u16(a) for a in (input, offset, mask, weight, bias)]

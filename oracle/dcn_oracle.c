@@ -424,7 +424,8 @@ void oracle_temporal_prepare_f16(int width, int height, int has_second_order,
 void oracle_conv3x3_f16(int cin, int cout, int height, int width, const uint16_t* input,
                         const uint16_t* weight, const uint16_t* bias, int activation,
                         float slope, const uint16_t* residual, uint16_t* output) {
-    /* activation: 0 none, 1 LeakyReLU(slope), 2 ReLU. out = half(act(acc) [+ residual]). */
+    /* activation: 0 none, 1 LeakyReLU(slope), 2 ReLU. out = half(residual + act(acc)):
+     * one rounding after the FP32 residual add, not half(residual + half(act(acc))). */
     const size_t plane = (size_t)width * height;
     /* Output channels are independent; each element is computed by the same serial code. */
 #pragma omp parallel for schedule(static)

@@ -102,8 +102,10 @@ void oracle_temporal_prepare_f16(int width, int height, int has_second_order,
                                  uint16_t* conditions, uint16_t* deform_input);
 
 /* 3x3 convolution, stride 1, pad 1, FP16 storage, FP32 accumulation in (ic, ky, kx)
- * order starting from the bias, optional LeakyReLU(slope) and optional residual add
- * (res + half(conv)), output rounded to FP16. The body's offset branch and backbone
+ * order starting from the bias, optional LeakyReLU(slope) and optional residual:
+ * out = half(residual + act(acc)), the residual added in FP32 to the unrounded activation
+ * and the sum rounded once (the GPU conv epilogue's first residual; a second residual is
+ * a separate FP16 add on that rounded output, oracle_add_f16). The body's offset branch and backbone
  * layers (conv_offset / backbone modules exported by tools/convert_basicvsrpp.py:181-197). */
 void oracle_conv3x3_f16(int cin, int cout, int height, int width, const uint16_t* input,
                         const uint16_t* weight, const uint16_t* bias, int activation,

@@ -183,6 +183,41 @@ def test_conv3x3_matches_oracle(gpu_ctx, dcn, oracle, torch, cin, cout, act, res
     conv.free()
 
 
+@pytest.mark.parametrize("two", [False, True])
+def test_conv3x3_residual_rounding_contract(gpu_ctx, dcn, oracle, torch, two):
+    """The epilogue adds the first residual to the unrounded FP32 result and rounds once:
+    acc = 1 + 2^-11 (a tie between FP16 neighbours) plus 2^-11 gives exactly 1 + 2^-10,
+    where rounding acc first would give 1.0. A second residual is a separate FP16 add
+    (1 + 2^-10 + 2^-11 ties to even: 1 + 2^-9). Bit-exact against the oracle's contract."""
+    cin = cout = 64
+    h = w = 5
+    x = np.zeros((cin, h, w), np.float16)
+    x[0, 2, 2] = 1.0
+    wt = np.zeros((cout, cin, 3, 3), np.float16)
+    wt[:, 0, 1, 1] = np.float16(2.0 ** -11)
+    b = np.ones(cout, np.float16)
+    r = np.full(cout * h * w, np.float16(2.0 ** -11))
+    log("case: conv3x3 residual rounding, second residual", two)
+    conv = gpu_ctx.conv3x3(cin, cout, h, w, dev(torch, wt), dev(torch, b))
+    out = torch.zeros(cout * h * w, dtype=torch.int16, device="cuda")
+    rd = dev(torch, r)
+    if two:
+        conv.run_dev(dev(torch, br.to_cb8(x.ravel(), cin, h, w)), out, 0, 0, 0.1, rd, 0, rd, 0)
+    else:
+        conv.run_dev(dev(torch, br.to_cb8(x.ravel(), cin, h, w)), out, 0, 0, 0.1, rd, 0)
+    torch.cuda.synchronize()
+    got = host(out).reshape(cout, h, w)
+    conv.free()
+    want = oracle.conv3x3_f16(cin, cout, h, w, x.ravel(), wt.ravel(), b, 0, 0.1, r)
+    if two:
+        want = oracle.add_f16(want, r)
+    assert np.array_equal(got.ravel().view(np.uint16), want.view(np.uint16))
+    centre = np.float16(1 + 2.0 ** -9) if two else np.float16(1 + 2.0 ** -10)
+    assert np.all(got[:, 2, 2] == centre)
+    got[:, 2, 2] = 1.0
+    assert np.all(got == np.float16(1.0))
+
+
 PAIR_CASES = [
     # h, w, act1, act2, res1 layout (None = none), res2 layout, out layout
     (13, 21, 2, 0, 1, None, 1),   # residual block, partial 2 x 8 tiles on both edges

@@ -349,11 +349,15 @@ def test_fused_c5_large_map(gpu_ctx, dcn, oracle, variant):
         gpu_ctx.set_fused_config(0, 0, -1, 0)
     w = widen(h)
     plane = s.output_height * s.output_width
-    oc_end = 4  # a bounded slice of output channels: every pixel, every sample, 4 channels
-    ref = oracle.forward_f32_oc_range(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"], 0, oc_end)
-    mx, mean = errors(out[:oc_end * plane], ref[:oc_end * plane])
-    log(f"  C5 oc 0..3: max {mx:.3e} mean {mean:.3e}")
-    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+    # Bounded slices of output channels, every pixel and sample: both ends of both
+    # 32-channel MFMA column blocks.
+    for lo in (0, 28, 60):
+        ocs = range(lo, lo + 4)
+        ref = oracle.forward_f32_ocs(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"], ocs)
+        sl = slice(lo * plane, (lo + 4) * plane)
+        mx, mean = errors(out[sl], ref[sl])
+        log(f"  C5 oc {lo}..{lo + 3}: max {mx:.3e} mean {mean:.3e}")
+        assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
     assert np.all(np.isfinite(out.astype(np.float32)))
 
 

@@ -220,6 +220,37 @@ def test_swapping_dy_dx_changes_result(oracle):
     assert np.array_equal(out, ref)
 
 
+@pytest.mark.parametrize("shape", [
+    DeformConvShape(2, 16, 9, 11, 8, 9, 11, 3, 3, 1, 1, 1, 1, 1, 1, 1, 4),
+    DeformConvShape(1, 12, 7, 8, 6, 4, 4, 3, 2, 1, 0, 2, 2, 1, 2, 3, 2),  # groups 3, stride 2, dilation
+])
+def test_threaded_and_oc_range_forms_equal_forward_bitwise(oracle, shape):
+    """The GPU tests' checkers at the config sizes are forward_f32_threads (output channels
+    spread over threads), forward_f32_oc_range (a slice of output channels) and
+    forward_f32_ocs (listed channels over a thread pool): each must be forward_f32 bit for
+    bit, whatever the thread count or the slicing."""
+    d = rand_inputs(shape, np.random.default_rng(17))
+    args = [d[k] for k in ("input", "offset", "mask", "weight", "bias")]
+    want = oracle.forward_f32(shape, *args).view(np.uint32)
+    for threads in (1, 3, 8):
+        assert np.array_equal(oracle.forward_f32_threads(shape, *args, threads=threads).view(np.uint32), want)
+    plane = shape.output_height * shape.output_width
+    got = np.zeros(shape.batch * shape.output_channels * plane, np.float32)
+    cuts = [0, 1, shape.output_channels // 2, shape.output_channels]
+    for lo, hi in zip(cuts, cuts[1:]):
+        part = oracle.forward_f32_oc_range(shape, *args, lo, hi).reshape(shape.batch, shape.output_channels, plane)
+        outside = np.ones(shape.output_channels, bool)
+        outside[lo:hi] = False
+        assert not part[:, outside].any()  # nothing written outside the slice
+        got.reshape(shape.batch, shape.output_channels, plane)[:, lo:hi] = part[:, lo:hi]
+    assert np.array_equal(got.view(np.uint32), want)
+    picked = [0, shape.output_channels - 1, 2]
+    some = oracle.forward_f32_ocs(shape, *args, picked, threads=3).reshape(shape.batch, shape.output_channels, plane)
+    full = want.view(np.float32).reshape(shape.batch, shape.output_channels, plane)
+    assert np.array_equal(some[:, picked].view(np.uint32), full[:, picked].view(np.uint32))
+    assert not np.delete(some, picked, axis=1).any()
+
+
 def test_f16_direct_is_rounded_f32_oracle(oracle):
     s = SHAPES[1]
     d = rand_inputs(s, np.random.default_rng(5))
@@ -377,6 +408,27 @@ def test_conv3x3_matches_torch(oracle):
     out = oracle.conv3x3_f16(cin, cout, hh, ww, x, w, b, 2, 0.1, res)
     np.testing.assert_allclose(out.astype(np.float64), F.relu(ref).numpy().ravel() + res.astype(np.float64),
                                rtol=0, atol=8e-3)
+
+
+def test_conv3x3_residual_is_added_before_the_one_rounding(oracle):
+    """acc = 1 + 2^-11 (bias 1, one input 1 times weight 2^-11, every other weight 0) lies
+    halfway between two FP16 values; the residual 2^-11 then makes 1 + 2^-10 exactly.
+    One rounding after the add gives 1 + 2^-10; rounding acc first (ties to even: 1.0) and
+    then adding would give half(1 + 2^-11) = 1.0. A second residual is a separate FP16 add."""
+    cin, cout, hh, ww = 2, 1, 3, 3
+    x = np.zeros(cin * hh * ww, np.float16)
+    x[4] = 1.0  # channel 0, centre pixel
+    w = np.zeros(cout * cin * 9, np.float16)
+    w[4] = np.float16(2.0 ** -11)  # ic 0, centre tap: only the centre output sees it
+    b = np.ones(cout, np.float16)
+    res = np.full(cout * hh * ww, np.float16(2.0 ** -11))
+    out = oracle.conv3x3_f16(cin, cout, hh, ww, x, w, b, 0, 0.1, res)
+    assert out[4] == np.float16(1 + 2.0 ** -10)
+    assert np.float16(np.float16(1 + 2.0 ** -11) + res[4]) == np.float16(1.0)  # the other order
+    # Elsewhere acc = 1 exactly: 1 + 2^-11 ties to even, 1.0.
+    assert np.all(np.delete(out, 4) == np.float16(1.0))
+    two = oracle.add_f16(out, res)
+    assert two[4] == np.float16(np.float32(out[4]) + np.float32(res[4]))
 
 
 # ---- property test over random shapes (Hypothesis) ------------------------------------
