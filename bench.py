@@ -38,7 +38,7 @@ MFMA_F16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 
 WORKLOADS = {
-    1: "C1: DCNv2 1x128x64x64 -> 64, 3x3, 16 deformable groups, FP32 (runFloat32: direct kernel, oracle summation order)",
+    1: "C1: DCNv2 1x128x64x64 -> 64, 3x3, 16 deformable groups, FP32 (runFloat32, oracle summation order, bit-exact)",
     2: "C2: DCNv2 1x128x64x64 -> 64, 3x3, 16 deformable groups, FP16 storage, FP32 accumulate, prepacked weights",
     3: "C3: DCNv2 16x128x64x64 -> 64, 3x3, 16 deformable groups, FP16, prepacked weights (batched 8K-eye tiles)",
     5: "C5: DCNv2 1x128x180x320 -> 64, 3x3, 16 deformable groups, FP16, prepacked weights (large map)",
@@ -46,7 +46,7 @@ WORKLOADS = {
 }
 
 
-KERNEL_NAMES = {0: "direct_kernel", 1: "fused_kernel", 2: "staged_kernel", 3: "window_kernel", 4: "window_kernel",
+KERNEL_NAMES = {0: "direct_shared_f32_kernel", 1: "fused_kernel", 2: "staged_kernel", 3: "window_kernel", 4: "window_kernel",
                 5: "narrow_kernel", 6: "window_async_kernel", 7: "tile_kernel"}
 
 
@@ -803,7 +803,7 @@ def main() -> int:
         achieved = flops / (k_us * 1e-6) / 1e12
         roofline = {"bound": "mfma", "achieved": achieved, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": achieved / FP32_PEAK_TFLOPS, "traffic": traffic,
-                    "kernel": kernel_name + " (FP32 direct, one thread per output)",
+                    "kernel": kernel_name + " (FP32, samples shared by 64 output channels, oracle summation order)",
                     "traffic_source": f"profiles/{kernel_name}_{workload_name}.md" if traffic else None,
                     "algorithmic_bytes_per_launch": nbytes,
                     "hbm_frac": nbytes / (k_us * 1e-6) / 1e9 / HBM_PEAK_GBS}

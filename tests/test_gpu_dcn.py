@@ -116,6 +116,30 @@ def test_fp32_general_shapes_bit_exact(gpu_ctx, dcn, oracle, dims):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
+SHARED_F32_SHAPES = [
+    # groups 1, Cin % 8 == 0: the shared-sample FP32 kernel (16 pixels x 64 channels)
+    ((1, 8, 7, 9, 96, 7, 9, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2), 3.0),       # 63 pixels, 2 channel blocks
+    ((2, 16, 10, 6, 16, 5, 3, 2, 3, 0, 1, 2, 2, 1, 1, 1, 4), 3.0),     # 2x3 taps, stride 2
+    ((1, 24, 9, 9, 40, 9, 9, 1, 1, 0, 0, 1, 1, 1, 1, 1, 3), 3.0),      # 1x1, 3 offset groups
+    ((1, 8, 12, 12, 8, 6, 6, 2, 2, 0, 0, 2, 2, 1, 1, 1, 1), 3.0),      # 2x2, stride 2
+    ((1, 32, 8, 8, 64, 8, 8, 1, 2, 0, 0, 1, 1, 2, 2, 1, 8), 3.0),      # 1x2, dilation 2
+    ((1, 16, 16, 16, 64, 16, 16, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2), 20.0),  # samples far outside
+]
+
+
+@pytest.mark.parametrize("dims,scale", SHARED_F32_SHAPES, ids=lambda t: "x".join(map(str, t)) if isinstance(t, tuple) else str(t))
+def test_fp32_shared_sample_kernel_bit_exact(gpu_ctx, dcn, oracle, dims, scale):
+    """The shared-sample FP32 kernel keeps the oracle's per-output summation order: bit
+    for bit over tail pixels, a partial second channel block, every supported tap count,
+    strides, dilation, offset groups and samples far outside the input."""
+    s = dcn.DeformConvShape(*dims)
+    d = rand_case(s, sum(dims), offset_scale=scale)
+    log("case: fp32 shared", dims, scale)
+    out = gpu_ctx.run_float32(s, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    ref = oracle.forward_f32(s, d["input"], d["offset"], d["mask"], d["weight"], d["bias"])
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+
+
 # ---- FP16 direct (reference semantics) ---------------------------------------------
 
 def test_fp16_direct_bit_exact_c2(gpu_ctx, c2):
