@@ -507,22 +507,33 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
         if (!d_prefix[i]) return fail(ctx, DCN_INVALID_ARGUMENT, "prefix pointer is null");
         prefix[i] = (const uint16_t*)d_prefix[i];
     }
-    // Second-order flow, conditions, DCN input and the backbone input's leading
-    // [feat_current, prefix...] in one kernel, straight into the CB8 tensors.
-    DCN_HIP(ctx, dcn::launch_body_temporal((const uint16_t*)d_feat_prop, (const uint16_t*)d_feat_current,
-                                           (const uint16_t*)d_feat_n2, (const uint16_t*)d_flow1,
-                                           (const uint16_t*)d_prev_flow, has_second_order ? 1 : 0,
-                                           prefix, body->branch, (uint16_t*)d_flow2_out, body->cond_cb8,
-                                           body->deform_cb8, body->bb_in, H, W, s, body->tiles));
     const long off_ts = cb8_image(body, 8);
+    const dcn_conv* c0 = body->offset_conv[0];
+    if (body->tiles == 1) {
+        // Second-order flow, the conditions (in LDS only), DCN input, the backbone input's
+        // leading [feat_current, prefix...] and the first conv_offset layer in one launch.
+        DCN_HIP(ctx, dcn::launch_temporal_conv(c0->g, (const uint16_t*)d_feat_prop, (const uint16_t*)d_feat_current,
+                                               (const uint16_t*)d_feat_n2, (const uint16_t*)d_flow1,
+                                               (const uint16_t*)d_prev_flow, has_second_order ? 1 : 0, prefix,
+                                               body->branch, (uint16_t*)d_flow2_out, body->deform_cb8, body->bb_in,
+                                               c0->wpk, c0->bias, 0.1f, body->off_a, s));
+    } else {
+        // Many tiles: the batched conv shares each workgroup's weight fragments over up to
+        // 16 images, which the per-image fused kernel cannot; the temporal preparation
+        // runs as its own kernel into the CB8 conditions.
+        DCN_HIP(ctx, dcn::launch_body_temporal((const uint16_t*)d_feat_prop, (const uint16_t*)d_feat_current,
+                                               (const uint16_t*)d_feat_n2, (const uint16_t*)d_flow1,
+                                               (const uint16_t*)d_prev_flow, has_second_order ? 1 : 0,
+                                               prefix, body->branch, (uint16_t*)d_flow2_out, body->cond_cb8,
+                                               body->deform_cb8, body->bb_in, H, W, s, body->tiles));
+        dcn::ConvBatch cond_conv;
+        cond_conv.images = body->tiles;
+        cond_conv.x = cb8_image(body, 25);
+        cond_conv.out = off_ts;
+        DCN_TRY(run_conv(ctx, c0, body->cond_cb8, 1, nullptr, NCHW, nullptr, NCHW, body->off_a, CB8, s, cond_conv));
+    }
     // conv_offset: 196 -> 64 -> 64 -> 64 (LeakyReLU 0.1) -> 432, the last one turning its
     // output into offsets and masks for the DCN of the same launch.
-    dcn::ConvBatch cond_conv;
-    cond_conv.images = body->tiles;
-    cond_conv.x = cb8_image(body, 25);
-    cond_conv.out = off_ts;
-    DCN_TRY(run_conv(ctx, body->offset_conv[0], body->cond_cb8, 1, nullptr, NCHW, nullptr, NCHW,
-                     body->off_a, CB8, s, cond_conv));
     const dcn_conv* c1 = body->offset_conv[1];
     const dcn_conv* c2 = body->offset_conv[2];
     dcn::ConvBatch off_pair;

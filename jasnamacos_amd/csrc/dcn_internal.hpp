@@ -186,6 +186,14 @@ struct ConvBatch {
     int images = 1;
     long x = 0, res1 = 0, res2 = 0, out = 0;
 };
+// The temporal preparation and the first conv_offset layer (196 -> 64, LeakyReLU) in one
+// launch (one image): writes flow2, the DCN input and the backbone input's leading blocks
+// as launch_body_temporal does, and the conv's output in CB8, without the conditions.
+hipError_t launch_temporal_conv(const ConvGeometry& g, const uint16_t* feat_prop, const uint16_t* feat_current,
+                                const uint16_t* feat_n2, const uint16_t* flow1, const uint16_t* prev_flow,
+                                int has_second_order, const uint16_t* const* prefix, int nprefix,
+                                uint16_t* flow2, uint16_t* deform_cb8, uint16_t* bb_cb8, const void* wpk,
+                                const float* bias, float slope, uint16_t* out_cb8, hipStream_t stream);
 hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                           const float* bias, int act, float slope, const uint16_t* res1,
                           int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,

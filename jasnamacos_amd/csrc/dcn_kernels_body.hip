@@ -12,6 +12,7 @@
 
 #include "dcn_device.hpp"
 #include "dcn_internal.hpp"
+#include "dcn_warp.hpp"
 
 #pragma clang fp contract(off)
 
@@ -19,9 +20,7 @@ namespace dcn {
 namespace {
 
 using namespace dev;
-
-__device__ __forceinline__ float h2f(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
-__device__ __forceinline__ uint16_t f2h(float v) { return __builtin_bit_cast(uint16_t, round_f16(v)); }
+using namespace warp;
 
 // Index of (channel c, pixel y, x) in a tensor of the given layout.
 __device__ __forceinline__ size_t tensor_index(int layout, int c, int y, int x, int H, int W) {
@@ -30,27 +29,6 @@ __device__ __forceinline__ size_t tensor_index(int layout, int c, int y, int x, 
         return ((size_t)((c >> 3) * Hp + y + kPad) * Wp + x + kPad) * 8 + (c & 7);
     }
     return ((size_t)c * H + y) * W + x;
-}
-
-// sample_fp16 (MetalShader.swift:51-74): zero-padded bilinear sample of one FP16 plane,
-// the reference's association.
-__device__ __forceinline__ float sample_zero(const uint16_t* plane, int H, int W, float y, float x) {
-    const float fy = floorf(y), fx = floorf(x);
-    const int y0 = (int)fminf(fmaxf(fy, -4.0f), (float)H + 4.0f);
-    const int x0 = (int)fminf(fmaxf(fx, -4.0f), (float)W + 4.0f);
-    const int y1 = y0 + 1, x1 = x0 + 1;
-    const float ly = y - fy, lx = x - fx;
-    // Every corner is loaded from an index clamped into the plane and zeroed afterwards
-    // when it lies outside: unconditional loads, all in flight together.
-    const int yc0 = min(max(y0, 0), H - 1), yc1 = min(max(y1, 0), H - 1);
-    const int xc0 = min(max(x0, 0), W - 1), xc1 = min(max(x1, 0), W - 1);
-    const float t00 = h2f(plane[(size_t)yc0 * W + xc0]), t01 = h2f(plane[(size_t)yc0 * W + xc1]);
-    const float t10 = h2f(plane[(size_t)yc1 * W + xc0]), t11 = h2f(plane[(size_t)yc1 * W + xc1]);
-    const bool r0 = y0 >= 0 && y0 < H, r1 = y1 >= 0 && y1 < H;
-    const bool c0 = x0 >= 0 && x0 < W, c1 = x1 >= 0 && x1 < W;
-    const float v00 = (r0 && c0) ? t00 : 0.0f, v01 = (r0 && c1) ? t01 : 0.0f;
-    const float v10 = (r1 && c0) ? t10 : 0.0f, v11 = (r1 && c1) ? t11 : 0.0f;
-    return v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx + v10 * ly * (1.0f - lx) + v11 * ly * lx;
 }
 
 // accumulate_second_order_flow_fp16 (MetalShader.swift:738-763):
@@ -189,43 +167,6 @@ __global__ __launch_bounds__(256) void cb8_to_nchw_kernel(const uint16_t* __rest
     out[gid] = cb8[tensor_index(kLayoutCB8, channel, y, x, H, W)];
 }
 
-// Bilinear sample of eight consecutive planes at one coordinate: sample_zero's arithmetic
-// per plane (same association), the corner set computed once.
-__device__ __forceinline__ void sample8_zero(const uint16_t* planes, size_t plane, int H, int W,
-                                             float y, float x, float (&v)[8]) {
-    const float fy = floorf(y), fx = floorf(x);
-    const int y0 = (int)fminf(fmaxf(fy, -4.0f), (float)H + 4.0f);
-    const int x0 = (int)fminf(fmaxf(fx, -4.0f), (float)W + 4.0f);
-    const int y1 = y0 + 1, x1 = x0 + 1;
-    const float ly = y - fy, lx = x - fx;
-    const bool r0 = y0 >= 0 && y0 < H, r1 = y1 >= 0 && y1 < H;
-    const bool c0 = x0 >= 0 && x0 < W, c1 = x1 >= 0 && x1 < W;
-    // Unconditional loads from clamped indices (32 in flight), out-of-plane corners
-    // zeroed afterwards: the same values as loading only the valid corners.
-    const size_t i00 = (size_t)min(max(y0, 0), H - 1) * W + min(max(x0, 0), W - 1);
-    const size_t i01 = (size_t)min(max(y0, 0), H - 1) * W + min(max(x1, 0), W - 1);
-    const size_t i10 = (size_t)min(max(y1, 0), H - 1) * W + min(max(x0, 0), W - 1);
-    const size_t i11 = (size_t)min(max(y1, 0), H - 1) * W + min(max(x1, 0), W - 1);
-    uint16_t t[8][4];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const uint16_t* p = planes + (size_t)c * plane;
-        t[c][0] = p[i00];
-        t[c][1] = p[i01];
-        t[c][2] = p[i10];
-        t[c][3] = p[i11];
-    }
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-        const float v00 = (r0 && c0) ? h2f(t[c][0]) : 0.0f;
-        const float v01 = (r0 && c1) ? h2f(t[c][1]) : 0.0f;
-        const float v10 = (r1 && c0) ? h2f(t[c][2]) : 0.0f;
-        const float v11 = (r1 && c1) ? h2f(t[c][3]) : 0.0f;
-        v[c] = v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx + v10 * ly * (1.0f - lx) +
-               v11 * ly * lx;
-    }
-}
-
 struct BodyTemporalArgs {
     const uint16_t *feat_prop, *feat_current, *feat_n2, *flow1, *prev_flow;
     const uint16_t* prefix[3];
@@ -284,62 +225,30 @@ __global__ __launch_bounds__(256) void body_temporal_kernel(BodyTemporalArgs a0)
     const int y = p / a.W;
     const int x = p - y * a.W;
     const size_t pl = (size_t)plane;
-    const float fx1 = h2f(a.flow1[p]);
-    const float fy1 = h2f(a.flow1[pl + p]);
-    float f2[2] = {0.0f, 0.0f};
-    uint16_t f2h16[2] = {0, 0};
-    if (kind >= 16 && kind < 25 && a.has_second_order) {
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const float prev = sample_zero(a.prev_flow + (size_t)c * pl, a.H, a.W, (float)y + fy1, (float)x + fx1);
-            f2h16[c] = f2h(h2f(a.flow1[(size_t)c * pl + p]) + prev);
-            f2[c] = h2f(f2h16[c]);
-        }
-    }
-    float v[8];
-    const uint16_t* copy_src = nullptr;  // eight planes copied as they are
     uint16_t* dst;
     int dblock;
+    u32x4 out;
     if (kind < 25) {
         dst = a.cond;
         dblock = kind;
-        if (kind < 8) {
-            sample8_zero(a.feat_prop + (size_t)kind * 8 * pl, pl, a.H, a.W, (float)y + fy1, (float)x + fx1, v);
-        } else if (kind < 16) {
-            copy_src = a.feat_current + (size_t)(kind - 8) * 8 * pl;
-        } else if (kind < 24) {
-            sample8_zero(a.feat_n2 + (size_t)(kind - 16) * 8 * pl, pl, a.H, a.W, (float)y + f2[1],
-                         (float)x + f2[0], v);
-        } else {
-            a.flow2[p] = f2h16[0];
-            a.flow2[pl + p] = f2h16[1];
+        uint16_t f2[2];
+        out = condition_block<u32x4>(a.feat_prop, a.feat_current, a.feat_n2, a.flow1, a.prev_flow,
+                                     a.has_second_order, a.H, a.W, kind, y, x, f2);
+        if (kind == 24) {
+            a.flow2[p] = f2[0];
+            a.flow2[pl + p] = f2[1];
         }
     } else if (kind < 41) {
         dst = a.deform;
         dblock = kind - 25;
-        copy_src = dblock < 8 ? a.feat_prop + (size_t)dblock * 8 * pl : a.feat_n2 + (size_t)(dblock - 8) * 8 * pl;
+        out = copy8<u32x4>(dblock < 8 ? a.feat_prop + (size_t)dblock * 8 * pl : a.feat_n2 + (size_t)(dblock - 8) * 8 * pl,
+                           pl, p);
     } else {
         dst = a.bb;
         dblock = kind - 41;
         const int src = dblock >> 3;
         const uint16_t* base = src == 0 ? a.feat_current : (src == 1 ? a.p0 : (src == 2 ? a.p1 : a.p2));
-        copy_src = base + (size_t)(dblock & 7) * 8 * pl;
-    }
-    u32x4 out;
-    if (copy_src) {
-        uint16_t h[8];
-#pragma unroll
-        for (int c = 0; c < 8; ++c) h[c] = copy_src[(size_t)c * pl + p];
-#pragma unroll
-        for (int d = 0; d < 4; ++d) out[d] = (uint32_t)h[2 * d] | ((uint32_t)h[2 * d + 1] << 16);
-    } else if (kind == 24) {
-        out[0] = (uint32_t)a.flow1[p] | ((uint32_t)a.flow1[pl + p] << 16);
-        out[1] = (uint32_t)f2h16[0] | ((uint32_t)f2h16[1] << 16);
-        out[2] = 0u;
-        out[3] = 0u;
-    } else {
-#pragma unroll
-        for (int d = 0; d < 4; ++d) out[d] = (uint32_t)f2h(v[2 * d]) | ((uint32_t)f2h(v[2 * d + 1]) << 16);
+        out = copy8<u32x4>(base + (size_t)(dblock & 7) * 8 * pl, pl, p);
     }
     const int Hp = a.H + 2 * kPad, Wp = a.W + 2 * kPad;
     reinterpret_cast<u32x4*>(dst)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = out;

@@ -20,6 +20,7 @@
 #include <algorithm>
 
 #include "dcn_device.hpp"
+#include "dcn_warp.hpp"
 #include "dcn_internal.hpp"
 
 #pragma clang fp contract(off)
@@ -754,6 +755,192 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
     }
 }
 
+// The temporal preparation and the first conv_offset layer (196 -> 64, LeakyReLU) in one
+// launch, for one image per workgroup. A workgroup owns a 2 x 8 output tile: it computes
+// the 25 condition blocks [warp(feat_prop, flow1), feat_current, warp(feat_n2, flow2),
+// flow1, flow2] on the tile's 4 x 10 halo straight into LDS (zero outside the image: the
+// conv's padding), writes the pointwise outputs of its own 16 pixels (flow2, the DCN
+// input [feat_prop, feat_n2] and the backbone input's [feat_current, prefix...] in CB8),
+// then runs the conv with A fragments from LDS. The conditions are condition_block's bits
+// (the separate body_temporal_kernel's), and the conv keeps conv3x3_kernel<8, 4>'s K split
+// (wave w owns K-steps [w * 57 / 8, (w + 1) * 57 / 8), K-block 4 s + lane / 16 = tap * 25
+// + block) and its wave-ordered sum, so the output is the two-launch result bit for bit.
+// The halo is 2.5 times the tile, so each workgroup samples 2.5 times the pixels it
+// outputs; in exchange the 200-channel condition tensor never reaches HBM and the step
+// loses a launch.
+constexpr int kTcTH = 2, kTcTW = 8;
+constexpr int kTcHW = kTcTW + 2;
+constexpr int kTcHalo = (kTcTH + 2) * kTcHW;
+constexpr int kTcBlocks = 25;  // 196 condition channels + 4 zero ones
+
+struct TemporalConvArgs {
+    const uint16_t *feat_prop, *feat_current, *feat_n2, *flow1, *prev_flow, *p0, *p1, *p2;
+    uint16_t *flow2, *deform, *bb, *out;
+    const void* wpk;     // conv_offset 1 B fragments [57][4][64][8]
+    const float* bias;   // [64]
+    uint32_t wpk_bytes, magic_cb;
+    int nprefix, has_second_order, H, W, tiles_x, tiles, KB, ksteps;
+    float slope;
+};
+
+template <int NW, int KMAX>
+__global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs a) {
+    constexpr int NB = kConvNbc;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    float* red = reinterpret_cast<float*>(lds);  // [NW][NB][4][65]
+    u32x4* cond = reinterpret_cast<u32x4*>(lds + (size_t)NW * NB * 4 * 65 * sizeof(float));  // [25][halo]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int quarter = lane >> 4;
+
+    const int per_xcd = (a.tiles + 7) / 8;
+    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+    const int ty = tile / a.tiles_x;
+    const int oy0 = ty * kTcTH;
+    const int ox0 = (tile - ty * a.tiles_x) * kTcTW;
+    const int H = a.H, W = a.W;
+    const size_t pl = (size_t)H * W;
+    const int Hp = H + 2 * kPad, Wp = W + 2 * kPad;
+
+    // This wave's weight fragments, requested first: they arrive during the sampling.
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+    const int s0 = wave * a.ksteps / NW;
+    const int s1 = (wave + 1) * a.ksteps / NW;
+    h8 Bf[KMAX][NB];
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i)
+        if (s0 + i < s1)  // uniform across the wave
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
+
+    // Flows of the halo pixels first (flow1, and flow2 from one warp of prev_flow), so that
+    // every condition below is one round of corner loads.
+    uint16_t* hflow = reinterpret_cast<uint16_t*>(cond + kTcBlocks * kTcHalo);  // [halo][f1x, f1y, f2x, f2y]
+    auto halo_xy = [&](int hp, int& y, int& x) {
+        const int hy = hp / kTcHW;
+        y = oy0 - 1 + hy;
+        x = ox0 - 1 + hp - hy * kTcHW;
+    };
+    if (tid < kTcHalo) {
+        int y, x;
+        halo_xy(tid, y, x);
+        uint16_t f1[2] = {0, 0}, f2[2] = {0, 0};
+        if (y >= 0 && y < H && x >= 0 && x < W) {
+            const int p = y * W + x;
+            f1[0] = a.flow1[p];
+            f1[1] = a.flow1[pl + p];
+            warp::temporal_flow2(a.flow1, a.prev_flow, a.has_second_order, H, W, y, x, f2);
+        }
+        hflow[tid * 4 + 0] = f1[0];
+        hflow[tid * 4 + 1] = f1[1];
+        hflow[tid * 4 + 2] = f2[0];
+        hflow[tid * 4 + 3] = f2[1];
+    }
+    __syncthreads();
+
+    // Conditions of the halo, block-major: item (block, halo pixel); then the pointwise
+    // outputs of the tile's pixels: item (kind, pixel), kind 0 flow2, 1-16 the DCN input
+    // blocks, then the backbone input's leading blocks. One loop, so that the loads of
+    // both kinds of item are in flight together.
+    constexpr int kCondItems = kTcBlocks * kTcHalo;
+    const int items = kCondItems + (17 + 8 * (1 + a.nprefix)) * kTcTH * kTcTW;
+    for (int it = tid; it < items; it += 64 * NW) {
+        if (it < kCondItems) {
+            const int blk = it / kTcHalo;
+            const int hp = it - blk * kTcHalo;
+            int y, x;
+            halo_xy(hp, y, x);
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (y >= 0 && y < H && x >= 0 && x < W) {
+                const uint16_t f1[2] = {hflow[hp * 4 + 0], hflow[hp * 4 + 1]};
+                const uint16_t f2[2] = {hflow[hp * 4 + 2], hflow[hp * 4 + 3]};
+                v = warp::condition_from_flows<u32x4>(a.feat_prop, a.feat_current, a.feat_n2, H, W, blk, y, x, f1, f2);
+            }
+            cond[blk * kTcHalo + hp] = v;
+            continue;
+        }
+        const int pt = it - kCondItems;
+        const int kind = pt >> 4;
+        const int op = pt & 15;
+        const int y = oy0 + (op >> 3);
+        const int x = ox0 + (op & 7);
+        if (y >= H || x >= W) continue;
+        const int p = y * W + x;
+        if (kind == 0) {
+            const int hp = ((op >> 3) + 1) * kTcHW + (op & 7) + 1;  // the pixel's halo slot
+            a.flow2[p] = hflow[hp * 4 + 2];
+            a.flow2[pl + p] = hflow[hp * 4 + 3];
+            continue;
+        }
+        uint16_t* dst;
+        int dblock;
+        const uint16_t* src;
+        if (kind <= 16) {
+            dst = a.deform;
+            dblock = kind - 1;
+            src = dblock < 8 ? a.feat_prop + (size_t)dblock * 8 * pl : a.feat_n2 + (size_t)(dblock - 8) * 8 * pl;
+        } else {
+            dst = a.bb;
+            dblock = kind - 17;
+            const int which = dblock >> 3;
+            const uint16_t* base = which == 0 ? a.feat_current : (which == 1 ? a.p0 : (which == 2 ? a.p1 : a.p2));
+            src = base + (size_t)(dblock & 7) * 8 * pl;
+        }
+        reinterpret_cast<u32x4*>(dst)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = warp::copy8<u32x4>(src, pl, p);
+    }
+    __syncthreads();
+
+    // The conv: lane l supplies tile pixel l % 16 (row (l % 16) / 8, column l % 8).
+    f32x4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{};
+    const int r = lane & 15;
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+        if (s0 + i < s1) {  // uniform across the wave
+            const int kb = 4 * (s0 + i) + quarter;
+            const int kbc = kb < a.KB ? kb : a.KB - 1;
+            const int tap = fast_div(kbc, a.magic_cb);
+            const int blk = kbc - tap * kTcBlocks;
+            const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
+            const int kx = tap - ky * 3;
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            const u32x4 q = cond[blk * kTcHalo + ((r >> 3) + ky) * kTcHW + (r & 7) + kx];
+            // Padding K-blocks multiply zero weights; zero A keeps a non-finite condition
+            // from turning 0 * inf into NaN there (as conv3x3_kernel).
+            const h8 A = __builtin_bit_cast(h8, kb < a.KB ? q : z);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+    __syncthreads();
+
+    for (int idx = tid; idx < 16 * kConvChunk; idx += 64 * NW) {
+        const int px = idx & 15;
+        const int ocl = idx >> 4;
+        const int nb = ocl >> 4;
+        const int src = ((px >> 2) << 4) + (ocl & 15);
+        const int v = px & 3;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
+        const int yy = oy0 + (px >> 3);
+        const int xx = ox0 + (px & 7);
+        if (yy >= H || xx >= W) continue;
+        float val = sum + a.bias[ocl];
+        if (val < 0.0f) val = val * a.slope;  // LeakyReLU
+        a.out[conv_index(kLayoutCB8, ocl, yy, xx, H, W, Hp, Wp)] = __builtin_bit_cast(uint16_t, round_f16(val));
+    }
+}
+
 }  // namespace
 
 ConvGeometry conv_geometry(int cin, int cout, int height, int width) {
@@ -874,6 +1061,51 @@ hipError_t launch_conv3x3_offsets(const ConvGeometry& g, const void* x_cb8, cons
     const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)((g.cout + 16 * NB - 1) / (16 * NB)),
                     (unsigned)images);
     hipLaunchKernelGGL(kernel, grid, dim3(64 * NW), lds, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_temporal_conv(const ConvGeometry& g, const uint16_t* feat_prop, const uint16_t* feat_current,
+                                const uint16_t* feat_n2, const uint16_t* flow1, const uint16_t* prev_flow,
+                                int has_second_order, const uint16_t* const* prefix, int nprefix,
+                                uint16_t* flow2, uint16_t* deform_cb8, uint16_t* bb_cb8, const void* wpk,
+                                const float* bias, float slope, uint16_t* out_cb8, hipStream_t stream) {
+    constexpr int NW = 8, KMAX = 8;
+    if (g.cin != 196 || g.cout != 64 || g.ksteps > NW * KMAX || nprefix < 0 || nprefix > 3)
+        return hipErrorInvalidValue;
+    TemporalConvArgs a{};
+    a.feat_prop = feat_prop;
+    a.feat_current = feat_current;
+    a.feat_n2 = feat_n2;
+    a.flow1 = flow1;
+    a.prev_flow = prev_flow;
+    const uint16_t* pre[3];
+    for (int i = 0; i < 3; ++i) pre[i] = i < nprefix ? prefix[i] : feat_current;
+    a.p0 = pre[0];
+    a.p1 = pre[1];
+    a.p2 = pre[2];
+    a.flow2 = flow2;
+    a.deform = deform_cb8;
+    a.bb = bb_cb8;
+    a.out = out_cb8;
+    a.wpk = wpk;
+    a.bias = bias;
+    a.wpk_bytes = (uint32_t)conv_packed_bytes(g);
+    a.magic_cb = magic_for(g.cb);
+    a.nprefix = nprefix;
+    a.has_second_order = has_second_order;
+    a.H = g.h;
+    a.W = g.w;
+    a.tiles_x = (g.w + kTcTW - 1) / kTcTW;
+    a.tiles = (g.h + kTcTH - 1) / kTcTH * a.tiles_x;
+    a.KB = g.kb;
+    a.ksteps = g.ksteps;
+    a.slope = slope;
+    const size_t lds = (size_t)NW * kConvNbc * 4 * 65 * sizeof(float) + (size_t)kTcBlocks * kTcHalo * 16 +
+                       (size_t)kTcHalo * 4 * sizeof(uint16_t);
+    auto kernel = &temporal_conv_kernel<NW, KMAX>;
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((a.tiles + 7) / 8 * 8)), dim3(64 * NW), lds, stream, a);
     return hipGetLastError();
 }
 
