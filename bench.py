@@ -170,6 +170,18 @@ def cpu_baseline(config: int, s, inputs: dict, gpu_out, budget_s: float = 25.0) 
     return baseline, check
 
 
+def calibration_copies(mib: int) -> None:
+    """Three device copies of `mib` MiB: the known-size kernel that scales rocprofv3's
+    FETCH_SIZE / WRITE_SIZE readings to bytes."""
+    import torch
+
+    src = torch.ones(mib << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def bench_body(args) -> int:
     """Config C4: one BasicVSR++ propagation body per frame, each frame one hipGraph launch.
 
@@ -219,8 +231,12 @@ def bench_body(args) -> int:
     for g in graphs:
         g.free()
     body.free()
-    clip_line = bench_clip(args, ctx, dc, clip, dev)
-    tiles_line = bench_body_tiles(args, ctx, dc, clip, dev)
+    clip_line = tiles_line = None
+    if not args.frames_only:
+        clip_line = bench_clip(args, ctx, dc, clip, dev)
+        tiles_line = bench_body_tiles(args, ctx, dc, clip, dev)
+    if args.calibration_copy_mib > 0:
+        calibration_copies(args.calibration_copy_mib)
     cpu = None if args.no_cpu_baseline else cpu_baseline_body(clip)
     line = {
         "metric": "BasicVSR++ propagation body us/frame (C4: offset convs + DCNv2 + 5-block backbone, hipGraph per frame)",
@@ -647,6 +663,8 @@ def main() -> int:
                     help="pin the fused variant (0 = the library's automatic choice)")
     ap.add_argument("--mt", type=int, default=0, help="pin the fused config's mt (0 = automatic)")
     ap.add_argument("--ks", type=int, default=0, help="pin the fused config's ks (0 = automatic)")
+    ap.add_argument("--frames-only", action="store_true",
+                    help="config 4: time the per-frame graphs only (no clip, no 16-tile step)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run three device copies of this many MiB (the known-size "
                          "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -780,12 +798,7 @@ def main() -> int:
         del scratch
 
     if args.calibration_copy_mib > 0:
-        src = torch.ones(args.calibration_copy_mib << 20, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        calibration_copies(args.calibration_copy_mib)
 
     # What was timed: the output of the last timed call (checked against the oracle in the
     # cpu_baseline leg below).
