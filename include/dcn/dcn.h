@@ -4,8 +4,8 @@
  * This header is the drop-in boundary for the deformable-convolution operator of
  * ken8303/jasnaMacOS. The reference's surface is Swift-internal; each declaration
  * below names the reference item (file:line under Sources/JasnaMetalPoC/ unless
- * stated) that it replaces. A SwiftPM C module target can wrap this header as is
- * (module.modulemap: `module CDCN { header "dcn.h" link "dcn" export * }`).
+ * stated) that it replaces. A SwiftPM C module target wraps this header as is
+ * (jasnamacos_amd/swift: module CDCN, link "dcn").
  *
  * Conventions
  *  - Plain pointers and element counts. Host-pointer entry points validate every
@@ -239,10 +239,11 @@ dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_sha
  * 5 = narrow 16-pixel tiles on 16x16x32 MFMA, one workgroup per CU on small maps
  * (mt = 1, ks = waves splitting K: 8 or 12), 6 = variant 3 on 8 x 32 tiles whose next
  * stage's windows and weights stream into LDS by DMA during the current stage (mt = ks
- * = 8; an even offset-group count), 7 = tile windows: 8 waves on a 16 x 16 (mt = 16) or
- * 8 x 32 (mt = 32) pixel tile, K ordered tap-major over two offset groups per stage, the
- * next stage's windows copied by LDS DMA during the current stage (ks = 8; 3x3 kernels,
- * 8 channels per group, an even group count, fast sampler). sampler: 0 = reference arithmetic
+ * = 8; an even offset-group count), 7 = tile windows: 4 waves on a 128-pixel tile, 8 x 16
+ * (mt = 16) or 4 x 32 (mt = 32), two offset groups per stage split by tap across the
+ * waves, each stage's offsets, masks and sample windows copied into LDS by DMA, global
+ * gathers for a stage whose windows do not fit (ks = 8; 3x3 kernels, 8 channels per group,
+ * an even group count, Cout 32 or 64, fast sampler). sampler: 0 = reference arithmetic
  * (FP32 bilinear in the reference's association, half(sampled*mask): the im2col
  * values of deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into
  * the bilinear weights, packed-FP16 blend). mt = 32-pixel row blocks per tile (1, 2),

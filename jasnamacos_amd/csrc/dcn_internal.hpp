@@ -88,10 +88,12 @@ enum FusedVariant : int {
     // windows and B fragments streamed into a double buffer by LDS DMA while the current
     // stage is multiplied. Needs an even group count.
     kVariantWindowAsync = 6,
-    // Tile windows (dcn_kernels_tile.hip): 8 waves on a 16 x 16 (mt 16) or 8 x 32 (mt 32)
-    // pixel tile, per-stage windows of two offset groups copied by LDS DMA into a double
-    // buffer while the previous stage is multiplied. 3x3 kernels, 8 channels per group, an
-    // even group count, Cout 32 or 64; fast sampler only. Config: mt = tile width, ks = 8.
+    // Tile windows (dcn_kernels_tile.hip): 4 waves on a 128-pixel tile, 8 x 16 (mt 16) or
+    // 4 x 32 (mt 32); two offset groups per stage, waves 0-1 taking taps 0-4 and waves 2-3
+    // taps 5-8 of both. Each stage's offsets and masks and the two groups' sample windows
+    // are copied into LDS by DMA (one 64 KB window buffer, two workgroups per CU); a stage
+    // whose windows do not fit gathers from global memory. 3x3 kernels, 8 channels per
+    // group, an even group count, Cout 32 or 64; fast sampler only. mt = tile width, ks = 8.
     kVariantTile = 7,
 };
 
