@@ -532,6 +532,27 @@ dcn_status dcn_body_initial_step_dev(dcn_body* body, const void* d_feat_current,
                                      const void* const* d_prefix, void* d_feat_prop_out,
                                      void* stream);
 
+/* The same step and first step with the warped features in CB8, for a recurrence that
+ * keeps its propagated features in both layouts (the clip does): feat_prop and feat_n2
+ * are 64-channel CB8 tensors ([8][H+4][W+4][8], zero border) and feat_prop_out_cb8
+ * receives a CB8 copy of the output beside the NCHW feat_prop_out. The warps then gather
+ * 8 channels per 16-byte load. Same bits as the NCHW entry points; single-tile bodies
+ * only (DCN_INVALID_SHAPE otherwise). No counterpart in the reference (its Metal buffers
+ * have one layout). */
+dcn_status dcn_body_step_cb8_dev(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                                 const void* d_prev_flow, const void* d_feat_prop_cb8,
+                                 const void* d_feat_n2_cb8, const void* const* d_prefix,
+                                 int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                                 void* d_feat_prop_out_cb8, void* stream);
+dcn_status dcn_body_initial_step_cb8_dev(dcn_body* body, const void* d_feat_current,
+                                         const void* const* d_prefix, void* d_feat_prop_out,
+                                         void* d_feat_prop_out_cb8, void* stream);
+dcn_status dcn_body_capture_cb8(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                                const void* d_prev_flow, const void* d_feat_prop_cb8,
+                                const void* d_feat_n2_cb8, const void* const* d_prefix,
+                                int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                                void* d_feat_prop_out_cb8, dcn_graph** out);
+
 /* ---- temporal schedule and the four-branch clip ------------------------------------
  * TemporalSchedule (TemporalSchedule.swift:27-68): branches backward_1, forward_1,
  * backward_2, forward_2 (branch index 0..3, backbone inputs (2 + index) * 64 channels)

@@ -185,6 +185,11 @@ SIGNATURES: dict[str, tuple] = {
     "dcn_graph_launch": (C.c_int, [c_void, c_void]),
     "dcn_graph_destroy": (None, [c_void]),
     "dcn_body_initial_step_dev": (C.c_int, [c_void, c_void, C.POINTER(c_void), c_void, c_void]),
+    "dcn_body_step_cb8_dev": (C.c_int, [c_void, c_void, c_void, c_void, c_void, c_void, C.POINTER(c_void),
+                                        C.c_int, c_void, c_void, c_void, c_void]),
+    "dcn_body_initial_step_cb8_dev": (C.c_int, [c_void, c_void, C.POINTER(c_void), c_void, c_void, c_void]),
+    "dcn_body_capture_cb8": (C.c_int, [c_void, c_void, c_void, c_void, c_void, c_void, C.POINTER(c_void),
+                                       C.c_int, c_void, c_void, c_void, C.POINTER(c_void)]),
     # temporal schedule and the four-branch clip
     "dcn_temporal_schedule": (C.c_int, [C.c_int, C.POINTER(DcnScheduleStep), c_size, C.POINTER(c_size)]),
     "dcn_schedule_persistent_bytes": (c_size, [C.c_int]),

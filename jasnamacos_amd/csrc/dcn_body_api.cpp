@@ -32,6 +32,12 @@ struct dcn_clip {
     uint16_t* zero_feat = nullptr;  // 64 x plane zeros: the feat_n2 of positions 0 and 1
     uint16_t* flow2 = nullptr;      // 2 x plane second-order flow scratch
     uint16_t* triplet_prop = nullptr;  // [4][3][64] x plane: the zero-motion triplet rung's output
+    // Single-tile clips: a CB8 copy of every propagated feature ([4][T] tensors of 8
+    // blocks), written by each step's last conv pair and warped by the next steps, a CB8
+    // zero feature, and the triplet rung's mirrors ([4][3]).
+    uint16_t* mirror = nullptr;
+    uint16_t* zero_cb8 = nullptr;
+    uint16_t* triplet_mirror = nullptr;
     std::vector<void*> buffers;
     hipStream_t capture_stream = nullptr;
 };
@@ -449,7 +455,7 @@ namespace {
 // with LeakyReLU 0.1, then residual blocks t = ReLU(conv(x)); x = x + conv(t). The last
 // one also adds the aligned feature: feat_prop = aligned + backbone
 // (add_propagation_residual_fp16).
-dcn_status run_backbone(dcn_body* body, void* d_feat_prop_out, hipStream_t s) {
+dcn_status run_backbone(dcn_body* body, void* d_feat_prop_out, hipStream_t s, void* d_out_cb8 = nullptr) {
     dcn_context* ctx = body->ctx;
     const int NCHW = DCN_TENSOR_NCHW, CB8 = DCN_TENSOR_CB8;
     const int aligned_c = 64 * (body->branch + 1);
@@ -474,30 +480,36 @@ dcn_status run_backbone(dcn_body* body, void* d_feat_prop_out, hipStream_t s) {
         pb.res1 = feat_ts;
         pb.res2 = last ? bb_ts : 0;
         pb.out = last ? out_ts : feat_ts;
+        pb.out2 = feat_ts;
         DCN_HIP(ctx, dcn::launch_conv3x3_pair(c1->g, c2->g, body->feat[x], c1->wpk, c1->bias, 2, c2->wpk,
                                               c2->bias, 0, 0.1f, body->feat[x], CB8,
                                               last ? body->bb_in : nullptr, CB8,
                                               last ? (uint16_t*)d_feat_prop_out : body->feat[y],
-                                              last ? NCHW : CB8, s, aligned_c, pb));
+                                              last ? NCHW : CB8, s, aligned_c, pb,
+                                              last ? (uint16_t*)d_out_cb8 : nullptr));
         x = y;
     }
     return DCN_OK;
 }
 
-}  // namespace
+// One step. With m.warp (single-tile bodies only) feat_prop and feat_n2 are CB8 tensors
+// (warped with 16-byte gathers) and m.out receives a CB8 copy of the output.
+struct Cb8Step {
+    bool warp = false;
+    void* out = nullptr;
+};
 
-extern "C" {
-
-dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const void* d_flow1,
-                             const void* d_prev_flow, const void* d_feat_prop,
-                             const void* d_feat_n2, const void* const* d_prefix,
-                             int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
-                             void* stream) {
+dcn_status body_step(dcn_body* body, const void* d_feat_current, const void* d_flow1, const void* d_prev_flow,
+                     const void* d_feat_prop, const void* d_feat_n2, const void* const* d_prefix,
+                     int has_second_order, void* d_flow2_out, void* d_feat_prop_out, const Cb8Step& m,
+                     void* stream) {
     if (!body) return DCN_INVALID_ARGUMENT;
     dcn_context* ctx = body->ctx;
     if (!d_feat_current || !d_flow1 || !d_prev_flow || !d_feat_prop || !d_feat_n2 || !d_flow2_out ||
-        !d_feat_prop_out || (body->branch > 0 && !d_prefix))
+        !d_feat_prop_out || (body->branch > 0 && !d_prefix) || (m.warp && !m.out))
         return fail(ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    if (m.warp && body->tiles != 1)
+        return fail(ctx, DCN_INVALID_SHAPE, "CB8 feature steps take single-tile bodies");
     DeviceGuard guard(ctx->device);
     const hipStream_t s = (hipStream_t)stream;
     const int H = body->h, W = body->w;
@@ -516,7 +528,7 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
                                                (const uint16_t*)d_feat_n2, (const uint16_t*)d_flow1,
                                                (const uint16_t*)d_prev_flow, has_second_order ? 1 : 0, prefix,
                                                body->branch, (uint16_t*)d_flow2_out, body->deform_cb8, body->bb_in,
-                                               c0->wpk, c0->bias, 0.1f, body->off_a, s));
+                                               c0->wpk, c0->bias, 0.1f, body->off_a, s, m.warp));
     } else {
         // Many tiles: the batched conv shares each workgroup's weight fragments over up to
         // 16 images, which the per-image fused kernel cannot; the temporal preparation
@@ -551,12 +563,11 @@ dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const v
                                          dcn::narrow_packed_bytes(body->dcn->geometry), body->dcn->bias,
                                          body->bb_in, 64 * (body->branch + 1), 8 * (body->branch + 2),
                                          body->tiles, s));
-    return run_backbone(body, d_feat_prop_out, s);
+    return run_backbone(body, d_feat_prop_out, s, m.out);
 }
 
-dcn_status dcn_body_initial_step_dev(dcn_body* body, const void* d_feat_current,
-                                     const void* const* d_prefix, void* d_feat_prop_out,
-                                     void* stream) {
+dcn_status body_initial(dcn_body* body, const void* d_feat_current, const void* const* d_prefix,
+                        void* d_feat_prop_out, void* d_out_cb8, void* stream) {
     if (!body) return DCN_INVALID_ARGUMENT;
     dcn_context* ctx = body->ctx;
     if (!d_feat_current || !d_feat_prop_out || (body->branch > 0 && !d_prefix))
@@ -570,23 +581,62 @@ dcn_status dcn_body_initial_step_dev(dcn_body* body, const void* d_feat_current,
     }
     DCN_HIP(ctx, dcn::launch_body_initial((const uint16_t*)d_feat_current, prefix, body->branch, body->bb_in,
                                           body->h, body->w, s, body->tiles));
-    return run_backbone(body, d_feat_prop_out, s);
+    return run_backbone(body, d_feat_prop_out, s, d_out_cb8);
 }
 
-dcn_status dcn_body_capture(dcn_body* body, const void* d_feat_current, const void* d_flow1,
-                            const void* d_prev_flow, const void* d_feat_prop,
-                            const void* d_feat_n2, const void* const* d_prefix,
-                            int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
-                            dcn_graph** out) {
+}  // namespace
+
+extern "C" {
+
+dcn_status dcn_body_step_dev(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                             const void* d_prev_flow, const void* d_feat_prop,
+                             const void* d_feat_n2, const void* const* d_prefix,
+                             int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                             void* stream) {
+    return body_step(body, d_feat_current, d_flow1, d_prev_flow, d_feat_prop, d_feat_n2, d_prefix, has_second_order,
+                     d_flow2_out, d_feat_prop_out, Cb8Step{}, stream);
+}
+
+dcn_status dcn_body_step_cb8_dev(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                                 const void* d_prev_flow, const void* d_feat_prop_cb8,
+                                 const void* d_feat_n2_cb8, const void* const* d_prefix,
+                                 int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                                 void* d_feat_prop_out_cb8, void* stream) {
+    Cb8Step m;
+    m.warp = true;
+    m.out = d_feat_prop_out_cb8;
+    return body_step(body, d_feat_current, d_flow1, d_prev_flow, d_feat_prop_cb8, d_feat_n2_cb8, d_prefix,
+                     has_second_order, d_flow2_out, d_feat_prop_out, m, stream);
+}
+
+dcn_status dcn_body_initial_step_dev(dcn_body* body, const void* d_feat_current,
+                                     const void* const* d_prefix, void* d_feat_prop_out,
+                                     void* stream) {
+    return body_initial(body, d_feat_current, d_prefix, d_feat_prop_out, nullptr, stream);
+}
+
+dcn_status dcn_body_initial_step_cb8_dev(dcn_body* body, const void* d_feat_current,
+                                         const void* const* d_prefix, void* d_feat_prop_out,
+                                         void* d_feat_prop_out_cb8, void* stream) {
+    if (!body) return DCN_INVALID_ARGUMENT;
+    if (!d_feat_prop_out_cb8) return fail(body->ctx, DCN_INVALID_ARGUMENT, "device pointer is null");
+    return body_initial(body, d_feat_current, d_prefix, d_feat_prop_out, d_feat_prop_out_cb8, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// `enqueue` (a step on the given stream) captured into one executable graph.
+template <class F>
+dcn_status capture_graph(dcn_body* body, dcn_graph** out, F&& enqueue) {
     if (!body || !out) return DCN_INVALID_ARGUMENT;
     *out = nullptr;
     dcn_context* ctx = body->ctx;
     DeviceGuard guard(ctx->device);
     const hipStream_t s = body->capture_stream;
     DCN_HIP(ctx, hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    const dcn_status st = dcn_body_step_dev(body, d_feat_current, d_flow1, d_prev_flow, d_feat_prop,
-                                            d_feat_n2, d_prefix, has_second_order, d_flow2_out,
-                                            d_feat_prop_out, s);
+    const dcn_status st = enqueue(s);
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(s, &graph);
     if (st != DCN_OK) {
@@ -604,6 +654,33 @@ dcn_status dcn_body_capture(dcn_body* body, const void* d_feat_current, const vo
     }
     *out = g;
     return DCN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+dcn_status dcn_body_capture(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                            const void* d_prev_flow, const void* d_feat_prop,
+                            const void* d_feat_n2, const void* const* d_prefix,
+                            int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                            dcn_graph** out) {
+    return capture_graph(body, out, [&](hipStream_t s) {
+        return dcn_body_step_dev(body, d_feat_current, d_flow1, d_prev_flow, d_feat_prop, d_feat_n2, d_prefix,
+                                 has_second_order, d_flow2_out, d_feat_prop_out, s);
+    });
+}
+
+dcn_status dcn_body_capture_cb8(dcn_body* body, const void* d_feat_current, const void* d_flow1,
+                                const void* d_prev_flow, const void* d_feat_prop_cb8,
+                                const void* d_feat_n2_cb8, const void* const* d_prefix,
+                                int has_second_order, void* d_flow2_out, void* d_feat_prop_out,
+                                void* d_feat_prop_out_cb8, dcn_graph** out) {
+    return capture_graph(body, out, [&](hipStream_t s) {
+        return dcn_body_step_cb8_dev(body, d_feat_current, d_flow1, d_prev_flow, d_feat_prop_cb8, d_feat_n2_cb8,
+                                     d_prefix, has_second_order, d_flow2_out, d_feat_prop_out,
+                                     d_feat_prop_out_cb8, s);
+    });
 }
 
 dcn_status dcn_graph_launch(dcn_graph* graph, void* stream) {
@@ -661,12 +738,17 @@ dcn_status dcn_clip_create_tiles(dcn_context* ctx, int height, int width, int fr
         if (st != DCN_OK) return bail(st);
     }
     const size_t plane = (size_t)width * height * tiles;
+    const size_t cb8 = (size_t)dcn::cb8_tensor_elems(64, height, width);  // one 64-channel CB8 feature
     dcn_status st = alloc(ctx, c->buffers, &c->zero_feat, 64 * plane);
     if (st == DCN_OK) st = alloc(ctx, c->buffers, &c->flow2, 2 * plane);
+    if (st == DCN_OK && tiles == 1) st = alloc(ctx, c->buffers, &c->mirror, 4 * (size_t)frames * cb8);
+    if (st == DCN_OK && tiles == 1) st = alloc(ctx, c->buffers, &c->zero_cb8, cb8);
     if (st != DCN_OK) return bail(st);
     const hipStream_t s = (hipStream_t)stream;
     if (hipMemsetAsync(c->zero_feat, 0, 64 * plane * 2, s) != hipSuccess ||
-        hipMemsetAsync(c->flow2, 0, 2 * plane * 2, s) != hipSuccess)
+        hipMemsetAsync(c->flow2, 0, 2 * plane * 2, s) != hipSuccess ||
+        (c->mirror && hipMemsetAsync(c->mirror, 0, 4 * (size_t)frames * cb8 * 2, s) != hipSuccess) ||
+        (c->zero_cb8 && hipMemsetAsync(c->zero_cb8, 0, cb8 * 2, s) != hipSuccess))
         return bail(fail(ctx, DCN_COMMAND_FAILED, "clearing clip buffers failed"));
     if (hipStreamCreateWithFlags(&c->capture_stream, hipStreamNonBlocking) != hipSuccess)
         return bail(fail(ctx, DCN_COMMAND_FAILED, "hipStreamCreate failed"));
@@ -679,12 +761,16 @@ dcn_status dcn_clip_create_tiles(dcn_context* ctx, int height, int width, int fr
 
 namespace {
 
+// Elements of one 64-channel CB8 feature of a clip.
+long cb8_feat(const dcn_clip* clip) { return dcn::cb8_tensor_elems(64, clip->h, clip->w); }
+
 // One recurrence of all four branches over n frames (frame indices 0 .. n-1 of the
 // accessors), in schedule order. feat(i) is frame i's spatial feature, flow(backward, i)
 // the flow that frame i's step reads (backward flows are indexed by the frame, forward
-// flows by the frame before it), prop(b, i) branch b's feat_prop of frame i.
-template <class Feat, class Flow, class Prop>
-dcn_status run_recurrence(dcn_clip* clip, int n, Feat feat, Flow flow, Prop prop, void* stream) {
+// flows by the frame before it), prop(b, i) branch b's feat_prop of frame i, and mir(b, i)
+// its CB8 copy (null for clips over several tiles, whose steps warp the NCHW features).
+template <class Feat, class Flow, class Prop, class Mir>
+dcn_status run_recurrence(dcn_clip* clip, int n, Feat feat, Flow flow, Prop prop, Mir mir, void* stream) {
     for (int b = 0; b < 4; ++b) {
         const bool backward = b % 2 == 0;
         auto frame_at = [&](int position) { return backward ? n - 1 - position : position; };
@@ -692,16 +778,26 @@ dcn_status run_recurrence(dcn_clip* clip, int n, Feat feat, Flow flow, Prop prop
             const int frame = frame_at(p);
             const void* prefix[3] = {};
             for (int i = 0; i < b; ++i) prefix[i] = prop(i, frame);
+            uint16_t* m = mir(b, frame);
             if (p == 0) {
-                DCN_TRY(dcn_body_initial_step_dev(clip->body[b], feat(frame), prefix, prop(b, frame), stream));
+                if (m)
+                    DCN_TRY(dcn_body_initial_step_cb8_dev(clip->body[b], feat(frame), prefix, prop(b, frame), m, stream));
+                else
+                    DCN_TRY(dcn_body_initial_step_dev(clip->body[b], feat(frame), prefix, prop(b, frame), stream));
                 continue;
             }
             const int prev = frame_at(p - 1);
             const uint16_t* flow1 = flow(backward, frame);
             const uint16_t* prev_flow = p >= 2 ? flow(backward, prev) : flow1;
-            const uint16_t* feat_n2 = p >= 2 ? prop(b, frame_at(p - 2)) : clip->zero_feat;
-            DCN_TRY(dcn_body_step_dev(clip->body[b], feat(frame), flow1, prev_flow, prop(b, prev), feat_n2,
-                                      prefix, p >= 2 ? 1 : 0, clip->flow2, prop(b, frame), stream));
+            if (m) {
+                const uint16_t* n2 = p >= 2 ? mir(b, frame_at(p - 2)) : clip->zero_cb8;
+                DCN_TRY(dcn_body_step_cb8_dev(clip->body[b], feat(frame), flow1, prev_flow, mir(b, prev), n2, prefix,
+                                              p >= 2 ? 1 : 0, clip->flow2, prop(b, frame), m, stream));
+            } else {
+                const uint16_t* feat_n2 = p >= 2 ? prop(b, frame_at(p - 2)) : clip->zero_feat;
+                DCN_TRY(dcn_body_step_dev(clip->body[b], feat(frame), flow1, prev_flow, prop(b, prev), feat_n2,
+                                          prefix, p >= 2 ? 1 : 0, clip->flow2, prop(b, frame), stream));
+            }
         }
     }
     return DCN_OK;
@@ -744,7 +840,10 @@ dcn_status dcn_clip_run_dev(dcn_clip* clip, const void* d_spatial, const void* d
             return backward ? bflows + (size_t)frame * 2 * plane : fflows + (size_t)(frame - 1) * 2 * plane;
         };
         auto prop = [&](int b, int i) { return propagated + ((size_t)b * T + c0 + i) * 64 * plane; };
-        DCN_TRY(run_recurrence(clip, sizes[r], feat, flow, prop, stream));
+        auto mir = [&](int b, int i) {
+            return clip->mirror ? clip->mirror + ((size_t)b * T + c0 + i) * (size_t)cb8_feat(clip) : nullptr;
+        };
+        DCN_TRY(run_recurrence(clip, sizes[r], feat, flow, prop, mir, stream));
     }
     return DCN_OK;
 }
@@ -793,13 +892,20 @@ dcn_status dcn_clip_run_with_fallback_dev(dcn_clip* clip, const void* d_spatial,
     // Independent zero-motion triplets: frame t alone as the clip [t, t, t] with zero
     // flows; every branch keeps the middle frame's feat_prop.
     if (!clip->triplet_prop) DCN_TRY(alloc(ctx, clip->buffers, &clip->triplet_prop, 12 * 64 * plane));
+    if (clip->mirror && !clip->triplet_mirror) {
+        DCN_TRY(alloc(ctx, clip->buffers, &clip->triplet_mirror, 12 * (size_t)cb8_feat(clip)));
+        DCN_HIP(ctx, hipMemsetAsync(clip->triplet_mirror, 0, 12 * (size_t)cb8_feat(clip) * 2, s));
+    }
     st = DCN_OK;
     for (int t = 0; t < T && st == DCN_OK; ++t) {
         const uint16_t* frame = spatial + (size_t)t * 64 * plane;
         auto feat = [&](int) { return frame; };
         auto flow = [&](bool, int) { return (const uint16_t*)clip->zero_feat; };  // >= 2 x plane zeros
         auto prop = [&](int b, int i) { return clip->triplet_prop + (size_t)(b * 3 + i) * 64 * plane; };
-        DCN_TRY(run_recurrence(clip, 3, feat, flow, prop, stream));
+        auto mir = [&](int b, int i) {
+            return clip->triplet_mirror ? clip->triplet_mirror + (size_t)(b * 3 + i) * (size_t)cb8_feat(clip) : nullptr;
+        };
+        DCN_TRY(run_recurrence(clip, 3, feat, flow, prop, mir, stream));
         st = dcn_check_nonfinite_f16_dev(ctx, clip->triplet_prop, 12 * 64 * plane, stream);
         if (st != DCN_OK) break;
         for (int b = 0; b < 4; ++b)

@@ -187,15 +187,18 @@ hipError_t launch_conv_prepack(const ConvGeometry& g, const uint16_t* w, const u
 struct ConvBatch {
     int images = 1;
     long x = 0, res1 = 0, res2 = 0, out = 0;
+    long out2 = 0;  // per-image stride of a conv pair's second (CB8) output
 };
 // The temporal preparation and the first conv_offset layer (196 -> 64, LeakyReLU) in one
 // launch (one image): writes flow2, the DCN input and the backbone input's leading blocks
 // as launch_body_temporal does, and the conv's output in CB8, without the conditions.
+// warp_cb8: feat_prop and feat_n2 are CB8 tensors (8 blocks) instead of NCHW.
 hipError_t launch_temporal_conv(const ConvGeometry& g, const uint16_t* feat_prop, const uint16_t* feat_current,
                                 const uint16_t* feat_n2, const uint16_t* flow1, const uint16_t* prev_flow,
                                 int has_second_order, const uint16_t* const* prefix, int nprefix,
                                 uint16_t* flow2, uint16_t* deform_cb8, uint16_t* bb_cb8, const void* wpk,
-                                const float* bias, float slope, uint16_t* out_cb8, hipStream_t stream);
+                                const float* bias, float slope, uint16_t* out_cb8, hipStream_t stream,
+                                bool warp_cb8 = false);
 hipError_t launch_conv3x3(const ConvGeometry& g, const void* x_cb8, const void* wpk,
                           const float* bias, int act, float slope, const uint16_t* res1,
                           int res1_layout, const uint16_t* res2, int res2_layout, uint16_t* out,
@@ -208,7 +211,7 @@ hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, c
                                const float* bias2, int act2, float slope, const uint16_t* res1,
                                int res1_layout, const uint16_t* res2, int res2_layout,
                                uint16_t* out, int out_layout, hipStream_t stream, int res2_coff = 0,
-                               const ConvBatch& batch = ConvBatch{});
+                               const ConvBatch& batch = ConvBatch{}, uint16_t* out2_cb8 = nullptr);
 // SPyNet (dcn_kernels_spynet.hip).
 constexpr int kSpynetMaxLevels = DCN_SPYNET_LEVELS;
 struct ConvKGeometry {

@@ -505,13 +505,14 @@ struct PairArgs {
     const uint16_t* res1;
     const uint16_t* res2;
     uint16_t* out;
+    uint16_t* out2;    // optional second copy of the output, CB8 (64 channels)
     uint32_t xin_bytes, wpk_bytes;
     int act1, act2;
     float slope;
     int res1_layout, res2_layout, out_layout, res2_coff;
     int H, W, Hp, Wp, tiles_x, tiles;
     int images, zpw;                        // batch size, images per workgroup
-    long xin_ts, res1_ts, res2_ts, out_ts;  // per-image strides of a batch
+    long xin_ts, res1_ts, res2_ts, out_ts, out2_ts;  // per-image strides of a batch
 };
 
 __host__ __device__ constexpr size_t pair_lds_bytes(int nw) {
@@ -611,7 +612,7 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
     const int epi_oc = ((tid >> 6) % NB) * 16 + (tid & 15);
     const float bias2v = epi ? a.bias2[epi_oc] : 0.0f;
     bool epi_in[4];
-    uint32_t epi_out[4], epi_r1[4], epi_r2[4];
+    uint32_t epi_out[4], epi_out2[4], epi_r1[4], epi_r2[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int op = 4 * ((tid & 63) >> 4) + v;
@@ -619,6 +620,7 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
         const int xx = ox0 + (op & 7);
         epi_in[v] = epi && yy < a.H && xx < a.W;
         epi_out[v] = (uint32_t)conv_index(a.out_layout, epi_oc, yy, xx, a.H, a.W, a.Hp, a.Wp);
+        epi_out2[v] = (uint32_t)conv_index(kLayoutCB8, epi_oc, yy, xx, a.H, a.W, a.Hp, a.Wp);
         epi_r1[v] = (uint32_t)conv_index(a.res1_layout, epi_oc, yy, xx, a.H, a.W, a.Hp, a.Wp);
         epi_r2[v] = (uint32_t)conv_index(a.res2_layout, a.res2_coff + epi_oc, yy, xx, a.H, a.W, a.Hp, a.Wp);
     }
@@ -627,6 +629,7 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
         const uint16_t* res1 = a.res1 ? a.res1 + (long)z * a.res1_ts : nullptr;
         const uint16_t* res2 = a.res2 ? a.res2 + (long)z * a.res2_ts : nullptr;
         uint16_t* out = a.out + (long)z * a.out_ts;
+        uint16_t* out2 = a.out2 ? a.out2 + (long)z * a.out2_ts : nullptr;
         // The epilogue's residual inputs, requested now so that they arrive during the convs.
         uint16_t r1v[4] = {0, 0, 0, 0}, r2v[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -748,7 +751,9 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
                     const float r1 = (float)round_f16(val);
                     val = (float)__builtin_bit_cast(_Float16, r2v[v]) + r1;
                 }
-                out[epi_out[v]] = __builtin_bit_cast(uint16_t, round_f16(val));
+                const uint16_t h = __builtin_bit_cast(uint16_t, round_f16(val));
+                out[epi_out[v]] = h;
+                if (out2 != nullptr) out2[epi_out2[v]] = h;
             }
         }
         if (z + 1 < z1) __syncthreads();  // sums read before the next image's partials
@@ -783,7 +788,10 @@ struct TemporalConvArgs {
     float slope;
 };
 
-template <int NW, int KMAX>
+// WARP_CB8: feat_prop and feat_n2 are CB8 tensors (the clip's mirrors of its propagated
+// features): each warped block is four 16-byte gathers instead of 32 two-byte ones, and
+// the DCN input blocks are 16-byte copies. Same bits either way.
+template <int NW, int KMAX, bool WARP_CB8>
 __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs a) {
     constexpr int NB = kConvNbc;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -857,7 +865,8 @@ __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs
             if (y >= 0 && y < H && x >= 0 && x < W) {
                 const uint16_t f1[2] = {hflow[hp * 4 + 0], hflow[hp * 4 + 1]};
                 const uint16_t f2[2] = {hflow[hp * 4 + 2], hflow[hp * 4 + 3]};
-                v = warp::condition_from_flows<u32x4>(a.feat_prop, a.feat_current, a.feat_n2, H, W, blk, y, x, f1, f2);
+                v = warp::condition_from_flows<u32x4, WARP_CB8>(a.feat_prop, a.feat_current, a.feat_n2, H, W, blk, y, x,
+                                                                 f1, f2);
             }
             cond[blk * kTcHalo + hp] = v;
             continue;
@@ -878,6 +887,14 @@ __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs
         uint16_t* dst;
         int dblock;
         const uint16_t* src;
+        if (WARP_CB8 && kind <= 16) {
+            dblock = kind - 1;
+            const uint16_t* t = dblock < 8 ? a.feat_prop : a.feat_n2;
+            const size_t unit = ((size_t)(dblock & 7) * Hp + y + kPad) * Wp + x + kPad;
+            reinterpret_cast<u32x4*>(a.deform)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] =
+                reinterpret_cast<const u32x4*>(t)[unit];
+            continue;
+        }
         if (kind <= 16) {
             dst = a.deform;
             dblock = kind - 1;
@@ -1068,7 +1085,8 @@ hipError_t launch_temporal_conv(const ConvGeometry& g, const uint16_t* feat_prop
                                 const uint16_t* feat_n2, const uint16_t* flow1, const uint16_t* prev_flow,
                                 int has_second_order, const uint16_t* const* prefix, int nprefix,
                                 uint16_t* flow2, uint16_t* deform_cb8, uint16_t* bb_cb8, const void* wpk,
-                                const float* bias, float slope, uint16_t* out_cb8, hipStream_t stream) {
+                                const float* bias, float slope, uint16_t* out_cb8, hipStream_t stream,
+                                bool warp_cb8) {
     constexpr int NW = 8, KMAX = 8;
     if (g.cin != 196 || g.cout != 64 || g.ksteps > NW * KMAX || nprefix < 0 || nprefix > 3)
         return hipErrorInvalidValue;
@@ -1102,7 +1120,7 @@ hipError_t launch_temporal_conv(const ConvGeometry& g, const uint16_t* feat_prop
     a.slope = slope;
     const size_t lds = (size_t)NW * kConvNbc * 4 * 65 * sizeof(float) + (size_t)kTcBlocks * kTcHalo * 16 +
                        (size_t)kTcHalo * 4 * sizeof(uint16_t);
-    auto kernel = &temporal_conv_kernel<NW, KMAX>;
+    auto kernel = warp_cb8 ? &temporal_conv_kernel<NW, KMAX, true> : &temporal_conv_kernel<NW, KMAX, false>;
     const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
     if (attr != hipSuccess) return attr;
     hipLaunchKernelGGL(kernel, dim3((unsigned)((a.tiles + 7) / 8 * 8)), dim3(64 * NW), lds, stream, a);
@@ -1134,7 +1152,7 @@ hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, c
                                const float* bias2, int act2, float slope, const uint16_t* res1,
                                int res1_layout, const uint16_t* res2, int res2_layout,
                                uint16_t* out, int out_layout, hipStream_t stream, int res2_coff,
-                               const ConvBatch& batch) {
+                               const ConvBatch& batch, uint16_t* out2_cb8) {
     if (g1.cin != 64 || g1.cout != 64 || g2.cin != 64 || g2.cout != 64 || g1.h != g2.h ||
         g1.w != g2.w || g1.ksteps != kPairKsteps || g1.nbt != kConvNbc || batch.images < 1)
         return hipErrorInvalidValue;
@@ -1159,6 +1177,8 @@ hipError_t launch_conv3x3_pair(const ConvGeometry& g1, const ConvGeometry& g2, c
     a.res1_ts = batch.res1;
     a.res2_ts = batch.res2;
     a.out_ts = batch.out;
+    a.out2 = out2_cb8;
+    a.out2_ts = batch.out2;
     a.images = batch.images;
     a.zpw = images_per_group<16>(batch.images);
     a.H = g1.h;

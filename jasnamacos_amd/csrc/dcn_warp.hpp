@@ -8,6 +8,7 @@
 
 #include <cstdint>
 
+#include "dcn_device.hpp"
 #include "dcn_internal.hpp"
 
 namespace dcn {
@@ -75,6 +76,37 @@ __device__ __forceinline__ void sample8_zero(const uint16_t* planes, size_t plan
 }
 
 
+// sample8_zero over one 8-channel block of a CB8 tensor ([Hp][Wp][8] with a kPad zero
+// border): the same corners, validity and per-channel arithmetic, four 16-byte gathers.
+__device__ __forceinline__ void sample8_cb8(const uint16_t* block, int H, int W, float y, float x,
+                                            float (&v)[8]) {
+    const int Wp = W + 2 * dev::kPad;
+    const float fy = floorf(y), fx = floorf(x);
+    const int y0 = (int)fminf(fmaxf(fy, -4.0f), (float)H + 4.0f);
+    const int x0 = (int)fminf(fmaxf(fx, -4.0f), (float)W + 4.0f);
+    const int y1 = y0 + 1, x1 = x0 + 1;
+    const float ly = y - fy, lx = x - fx;
+    const bool r0 = y0 >= 0 && y0 < H, r1 = y1 >= 0 && y1 < H;
+    const bool c0 = x0 >= 0 && x0 < W, c1 = x1 >= 0 && x1 < W;
+    const int yc0 = min(max(y0, 0), H - 1) + dev::kPad, yc1 = min(max(y1, 0), H - 1) + dev::kPad;
+    const int xc0 = min(max(x0, 0), W - 1) + dev::kPad, xc1 = min(max(x1, 0), W - 1) + dev::kPad;
+    typedef const dev::u32x4* row_t;
+    const dev::u32x4 t00 = reinterpret_cast<row_t>(block)[(size_t)yc0 * Wp + xc0];
+    const dev::u32x4 t01 = reinterpret_cast<row_t>(block)[(size_t)yc0 * Wp + xc1];
+    const dev::u32x4 t10 = reinterpret_cast<row_t>(block)[(size_t)yc1 * Wp + xc0];
+    const dev::u32x4 t11 = reinterpret_cast<row_t>(block)[(size_t)yc1 * Wp + xc1];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int sh = (c & 1) * 16;
+        const float v00 = (r0 && c0) ? h2f((uint16_t)(t00[c >> 1] >> sh)) : 0.0f;
+        const float v01 = (r0 && c1) ? h2f((uint16_t)(t01[c >> 1] >> sh)) : 0.0f;
+        const float v10 = (r1 && c0) ? h2f((uint16_t)(t10[c >> 1] >> sh)) : 0.0f;
+        const float v11 = (r1 && c1) ? h2f((uint16_t)(t11[c >> 1] >> sh)) : 0.0f;
+        v[c] = v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx + v10 * ly * (1.0f - lx) +
+               v11 * ly * lx;
+    }
+}
+
 // The eight channels of condition block `kind` (0-24) at pixel (y, x), as CB8 halves:
 // 0-7 warp(feat_prop, flow1), 8-15 feat_current, 16-23 warp(feat_n2, flow2), 24
 // [flow1 (x, y), flow2 (x, y), 0, 0, 0, 0] (assemble_temporal_alignment_fp16,
@@ -113,7 +145,9 @@ __device__ __forceinline__ V4 copy8(const uint16_t* planes, size_t pl, int p) {
 
 // Condition block `kind` at (y, x) from the pixel's FP16 flows f1 = flow1 (x, y) and
 // f2 = flow2 (x, y) (both as bits).
-template <typename V4>
+// With WARP_CB8, feat_prop and feat_n2 are CB8 tensors (8 blocks) and are warped through
+// sample8_cb8; feat_current is NCHW either way.
+template <typename V4, bool WARP_CB8 = false>
 __device__ __forceinline__ V4 condition_from_flows(const uint16_t* feat_prop, const uint16_t* feat_current,
                                                    const uint16_t* feat_n2, int H, int W, int kind, int y, int x,
                                                    const uint16_t (&f1)[2], const uint16_t (&f2)[2]) {
@@ -129,10 +163,17 @@ __device__ __forceinline__ V4 condition_from_flows(const uint16_t* feat_prop, co
         return out;
     }
     float v[8];
-    if (kind < 8)
+    if (WARP_CB8) {
+        const size_t blk = (size_t)(H + 2 * dev::kPad) * (W + 2 * dev::kPad) * 8;  // elements per block
+        if (kind < 8)
+            sample8_cb8(feat_prop + (size_t)kind * blk, H, W, (float)y + h2f(f1[1]), (float)x + h2f(f1[0]), v);
+        else
+            sample8_cb8(feat_n2 + (size_t)(kind - 16) * blk, H, W, (float)y + h2f(f2[1]), (float)x + h2f(f2[0]), v);
+    } else if (kind < 8) {
         sample8_zero(feat_prop + (size_t)kind * 8 * pl, pl, H, W, (float)y + h2f(f1[1]), (float)x + h2f(f1[0]), v);
-    else
+    } else {
         sample8_zero(feat_n2 + (size_t)(kind - 16) * 8 * pl, pl, H, W, (float)y + h2f(f2[1]), (float)x + h2f(f2[0]), v);
+    }
 #pragma unroll
     for (int d = 0; d < 4; ++d) out[d] = pack_halves(f2h(v[2 * d]), f2h(v[2 * d + 1]));
     return out;

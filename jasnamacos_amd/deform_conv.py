@@ -627,6 +627,31 @@ class PropagationBody:
         self.ctx._check(self.ctx._lib.dcn_body_initial_step_dev(self.handle, _ptr(feat_current), pre,
                                                                 _ptr(feat_prop_out), _stream(stream)))
 
+    def step_cb8_dev(self, feat_current, flow1, prev_flow, feat_prop_cb8, feat_n2_cb8, flow2_out, feat_prop_out,
+                     feat_prop_out_cb8, has_second_order=True, prefix=None, stream=None) -> None:
+        """dcn_body_step_cb8_dev: feat_prop / feat_n2 as 64-channel CB8 tensors, the output
+        in NCHW and in CB8 (single-tile bodies)."""
+        self.ctx._check(self.ctx._lib.dcn_body_step_cb8_dev(
+            self.handle, *self._args(feat_current, flow1, prev_flow, feat_prop_cb8, feat_n2_cb8, prefix,
+                                     has_second_order, flow2_out, feat_prop_out), _ptr(feat_prop_out_cb8),
+            _stream(stream)))
+
+    def initial_step_cb8_dev(self, feat_current, feat_prop_out, feat_prop_out_cb8, prefix=None, stream=None) -> None:
+        pre = None
+        if prefix:
+            pre = (C.c_void_p * len(prefix))(*[_ptr(x) for x in prefix])
+        self.ctx._check(self.ctx._lib.dcn_body_initial_step_cb8_dev(
+            self.handle, _ptr(feat_current), pre, _ptr(feat_prop_out), _ptr(feat_prop_out_cb8), _stream(stream)))
+
+    def capture_cb8(self, feat_current, flow1, prev_flow, feat_prop_cb8, feat_n2_cb8, flow2_out, feat_prop_out,
+                    feat_prop_out_cb8, has_second_order=True, prefix=None) -> BodyGraph:
+        handle = C.c_void_p()
+        self.ctx._check(self.ctx._lib.dcn_body_capture_cb8(
+            self.handle, *self._args(feat_current, flow1, prev_flow, feat_prop_cb8, feat_n2_cb8, prefix,
+                                     has_second_order, flow2_out, feat_prop_out), _ptr(feat_prop_out_cb8),
+            C.byref(handle)))
+        return BodyGraph(self.ctx, handle.value)
+
     def capture(self, feat_current, flow1, prev_flow, feat_prop, feat_n2, flow2_out, feat_prop_out,
                 has_second_order=True, prefix=None) -> BodyGraph:
         handle = C.c_void_p()

@@ -329,6 +329,40 @@ def test_body_step_matches_oracle_chain(gpu_ctx, torch, h, w, branch, blocks):
     body.free()
 
 
+@pytest.mark.parametrize("h,w,branch,blocks,second", [(16, 24, 1, 2, True), (13, 21, 0, 1, False),
+                                                      (64, 64, 3, 5, True), (5, 3, 2, 1, True)])
+def test_body_cb8_steps_equal_nchw_steps(gpu_ctx, dcn, torch, h, w, branch, blocks, second):
+    """dcn_body_step_cb8_dev / _initial_step_cb8_dev (feat_prop and feat_n2 warped from CB8
+    copies) give the NCHW entry points' bits, and their CB8 output is the NCHW output in
+    CB8 with a zero border."""
+    weights, x, wd, body, xd = _body_case(torch, gpu_ctx, h, w, branch, blocks, 80 + h + branch)
+    plane = h * w
+    n = dcn.cb8_tensor_count(64, h, w)
+    log("case: body cb8 step", h, w, "branch", branch, "blocks", blocks, "second order", second)
+    cb8 = lambda a: dev(torch, br.to_cb8(a, 64, h, w))  # noqa: E731
+    f2a = torch.zeros(2 * plane, dtype=torch.int16, device="cuda")
+    f2b = torch.zeros_like(f2a)
+    outs = [torch.zeros(64 * plane, dtype=torch.int16, device="cuda") for _ in range(4)]
+    mirrors = [torch.full((n,), 0x5555, dtype=torch.int16, device="cuda") for _ in range(2)]
+    body.step_dev(xd["feat_current"], xd["flow1"], xd["prev_flow"], xd["feat_prop"], xd["feat_n2"], f2a, outs[0],
+                  second, xd["prefix"] or None)
+    body.step_cb8_dev(xd["feat_current"], xd["flow1"], xd["prev_flow"], cb8(x["feat_prop"]), cb8(x["feat_n2"]), f2b,
+                      outs[1], mirrors[0], second, xd["prefix"] or None)
+    body.initial_step_dev(xd["feat_current"], outs[2], xd["prefix"] or None)
+    body.initial_step_cb8_dev(xd["feat_current"], outs[3], mirrors[1], xd["prefix"] or None)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(f2a).view(np.uint16), host(f2b).view(np.uint16))
+    for nchw, cb, mirror in ((outs[0], outs[1], mirrors[0]), (outs[2], outs[3], mirrors[1])):
+        a, b = host(nchw).copy(), host(cb).copy()
+        assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+        m = host(mirror).copy().view(np.uint16).reshape(8, h + 4, w + 4, 8)
+        want = br.to_cb8(a, 64, h, w).view(np.uint16)
+        # The interior is the output; the border keeps whatever the owner put there.
+        assert np.array_equal(m[:, 2:2 + h, 2:2 + w], want[:, 2:2 + h, 2:2 + w])
+        assert np.all(m[:, :2] == 0x5555) and np.all(m[:, :, :2] == 0x5555)
+    body.free()
+
+
 @pytest.mark.parametrize("h,w,branch,tiles", [(16, 24, 1, 3), (13, 21, 0, 2), (16, 16, 0, 5)])
 def test_body_tiles_equal_single_tiles(gpu_ctx, torch, h, w, branch, tiles):
     """A body over `tiles` tiles per step == one single-tile body per tile, bit for bit
