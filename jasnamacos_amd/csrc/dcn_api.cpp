@@ -37,9 +37,16 @@ bool packed_matches(const dcn_packed* p, const dcn_shape* s) {
            p->shape.offset_groups == s->offset_groups;
 }
 
-dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry& g,
+dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry& g, const dcn_shape& shape,
                                bool window_ok, bool tile_ok) {
     dcn::FusedConfig o = ctx->fused_override;
+    // Batches of small maps (C3: 16 x 64 x 64) run fastest on the tile kernel (C3 49.7 us
+    // against 55.2 us for the window kernel); a single large map keeps the window kernel
+    // (C5 70.9 against 75.0 us: its wide-flow windows overflow LDS more often on 128-pixel
+    // tiles).
+    if (o.variant == 0 && tile_ok && o.sampler != dcn::kSamplerExact && shape.batch >= 2 &&
+        (long long)shape.output_height * shape.output_width <= 128 * 128 && (g.m + 31) / 32 > 1024)
+        o.variant = dcn::kVariantTile;
     // The tile variant implements the fast sampler only: with the exact one (or a shape
     // it does not cover) the automatic choice below applies, with only the sampler pinned.
     if (o.variant == dcn::kVariantTile) {
@@ -142,8 +149,11 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
         return fail(ctx, DCN_INVALID_ARGUMENT, "packed weights live on another device");
     if (dcn::cb8_bytes(*shape, g) >= ((size_t)1 << 31))
         return fail(ctx, DCN_INVALID_SHAPE, "padded input too large for 32-bit device indexing");
+    // The packed weights carry the window / tile fragments only when the layer's shape at
+    // prepack allowed those kernels; this call's shape must allow them too.
     const dcn::FusedConfig cfg =
-        choose_config(ctx, g, packed->weights_group != nullptr, packed->weights_tile != nullptr);
+        choose_config(ctx, g, *shape, packed->weights_group != nullptr && dcn::window_supported(*shape),
+                      packed->weights_tile != nullptr && dcn::tile_supported(*shape));
     if (!config_supported(cfg, g))
         return fail(ctx, DCN_INVALID_ARGUMENT,
                     "unsupported fused config (variant " + std::to_string(cfg.variant) + ", mt " +
@@ -345,7 +355,7 @@ dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* v
     dcn::FusedGeometry g;
     if (!dcn::fused_geometry(*shape, &g)) return fail(ctx, DCN_INVALID_SHAPE, "not a fused shape");
     const dcn::FusedConfig cfg =
-        choose_config(ctx, g, dcn::window_supported(*shape), dcn::tile_supported(*shape));
+        choose_config(ctx, g, *shape, dcn::window_supported(*shape), dcn::tile_supported(*shape));
     *variant = cfg.variant;
     *mt = cfg.mt;
     *ks = cfg.ks;

@@ -176,17 +176,24 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         constexpr int kChunksPerCh = kTilePix / 8;  // 16
         constexpr int kRowChunks = TW / 8;
         constexpr int kChunks = kTileOffCh * kChunksPerCh;  // 864
+        constexpr int kOffInstr = 36 * kChunksPerCh / 64;   // instructions of the 36 offset channels
+        // Chunk c = 64 i + lane is channel c / 16 = 4 i + lane / 16 at tile position c % 16 =
+        // lane % 16 for every i, so a lane's source only steps by 4 NW channels per
+        // instruction: the address is set up once and then advanced by one add.
+        const int rem = lane % kChunksPerCh;
+        const int y = min(ty * TH + rem / kRowChunks, a.Ho - 1);
+        const int x = tx * TW + (rem % kRowChunks) * 8;
+        const uint32_t pix = (uint32_t)(y * a.Wo + x);
+        const int ch0 = wave * 4 + lane / kChunksPerCh;  // channel of instruction i = wave
+        const uint32_t step = (uint32_t)(4 * NW) * (uint32_t)a.HWo * 2u;
+        // (Modular arithmetic: the mask address is only used once it is past channel 36.)
+        uint32_t off_src = ((uint32_t)(b * 2 * a.G * 9 + 36 * st + ch0) * (uint32_t)a.HWo + pix) * 2u;
+        uint32_t msk_src = ((uint32_t)(b * a.G * 9 + 18 * st + ch0 - 36) * (uint32_t)a.HWo + pix) * 2u;
         for (int i = wave; i * 64 < kChunks; i += NW) {
-            const int c = i * 64 + lane;
-            const bool is_off = i < 36 * kChunksPerCh / 64;  // uniform per instruction
-            const int ch = (is_off ? c : c - 36 * kChunksPerCh) / kChunksPerCh;
-            const int rem = c % kChunksPerCh;
-            const int y = min(ty * TH + rem / kRowChunks, a.Ho - 1);
-            const int x = tx * TW + (rem % kRowChunks) * 8;
-            const uint32_t plane = is_off ? (uint32_t)(b * 2 * a.G * 9 + 36 * st + ch)
-                                          : (uint32_t)(b * a.G * 9 + 18 * st + ch);
-            const uint32_t src = (plane * (uint32_t)a.HWo + (uint32_t)(y * a.Wo + x)) * 2u;
-            if (c < kChunks) dma16(is_off ? orr : mr, src, offs + i * 64 * 16);
+            const bool is_off = i < kOffInstr;  // uniform per instruction
+            if (i * 64 + lane < kChunks) dma16(is_off ? orr : mr, is_off ? off_src : msk_src, offs + i * 64 * 16);
+            off_src += step;
+            msk_src += step;
         }
     };
 
@@ -223,31 +230,38 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         return w;
     };
     // LDS DMA of the windows of stage st as chunks of 64 consecutive window units (one
-    // instruction each; unit f of window g is row f / ww, column f % ww). Chunk i of the
-    // stage (window 0's chunks, then window 1's) is issued by wave i % 4.
+    // instruction each), window g's chunks at LDS offset off[g] + 1024 c.
     auto copy_windows = [&](int st, const Win& w) {
         if (!w.lds) return;
-        const int n0 = (w.hh[0] * w.ww[0] + 63) >> 6;
-        const int n = n0 + ((w.hh[1] * w.ww[1] + 63) >> 6);
-        for (int i = wave; i < n; i += NW) {
-            const int g = i < n0 ? 0 : 1;
-            const int c = i - (g ? n0 : 0);
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
             const int ww = g ? w.ww[1] : w.ww[0];
             const int units = ww * (g ? w.hh[1] : w.hh[0]);
-            const int f = c * 64 + lane;
-            if (f < units) {
-                // f / ww through the FP32 reciprocal ((f + 0.5) / ww is at least 0.5 / ww
-                // from an integer: exact for narrow windows), then corrected by one either
-                // way for wide ones.
-                int r = (int)(((float)f + 0.5f) * __builtin_amdgcn_rcpf((float)ww));
-                r -= r * ww > f ? 1 : 0;
-                r += (r + 1) * ww <= f ? 1 : 0;
-                const int col = f - r * ww;
-                const uint32_t row0 = (uint32_t)(b * a.CBLK + 2 * st + g) * a.Hp +
-                                      (uint32_t)((g ? w.y0[1] : w.y0[0]) + kPad);
-                const uint32_t src =
-                    ((row0 + (uint32_t)r) * a.Wp + (uint32_t)((g ? w.x0[1] : w.x0[0]) + kPad + col)) * 16u;
-                dma16(xr, src, lds + (g ? w.off[1] : w.off[0]) + c * 1024);
+            const int chunks = (units + 63) >> 6;
+            // Wave `wave` issues chunks wave, wave + NW, ... A lane's unit f = 64 c + lane is
+            // row f / ww, column f % ww: found once (the FP32 reciprocal, then corrected by
+            // one either way), then stepped by NW * 64 units = dq rows + dr columns.
+            int f = wave * 64 + lane;
+            int r = (int)(((float)f + 0.5f) * __builtin_amdgcn_rcpf((float)ww));
+            r -= r * ww > f ? 1 : 0;
+            r += (r + 1) * ww <= f ? 1 : 0;
+            int col = f - r * ww;
+            const int dq = (NW * 64) / ww, dr = NW * 64 - dq * ww;  // wave-uniform
+            const uint32_t row0 = (uint32_t)(b * a.CBLK + 2 * st + g) * a.Hp + (uint32_t)((g ? w.y0[1] : w.y0[0]) + kPad);
+            uint32_t unit = (row0 + (uint32_t)r) * a.Wp + (uint32_t)((g ? w.x0[1] : w.x0[0]) + kPad + col);
+            const uint32_t unit_step = (uint32_t)dq * a.Wp + (uint32_t)dr;
+            const uint32_t wrap = (uint32_t)(a.Wp - ww);  // next row's first column
+            uint8_t* dst = lds + (g ? w.off[1] : w.off[0]) + wave * 1024;
+            for (int c = wave; c < chunks; c += NW) {
+                if (f < units) dma16(xr, unit * 16u, dst);
+                f += NW * 64;
+                col += dr;
+                unit += unit_step;
+                if (col >= ww) {
+                    col -= ww;
+                    unit += wrap;
+                }
+                dst += NW * 1024;
             }
         }
     };

@@ -251,7 +251,21 @@ def test_fused_configs(gpu_ctx, dcn, c2, variant, mt, ks, sampler):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
-@pytest.mark.parametrize("variant", [0, 5, 6, 7])
+def test_automatic_config_per_workload(gpu_ctx, dcn):
+    """The automatic choice: narrow 16-pixel tiles for one 64 x 64 map (C2), the tile kernel
+    for batches of small maps (C3), the window kernel for one large map (C5); the exact
+    sampler never gets the tile kernel (it implements the fast one only)."""
+    want = {2: dcn.VARIANT_NARROW, 3: 7, 5: 3}
+    for c, v in want.items():
+        assert gpu_ctx.get_fused_config(dcn.config_shape(c))["variant"] == v, c
+    gpu_ctx.set_fused_config(0, 0, dcn.SAMPLER_EXACT)
+    try:
+        assert gpu_ctx.get_fused_config(dcn.config_shape(3))["variant"] == 3
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1)
+
+
+@pytest.mark.parametrize("variant", [0, 3, 5, 6, 7])
 def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle, variant):
     d = dcn.generate_config_inputs(3, 3)
     s = d["shape"]
