@@ -169,6 +169,15 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         offs_lane[s] = (uint32_t)((18 * half * kTilePix + lp) * 2);
         mask_lane[s] = (uint32_t)(((36 + 9 * half) * kTilePix + lp) * 2);
     }
+    // The same bases per kernel row / column, as floats (exact: small integers).
+    float ybf[NS][3], xbf[NS][3];
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+            ybf[s][t] = (float)(ybi[s] + t * a.dh);
+            xbf[s][t] = (float)(xbi[s] + t * a.dw);
+        }
     // LDS DMA of stage st's offsets (channels 36st .. 36st+35) and masks (18st .. 18st+17)
     // of the tile: 864 chunks of 8 pixels, chunk c -> LDS offs + 16c ([channel][128 px]).
     // Rows past the map repeat its last row (the clamped pixels read those).
@@ -278,13 +287,16 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         constexpr int NTW = decltype(ntw_c)::value;
         constexpr int NSMP = NS * NTW;  // samples per lane and stage, j = kk * NS + s
 
-        // A sample's dy, dx and mask from the LDS copy of the stage's offsets.
+        // A sample's dy, dx and mask from the LDS copy of the stage's offsets (an LDS
+        // pointer, so each read is one ds_read_u16 with an immediate offset from the lane's
+        // base).
         typedef const __attribute__((address_space(3))) _Float16* lds_h;
+        const lds_h offs_h = (lds_h)(const __attribute__((address_space(3))) uint8_t*)(lds + kTileBuf);
         auto offset_of = [&](int j, int which) {  // which: 0 = dy, 1 = dx, 2 = mask
             const int kk = j / NS, s = j % NS, k = T0 + kk;
             const uint32_t at = which == 2 ? mask_lane[s] + (uint32_t)(k * kTilePix * 2)
                                            : offs_lane[s] + (uint32_t)((2 * k + which) * kTilePix * 2);
-            return *(lds_h)(uintptr_t)((uint32_t)(uintptr_t)offs + at);
+            return offs_h[at / 2];
         };
         // Sample state of a stage: a[] = clamped corner (iy, ix) as a 16-bit pair, then
         // the sample's address; w0/w1 = the FP16 corner weights.
@@ -298,9 +310,10 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         };
         auto coords = [&](int j, Samples& C) {
             const int kk = j / NS, s = j % NS, k = T0 + kk;
-            // float(oy*sh - ph + ky*dh) + dy (MetalShader.swift:327-332), one rounding.
-            const float y = (float)(ybi[s] + (k / 3) * a.dh) + (float)offset_of(j, 0);
-            const float x = (float)(xbi[s] + (k % 3) * a.dw) + (float)offset_of(j, 1);
+            // float(oy*sh - ph + ky*dh) + dy (MetalShader.swift:327-332), one rounding: an
+            // fma with 1 is the same single rounding and takes the FP16 offset as it is.
+            const float y = __builtin_fmaf((float)offset_of(j, 0), 1.0f, ybf[s][k / 3]);
+            const float x = __builtin_fmaf((float)offset_of(j, 1), 1.0f, xbf[s][k % 3]);
             const float fy = floorf(y), fx = floorf(x);
             const float ly = y - fy, lx = x - fx;
             // Clamped so both rows/columns of the corner pair stay in the padded plane.
@@ -309,10 +322,12 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             C.a[j] = __builtin_amdgcn_perm((uint32_t)ix, (uint32_t)iy, 0x05040100u);
             bmin = __builtin_elementwise_min(bmin, as_s16x2(C.a[j]));
             bmax = __builtin_elementwise_max(bmax, as_s16x2(C.a[j]));
-            // Mask folded into the four bilinear weights, each rounded once to FP16.
+            // Mask folded into the four bilinear weights, each rounded once to FP16 (the
+            // mask products as fmas with +0: the products are not negative, so the same
+            // single rounding, with the FP16 mask taken as it is).
             const float m = (float)offset_of(j, 2);
-            const float t0 = m * (1.0f - ly);
-            const float t1 = m * ly;
+            const float t0 = __builtin_fmaf(m, 1.0f - ly, 0.0f);
+            const float t1 = __builtin_fmaf(m, ly, 0.0f);
             C.w0[j] = __builtin_bit_cast(uint32_t, h2{(_Float16)(t0 * (1.0f - lx)), (_Float16)(t0 * lx)});
             C.w1[j] = __builtin_bit_cast(uint32_t, h2{(_Float16)(t1 * (1.0f - lx)), (_Float16)(t1 * lx)});
         };
