@@ -378,19 +378,28 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
                 Bq[kk][nb] = __builtin_bit_cast(
                     h8, load16(wr, (uint32_t)(((st * 9 + T0 + kk) * NB + nb) * 64 + lane) * 16u, 0));
         };
+        // The LDS reads are issued in both modes (from LDS address 0 when the stage
+        // gathers from global memory; the global loads then replace them, and this branch
+        // waits for them at once). The compiler's waits are placed for every path of the
+        // control flow and count memory operations in issue order: with the LDS reads
+        // inside the branch (or global loads left in flight), the blend of each sample
+        // waited for the next sample's corner reads, or for the weight fragments requested
+        // after them, and the prefetch hid nothing. Only stages whose windows overflow the
+        // buffer take the global branch.
         auto corners = [&](int j, const Samples& C, const Addressing& r, bool from_lds, u32x4 (&q)[4]) {
             const uint32_t a0 = C.a[j], a1 = C.a[j] + r.pitch;
-            if (from_lds) {
-                typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
-                q[0] = *(lds_u32x4)(uintptr_t)a0;
-                q[1] = *(lds_u32x4)(uintptr_t)(a0 + 16);
-                q[2] = *(lds_u32x4)(uintptr_t)a1;
-                q[3] = *(lds_u32x4)(uintptr_t)(a1 + 16);
-            } else {
+            const uint32_t l0 = from_lds ? a0 : 0u, l1 = from_lds ? a1 : 0u;
+            typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
+            q[0] = *(lds_u32x4)(uintptr_t)l0;
+            q[1] = *(lds_u32x4)(uintptr_t)(l0 + 16);
+            q[2] = *(lds_u32x4)(uintptr_t)l1;
+            q[3] = *(lds_u32x4)(uintptr_t)(l1 + 16);
+            if (!from_lds) {
                 q[0] = load16(xr, a0, 0);
                 q[1] = load16(xr, a0 + 16u, 0);
                 q[2] = load16(xr, a1, 0);
                 q[3] = load16(xr, a1 + 16u, 0);
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             }
         };
         // K-loop of one stage: per sample j (tap kk, segment s) the next sample's corners
