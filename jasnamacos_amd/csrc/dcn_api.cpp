@@ -40,12 +40,11 @@ bool packed_matches(const dcn_packed* p, const dcn_shape* s) {
 dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry& g, const dcn_shape& shape,
                                bool window_ok, bool tile_ok) {
     dcn::FusedConfig o = ctx->fused_override;
-    // Batches of small maps (C3: 16 x 64 x 64) run fastest on the tile kernel (C3 49.7 us
-    // against 55.2 us for the window kernel); a single large map keeps the window kernel
-    // (C5 70.9 against 75.0 us: its wide-flow windows overflow LDS more often on 128-pixel
-    // tiles).
-    if (o.variant == 0 && tile_ok && o.sampler != dcn::kSamplerExact && shape.batch >= 2 &&
-        (long long)shape.output_height * shape.output_width <= 128 * 128 && (g.m + 31) / 32 > 1024)
+    // Problems of more than 32K output pixels run fastest on the tile kernel: batches of
+    // small maps (C3: 16 x 64 x 64, 48.6 us against 55.2 us for the window kernel) and
+    // single large maps (C5: 1 x 180 x 320, 60.2 us against 70.9 us; its wide-flow stages
+    // whose two windows do not fit LDS together run one pass per window).
+    if (o.variant == 0 && tile_ok && o.sampler != dcn::kSamplerExact && (g.m + 31) / 32 > 1024)
         o.variant = dcn::kVariantTile;
     // The tile variant implements the fast sampler only: with the exact one (or a shape
     // it does not cover) the automatic choice below applies, with only the sampler pinned.

@@ -72,7 +72,8 @@ constexpr int kTileBuf = 64 * 1024;                   // the window buffer (a st
 constexpr int kTileOffCh = 54;                        // offset + mask channels of a stage
 constexpr int kTileOff = kTileOffCh * kTilePix * 2;   // [36 dy/dx + 18 mask][128 px] FP16
 constexpr int kTileBox = 2 * kTileWaves * 2 * 4;      // [group][wave][min, max]
-constexpr int kTileLds = kTileBuf + kTileOff + kTileBox;  // 79,424 B: two workgroups per CU
+constexpr int kTileZero = kTileBuf + kTileOff + kTileBox;  // 32 zero bytes (masked lanes' corners)
+constexpr int kTileLds = kTileZero + 32;               // 79,456 B: two workgroups per CU
 
 struct TileArgs {
     const void* xin;      // CB8 input [B][CBLK][Hp][Wp][8]
@@ -84,6 +85,7 @@ struct TileArgs {
     uint32_t xin_bytes, off_bytes, msk_bytes, wpk_bytes;
     int H, W, Ho, Wo, HWo, ph, pw, sh, sw, dh, dw;
     int G, CBLK, Hp, Wp, Cout;
+    float one;  // 1.0f, opaque to the compiler (see coords)
     int tiles_y, tiles_x, tiles;
 };
 
@@ -209,7 +211,9 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     // Window geometry of a stage (wave-uniform): origin, size in units, LDS placement.
     struct Win {
         int y0[2], x0[2], ww[2], hh[2], off[2];
-        bool lds;  // both windows are in LDS (else the stage gathers from global memory)
+        bool lds;    // both windows are in LDS
+        bool split;  // else each fits alone: one pass per group, its window at 0
+                     // (neither: the stage gathers from global memory)
     };
     auto read_windows = [&]() {
         // Lanes 0-7 read one wave's box of group lane / 4; reduce over the 4 waves.
@@ -234,16 +238,19 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             size[g] = w.hh[g] * w.ww[g] * 16;
         }
         w.lds = size[0] + size[1] <= kTileBuf;
+        w.split = !w.lds && size[0] <= kTileBuf && size[1] <= kTileBuf;
         w.off[0] = 0;
-        w.off[1] = size[0];
+        w.off[1] = w.split ? 0 : size[0];
         return w;
     };
-    // LDS DMA of the windows of stage st as chunks of 64 consecutive window units (one
-    // instruction each), window g's chunks at LDS offset off[g] + 1024 c.
-    auto copy_windows = [&](int st, const Win& w) {
-        if (!w.lds) return;
+    // LDS DMA of the windows of stage st (both, or only window `only` of a split stage) as
+    // chunks of 64 consecutive window units (one instruction each), window g's chunks at
+    // LDS offset off[g] + 1024 c.
+    auto copy_windows = [&](int st, const Win& w, int only) {
+        if (!w.lds && !w.split) return;
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
+            if (only >= 0 && g != only) continue;
             const int ww = g ? w.ww[1] : w.ww[0];
             const int units = ww * (g ? w.hh[1] : w.hh[0]);
             const int chunks = (units + 63) >> 6;
@@ -311,9 +318,10 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         auto coords = [&](int j, Samples& C) {
             const int kk = j / NS, s = j % NS, k = T0 + kk;
             // float(oy*sh - ph + ky*dh) + dy (MetalShader.swift:327-332), one rounding: an
-            // fma with 1 is the same single rounding and takes the FP16 offset as it is.
-            const float y = __builtin_fmaf((float)offset_of(j, 0), 1.0f, ybf[s][k / 3]);
-            const float x = __builtin_fmaf((float)offset_of(j, 1), 1.0f, xbf[s][k % 3]);
+            // fma with 1 is the same single rounding and takes the FP16 offset as it is
+            // (v_fma_mix_f32; with a literal 1 the compiler folds it back into convert + add).
+            const float y = __builtin_fmaf((float)offset_of(j, 0), a.one, ybf[s][k / 3]);
+            const float x = __builtin_fmaf((float)offset_of(j, 1), a.one, xbf[s][k % 3]);
             const float fy = floorf(y), fx = floorf(x);
             const float ly = y - fy, lx = x - fx;
             // Clamped so both rows/columns of the corner pair stay in the padded plane.
@@ -357,11 +365,12 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             const int x0 = g ? w.x0[1] : w.x0[0];
             const int ww = g ? w.ww[1] : w.ww[0];
             const int off = g ? w.off[1] : w.off[0];
+            const bool in_lds = w.lds || w.split;
             Addressing r;
-            r.rs = w.lds ? ww * 16 : a.Wp * 16;
+            r.rs = in_lds ? ww * 16 : a.Wp * 16;
             r.pitch = (uint32_t)r.rs;
-            r.c = w.lds ? off - y0 * ww * 16 - x0 * 16
-                        : ((((b * a.CBLK + 2 * st + g) * a.Hp + kPad) * a.Wp) + kPad) * 16;
+            r.c = in_lds ? off - y0 * ww * 16 - x0 * 16
+                         : ((((b * a.CBLK + 2 * st + g) * a.Hp + kPad) * a.Wp) + kPad) * 16;
             return r;
         };
         auto make_address = [&](int j, Samples& C, const Addressing& r) {
@@ -378,23 +387,26 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
                 Bq[kk][nb] = __builtin_bit_cast(
                     h8, load16(wr, (uint32_t)(((st * 9 + T0 + kk) * NB + nb) * 64 + lane) * 16u, 0));
         };
-        // The LDS reads are issued in both modes (from LDS address 0 when the stage
-        // gathers from global memory; the global loads then replace them, and this branch
-        // waits for them at once). The compiler's waits are placed for every path of the
-        // control flow and count memory operations in issue order: with the LDS reads
-        // inside the branch (or global loads left in flight), the blend of each sample
-        // waited for the next sample's corner reads, or for the weight fragments requested
-        // after them, and the prefetch hid nothing. Only stages whose windows overflow the
-        // buffer take the global branch.
-        auto corners = [&](int j, const Samples& C, const Addressing& r, bool from_lds, u32x4 (&q)[4]) {
-            const uint32_t a0 = C.a[j], a1 = C.a[j] + r.pitch;
-            const uint32_t l0 = from_lds ? a0 : 0u, l1 = from_lds ? a1 : 0u;
+        // The LDS reads are issued in both modes: lanes that are not `active` (all of them
+        // when the stage gathers from global memory, the other group's in a pass of a
+        // split stage) read the 32 zero bytes, so their blend is 0 (their global loads then
+        // replace them, and this branch waits for those at once). The compiler's waits are
+        // placed for every path of the control flow and count memory operations in issue
+        // order: with the LDS reads inside the branch (or global loads left in flight), the
+        // blend of each sample waited for the next sample's corner reads, or for the weight
+        // fragments requested after them, and the prefetch hid nothing. Only stages whose
+        // windows do not fit the buffer one at a time take the global branch.
+        auto corners = [&](int j, const Samples& C, const Addressing& r, bool from_lds, bool active,
+                           uint32_t lds_pitch, u32x4 (&q)[4]) {
+            const uint32_t a0 = C.a[j];
+            const uint32_t l0 = active ? a0 : (uint32_t)kTileZero, l1 = l0 + lds_pitch;
             typedef const __attribute__((address_space(3))) u32x4* lds_u32x4;
             q[0] = *(lds_u32x4)(uintptr_t)l0;
             q[1] = *(lds_u32x4)(uintptr_t)(l0 + 16);
             q[2] = *(lds_u32x4)(uintptr_t)l1;
             q[3] = *(lds_u32x4)(uintptr_t)(l1 + 16);
             if (!from_lds) {
+                const uint32_t a1 = a0 + r.pitch;
                 q[0] = load16(xr, a0, 0);
                 q[1] = load16(xr, a0 + 16u, 0);
                 q[2] = load16(xr, a1, 0);
@@ -402,25 +414,28 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             }
         };
-        // K-loop of one stage: per sample j (tap kk, segment s) the next sample's corners
-        // are requested before this one is blended and multiplied; after both segments of
-        // a tap the weight slot is refilled and side(kk) runs (the next stage's work).
-        auto kloop = [&](int st, const Samples& C, const Addressing& r, bool from_lds, auto&& side) {
+        // K-loop of one stage (or one pass of a split stage): per sample j (tap kk, segment
+        // s) the next sample's corners are requested before this one is blended and
+        // multiplied; after both segments of a tap the weight slot is refilled (in the
+        // stage's last pass) and side(kk) runs (the next stage's work, in its first pass).
+        auto kloop = [&](int st, const Samples& C, const Addressing& r, bool from_lds, bool active,
+                         bool last_pass, bool first_pass, auto&& side) {
+            const uint32_t lds_pitch = active ? r.pitch : 0u;
             u32x4 qa[4], qb[4];
-            corners(0, C, r, from_lds, qa);
+            corners(0, C, r, from_lds, active, lds_pitch, qa);
 #pragma unroll
             for (int j = 0; j < NSMP; ++j) {
                 u32x4(&cur)[4] = (j & 1) ? qb : qa;
                 u32x4(&nxt)[4] = (j & 1) ? qa : qb;
-                if (j + 1 < NSMP) corners(j + 1, C, r, from_lds, nxt);
+                if (j + 1 < NSMP) corners(j + 1, C, r, from_lds, active, lds_pitch, nxt);
                 const int kk = j / NS, s = j % NS;
                 const h8 A = blend_w(cur, C.w0[j], C.w1[j]);
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
                     acc[s][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bq[kk][nb], acc[s][nb], 0, 0, 0);
                 if (s == NS - 1) {
-                    if (st + 1 < stages) load_b(st + 1, kk);
-                    side(kk);
+                    if (last_pass && st + 1 < stages) load_b(st + 1, kk);
+                    if (first_pass) side(kk);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -433,7 +448,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             publish_box();
             __syncthreads();  // every box; every wave past its corner and offset reads
             win = read_windows();
-            copy_windows(st1, win);
+            copy_windows(st1, win, win.split ? 0 : -1);
             if (st1 + 1 < stages) copy_offsets(st1 + 1);
             ad = addressing(st1, win);
 #pragma unroll
@@ -447,16 +462,19 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
 #pragma unroll
         for (int kk = 0; kk < NTW; ++kk) load_b(0, kk);
         copy_offsets(0);
+        if (tid < 8) reinterpret_cast<uint32_t*>(lds + kTileZero)[tid] = 0u;
         __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();  // stage 0's offsets in LDS
+        __syncthreads();  // stage 0's offsets in LDS; the zero bytes
         box_reset();
 #pragma unroll
         for (int j = 0; j < NSMP; ++j) coords(j, ca);
         next_stage(0, ca);
 
-        // Iteration st: `cur` holds stage st's addresses; K-steps 0-1 also compute stage
-        // st+1's coordinates into `nxt` (from the offsets copied with st's windows).
-        auto iteration = [&](int st, Samples& cur, Samples& nxt) {
+        // Stage st: `ca` holds its addresses; K-steps 0-1 also compute stage st+1's
+        // coordinates into `cb` (from the offsets copied with st's windows), which then
+        // become `ca`. A split stage has a second pass: group 0's window is in LDS
+        // (next_stage), then group 1's.
+        for (int st = 0; st < stages; ++st) {
             const bool more = st + 1 < stages;
             if (more) box_reset();
             constexpr int kPerCoord = (NSMP + 1) / 2;
@@ -464,14 +482,21 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
                 if (!more || kk >= 2) return;
 #pragma unroll
                 for (int i = 0; i < kPerCoord; ++i)
-                    if (kk * kPerCoord + i < NSMP) coords(kk * kPerCoord + i, nxt);
+                    if (kk * kPerCoord + i < NSMP) coords(kk * kPerCoord + i, cb);
             };
-            kloop(st, cur, ad, win.lds, side);
-            if (more) next_stage(st + 1, nxt);
-        };
-        for (int st = 0; st < stages; st += 2) {
-            iteration(st, ca, cb);
-            if (st + 1 < stages) iteration(st + 1, cb, ca);
+            const bool in_lds = win.lds || win.split;
+            kloop(st, ca, ad, in_lds, win.lds || (win.split && half == 0), !win.split, true, side);
+            if (win.split) {
+                __syncthreads();  // every wave is done with group 0's window
+                copy_windows(st, win, 1);
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();  // group 1's window in LDS
+                kloop(st, ca, ad, true, half == 1, true, false, side);
+            }
+            if (more) {
+                next_stage(st + 1, cb);
+                ca = cb;
+            }
         }
     };
     if (wave < 2) run(std::integral_constant<int, 0>{}, std::integral_constant<int, 5>{});
@@ -627,6 +652,7 @@ hipError_t launch_tile_f16(const KShape& s, const FusedGeometry& g, const FusedC
     a.Hp = g.hp;
     a.Wp = g.wp;
     a.Cout = s.Cout;
+    a.one = 1.0f;
     const int tw = cfg.mt == 32 ? 32 : 16;  // for this variant, mt carries the tile width
     const int th = 4 * 32 / tw;  // 2 pixel blocks x 2 segments of 32 pixels
     a.tiles_y = (s.Ho + th - 1) / th;

@@ -253,9 +253,9 @@ def test_fused_configs(gpu_ctx, dcn, c2, variant, mt, ks, sampler):
 
 def test_automatic_config_per_workload(gpu_ctx, dcn):
     """The automatic choice: narrow 16-pixel tiles for one 64 x 64 map (C2), the tile kernel
-    for batches of small maps (C3), the window kernel for one large map (C5); the exact
-    sampler never gets the tile kernel (it implements the fast one only)."""
-    want = {2: dcn.VARIANT_NARROW, 3: 7, 5: 3}
+    for batches of small maps (C3) and for one large map (C5); the exact sampler never gets
+    the tile kernel (it implements the fast one only)."""
+    want = {2: dcn.VARIANT_NARROW, 3: 7, 5: 7}
     for c, v in want.items():
         assert gpu_ctx.get_fused_config(dcn.config_shape(c))["variant"] == v, c
     gpu_ctx.set_fused_config(0, 0, dcn.SAMPLER_EXACT)
@@ -472,6 +472,66 @@ def test_tile_stages_lds_and_global(gpu_ctx, dcn, oracle, tw):
          "weight": (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16),
          "bias": (rng.standard_normal(64) * 0.1).astype(np.float16)}
     log("case: tile variant, LDS and global stages, width", tw)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(tw, 8, -1, 7)
+    try:
+        assert gpu_ctx.get_fused_config(s)["variant"] == 7
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+        again = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    assert np.array_equal(out.view(np.uint16), again.view(np.uint16))
+    w = widen(h)
+    ref = oracle.forward_f32_threads(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    mx, mean = errors(out, ref)
+    log(f"  max {mx:.3e} mean {mean:.3e}")
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
+def tile_stage_windows(off, H, W, G, th, tw):
+    """Bytes of the two CB8 windows of every (map, tile, stage) of the tile variant: each
+    window is the bounding box of the clamped sample corners of the stage's group over the
+    tile, plus one row and column (16 bytes per pixel)."""
+    off = off.astype(np.float32).reshape(-1, G, 9, 2, H, W)
+    ky = (np.arange(9) // 3)[None, :, None, None] - 1
+    kx = (np.arange(9) % 3)[None, :, None, None] - 1
+    sizes = []
+    for b in range(off.shape[0]):
+        iy = np.clip(np.floor(np.arange(H)[None, None, :, None] + ky + off[b, :, :, 0]), -2, H).astype(int)
+        ix = np.clip(np.floor(np.arange(W)[None, None, None, :] + kx + off[b, :, :, 1]), -2, W).astype(int)
+        for ty in range(0, H, th):
+            for tx in range(0, W, tw):
+                for st in range(G // 2):
+                    pair = []
+                    for g in (2 * st, 2 * st + 1):
+                        y = iy[g, :, ty:ty + th, tx:tx + tw]
+                        x = ix[g, :, ty:ty + th, tx:tx + tw]
+                        pair.append((y.max() - y.min() + 2) * (x.max() - x.min() + 2) * 16)
+                    sizes.append(pair)
+    return np.array(sizes)
+
+
+@pytest.mark.parametrize("tw", [16, 32])
+def test_tile_split_stages(gpu_ctx, dcn, oracle, tw):
+    """The tile variant with offsets of +-3 px in groups 0-7 and +-20 px in groups 8-15:
+    stages 4-7 have windows that fit the 64 KB LDS buffer one at a time but not together,
+    so each runs one pass per group (the other group's lanes masked to zero); within the
+    FP16 bars of the FP32 oracle, and deterministic."""
+    s = dcn.DeformConvShape(2, 128, 64, 64, 64, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    rng = np.random.default_rng(100 + tw)
+    c = s.counts()
+    off = rng.uniform(-3, 3, c["offset"]).reshape(2, 16, 18, 64 * 64)
+    off[:, 8:] = rng.uniform(-20, 20, off[:, 8:].shape)
+    off = off.reshape(-1).astype(np.float16)
+    sizes = tile_stage_windows(off, 64, 64, 16, 8 * 16 // tw, tw)
+    split = (sizes.sum(axis=1) > 65536) & (sizes.max(axis=1) <= 65536)
+    assert split.sum() >= 8, "the case must exercise split stages"
+    h = {"input": rng.standard_normal(c["input"]).astype(np.float16),
+         "offset": off,
+         "mask": rng.random(c["mask"]).astype(np.float16),
+         "weight": (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16),
+         "bias": (rng.standard_normal(64) * 0.1).astype(np.float16)}
+    log("case: tile variant, split stages, width", tw, "split stages", int(split.sum()), "of", len(split))
     packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
     gpu_ctx.set_fused_config(tw, 8, -1, 7)
     try:
