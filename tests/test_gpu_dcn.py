@@ -708,6 +708,30 @@ def test_fp16_overflow_is_flagged(gpu_ctx, dcn, c2):
     assert e.value.is_recoverable_numerical_failure
 
 
+@pytest.mark.parametrize("dims", [(2, 16, 7, 24), (1, 128, 64, 64), (3, 8, 5, 13), (1, 32, 9, 8)],
+                         ids=lambda t: "x".join(map(str, t)))
+def test_pack_input_cb8_layout(gpu_ctx, dcn, dims):
+    """The CB8 repack equals the padded channel-block transpose of the input, border
+    included, bit for bit, over an output buffer that held other values (widths that are
+    and are not multiples of 8, batches, odd heights)."""
+    import torch
+
+    b, c, h, w = dims
+    s = dcn.DeformConvShape(b, c, h, w, 32, h, w, 3, 3, 1, 1, 1, 1, 1, 1, 1, c // 8)
+    log("case: CB8 repack", dims)
+    rng = np.random.default_rng(sum(dims))
+    x = rng.integers(0, 1 << 16, b * c * h * w, dtype=np.uint16)
+    xd = torch.tensor(x.view(np.int16)).cuda()
+    cb8 = torch.full((gpu_ctx.cb8_count(s),), -1, dtype=torch.int16, device="cuda")
+    gpu_ctx.pack_input_cb8_dev(s, xd, cb8)
+    torch.cuda.synchronize()
+    ref = np.zeros((b, c // 8, h + 4, w + 4, 8), np.uint16)
+    ref[:, :, 2:h + 2, 2:w + 2] = x.reshape(b, c // 8, 8, h, w).transpose(0, 1, 3, 4, 2)
+    got = cb8.cpu().numpy().view(np.uint16)
+    assert got.size >= ref.size
+    assert np.array_equal(got[:ref.size].reshape(ref.shape), ref)
+
+
 def test_device_entry_points_and_graph_replay(gpu_ctx, dcn, c2):
     import torch
 
