@@ -14,6 +14,11 @@ algorithmic bytes per launch over that duration.
 Config 1 is the FP32 entry point (runFloat32): one direct kernel per call, in the CPU
 oracle's summation order, priced against the FP32 matrix peak.
 
+--dtype bf16 (configs 2, 3, 5) measures the BF16 storage path instead (dcn_forward_bf16_
+prepacked_dev: the same repack, then the register-variant fused kernel with the BF16
+sampler and BF16 MFMA); its timed output is checked against the FP32 oracle on the
+widened BF16 inputs with bars 8x the FP16 ones.
+
 cpu_baseline: the CPU oracle (a C restatement of the reference's DeformConvCPU.run),
 single thread, on a bounded sample of the benchmarked workload with the same inputs; its
 output of that sample also checks the GPU's timed output (timed_output_check).
@@ -81,7 +86,8 @@ def _cpu_name() -> str:
     return "unknown"
 
 
-def cpu_baseline(config: int, s, inputs: dict, gpu_out, budget_s: float = 25.0) -> tuple[dict, dict]:
+def cpu_baseline(config: int, s, inputs: dict, gpu_out, budget_s: float = 25.0,
+                 bars: tuple[float, float] = (MAX_ABS_F16, MEAN_ABS_F16)) -> tuple[dict, dict]:
     """The CPU oracle (C restatement of DeformConvCPU.run, DeformConv.swift:76-138) timed on
     a bounded sample of the benchmarked workload, single thread, on the same (FP16-rounded
     for C2/C3/C5) inputs the GPU ran; value is scaled to one whole call. Its output of the
@@ -165,8 +171,8 @@ def cpu_baseline(config: int, s, inputs: dict, gpu_out, budget_s: float = 25.0) 
         check["bound"] = "bit-exact"
         check["within"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
     else:
-        check["bound"] = {"max": MAX_ABS_F16, "mean": MEAN_ABS_F16}
-        check["within"] = bool(check["max_abs_err"] <= MAX_ABS_F16 and check["mean_abs_err"] <= MEAN_ABS_F16)
+        check["bound"] = {"max": bars[0], "mean": bars[1]}
+        check["within"] = bool(check["max_abs_err"] <= bars[0] and check["mean_abs_err"] <= bars[1])
     return baseline, check
 
 
@@ -668,6 +674,9 @@ def main() -> int:
     ap.add_argument("--ks", type=int, default=0, help="pin the fused config's ks (0 = automatic)")
     ap.add_argument("--frames-only", action="store_true",
                     help="config 4: time the per-frame graphs only (no clip, no 16-tile step)")
+    ap.add_argument("--dtype", choices=("f16", "bf16"), default="f16",
+                    help="configs 2, 3, 5: FP16 storage (the reference's) or BF16 storage (the BF16 "
+                         "fused path, register variant)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run three device copies of this many MiB (the known-size "
                          "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -679,6 +688,11 @@ def main() -> int:
         return 2
     if args.steps < 1:
         print("--steps must be >= 1", file=sys.stderr)
+        return 2
+    bf16 = args.dtype == "bf16"
+    if bf16 and (args.spynet or args.config in (1, 4) or args.variant or args.mt or args.ks):
+        print("--dtype bf16 measures the BF16 fused forward of configs 2, 3 and 5 (register variant, "
+              "automatic tiles)", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -698,6 +712,9 @@ def main() -> int:
     if f32:
         h = {k: np.asarray(d[k], np.float32) for k in keys}
         dev = {k: torch.from_numpy(h[k]).cuda() for k in keys}
+    elif bf16:
+        h = {k: dc.f32_to_bf16_bits(d[k]) for k in keys}
+        dev = {k: torch.from_numpy(h[k].view(np.int16)).cuda() for k in keys}
     else:
         h = {k: np.asarray(d[k], np.float32).astype(np.float16) for k in keys}
         dev = {k: torch.from_numpy(h[k].view(np.int16)).cuda() for k in keys}
@@ -713,6 +730,21 @@ def main() -> int:
                                 stream=cur)
 
         fused_only = step  # one kernel per call
+    elif bf16:
+        packed = ctx.prepack_bf16_dev(s, dev["weight"], dev["bias"])
+        ctx.reserve(s)
+        # The BF16 forward's fixed choice: the register variant, 64-pixel tiles split over
+        # 4 K-waves once there are more than 1024 tiles of 32 pixels, else 32 over 8.
+        many = (s.batch * s.output_height * s.output_width + 31) // 32 > 1024
+        fused_cfg = {"variant": 1, "mt": 2 if many else 1, "ks": 4 if many else 8, "sampler": "bf16"}
+        out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
+        cb8 = torch.empty(ctx.cb8_count(s), dtype=torch.int16, device="cuda")
+
+        def step(cur):
+            ctx.forward_bf16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out, stream=cur)
+
+        def fused_only(cur):
+            ctx.forward_bf16_prepacked_cb8_dev(s, cb8, dev["offset"], dev["mask"], packed, out, stream=cur)
     else:
         packed = ctx.prepack_dev(s, dev["weight"], dev["bias"])
         ctx.reserve(s)
@@ -805,12 +837,19 @@ def main() -> int:
 
     # What was timed: the output of the last timed call (checked against the oracle in the
     # cpu_baseline leg below).
-    res = out.cpu().numpy() if f32 else out.cpu().numpy().view(np.float16).astype(np.float32)
+    if f32:
+        res = out.cpu().numpy()
+    elif bf16:
+        res = dc.bf16_bits_to_f32(out.cpu().numpy().view(np.uint16))
+    else:
+        res = out.cpu().numpy().view(np.float16).astype(np.float32)
     finite = bool(np.all(np.isfinite(res)))
 
     nbytes = algorithmic_bytes(s, elem=4 if f32 else 2)
     flops = s.flops
     workload_name = {1: "dcn_c1_fp32", 2: "dcn_c2_fp16", 3: "dcn_c3_fp16", 5: "dcn_c5_fp16"}[args.config]
+    if bf16:
+        workload_name = workload_name.replace("fp16", "bf16")
     kernel_name = KERNEL_NAMES[0] if f32 else KERNEL_NAMES.get(fused_cfg["variant"], "fused_kernel")
     traffic = read_traffic(f"{kernel_name}_{workload_name}")
     if f32:
@@ -842,10 +881,10 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if f32 else "f16",
+        "dtype": "f32" if f32 else args.dtype,
         "data": "synthetic (seeded SplitMix64/Box-Muller inputs of the benchmark distributions; random weights)",
         "config": {
-            "workload": WORKLOADS[args.config],
+            "workload": WORKLOADS[args.config].replace("FP16", "BF16") if bf16 else WORKLOADS[args.config],
             "batch": s.batch, "in_channels": s.input_channels, "height": s.input_height, "width": s.input_width,
             "out_channels": s.output_channels, "kernel": [s.kernel_height, s.kernel_width],
             "deformable_groups": s.offset_groups, "fused_config": fused_cfg,
@@ -866,12 +905,15 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": None,
     }
-    if args.config == 3:
+    if args.config == 3 and not bf16:
         line["per_gpu_share"] = bench_share(args, ctx, dc, d, dev)
     line["timed_output_check"] = None
     if not args.no_cpu_baseline:
+        # BF16 keeps 3 fewer significant bits than FP16: bars 8x the FP16 ones.
+        widened = {k: dc.bf16_bits_to_f32(h[k]) if bf16 else h[k].astype(np.float32) for k in keys}
         line["cpu_baseline"], line["timed_output_check"] = cpu_baseline(
-            args.config, s, {k: h[k].astype(np.float32) for k in keys}, res)
+            args.config, s, widened, res,
+            bars=(8 * MAX_ABS_F16, 8 * MEAN_ABS_F16) if bf16 else (MAX_ABS_F16, MEAN_ABS_F16))
     if packed is not None:
         packed.free()
     ctx.close()

@@ -213,6 +213,40 @@ dcn_status dcn_forward_f16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape* 
                                              const void* d_mask, const dcn_packed* packed,
                                              void* d_output, void* stream);
 
+/* ---- BF16 storage ------------------------------------------------------------- */
+/* The fused sampler + MFMA GEMM over BF16 tensors (input, offsets, mask, weight, bias,
+ * output as 16-bit BF16 bit patterns; FP32 accumulation). No counterpart in the
+ * reference, which computes in FP16 and FP32 only: this is the BF16 form of the fused
+ * FP16 GEMM that DCN's hot path asks for. The arithmetic is the FP16 exact sampler's
+ * (the reference gather of MetalShader.swift:299-381 in FP32, each sample rounded once,
+ * here to BF16), then bf16(acc + bias). Packed weights from dcn_prepack_bf16* only work
+ * with these entry points, and FP16 ones only with the FP16 entry points (a mismatch
+ * fails with DCN_INVALID_ARGUMENT). */
+dcn_status dcn_prepack_bf16(dcn_context* ctx, const dcn_shape* shape,
+                            const uint16_t* weight, size_t weight_count,
+                            dcn_weight_layout layout,
+                            const uint16_t* bias, size_t bias_count,
+                            dcn_packed** out);
+dcn_status dcn_prepack_bf16_dev(dcn_context* ctx, const dcn_shape* shape,
+                                const void* d_weight, dcn_weight_layout layout,
+                                const void* d_bias, void* stream, dcn_packed** out);
+dcn_status dcn_forward_bf16_prepacked(dcn_context* ctx, const dcn_shape* shape,
+                                      const uint16_t* input, size_t input_count,
+                                      const uint16_t* offset, size_t offset_count,
+                                      const uint16_t* mask, size_t mask_count,
+                                      const dcn_packed* packed,
+                                      uint16_t* output, size_t output_count);
+dcn_status dcn_forward_bf16_prepacked_dev(dcn_context* ctx, const dcn_shape* shape,
+                                          const void* d_input, const void* d_offset,
+                                          const void* d_mask, const dcn_packed* packed,
+                                          void* d_output, void* stream);
+/* The same from an input already in the padded channel-block layout (BF16 bits in the
+ * FP16 layout's places; dcn_pack_input_cb8_dev copies 16-bit words, so it makes it). */
+dcn_status dcn_forward_bf16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape* shape,
+                                              const void* d_cb8, const void* d_offset,
+                                              const void* d_mask, const dcn_packed* packed,
+                                              void* d_output, void* stream);
+
 /* Allocation-free variant of dcn_forward_f16_prepacked_dev. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under hipGraph
  * capture, tight serving loops, harnesses that forbid hipMalloc). The padded

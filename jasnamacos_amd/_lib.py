@@ -108,6 +108,16 @@ SIGNATURES: dict[str, tuple] = {
                                   C.POINTER(PackedP)]),
     "dcn_prepack_f16_dev": (C.c_int, [CtxP, ShapeP, c_void, C.c_int, c_void, c_void,
                                       C.POINTER(PackedP)]),
+    "dcn_prepack_bf16": (C.c_int, [CtxP, ShapeP, c_u16p, c_size, C.c_int, c_u16p, c_size,
+                                   C.POINTER(PackedP)]),
+    "dcn_prepack_bf16_dev": (C.c_int, [CtxP, ShapeP, c_void, C.c_int, c_void, c_void,
+                                       C.POINTER(PackedP)]),
+    "dcn_forward_bf16_prepacked": (C.c_int, [CtxP, ShapeP, c_u16p, c_size, c_u16p, c_size,
+                                             c_u16p, c_size, PackedP, c_u16p, c_size]),
+    "dcn_forward_bf16_prepacked_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void, PackedP,
+                                                 c_void, c_void]),
+    "dcn_forward_bf16_prepacked_cb8_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void, PackedP,
+                                                     c_void, c_void]),
     "dcn_packed_free": (None, [PackedP]),
     "dcn_load_dcnfp16": (C.c_int, [CtxP, C.c_char_p, C.POINTER(PackedP)]),
     "dcn_dcnfp16_bytes": (c_size, []),

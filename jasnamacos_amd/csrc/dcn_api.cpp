@@ -132,7 +132,7 @@ dcn_status ensure_workspace(dcn_context* ctx, size_t bytes, hipStream_t stream) 
 dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const void* d_input,
                                bool input_is_cb8, const void* d_offset, const void* d_mask,
                                const dcn_packed* packed, void* d_output, hipStream_t stream,
-                               void* repack = nullptr, size_t repack_bytes = 0) {
+                               void* repack = nullptr, size_t repack_bytes = 0, bool bf16 = false) {
     dcn_counts c;
     DCN_TRY(validated_counts(ctx, shape, &c));
     if (!packed) return fail(ctx, DCN_INVALID_ARGUMENT, "packed weights are null");
@@ -146,13 +146,21 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
         return fail(ctx, DCN_INVALID_SHAPE, "packed weights were prepared for another layer shape");
     if (packed->device != ctx->device)
         return fail(ctx, DCN_INVALID_ARGUMENT, "packed weights live on another device");
+    if (packed->bf16 != bf16)
+        return fail(ctx, DCN_INVALID_ARGUMENT,
+                    packed->bf16 ? "packed weights are BF16: use dcn_forward_bf16_prepacked*"
+                                 : "packed weights are FP16: use dcn_forward_f16_prepacked*");
     if (dcn::cb8_bytes(*shape, g) >= ((size_t)1 << 31))
         return fail(ctx, DCN_INVALID_SHAPE, "padded input too large for 32-bit device indexing");
     // The packed weights carry the window / tile fragments only when the layer's shape at
     // prepack allowed those kernels; this call's shape must allow them too.
+    // BF16: the register variant, 64- or 32-pixel tiles by problem size.
+    const long long tiles32 = (g.m + 31) / 32;
     const dcn::FusedConfig cfg =
-        choose_config(ctx, g, *shape, packed->weights_group != nullptr && dcn::window_supported(*shape),
-                      packed->weights_tile != nullptr && dcn::tile_supported(*shape));
+        bf16 ? dcn::FusedConfig{dcn::kVariantRegister, tiles32 > 1024 ? 2 : 1, tiles32 > 1024 ? 4 : 8,
+                                dcn::kSamplerBf16}
+             : choose_config(ctx, g, *shape, packed->weights_group != nullptr && dcn::window_supported(*shape),
+                             packed->weights_tile != nullptr && dcn::tile_supported(*shape));
     if (!config_supported(cfg, g))
         return fail(ctx, DCN_INVALID_ARGUMENT,
                     "unsupported fused config (variant " + std::to_string(cfg.variant) + ", mt " +
@@ -418,7 +426,8 @@ dcn_status dcn_forward_f16(dcn_context* ctx, const dcn_shape* shape, const uint1
 
 // ---- prepack -------------------------------------------------------------------
 
-static dcn_status make_packed(dcn_context* ctx, const dcn_shape* shape, dcn_packed** created) {
+static dcn_status make_packed(dcn_context* ctx, const dcn_shape* shape, dcn_packed** created,
+                              bool bf16) {
     dcn::FusedGeometry g;
     if (!dcn::fused_geometry(*shape, &g))
         return fail(ctx, DCN_INVALID_SHAPE,
@@ -427,12 +436,14 @@ static dcn_status make_packed(dcn_context* ctx, const dcn_shape* shape, dcn_pack
     p->shape = *shape;
     p->geometry = g;
     p->device = ctx->device;
+    p->bf16 = bf16;
+    // BF16 runs the register variant only: no narrow, window or tile fragments.
     if (hipMalloc(&p->weights, dcn::packed_weight_bytes(g)) != hipSuccess ||
         hipMalloc((void**)&p->bias, (size_t)shape->output_channels * sizeof(float)) != hipSuccess ||
-        hipMalloc(&p->weights_narrow, dcn::narrow_packed_bytes(g)) != hipSuccess ||
-        (dcn::window_supported(*shape) &&
+        (!bf16 && hipMalloc(&p->weights_narrow, dcn::narrow_packed_bytes(g)) != hipSuccess) ||
+        (!bf16 && dcn::window_supported(*shape) &&
          hipMalloc(&p->weights_group, dcn::window_packed_bytes(*shape)) != hipSuccess) ||
-        (dcn::tile_supported(*shape) &&
+        (!bf16 && dcn::tile_supported(*shape) &&
          hipMalloc(&p->weights_tile, dcn::tile_packed_bytes(*shape)) != hipSuccess)) {
         dcn_packed_free(p);
         return fail(ctx, DCN_COMMAND_FAILED, "hipMalloc of packed weights failed");
@@ -441,9 +452,9 @@ static dcn_status make_packed(dcn_context* ctx, const dcn_shape* shape, dcn_pack
     return DCN_OK;
 }
 
-dcn_status dcn_prepack_f16_dev(dcn_context* ctx, const dcn_shape* shape, const void* d_weight,
-                               dcn_weight_layout layout, const void* d_bias, void* stream,
-                               dcn_packed** out) {
+static dcn_status prepack_dev(dcn_context* ctx, const dcn_shape* shape, const void* d_weight,
+                              dcn_weight_layout layout, const void* d_bias, void* stream,
+                              dcn_packed** out, bool bf16) {
     if (!ctx || !out) return DCN_INVALID_ARGUMENT;
     *out = nullptr;
     DeviceGuard guard(ctx->device);
@@ -453,12 +464,12 @@ dcn_status dcn_prepack_f16_dev(dcn_context* ctx, const dcn_shape* shape, const v
     if (layout != DCN_LAYOUT_OIHW && layout != DCN_LAYOUT_IC_K_OC)
         return fail(ctx, DCN_INVALID_ARGUMENT, "unknown weight layout");
     dcn_packed* p = nullptr;
-    DCN_TRY(make_packed(ctx, shape, &p));
+    DCN_TRY(make_packed(ctx, shape, &p, bf16));
     hipError_t e = dcn::launch_prepack_weights(dcn::to_kshape(*shape), p->geometry,
                                                (const uint16_t*)d_weight, (int)layout,
                                                (const uint16_t*)d_bias, p->weights, p->bias,
-                                               (hipStream_t)stream);
-    if (e == hipSuccess)
+                                               (hipStream_t)stream, bf16);
+    if (e == hipSuccess && p->weights_narrow)
         e = dcn::launch_prepack_narrow(dcn::to_kshape(*shape), p->geometry, (const uint16_t*)d_weight,
                                        (int)layout, p->weights_narrow, (hipStream_t)stream);
     if (e == hipSuccess && p->weights_group)
@@ -475,9 +486,21 @@ dcn_status dcn_prepack_f16_dev(dcn_context* ctx, const dcn_shape* shape, const v
     return DCN_OK;
 }
 
-dcn_status dcn_prepack_f16(dcn_context* ctx, const dcn_shape* shape, const uint16_t* weight,
-                           size_t weight_count, dcn_weight_layout layout, const uint16_t* bias,
-                           size_t bias_count, dcn_packed** out) {
+dcn_status dcn_prepack_f16_dev(dcn_context* ctx, const dcn_shape* shape, const void* d_weight,
+                               dcn_weight_layout layout, const void* d_bias, void* stream,
+                               dcn_packed** out) {
+    return prepack_dev(ctx, shape, d_weight, layout, d_bias, stream, out, false);
+}
+
+dcn_status dcn_prepack_bf16_dev(dcn_context* ctx, const dcn_shape* shape, const void* d_weight,
+                                dcn_weight_layout layout, const void* d_bias, void* stream,
+                                dcn_packed** out) {
+    return prepack_dev(ctx, shape, d_weight, layout, d_bias, stream, out, true);
+}
+
+static dcn_status prepack_host(dcn_context* ctx, const dcn_shape* shape, const uint16_t* weight,
+                               size_t weight_count, dcn_weight_layout layout, const uint16_t* bias,
+                               size_t bias_count, dcn_packed** out, bool bf16) {
     if (!ctx || !out) return DCN_INVALID_ARGUMENT;
     *out = nullptr;
     DeviceGuard guard(ctx->device);
@@ -490,7 +513,7 @@ dcn_status dcn_prepack_f16(dcn_context* ctx, const dcn_shape* shape, const uint1
     DCN_TRY(upload(ctx, dw, weight, c.weight));
     DCN_TRY(upload(ctx, db, bias, c.bias));
     dcn_packed* p = nullptr;
-    DCN_TRY(dcn_prepack_f16_dev(ctx, shape, dw.p, layout, db.p, nullptr, &p));
+    DCN_TRY(prepack_dev(ctx, shape, dw.p, layout, db.p, nullptr, &p, bf16));
     const hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         dcn_packed_free(p);
@@ -498,6 +521,18 @@ dcn_status dcn_prepack_f16(dcn_context* ctx, const dcn_shape* shape, const uint1
     }
     *out = p;
     return DCN_OK;
+}
+
+dcn_status dcn_prepack_f16(dcn_context* ctx, const dcn_shape* shape, const uint16_t* weight,
+                           size_t weight_count, dcn_weight_layout layout, const uint16_t* bias,
+                           size_t bias_count, dcn_packed** out) {
+    return prepack_host(ctx, shape, weight, weight_count, layout, bias, bias_count, out, false);
+}
+
+dcn_status dcn_prepack_bf16(dcn_context* ctx, const dcn_shape* shape, const uint16_t* weight,
+                            size_t weight_count, dcn_weight_layout layout, const uint16_t* bias,
+                            size_t bias_count, dcn_packed** out) {
+    return prepack_host(ctx, shape, weight, weight_count, layout, bias, bias_count, out, true);
 }
 
 void dcn_packed_free(dcn_packed* p) {
@@ -600,12 +635,32 @@ dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_sha
                                (hipStream_t)stream, scratch, DCN_NOALLOC_SCRATCH_BYTES);
 }
 
-dcn_status dcn_forward_f16_prepacked(dcn_context* ctx, const dcn_shape* shape,
-                                     const uint16_t* input, size_t input_count,
-                                     const uint16_t* offset, size_t offset_count,
-                                     const uint16_t* mask, size_t mask_count,
-                                     const dcn_packed* packed, uint16_t* output,
-                                     size_t output_count) {
+dcn_status dcn_forward_bf16_prepacked_dev(dcn_context* ctx, const dcn_shape* shape,
+                                          const void* d_input, const void* d_offset,
+                                          const void* d_mask, const dcn_packed* packed,
+                                          void* d_output, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    DeviceGuard guard(ctx->device);
+    return fused_prepacked_dev(ctx, shape, d_input, false, d_offset, d_mask, packed, d_output,
+                               (hipStream_t)stream, nullptr, 0, true);
+}
+
+dcn_status dcn_forward_bf16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape* shape,
+                                              const void* d_cb8, const void* d_offset,
+                                              const void* d_mask, const dcn_packed* packed,
+                                              void* d_output, void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    DeviceGuard guard(ctx->device);
+    return fused_prepacked_dev(ctx, shape, d_cb8, true, d_offset, d_mask, packed, d_output,
+                               (hipStream_t)stream, nullptr, 0, true);
+}
+
+static dcn_status forward_prepacked_host(dcn_context* ctx, const dcn_shape* shape,
+                                         const uint16_t* input, size_t input_count,
+                                         const uint16_t* offset, size_t offset_count,
+                                         const uint16_t* mask, size_t mask_count,
+                                         const dcn_packed* packed, uint16_t* output,
+                                         size_t output_count, bool bf16) {
     if (!ctx) return DCN_INVALID_ARGUMENT;
     DeviceGuard guard(ctx->device);
     dcn_counts c;
@@ -621,10 +676,31 @@ dcn_status dcn_forward_f16_prepacked(dcn_context* ctx, const dcn_shape* shape,
     DCN_TRY(upload(ctx, doff, offset, c.offset));
     DCN_TRY(upload(ctx, dm, mask, c.mask));
     DCN_HIP(ctx, hipMalloc(&dout.p, c.output * sizeof(uint16_t)));
-    DCN_TRY(fused_prepacked_dev(ctx, shape, di.p, false, doff.p, dm.p, packed, dout.p, nullptr));
+    DCN_TRY(fused_prepacked_dev(ctx, shape, di.p, false, doff.p, dm.p, packed, dout.p, nullptr,
+                                nullptr, 0, bf16));
     DCN_HIP(ctx, hipMemcpy(output, dout.p, c.output * sizeof(uint16_t), hipMemcpyDeviceToHost));
     DCN_HIP(ctx, hipDeviceSynchronize());
     return DCN_OK;
+}
+
+dcn_status dcn_forward_f16_prepacked(dcn_context* ctx, const dcn_shape* shape,
+                                     const uint16_t* input, size_t input_count,
+                                     const uint16_t* offset, size_t offset_count,
+                                     const uint16_t* mask, size_t mask_count,
+                                     const dcn_packed* packed, uint16_t* output,
+                                     size_t output_count) {
+    return forward_prepacked_host(ctx, shape, input, input_count, offset, offset_count, mask,
+                                  mask_count, packed, output, output_count, false);
+}
+
+dcn_status dcn_forward_bf16_prepacked(dcn_context* ctx, const dcn_shape* shape,
+                                      const uint16_t* input, size_t input_count,
+                                      const uint16_t* offset, size_t offset_count,
+                                      const uint16_t* mask, size_t mask_count,
+                                      const dcn_packed* packed, uint16_t* output,
+                                      size_t output_count) {
+    return forward_prepacked_host(ctx, shape, input, input_count, offset, offset_count, mask,
+                                  mask_count, packed, output, output_count, true);
 }
 
 dcn_status dcn_im2col_f16_dev(dcn_context* ctx, const dcn_shape* shape, const void* d_input,

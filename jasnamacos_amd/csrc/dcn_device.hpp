@@ -34,6 +34,12 @@ __device__ __forceinline__ float load_half(__amdgpu_buffer_rsrc_t r, uint32_t vo
     const short v = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
     return (float)__builtin_bit_cast(_Float16, v);
 }
+// A BF16 value widened exactly: its 16 bits are the high half of the FP32 value.
+__device__ __forceinline__ float load_bf16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                           uint32_t soff = 0) {
+    const short v = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+    return __builtin_bit_cast(float, (uint32_t)(uint16_t)v << 16);
+}
 
 // floor(x / d) for 0 <= x < 2^16 and 0 < d < 2^16, magic = ceil(2^32 / d) for d > 1
 // and 0 for d == 1 (magic_for on the host).
@@ -74,9 +80,35 @@ __device__ __forceinline__ h8 blend_fast(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 
     return r;
 }
 
+// blend_exact for BF16 storage: the eight BF16 channels of each corner widened exactly,
+// the same FP32 arithmetic and association, each sample rounded once to BF16. Returns
+// the eight BF16 values' bits in an h8 (the MFMA operand register layout is the same).
+__device__ __forceinline__ h8 blend_bf16(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 q11, float ly,
+                                         float lx, float m) {
+    u32x4 r;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint32_t packed = 0u;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // channel 2d + h: the low (h = 0) or high (h = 1) 16 bits of dword d
+            auto widen = [&](uint32_t w) {
+                return __builtin_bit_cast(float, h ? (w & 0xffff0000u) : (w << 16));
+            };
+            const float s = widen(q00[d]) * (1.0f - ly) * (1.0f - lx) +
+                            widen(q01[d]) * (1.0f - ly) * lx + widen(q10[d]) * ly * (1.0f - lx) +
+                            widen(q11[d]) * ly * lx;
+            packed |= (uint32_t)round_bf16_bits(s * m) << (16 * h);
+        }
+        r[d] = packed;
+    }
+    return __builtin_bit_cast(h8, r);
+}
+
 template <int SAMPLER>
 __device__ __forceinline__ h8 blend(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 q11, float ly, float lx,
                                     float m) {
+    if constexpr (SAMPLER == kSamplerBf16) return blend_bf16(q00, q01, q10, q11, ly, lx, m);
     return SAMPLER == kSamplerExact ? blend_exact(q00, q01, q10, q11, ly, lx, m)
                                     : blend_fast(q00, q01, q10, q11, ly, lx, m);
 }

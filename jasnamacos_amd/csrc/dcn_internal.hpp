@@ -64,6 +64,10 @@ enum SamplerMode : int {
     // Mask folded into the four bilinear weights, packed-FP16 blend. Faster; within
     // the FP16 tolerance against the FP32 oracle.
     kSamplerFast = 1,
+    // BF16 storage (input, offsets, mask, weights, output): the exact sampler's FP32
+    // arithmetic on the widened BF16 corners, each sample rounded once to BF16, and the
+    // BF16 MFMA (the register variant only).
+    kSamplerBf16 = 2,
 };
 
 enum FusedVariant : int {
@@ -139,7 +143,7 @@ hipError_t noalloc_scratch_init(int device);
 void* noalloc_scratch(int device);
 hipError_t launch_prepack_weights(const KShape& s, const FusedGeometry& g, const uint16_t* w,
                                   int layout, const uint16_t* bias, void* packed_w,
-                                  float* packed_b, hipStream_t stream);
+                                  float* packed_b, hipStream_t stream, bool bias_bf16 = false);
 hipError_t launch_fused_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
                             const void* cb8, const uint16_t* off, const uint16_t* mask,
                             const void* packed_w, const float* packed_b, uint16_t* out,
@@ -319,6 +323,11 @@ __device__ __forceinline__ _Float16 round_f16(float v) {
     __asm__ volatile("" : "+v"(v));
     return (_Float16)v;
 }
+// The same for BF16 (nearest even, v_cvt_pk_bf16_f32), returned as its 16 bits.
+__device__ __forceinline__ uint16_t round_bf16_bits(float v) {
+    __asm__ volatile("" : "+v"(v));
+    return __builtin_bit_cast(uint16_t, (__bf16)v);
+}
 #endif
 
 // Host utilities (dcn_host_util.cpp).
@@ -346,4 +355,5 @@ struct dcn_packed {
     void* weights_tile = nullptr;   // tap-major B fragments of the tile variant (or null)
     float* bias = nullptr;      // Cout floats
     int device = 0;
+    bool bf16 = false;          // BF16 weights (dcn_prepack_bf16*): the register variant only
 };

@@ -41,6 +41,8 @@ namespace {
 
 using namespace dev;
 
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 
 struct FusedArgs {
@@ -113,9 +115,13 @@ __global__ __launch_bounds__(64 * KS) void fused_kernel(FusedArgs a) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const bool live = pvalid[mt] && kvalid;
-            const float dy = load_half(orr, (offb[mt] + (uint32_t)(2 * gt) * a.HWo) * 2u);
-            const float dx = load_half(orr, (offb[mt] + (uint32_t)(2 * gt + 1) * a.HWo) * 2u);
-            float m = load_half(mr, (mskb[mt] + (uint32_t)gt * a.HWo) * 2u);
+            constexpr bool kBf16 = SAMPLER == kSamplerBf16;
+            const uint32_t dyo = (offb[mt] + (uint32_t)(2 * gt) * a.HWo) * 2u;
+            const uint32_t dxo = (offb[mt] + (uint32_t)(2 * gt + 1) * a.HWo) * 2u;
+            const uint32_t mo = (mskb[mt] + (uint32_t)gt * a.HWo) * 2u;
+            const float dy = kBf16 ? load_bf16(orr, dyo) : load_half(orr, dyo);
+            const float dx = kBf16 ? load_bf16(orr, dxo) : load_half(orr, dxo);
+            float m = kBf16 ? load_bf16(mr, mo) : load_half(mr, mo);
             // y = float(oy*sh - ph + ky*dh) + dy, as MetalShader.swift:327-332.
             float y = (float)(base_y[mt] + ky * a.dh) + dy;
             float x = (float)(base_x[mt] + kx * a.dw) + dx;
@@ -145,9 +151,14 @@ __global__ __launch_bounds__(64 * KS) void fused_kernel(FusedArgs a) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                acc[mt][nb] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_f16(A[mt], Bf[nb], acc[mt][nb], 0, 0, 0);
+            for (int nb = 0; nb < NB; ++nb) {
+                if constexpr (SAMPLER == kSamplerBf16)
+                    acc[mt][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf8, A[mt]), __builtin_bit_cast(bf8, Bf[nb]), acc[mt][nb], 0, 0, 0);
+                else
+                    acc[mt][nb] =
+                        __builtin_amdgcn_mfma_f32_32x32x16_f16(A[mt], Bf[nb], acc[mt][nb], 0, 0, 0);
+            }
     }
 
     // Accumulator layout of a 32x32 MFMA: lane l holds column j = l%32 and rows
@@ -179,7 +190,8 @@ __global__ __launch_bounds__(64 * KS) void fused_kernel(FusedArgs a) {
             const int b = p / a.HWo;
             const int sp = p - b * a.HWo;
             a.out[((size_t)b * a.Cout + oc) * a.HWo + sp] =
-                __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
+                SAMPLER == kSamplerBf16 ? round_bf16_bits(sum + a.bias[oc])
+                                        : __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
         }
     }
 }
@@ -390,9 +402,11 @@ __global__ __launch_bounds__(256) void prepack_kernel(const uint16_t* __restrict
                                                       uint16_t* __restrict__ wpk,
                                                       float* __restrict__ bpk, int Cin, int Cout,
                                                       int KA, int CB, int KB, int NB, int MW,
-                                                      long total) {
+                                                      long total, int bias_bf16) {
     const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (bpk != nullptr && gid < Cout) bpk[gid] = (float)__builtin_bit_cast(_Float16, bias[gid]);
+    if (bpk != nullptr && gid < Cout)
+        bpk[gid] = bias_bf16 ? __builtin_bit_cast(float, (uint32_t)bias[gid] << 16)
+                             : (float)__builtin_bit_cast(_Float16, bias[gid]);
     if (gid >= total) return;
     const int e = (int)(gid & 7);
     const int lane = (int)((gid >> 3) & 63);
@@ -569,12 +583,12 @@ hipError_t launch_pack_cb8(const KShape& s, const FusedGeometry& g, const uint16
 
 hipError_t launch_prepack_weights(const KShape& s, const FusedGeometry& g, const uint16_t* w,
                                   int layout, const uint16_t* bias, void* packed_w,
-                                  float* packed_b, hipStream_t stream) {
+                                  float* packed_b, hipStream_t stream, bool bias_bf16) {
     const long total = (long)g.ksteps * g.nb * 64 * 8;
     const long grid = (std::max<long>(total, s.Cout) + 255) / 256;
     hipLaunchKernelGGL(prepack_kernel, dim3((unsigned)grid), dim3(256), 0, stream, w, layout, bias,
                        (uint16_t*)packed_w, packed_b, s.Cin, s.Cout, g.ka, g.cb, g.kb, g.nb, 32,
-                       total);
+                       total, bias_bf16 ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -584,7 +598,7 @@ hipError_t launch_prepack_narrow(const KShape& s, const FusedGeometry& g, const 
     const long grid = (total + 255) / 256;
     hipLaunchKernelGGL(prepack_kernel, dim3((unsigned)grid), dim3(256), 0, stream, w, layout,
                        (const uint16_t*)nullptr, (uint16_t*)packed_w, (float*)nullptr, s.Cin,
-                       s.Cout, g.ka, g.cb, g.kb, 2 * g.nb, 16, total);
+                       s.Cout, g.ka, g.cb, g.kb, 2 * g.nb, 16, total, 0);
     return hipGetLastError();
 }
 
@@ -631,6 +645,10 @@ hipError_t launch_fused_f16(const KShape& s, const FusedGeometry& g, const Fused
         if (lds > kMaxLds) return hipErrorInvalidValue;
         if (cfg.sampler == kSamplerExact) return launch_staged_s<kSamplerExact>(sa, g.nb, cfg, lds, stream);
         return launch_staged_s<kSamplerFast>(sa, g.nb, cfg, lds, stream);
+    }
+    if (cfg.sampler == kSamplerBf16) {
+        if (cfg.variant != kVariantRegister) return hipErrorInvalidValue;
+        return launch_fused_s<kSamplerBf16>(a, g.nb, cfg, stream);
     }
     if (cfg.sampler == kSamplerExact) return launch_fused_s<kSamplerExact>(a, g.nb, cfg, stream);
     return launch_fused_s<kSamplerFast>(a, g.nb, cfg, stream);

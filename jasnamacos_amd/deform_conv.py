@@ -157,6 +157,28 @@ def _u16(a) -> np.ndarray:
     raise TypeError(f"expected float16 or uint16 array, got {a.dtype}")
 
 
+def _bits16(a) -> np.ndarray:
+    """16-bit patterns of a BF16 tensor (numpy has no BF16 type: uint16 arrays)."""
+    a = np.asarray(a)
+    if a.dtype != np.uint16:
+        raise TypeError(f"expected BF16 bit patterns as a uint16 array, got {a.dtype}")
+    return np.ascontiguousarray(a)
+
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """Round FP32 values to BF16 (nearest, ties to even) and return the bit patterns;
+    NaN stays a quiet NaN."""
+    u = np.ascontiguousarray(np.asarray(x, np.float32)).view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(np.asarray(x, np.float32))
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded)
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    """Widen BF16 bit patterns to FP32 exactly."""
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
 def _fp(a: np.ndarray):
     return a.ctypes.data_as(_lib.c_f32p)
 
@@ -290,6 +312,46 @@ class HipDeformConv:
         self._check(self._lib.dcn_forward_f16_prepacked(self.ctx, C.byref(shape.to_c()), *args,
                                                         packed.handle, _hp(out), out.size))
         return out.view(np.float16)
+
+    # ---- BF16 storage (no counterpart in the reference) ----------------------------
+    def prepack_bf16(self, shape: DeformConvShape, weight, bias, layout: int = LAYOUT_OIHW) -> PackedWeights:
+        """Weights and bias as BF16 bit patterns (uint16 arrays); packed for
+        run_bfloat16_prepacked only."""
+        w = _bits16(weight).ravel()
+        b = _bits16(bias).ravel()
+        handle = C.c_void_p()
+        self._check(self._lib.dcn_prepack_bf16(self.ctx, C.byref(shape.to_c()), _hp(w), w.size, int(layout),
+                                               _hp(b), b.size, C.byref(handle)))
+        return PackedWeights(handle.value, shape)
+
+    def run_bfloat16_prepacked(self, shape: DeformConvShape, input, offset, mask,
+                               packed: PackedWeights) -> np.ndarray:
+        """The fused sampler + MFMA GEMM over BF16 tensors (uint16 bit patterns in and
+        out): FP32 bilinear in the reference's association, each sample rounded once to
+        BF16, BF16 MFMA with FP32 accumulation, bf16(acc + bias)."""
+        arrs = [_bits16(a).ravel() for a in (input, offset, mask)]
+        out = np.empty(shape.output_count, dtype=np.uint16)
+        args = []
+        for a in arrs:
+            args += [_hp(a), a.size]
+        self._check(self._lib.dcn_forward_bf16_prepacked(self.ctx, C.byref(shape.to_c()), *args,
+                                                         packed.handle, _hp(out), out.size))
+        return out
+
+    def prepack_bf16_dev(self, shape, w, b, layout: int = LAYOUT_OIHW, stream=None) -> PackedWeights:
+        handle = C.c_void_p()
+        self._check(self._lib.dcn_prepack_bf16_dev(self.ctx, C.byref(shape.to_c()), _ptr(w), int(layout), _ptr(b),
+                                                   _stream(stream), C.byref(handle)))
+        return PackedWeights(handle.value, shape)
+
+    def forward_bf16_prepacked_dev(self, shape, x, off, msk, packed: PackedWeights, out, stream=None) -> None:
+        self._check(self._lib.dcn_forward_bf16_prepacked_dev(self.ctx, C.byref(shape.to_c()), _ptr(x), _ptr(off),
+                                                             _ptr(msk), packed.handle, _ptr(out), _stream(stream)))
+
+    def forward_bf16_prepacked_cb8_dev(self, shape, cb8, off, msk, packed: PackedWeights, out, stream=None) -> None:
+        self._check(self._lib.dcn_forward_bf16_prepacked_cb8_dev(self.ctx, C.byref(shape.to_c()), _ptr(cb8),
+                                                                 _ptr(off), _ptr(msk), packed.handle, _ptr(out),
+                                                                 _stream(stream)))
 
     # ---- device-pointer entry points (torch tensors as plumbing) ------------------
     def forward_f32_dev(self, shape, x, off, msk, w, b, out, stream=None) -> None:

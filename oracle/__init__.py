@@ -39,6 +39,9 @@ _SIG = {
     "oracle_dcn_forward_f16_direct": (C.c_int, [_S, _h, _h, _h, _h, _h, _h]),
     "oracle_dcn_im2col_f16": (C.c_int, [_S, _h, _h, _h, _h]),
     "oracle_dcn_gemm_f16": (C.c_int, [_S, _h, _h, _h, _h]),
+    "oracle_dcn_im2col_bf16": (C.c_int, [_S, _h, _h, _h, _h]),
+    "oracle_f32_to_bf16": (C.c_uint16, [C.c_float]),
+    "oracle_bf16_to_f32": (C.c_float, [C.c_uint16]),
     "oracle_f32_to_f16": (C.c_uint16, [C.c_float]),
     "oracle_f16_to_f32": (C.c_float, [C.c_uint16]),
     "oracle_flag_nonfinite_f16": (C.c_uint32, [_h, C.c_size_t]),
@@ -87,6 +90,15 @@ def _u16(a):
     if a.dtype == np.float16:
         a = a.view(np.uint16)
     a = np.ascontiguousarray(a, dtype=np.uint16).ravel()
+    return a, a.ctypes.data_as(_h)
+
+
+def _bits(a):
+    """BF16 bit patterns (uint16 arrays; numpy has no BF16 type)."""
+    a = np.asarray(a)
+    if a.dtype != np.uint16:
+        raise TypeError(f"expected BF16 bit patterns as uint16, got {a.dtype}")
+    a = np.ascontiguousarray(a).ravel()
     return a, a.ctypes.data_as(_h)
 
 
@@ -170,6 +182,17 @@ def forward_f16_direct(shape, input, offset, mask, weight, bias) -> np.ndarray:
     if rc:
         raise ValueError("invalid shape")
     return out.view(np.float16)
+
+
+def im2col_bf16(shape, input, offset, mask) -> np.ndarray:
+    """The gather of im2col_f16 over BF16 storage (uint16 bit patterns in and out), each
+    sample rounded once to BF16: the columns of the library's BF16 fused path."""
+    keep = [_bits(a) for a in (input, offset, mask)]
+    out = np.empty(_counts(shape)["columns"], dtype=np.uint16)
+    rc = load().oracle_dcn_im2col_bf16(C.byref(_shape(shape)), *[p for _, p in keep], out.ctypes.data_as(_h))
+    if rc:
+        raise ValueError("invalid shape")
+    return out
 
 
 def im2col_f16(shape, input, offset, mask) -> np.ndarray:

@@ -309,6 +309,85 @@ int oracle_dcn_im2col_f16(const oracle_shape* s, const uint16_t* input,
     return 0;
 }
 
+uint16_t oracle_f32_to_bf16(float value) {
+    uint32_t x;
+    memcpy(&x, &value, sizeof x);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u); /* NaN */
+    x += 0x7fffu + ((x >> 16) & 1u); /* nearest, ties to even; a carry may reach Inf */
+    return (uint16_t)(x >> 16);
+}
+
+float oracle_bf16_to_f32(uint16_t bits) {
+    const uint32_t x = (uint32_t)bits << 16;
+    float f;
+    memcpy(&f, &x, sizeof f);
+    return f;
+}
+
+/* oracle_sample_zero_f16 over BF16 storage: the same corners, zero padding and
+ * association, values widened from BF16. */
+static float sample_zero_bf16(const uint16_t* values, size_t base, int height, int width,
+                              float y, float x) {
+    long y0 = (long)floorf(y);
+    long x0 = (long)floorf(x);
+    long y1 = y0 + 1;
+    long x1 = x0 + 1;
+    float ly = y - (float)y0;
+    float lx = x - (float)x0;
+#define ORACLE_VALUE_BF16(yy, xx)                                                       \
+    (((yy) >= 0 && (yy) < height && (xx) >= 0 && (xx) < width)                           \
+         ? oracle_bf16_to_f32(values[base + (size_t)(yy) * (size_t)width + (size_t)(xx)]) \
+         : 0.0f)
+    float v00 = ORACLE_VALUE_BF16(y0, x0);
+    float v01 = ORACLE_VALUE_BF16(y0, x1);
+    float v10 = ORACLE_VALUE_BF16(y1, x0);
+    float v11 = ORACLE_VALUE_BF16(y1, x1);
+#undef ORACLE_VALUE_BF16
+    return v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx +
+           v10 * ly * (1.0f - lx) + v11 * ly * lx;
+}
+
+int oracle_dcn_im2col_bf16(const oracle_shape* s, const uint16_t* input,
+                           const uint16_t* offset, const uint16_t* mask, uint16_t* columns) {
+    if (oracle_shape_validate(s)) return 1;
+    const long plane = (long)s->output_height * s->output_width;
+    const long input_plane = (long)s->input_height * s->input_width;
+    const long kernel_area = (long)s->kernel_height * s->kernel_width;
+    const long cpog = s->input_channels / s->offset_groups;
+    const long columns_per_row = (long)s->input_channels * kernel_area;
+    const long rows = (long)s->batch * plane;
+    for (long row = 0; row < rows; ++row) {
+        const long n = row / plane;
+        const long spatial = row % plane;
+        const long oy = spatial / s->output_width;
+        const long ox = spatial % s->output_width;
+        const long offset_base = n * 2 * s->offset_groups * kernel_area * plane;
+        const long mask_base = n * s->offset_groups * kernel_area * plane;
+        for (long ic = 0; ic < s->input_channels; ++ic) {
+            const long og = ic / cpog;
+            for (long k = 0; k < kernel_area; ++k) {
+                const long ky = k / s->kernel_width;
+                const long kx = k % s->kernel_width;
+                const long sample = og * kernel_area + k;
+                /* the coordinate arithmetic of oracle_dcn_im2col_f16 */
+                const float y = (float)(oy * s->stride_height + ky * s->dilation_height -
+                                        s->pad_height) +
+                                oracle_bf16_to_f32(offset[offset_base + 2 * sample * plane + spatial]);
+                const float x =
+                    (float)(ox * s->stride_width + kx * s->dilation_width - s->pad_width) +
+                    oracle_bf16_to_f32(offset[offset_base + (2 * sample + 1) * plane + spatial]);
+                const float sampled = sample_zero_bf16(
+                    input, (size_t)((n * s->input_channels + ic) * input_plane),
+                    s->input_height, s->input_width, y, x);
+                const float m = oracle_bf16_to_f32(mask[mask_base + sample * plane + spatial]);
+                columns[row * columns_per_row + ic * kernel_area + k] =
+                    oracle_f32_to_bf16(sampled * m);
+            }
+        }
+    }
+    return 0;
+}
+
 int oracle_dcn_gemm_f16(const oracle_shape* s, const uint16_t* columns,
                         const uint16_t* weight, const uint16_t* bias, uint16_t* output) {
     if (oracle_shape_validate(s) || s->groups != 1) return 1;

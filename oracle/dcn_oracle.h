@@ -66,6 +66,16 @@ int oracle_dcn_forward_f16_direct(const oracle_shape* s, const uint16_t* input,
 int oracle_dcn_im2col_f16(const oracle_shape* s, const uint16_t* input,
                           const uint16_t* offset, const uint16_t* mask, uint16_t* columns);
 
+/* BF16 storage (no counterpart in the reference, which has FP16 and FP32 only): the
+ * same gather as oracle_dcn_im2col_f16 over BF16 input, offsets and mask, each sample
+ * rounded once to BF16. The library's BF16 fused path computes these columns. */
+int oracle_dcn_im2col_bf16(const oracle_shape* s, const uint16_t* input,
+                           const uint16_t* offset, const uint16_t* mask, uint16_t* columns);
+/* IEEE binary32 -> bfloat16, round to nearest even (NaN -> quiet NaN); bfloat16 ->
+ * binary32 exactly (the 16 bits are the high half). */
+uint16_t oracle_f32_to_bf16(float value);
+float oracle_bf16_to_f32(uint16_t bits);
+
 /* deform_conv2d_fp16_jasna_simdgroup_gemm_fused (MetalShader.swift:387-452), groups 1:
  * out[n][oc][sp] = half(sum_k col[row][k] * w[oc][k] + bias[oc]), FP32 sum in k order.
  * Weight OIHW FP16. */

@@ -548,6 +548,102 @@ def test_tile_split_stages(gpu_ctx, dcn, oracle, tw):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
 
 
+def bf16_case(dcn, shape, seed, offset_scale=3.0):
+    """A random case as BF16 bit patterns (the FP32 draws of rand_case, rounded)."""
+    return {k: dcn.f32_to_bf16_bits(v) for k, v in rand_case(shape, seed, offset_scale).items()}
+
+
+def bf16_reference(dcn, oracle, s, b):
+    """The BF16 path's output before its final rounding: the oracle's BF16 columns times the
+    widened BF16 weights plus the bias, in float64; and the same with absolute values (the
+    scale of the FP32 summation-order error)."""
+    f = dcn.bf16_bits_to_f32
+    plane = s.output_height * s.output_width
+    kdim = s.input_channels * s.kernel_height * s.kernel_width // s.groups
+    cols = f(oracle.im2col_bf16(s, b["input"], b["offset"], b["mask"])).astype(np.float64)
+    cols = cols.reshape(s.batch, plane, s.groups, kdim)
+    W = f(b["weight"]).astype(np.float64).reshape(s.groups, s.output_channels // s.groups, kdim)
+    bias = f(b["bias"]).astype(np.float64).reshape(s.groups, -1)[None, :, :, None]
+    exact = np.einsum("bpgk,gok->bgop", cols, W) + bias
+    scale = np.einsum("bpgk,gok->bgop", np.abs(cols), np.abs(W)) + np.abs(bias)
+    return exact.ravel(), scale.ravel(), kdim
+
+
+def assert_within_one_bf16_step(dcn, got_bits, exact, scale, kdim):
+    """Each output lies within one BF16 step of the exact product, after allowing for the
+    FP32 summation-order error bound kdim * 2^-24 * sum |terms| (the GPU sums the same BF16
+    products in FP32 in another order and rounds once)."""
+    got = dcn.bf16_bits_to_f32(got_bits).astype(np.float64)
+    near = dcn.f32_to_bf16_bits(exact.astype(np.float32))
+    up = dcn.bf16_bits_to_f32(near | 1).astype(np.float64)
+    down = dcn.bf16_bits_to_f32(near & 0xFFFE).astype(np.float64)
+    step = np.maximum(np.abs(up - down), 2.0 ** -133)
+    bound = step + (kdim + 1) * 2.0 ** -24 * scale
+    err = np.abs(got - exact)
+    log(f"  BF16: max |got - exact| {float(err.max()):.3e}, {float(np.max(err / step)):.2f} BF16 steps")
+    assert np.all(err <= bound), float(np.max(err / bound))
+
+
+@pytest.mark.parametrize("dims", [(1, 128, 64, 64, 64, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16),
+                                  (2, 16, 17, 15, 32, 9, 8, 3, 3, 1, 1, 2, 2, 1, 1, 1, 2),
+                                  (1, 64, 10, 10, 96, 10, 10, 3, 3, 1, 1, 1, 1, 1, 1, 1, 8)],
+                         ids=lambda t: "x".join(map(str, t)))
+def test_bf16_fused_matches_oracle_columns(gpu_ctx, dcn, oracle, dims):
+    """The BF16 fused path against the oracle's BF16 gather times the weights (C2's shape,
+    stride 2 over a batch, 96 output channels); and against the FP32 oracle on the widened
+    inputs within bars 8x the FP16 ones (BF16 keeps 3 fewer significant bits)."""
+    s = dcn.DeformConvShape(*dims)
+    b = bf16_case(dcn, s, sum(dims))
+    log("case: BF16 fused", dims)
+    packed = gpu_ctx.prepack_bf16(s, b["weight"], b["bias"])
+    out = gpu_ctx.run_bfloat16_prepacked(s, b["input"], b["offset"], b["mask"], packed)
+    again = gpu_ctx.run_bfloat16_prepacked(s, b["input"], b["offset"], b["mask"], packed)
+    assert np.array_equal(out, again)
+    assert_within_one_bf16_step(dcn, out, *bf16_reference(dcn, oracle, s, b))
+    f = dcn.bf16_bits_to_f32
+    ref32 = oracle.forward_f32_threads(s, *[f(b[k]) for k in ("input", "offset", "mask", "weight", "bias")])
+    mx, mean = errors(f(out), ref32)
+    log(f"  vs FP32 oracle: max {mx:.3e} mean {mean:.3e}")
+    assert mx <= 8 * MAX_ABS_F16 and mean <= 8 * MEAN_ABS_F16
+
+
+def test_bf16_and_f16_packs_do_not_mix(gpu_ctx, dcn, c2):
+    s, h, _ = c2
+    p16 = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    pbf = gpu_ctx.prepack_bf16(s, h["weight"].view(np.uint16), h["bias"].view(np.uint16))
+    x = h["input"].view(np.uint16)
+    with pytest.raises(dcn.DeformConvError):
+        gpu_ctx.run_bfloat16_prepacked(s, x, h["offset"].view(np.uint16), h["mask"].view(np.uint16), p16)
+    with pytest.raises(dcn.DeformConvError):
+        gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], pbf)
+
+
+def test_bf16_device_entry_points(gpu_ctx, dcn, oracle):
+    import torch
+
+    s = dcn.DeformConvShape(1, 32, 12, 12, 32, 12, 12, 3, 3, 1, 1, 1, 1, 1, 1, 1, 4)
+    b = bf16_case(dcn, s, 77)
+    log("case: BF16 device entry points")
+    host = gpu_ctx.run_bfloat16_prepacked(s, b["input"], b["offset"], b["mask"],
+                                          gpu_ctx.prepack_bf16(s, b["weight"], b["bias"]))
+    dev = {k: torch.tensor(v.view(np.int16)).cuda() for k, v in b.items()}
+    packed = gpu_ctx.prepack_bf16_dev(s, dev["weight"], dev["bias"])
+    out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
+    gpu_ctx.forward_bf16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), host)
+    # From the channel-block copy: the repack moves 16-bit words, whatever their format.
+    cb8 = torch.empty(gpu_ctx.cb8_count(s), dtype=torch.int16, device="cuda")
+    gpu_ctx.pack_input_cb8_dev(s, dev["input"], cb8)
+    out.zero_()
+    gpu_ctx.forward_bf16_prepacked_cb8_dev(s, cb8, dev["offset"], dev["mask"], packed, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), host)
+    with pytest.raises(dcn.DeformConvError):
+        gpu_ctx.forward_f16_prepacked_cb8_dev(s, cb8, dev["offset"], dev["mask"], packed, out)
+    packed.free()
+
+
 def test_zero_padding_exact(gpu_ctx, dcn, c2):
     s, h, _ = c2
     log("case: zero padding")

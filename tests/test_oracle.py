@@ -312,6 +312,64 @@ def test_f32_to_f16_matches_numpy(oracle):
     assert np.array_equal(got, ref)
 
 
+def test_f32_to_bf16_matches_torch(oracle):
+    """The oracle's BF16 rounding (nearest, ties to even) against torch's conversion,
+    over random magnitudes, ties, subnormals, overflow and infinities; the widening is
+    exact (bits in the high half)."""
+    rng = np.random.default_rng(18)
+    vals = np.concatenate([
+        rng.standard_normal(4000).astype(np.float32) * np.float32(10.0) ** rng.integers(-30, 30, 4000).astype(np.float32),
+        np.array([0.0, -0.0, 1e-40, -1e-40, 3.3895e38, 3.4e38, np.inf, -np.inf], np.float32),
+        # ties: exactly halfway between two BF16 values (both parities)
+        (np.arange(1, 600, dtype=np.float32) * np.float32(2.0 ** -8) + np.float32(1.0)),
+    ])
+    lib = oracle.load()
+    got = np.array([lib.oracle_f32_to_bf16(float(v)) for v in vals], np.uint16)
+    ref = torch.tensor(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    back = np.array([lib.oracle_bf16_to_f32(int(b)) for b in got[:4000]], np.float32)
+    assert np.array_equal(back, torch.tensor(ref[:4000].view(np.int16)).view(torch.bfloat16).float().numpy())
+    nan = lib.oracle_f32_to_bf16(float("nan"))
+    assert (nan & 0x7f80) == 0x7f80 and (nan & 0x7f) != 0
+
+
+def _bf16(x):
+    return torch.tensor(np.asarray(x, np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def test_im2col_bf16_integer_offsets_copy_input(oracle):
+    """Integer offsets and a unit mask gather the input itself: a shifted copy, bit for bit."""
+    s = DeformConvShape(1, 8, 5, 5, 8, 5, 5, 1, 1, 0, 0, 1, 1, 1, 1, 1, 1)
+    x = _bf16(np.random.default_rng(19).standard_normal(200))
+    off = np.zeros(50, np.float32)
+    off[25:] = 1  # dx = +1: the column to the right
+    cols = oracle.im2col_bf16(s, x, _bf16(off), _bf16(np.ones(25))).reshape(25, 8)
+    X = x.reshape(8, 5, 5)
+    for p in range(25):
+        y, xx = divmod(p, 5)
+        ref = X[:, y, xx + 1] if xx + 1 < 5 else np.zeros(8, np.uint16)
+        assert np.array_equal(cols[p], ref)
+
+
+def test_im2col_bf16_equals_f16_where_both_are_exact(oracle):
+    """Inputs that are integers in [-4, 4], offsets on a quarter-pixel grid and masks that
+    are multiples of 1/4: every modulated sample is a multiple of 1/64 below 4 in magnitude,
+    which BF16 (8 significant bits) and FP16 hold exactly, so the BF16 gather must equal the
+    (separately pinned) FP16 gather value for value, padding, coordinates and association
+    included."""
+    s = DeformConvShape(2, 16, 7, 6, 8, 7, 6, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)
+    rng = np.random.default_rng(20)
+    c = s.counts()
+    x = rng.integers(-4, 5, c["input"]).astype(np.float32)
+    off = rng.integers(-12, 13, c["offset"]).astype(np.float32) / 4
+    m = rng.integers(0, 5, c["mask"]).astype(np.float32) / 4
+    cb = oracle.im2col_bf16(s, _bf16(x), _bf16(off), _bf16(m))
+    ch = oracle.im2col_f16(s, x.astype(np.float16), off.astype(np.float16), m.astype(np.float16))
+    widened = torch.tensor(cb.view(np.int16)).view(torch.bfloat16).float().numpy()
+    assert np.array_equal(widened, ch.astype(np.float32))
+    assert np.count_nonzero(widened) > widened.size // 4
+
+
 def test_nonfinite_flag(oracle):
     # MetalNonFiniteFlagTests.swift:50-52
     assert oracle.flag_nonfinite_f16(np.array([0, 1, -2, 0.5], np.float16)) == 0
