@@ -54,7 +54,7 @@ struct NarrowArgs {
 
 template <int NB, int NW, int U, int SAMPLER>
 __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
-    extern __shared__ float red[];  // [NW][NB][4][65]
+    extern __shared__ __attribute__((aligned(16))) float red[];  // [NW][NB][64] f32x4
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -94,6 +94,9 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
     const uint32_t mskb = (uint32_t)(b * a.GKA) * a.HWo + sp;
     // 16-byte units; includes the border shift so (iy, ix) may be negative down to -2.
     const uint32_t xinb = (uint32_t)(b * a.CBLK * a.Hp + kPad) * a.Wp + kPad;
+    // This pixel's place in an output plane (NCHW) or CB8 channel block.
+    const uint32_t pix_out = a.out_cb8 ? (uint32_t)(((oy + kPad) * (a.Wo + 2 * kPad) + ox + kPad) * 8)
+                                       : (uint32_t)sp;
 
     f32x4 acc[NB];
 #pragma unroll
@@ -163,31 +166,36 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
         }
     }
 
+    // Cross-wave sum: each wave's MFMA rows go to LDS as f32x4 rows [NW][NB][64]; lane l of
+    // wave nb (mod NW) adds rows (w, nb, l) over the waves in wave order (consecutive
+    // lanes read consecutive 16-byte rows: no bank conflicts), giving pixels 4 (l / 16) + v
+    // of channel 16 nb + l % 16, whose output positions come from the lanes owning them.
+    f32x4* red4 = reinterpret_cast<f32x4*>(red);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+    for (int nb = 0; nb < NB; ++nb) red4[(wave * NB + nb) * 64 + lane] = acc[nb];
     __syncthreads();
-
-    for (int idx = tid; idx < 16 * NB * 16; idx += 64 * NW) {
-        const int pl = idx & 15;
-        const int oc = idx >> 4;
-        const int nb = oc >> 4;
-        const int src = ((pl >> 2) << 4) + (oc & 15);
-        const int v = pl & 3;
-        float sum = 0.0f;
+    for (int nb = wave; nb < NB; nb += NW) {  // uniform per wave
+        const int oc = nb * 16 + (lane & 15);
+        f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
-        if (pvalid) {  // pl == lane % 16: this lane's pixel (b, sp)
-            size_t dst;
-            if (a.out_cb8) {
-                const int c = a.out_coff + oc;
-                dst = (((size_t)b * a.out_cblk + (c >> 3)) * (a.Ho + 2 * kPad) + oy + kPad) *
-                          (size_t)(a.Wo + 2 * kPad) * 8 + (size_t)(ox + kPad) * 8 + (c & 7);
-            } else {
-                dst = ((size_t)b * a.Cout + oc) * a.HWo + sp;
+        for (int w = 0; w < NW; ++w) {
+            const f32x4 t = red4[(w * NB + nb) * 64 + lane];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sum[v] += t[v];
+        }
+        const float bias = a.bias[oc];
+        const int c = a.out_coff + oc;
+        const size_t plane_cb8 = (size_t)(a.Ho + 2 * kPad) * (a.Wo + 2 * kPad) * 8;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int pe = 4 * (lane >> 4) + v;  // owned by lane pe
+            const uint32_t pix = (uint32_t)__shfl((int)pix_out, pe);
+            const int pb = __shfl(b, pe);
+            if (p0 + pe < a.M) {
+                const size_t dst = a.out_cb8 ? ((size_t)pb * a.out_cblk + (c >> 3)) * plane_cb8 + pix + (c & 7)
+                                             : ((size_t)pb * a.Cout + oc) * a.HWo + pix;
+                a.out[dst] = __builtin_bit_cast(uint16_t, round_f16(sum[v] + bias));
             }
-            a.out[dst] = __builtin_bit_cast(uint16_t, round_f16(sum + a.bias[oc]));
         }
     }
 }
@@ -374,7 +382,7 @@ hipError_t launch_narrow_t(const NarrowArgs& a, hipStream_t stream) {
     // K-steps whose loads are in flight at once, sized to the register budget of
     // NW / 4 waves per SIMD (more output columns hold more weight fragments).
     constexpr int U = NB >= 6 ? (NW == 12 ? 2 : 3) : (NW == 12 ? 3 : 5);
-    const size_t lds = (size_t)NW * NB * 4 * 65 * sizeof(float);
+    const size_t lds = (size_t)NW * NB * 64 * 4 * sizeof(float);
     auto kernel = &narrow_kernel<NB, NW, U, SAMPLER>;
     const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
     if (attr != hipSuccess) return attr;
