@@ -15,9 +15,9 @@ Config 1 is the FP32 entry point (runFloat32): one direct kernel per call, in th
 oracle's summation order, priced against the FP32 matrix peak.
 
 --dtype bf16 (configs 2, 3, 5) measures the BF16 storage path instead (dcn_forward_bf16_
-prepacked_dev: the same repack, then the register-variant fused kernel with the BF16
-sampler and BF16 MFMA); its timed output is checked against the FP32 oracle on the
-widened BF16 inputs with bars 8x the FP16 ones.
+prepacked_dev: the same repack, then the narrow kernel (C2) or the register variant (C3,
+C5) with the BF16 sampler and BF16 MFMA); its timed output is checked against the FP32
+oracle on the widened BF16 inputs with bars 8x the FP16 ones.
 
 cpu_baseline: the CPU oracle (a C restatement of the reference's DeformConvCPU.run),
 single thread, on a bounded sample of the benchmarked workload with the same inputs; its
@@ -676,7 +676,7 @@ def main() -> int:
                     help="config 4: time the per-frame graphs only (no clip, no 16-tile step)")
     ap.add_argument("--dtype", choices=("f16", "bf16"), default="f16",
                     help="configs 2, 3, 5: FP16 storage (the reference's) or BF16 storage (the BF16 "
-                         "fused path, register variant)")
+                         "fused path)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run three device copies of this many MiB (the known-size "
                          "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -691,8 +691,8 @@ def main() -> int:
         return 2
     bf16 = args.dtype == "bf16"
     if bf16 and (args.spynet or args.config in (1, 4) or args.variant or args.mt or args.ks):
-        print("--dtype bf16 measures the BF16 fused forward of configs 2, 3 and 5 (register variant, "
-              "automatic tiles)", file=sys.stderr)
+        print("--dtype bf16 measures the BF16 fused forward of configs 2, 3 and 5 (its automatic "
+              "kernel choice)", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -733,10 +733,11 @@ def main() -> int:
     elif bf16:
         packed = ctx.prepack_bf16_dev(s, dev["weight"], dev["bias"])
         ctx.reserve(s)
-        # The BF16 forward's fixed choice: the register variant, 64-pixel tiles split over
-        # 4 K-waves once there are more than 1024 tiles of 32 pixels, else 32 over 8.
+        # The BF16 forward's fixed choice: 16-pixel tiles on 12 waves (the narrow kernel) up
+        # to 1024 tiles of 32 pixels, else the register variant (64-pixel tiles, 4 K-waves).
         many = (s.batch * s.output_height * s.output_width + 31) // 32 > 1024
-        fused_cfg = {"variant": 1, "mt": 2 if many else 1, "ks": 4 if many else 8, "sampler": "bf16"}
+        fused_cfg = ({"variant": 1, "mt": 2, "ks": 4, "sampler": "bf16"} if many
+                     else {"variant": 5, "mt": 1, "ks": 12, "sampler": "bf16"})
         out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
         cb8 = torch.empty(ctx.cb8_count(s), dtype=torch.int16, device="cuda")
 

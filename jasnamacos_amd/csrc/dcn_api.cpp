@@ -154,11 +154,12 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
         return fail(ctx, DCN_INVALID_SHAPE, "padded input too large for 32-bit device indexing");
     // The packed weights carry the window / tile fragments only when the layer's shape at
     // prepack allowed those kernels; this call's shape must allow them too.
-    // BF16: the register variant, 64- or 32-pixel tiles by problem size.
+    // BF16: 16-pixel tiles on 12 waves (the narrow kernel) up to 1024 tiles of 32 pixels,
+    // as FP16 does; above, the register variant with 64-pixel tiles over 4 K-waves.
     const long long tiles32 = (g.m + 31) / 32;
     const dcn::FusedConfig cfg =
-        bf16 ? dcn::FusedConfig{dcn::kVariantRegister, tiles32 > 1024 ? 2 : 1, tiles32 > 1024 ? 4 : 8,
-                                dcn::kSamplerBf16}
+        bf16 ? (tiles32 > 1024 ? dcn::FusedConfig{dcn::kVariantRegister, 2, 4, dcn::kSamplerBf16}
+                               : dcn::FusedConfig{dcn::kVariantNarrow, 1, 12, dcn::kSamplerBf16})
              : choose_config(ctx, g, *shape, packed->weights_group != nullptr && dcn::window_supported(*shape),
                              packed->weights_tile != nullptr && dcn::tile_supported(*shape));
     if (!config_supported(cfg, g))
@@ -437,10 +438,10 @@ static dcn_status make_packed(dcn_context* ctx, const dcn_shape* shape, dcn_pack
     p->geometry = g;
     p->device = ctx->device;
     p->bf16 = bf16;
-    // BF16 runs the register variant only: no narrow, window or tile fragments.
+    // BF16 runs the register and narrow variants: no window or tile fragments.
     if (hipMalloc(&p->weights, dcn::packed_weight_bytes(g)) != hipSuccess ||
         hipMalloc((void**)&p->bias, (size_t)shape->output_channels * sizeof(float)) != hipSuccess ||
-        (!bf16 && hipMalloc(&p->weights_narrow, dcn::narrow_packed_bytes(g)) != hipSuccess) ||
+        hipMalloc(&p->weights_narrow, dcn::narrow_packed_bytes(g)) != hipSuccess ||
         (!bf16 && dcn::window_supported(*shape) &&
          hipMalloc(&p->weights_group, dcn::window_packed_bytes(*shape)) != hipSuccess) ||
         (!bf16 && dcn::tile_supported(*shape) &&

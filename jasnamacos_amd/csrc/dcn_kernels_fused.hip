@@ -41,8 +41,6 @@ namespace {
 
 using namespace dev;
 
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-
 constexpr size_t kMaxLds = 160 * 1024;  // LDS per workgroup on gfx950
 
 struct FusedArgs {

@@ -54,6 +54,10 @@ struct NarrowArgs {
 
 template <int NB, int NW, int U, int SAMPLER>
 __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
+    // BF16 storage (kSamplerBf16): offsets, masks, input and weights are BF16 bits, the
+    // samples are the exact sampler's FP32 bilinear rounded once to BF16, the products
+    // run on the BF16 MFMA, the output is bf16(sum + bias).
+    constexpr bool kBf16 = SAMPLER == kSamplerBf16;
     extern __shared__ __attribute__((aligned(16))) float red[];  // [NW][NB][64] f32x4
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -128,9 +132,12 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
             plane[i] = g * a.CB + cb;
             yb[i] = base_y + ky * a.dh;
             xb[i] = base_x + kx * a.dw;
-            dy[i] = load_half(orr, (offb + (uint32_t)(2 * gt) * a.HWo) * 2u);
-            dx[i] = load_half(orr, (offb + (uint32_t)(2 * gt + 1) * a.HWo) * 2u);
-            m[i] = load_half(mr, (mskb + (uint32_t)gt * a.HWo) * 2u);
+            const uint32_t dyo = (offb + (uint32_t)(2 * gt) * a.HWo) * 2u;
+            const uint32_t dxo = (offb + (uint32_t)(2 * gt + 1) * a.HWo) * 2u;
+            const uint32_t mo = (mskb + (uint32_t)gt * a.HWo) * 2u;
+            dy[i] = kBf16 ? load_bf16(orr, dyo) : load_half(orr, dyo);
+            dx[i] = kBf16 ? load_bf16(orr, dxo) : load_half(orr, dxo);
+            m[i] = kBf16 ? load_bf16(mr, mo) : load_half(mr, mo);
         }
         u32x4 q[U][4];
         float ly[U], lx[U];
@@ -160,8 +167,13 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
             if (sb + i < s1) {  // uniform across the wave
                 const h8 A = blend<SAMPLER>(q[i][0], q[i][1], q[i][2], q[i][3], ly[i], lx[i], m[i]);
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+                for (int nb = 0; nb < NB; ++nb) {
+                    if constexpr (kBf16)
+                        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf8, A), __builtin_bit_cast(bf8, Bf[i][nb]), acc[nb], 0, 0, 0);
+                    else
+                        acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bf[i][nb], acc[nb], 0, 0, 0);
+                }
             }
         }
     }
@@ -194,7 +206,8 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
             if (p0 + pe < a.M) {
                 const size_t dst = a.out_cb8 ? ((size_t)pb * a.out_cblk + (c >> 3)) * plane_cb8 + pix + (c & 7)
                                              : ((size_t)pb * a.Cout + oc) * a.HWo + pix;
-                a.out[dst] = __builtin_bit_cast(uint16_t, round_f16(sum[v] + bias));
+                a.out[dst] = kBf16 ? round_bf16_bits(sum[v] + bias)
+                                   : __builtin_bit_cast(uint16_t, round_f16(sum[v] + bias));
             }
         }
     }
@@ -468,6 +481,7 @@ hipError_t launch_narrow_f16(const KShape& s, const FusedGeometry& g, const Fuse
     // DCN over many tiles): weights stay in registers across the images of a workgroup.
     // From four images on (C3's tiles at batch 2: 19.5 us against 18.6 us for
     // narrow_kernel; at batch 4: 33.0 against 33.7 us).
+    if (cfg.sampler == kSamplerBf16) return launch_narrow_s<kSamplerBf16>(a, g.nb * 2, cfg.ks, stream);
     if (s.B >= 4 && g.nb * 2 == 4 && cfg.ks == 12 && (a.ksteps + 11) / 12 <= 3)
         return cfg.sampler == kSamplerExact ? launch_narrow_images_t<4, 12, kSamplerExact>(a, s.B, stream)
                                             : launch_narrow_images_t<4, 12, kSamplerFast>(a, s.B, stream);
