@@ -15,7 +15,7 @@ Config 1 is the FP32 entry point (runFloat32): one direct kernel per call, in th
 oracle's summation order, priced against the FP32 matrix peak.
 
 --dtype bf16 (configs 2, 3, 5) measures the BF16 storage path instead (dcn_forward_bf16_
-prepacked_dev: the same repack, then the narrow kernel (C2) or the register variant (C3,
+prepacked_dev: the same repack, then the narrow kernel (C2) or the window kernel (C3,
 C5) with the BF16 sampler and BF16 MFMA); its timed output is checked against the FP32
 oracle on the widened BF16 inputs with bars 8x the FP16 ones.
 
@@ -734,10 +734,15 @@ def main() -> int:
         packed = ctx.prepack_bf16_dev(s, dev["weight"], dev["bias"])
         ctx.reserve(s)
         # The BF16 forward's fixed choice: 16-pixel tiles on 12 waves (the narrow kernel) up
-        # to 1024 tiles of 32 pixels, else the register variant (64-pixel tiles, 4 K-waves).
+        # to 1024 tiles of 32 pixels; above, LDS windows over 4 x 32 tiles on 4 waves for the
+        # shapes the window kernel takes (all of C3 and C5), else the register variant.
         many = (s.batch * s.output_height * s.output_width + 31) // 32 > 1024
-        fused_cfg = ({"variant": 1, "mt": 2, "ks": 4, "sampler": "bf16"} if many
-                     else {"variant": 5, "mt": 1, "ks": 12, "sampler": "bf16"})
+        window_ok = (s.groups == 1 and s.kernel_height == 3 and s.kernel_width == 3 and
+                     s.input_channels == 8 * s.offset_groups and s.output_channels % 32 == 0 and
+                     s.output_channels <= 128)
+        fused_cfg = ({"variant": 5, "mt": 1, "ks": 12, "sampler": "bf16"} if not many
+                     else {"variant": 3, "mt": 4, "ks": 4, "sampler": "bf16"} if window_ok
+                     else {"variant": 1, "mt": 2, "ks": 4, "sampler": "bf16"})
         out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
         cb8 = torch.empty(ctx.cb8_count(s), dtype=torch.int16, device="cuda")
 

@@ -155,11 +155,14 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
     // The packed weights carry the window / tile fragments only when the layer's shape at
     // prepack allowed those kernels; this call's shape must allow them too.
     // BF16: 16-pixel tiles on 12 waves (the narrow kernel) up to 1024 tiles of 32 pixels,
-    // as FP16 does; above, the register variant with 64-pixel tiles over 4 K-waves.
+    // as FP16 does; above, LDS windows over 4 x 32 tiles where the shape allows them, else
+    // the register variant with 64-pixel tiles over 4 K-waves.
     const long long tiles32 = (g.m + 31) / 32;
+    const bool bf16_window = packed->weights_group != nullptr && dcn::window_supported(*shape);
     const dcn::FusedConfig cfg =
-        bf16 ? (tiles32 > 1024 ? dcn::FusedConfig{dcn::kVariantRegister, 2, 4, dcn::kSamplerBf16}
-                               : dcn::FusedConfig{dcn::kVariantNarrow, 1, 12, dcn::kSamplerBf16})
+        bf16 ? (tiles32 <= 1024 ? dcn::FusedConfig{dcn::kVariantNarrow, 1, 12, dcn::kSamplerBf16}
+                : bf16_window   ? dcn::FusedConfig{dcn::kVariantWindow, 4, 4, dcn::kSamplerBf16}
+                                : dcn::FusedConfig{dcn::kVariantRegister, 2, 4, dcn::kSamplerBf16})
              : choose_config(ctx, g, *shape, packed->weights_group != nullptr && dcn::window_supported(*shape),
                              packed->weights_tile != nullptr && dcn::tile_supported(*shape));
     if (!config_supported(cfg, g))
@@ -438,11 +441,11 @@ static dcn_status make_packed(dcn_context* ctx, const dcn_shape* shape, dcn_pack
     p->geometry = g;
     p->device = ctx->device;
     p->bf16 = bf16;
-    // BF16 runs the register and narrow variants: no window or tile fragments.
+    // BF16 runs the register, narrow and window variants: no tile fragments.
     if (hipMalloc(&p->weights, dcn::packed_weight_bytes(g)) != hipSuccess ||
         hipMalloc((void**)&p->bias, (size_t)shape->output_channels * sizeof(float)) != hipSuccess ||
         hipMalloc(&p->weights_narrow, dcn::narrow_packed_bytes(g)) != hipSuccess ||
-        (!bf16 && dcn::window_supported(*shape) &&
+        (dcn::window_supported(*shape) &&
          hipMalloc(&p->weights_group, dcn::window_packed_bytes(*shape)) != hipSuccess) ||
         (!bf16 && dcn::tile_supported(*shape) &&
          hipMalloc(&p->weights_tile, dcn::tile_packed_bytes(*shape)) != hipSuccess)) {

@@ -71,6 +71,16 @@ __host__ __device__ constexpr int unit_tap(int u) {
 
 template <int NB, int NW, int TR, int GPS, int SAMPLER, int SPLIT, int NBUF, int UNI>
 __global__ __launch_bounds__(64 * NW, UNI ? 2 : 1) void window_kernel(WindowArgs a) {
+    // BF16 storage (kSamplerBf16): BF16 offsets, masks, windows and weights; the exact
+    // sampler's FP32 bilinear rounded once to BF16, the BF16 MFMA, bf16(sum + bias).
+    constexpr bool kBf16 = SAMPLER == kSamplerBf16;
+    auto mfma32 = [](const h8& A, const h8& B, const f32x16& c) {
+        if constexpr (kBf16)
+            return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf8, A), __builtin_bit_cast(bf8, B),
+                                                           c, 0, 0, 0);
+        else
+            return __builtin_amdgcn_mfma_f32_32x32x16_f16(A, B, c, 0, 0, 0);
+    };
     constexpr int kWindowLds = window_lds(NBUF);
     constexpr int TCB = NW / TR;              // row blocks across the tile
     constexpr int T = 64 * NW;
@@ -131,9 +141,15 @@ __global__ __launch_bounds__(64 * NW, UNI ? 2 : 1) void window_kernel(WindowArgs
             int tap, go;
             unit_of(k, tap, go);
             const uint32_t ch = (uint32_t)(go * 9 + tap);
-            rdy[k] = load_half(orr, off_lane + 2u * ch * hwo2, so);
-            rdx[k] = load_half(orr, off_lane + (2u * ch + 1u) * hwo2, so);
-            rm[k] = load_half(mr, msk_lane + ch * hwo2, sm);
+            if constexpr (kBf16) {
+                rdy[k] = load_bf16(orr, off_lane + 2u * ch * hwo2, so);
+                rdx[k] = load_bf16(orr, off_lane + (2u * ch + 1u) * hwo2, so);
+                rm[k] = load_bf16(mr, msk_lane + ch * hwo2, sm);
+            } else {
+                rdy[k] = load_half(orr, off_lane + 2u * ch * hwo2, so);
+                rdx[k] = load_half(orr, off_lane + (2u * ch + 1u) * hwo2, so);
+                rm[k] = load_half(mr, msk_lane + ch * hwo2, sm);
+            }
         }
     };
     int iy[KS], ix[KS];
@@ -307,7 +323,7 @@ __global__ __launch_bounds__(64 * NW, UNI ? 2 : 1) void window_kernel(WindowArgs
                 if (GPS == 1 && k == KS - 1 && half) A = h8{};  // the zero tenth unit
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
-                    acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bq[k % kBDepth][nb], acc[nb], 0, 0, 0);
+                    acc[nb] = mfma32(A, Bq[k % kBDepth][nb], acc[nb]);
                 if (k + kBDepth < KS) load_b(k % kBDepth, st, k + kBDepth);
                 else if (more) load_b(k % kBDepth, st + 1, k + kBDepth - KS);
                 __builtin_amdgcn_sched_barrier(0);  // keep K-steps apart (register pressure)
@@ -346,7 +362,7 @@ __global__ __launch_bounds__(64 * NW, UNI ? 2 : 1) void window_kernel(WindowArgs
             if (GPS == 1 && k == KS - 1 && half) A = h8{};  // the zero tenth unit
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
-                acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bq[k % kBDepth][nb], acc[nb], 0, 0, 0);
+                acc[nb] = mfma32(A, Bq[k % kBDepth][nb], acc[nb]);
             if (k + kBDepth < KS) load_b(k % kBDepth, st, k + kBDepth);
             else if (more) load_b(k % kBDepth, st + 1, k + kBDepth - KS);
         }
@@ -375,7 +391,8 @@ __global__ __launch_bounds__(64 * NW, UNI ? 2 : 1) void window_kernel(WindowArgs
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int i = 8 * (v >> 2) + 4 * half + (v & 3);  // pixel within the row block
-            stage[oc * 32 + i] = __builtin_bit_cast(uint16_t, round_f16(acc[nb][v] + bias));
+            stage[oc * 32 + i] = kBf16 ? round_bf16_bits(acc[nb][v] + bias)
+                                       : __builtin_bit_cast(uint16_t, round_f16(acc[nb][v] + bias));
         }
     }
     __syncthreads();
@@ -876,6 +893,11 @@ hipError_t launch_window_f16(const KShape& s, const FusedGeometry& g, const Fuse
     a.tiles = a.tiles_y * a.tiles_x * s.B;
     const int gps = window_gps(shape);
     const bool split = cfg.split != 0;
+    if (cfg.sampler == kSamplerBf16) {  // BF16: 4 x 32 tiles on 4 waves, one window per group
+        if (nw != 4 || tr != 4 || split) return hipErrorInvalidValue;
+        return gps == 2 ? launch_window_nb<4, 4, 2, kSamplerBf16, 0>(a, g.nb, stream)
+                        : launch_window_nb<4, 4, 1, kSamplerBf16, 0>(a, g.nb, stream);
+    }
     if (cfg.sampler == kSamplerExact) {
         if (gps == 2) return split ? launch_window_g<2, kSamplerExact, 1>(a, g.nb, nw, tr, stream)
                                    : launch_window_g<2, kSamplerExact, 0>(a, g.nb, nw, tr, stream);

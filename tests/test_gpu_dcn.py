@@ -587,13 +587,17 @@ def assert_within_one_bf16_step(dcn, got_bits, exact, scale, kdim):
 @pytest.mark.parametrize("dims", [(1, 128, 64, 64, 64, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16),
                                   (2, 16, 17, 15, 32, 9, 8, 3, 3, 1, 1, 2, 2, 1, 1, 1, 2),
                                   (1, 64, 10, 10, 96, 10, 10, 3, 3, 1, 1, 1, 1, 1, 1, 1, 8),
-                                  (9, 16, 64, 64, 32, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)],
+                                  (9, 16, 64, 64, 32, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2),
+                                  (1, 16, 180, 200, 32, 180, 200, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2),
+                                  (9, 32, 64, 64, 32, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)],
                          ids=lambda t: "x".join(map(str, t)))
 def test_bf16_fused_matches_oracle_columns(gpu_ctx, dcn, oracle, dims):
-    """The BF16 fused path against the oracle's BF16 gather times the weights (C2's shape,
-    stride 2 over a batch and 96 output channels on the narrow kernel; 9 x 64 x 64, more
-    than 1024 tiles of 32 pixels, on the register variant); and against the FP32 oracle on
-    the widened inputs within bars 8x the FP16 ones (BF16 keeps 3 fewer significant bits)."""
+    """The BF16 fused path against the oracle's BF16 gather times the weights: C2's shape,
+    stride 2 over a batch and 96 output channels on the narrow kernel; above 1024 tiles of
+    32 pixels the window kernel (a batch of 64 x 64 maps, one 180 x 200 map) or, for a shape
+    it does not take (32 channels per offset group), the register variant. Also against the
+    FP32 oracle on the widened inputs within bars 8x the FP16 ones (BF16 keeps 3 fewer
+    significant bits)."""
     s = dcn.DeformConvShape(*dims)
     b = bf16_case(dcn, s, sum(dims))
     log("case: BF16 fused", dims)
