@@ -282,10 +282,13 @@ dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_sha
  * values of deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into
  * the bilinear weights, packed-FP16 blend). mt = 32-pixel row blocks per tile (1, 2),
  * ks = waves per workgroup (register: 2, 4, 8; staged: 8, 16). 0 / -1 = automatic.
+ * The setting applies to the FP16 prepacked forwards; the BF16 forwards choose their
+ * kernel themselves (narrow up to 1024 tiles of 32 pixels, then windows where the shape
+ * allows them, else register sampling).
  * No counterpart in the reference (its tile size is the compile-time
  * fusedGEMMRowsPerTile, MetalShader.swift:2). */
 dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, int sampler);
-/* The configuration the next fused call on `shape` would use. */
+/* The configuration the next FP16 fused call on `shape` would use. */
 dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* variant, int* mt,
                                 int* ks, int* sampler);
 
