@@ -631,11 +631,20 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
         uint16_t* out = a.out + (long)z * a.out_ts;
         uint16_t* out2 = a.out2 ? a.out2 + (long)z * a.out2_ts : nullptr;
         // The epilogue's residual inputs, requested now so that they arrive during the convs.
-        uint16_t r1v[4] = {0, 0, 0, 0}, r2v[4] = {0, 0, 0, 0};
+        // Every lane issues the same loads on every path (clamped index; an absent tensor is
+        // a buffer of 0 bytes, whose loads return 0 without touching memory) into 32-bit
+        // registers: a per-lane branch around a 16-bit load, or registers zeroed on one
+        // path, make the compiler wait for that load, and so for every load issued before
+        // it (conv2's weights included), before conv1 can start.
+        const __amdgpu_buffer_rsrc_t r1r = make_rsrc(res1 ? (const void*)res1 : (const void*)a.out,
+                                                     res1 ? 0x7ffffffeu : 0u);
+        const __amdgpu_buffer_rsrc_t r2r = make_rsrc(res2 ? (const void*)res2 : (const void*)a.out,
+                                                     res2 ? 0x7ffffffeu : 0u);
+        uint32_t r1v[4], r2v[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            if (epi_in[v] && res1 != nullptr) r1v[v] = res1[epi_r1[v]];
-            if (epi_in[v] && res2 != nullptr) r2v[v] = res2[epi_r2[v]];
+            r1v[v] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r1r, (int)((epi_in[v] ? epi_r1[v] : 0u) * 2u), 0, 0);
+            r2v[v] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r2r, (int)((epi_in[v] ? epi_r2[v] : 0u) * 2u), 0, 0);
         }
         f32x4 acc1[kPairRT1][NB];
 #pragma unroll
@@ -746,10 +755,10 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
                 float val = sum[v] + bias2v;
                 if (a.act2 == 1 && val < 0.0f) val = val * a.slope;
                 if (a.act2 == 2 && val < 0.0f) val = 0.0f;
-                if (res1 != nullptr) val = (float)__builtin_bit_cast(_Float16, r1v[v]) + val;
+                if (res1 != nullptr) val = (float)__builtin_bit_cast(_Float16, (uint16_t)r1v[v]) + val;
                 if (res2 != nullptr) {
                     const float r1 = (float)round_f16(val);
-                    val = (float)__builtin_bit_cast(_Float16, r2v[v]) + r1;
+                    val = (float)__builtin_bit_cast(_Float16, (uint16_t)r2v[v]) + r1;
                 }
                 const uint16_t h = __builtin_bit_cast(uint16_t, round_f16(val));
                 out[epi_out[v]] = h;
