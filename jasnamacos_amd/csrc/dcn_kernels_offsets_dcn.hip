@@ -103,35 +103,6 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wdcn, a.wdcn_bytes);
 
     // ---- phase A: the offsets conv on this tile ----------------------------------------
-    // A fragment of K-step s, lane l: pixel l % 16 (clamped into the image), K-block
-    // 4 s + l / 16 = tap * 8 + cb, as conv_offsets_kernel loads it.
-    for (int u = tid; u < nimg * kOffKsteps * 64; u += kOdThreads) {
-        const int img = u / (kOffKsteps * 64);
-        const int r = u - img * (kOffKsteps * 64);
-        const int s = r >> 6;
-        const int l = r & 63;
-        const __amdgpu_buffer_rsrc_t xor_ =
-            make_rsrc(static_cast<const uint16_t*>(a.xoff) + (z0 + img) * a.xoff_ts, a.xoff_bytes);
-        const int pc = min(tile * 16 + (l & 15), M - 1);
-        const int y = pc / a.W;
-        const uint32_t base = (uint32_t)(y + kPad - 1) * a.Wp + (pc - y * a.W) + kPad - 1;
-        const int kb = 4 * s + (l >> 4);
-        const int tap = kb >> 3;
-        const int cb = kb & 7;
-        const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
-        const int kx = tap - ky * 3;
-        stage[u] = load16(xor_, (base + (uint32_t)(cb * a.Hp + ky) * a.Wp + kx) * 16u);
-    }
-
-    // The tile's flows (both flows, both channels, 16 pixels per image) into LDS.
-    if (tid < nimg * 64) {
-        const int img = tid >> 6;
-        const int f = (tid >> 5) & 1;
-        const int c = (tid >> 4) & 1;
-        const int px = tile * 16 + (tid & 15);
-        const uint16_t* flow = (f == 0 ? a.flow1 : a.flow2) + (z0 + img) * a.flow_ts;
-        flows[tid] = px < M ? flow[c * (size_t)M + px] : (uint16_t)0;
-    }
     // Column blocks of this wave.
     const int nblocks = wave < kOffBlocks - 2 * kOdWaves ? 3 : 2;
 
@@ -145,7 +116,46 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     };
 #pragma unroll
     for (int s = 0; s < kOffRing; ++s) load_b(s, s);
-    __syncthreads();  // A fragments staged
+
+    // The tile's flows (both flows, both channels, 16 pixels per image; a clamped pixel,
+    // zeroed when written), requested before the A fragments.
+    const int px_flow = tile * 16 + (tid & 15);
+    uint16_t flow_v = 0;
+    if (tid < nimg * 64) {  // whole waves
+        const int img = tid >> 6;
+        const int f = (tid >> 5) & 1;
+        const int c = (tid >> 4) & 1;
+        const uint16_t* flow = (f == 0 ? a.flow1 : a.flow2) + (z0 + img) * a.flow_ts;
+        flow_v = flow[c * (size_t)M + min(px_flow, M - 1)];
+    }
+    // A fragment of K-step s, lane l: pixel l % 16 (clamped into the image), K-block
+    // 4 s + l / 16 = tap * 8 + cb, as conv_offsets_kernel loads it; copied straight into
+    // LDS (buffer_load ... lds: lane l's 16 bytes land at the wave's base + 16 l), so no
+    // load waits for the one before it.
+    for (int u0 = __builtin_amdgcn_readfirstlane(wave) * 64; u0 < nimg * kOffKsteps * 64; u0 += kOdThreads) {
+        const int u = u0 + lane;
+        const int img = u0 / (kOffKsteps * 64);  // wave-uniform: 64 divides an image's units
+        const int r = u - img * (kOffKsteps * 64);
+        const int s = r >> 6;
+        const int l = r & 63;
+        const __amdgpu_buffer_rsrc_t xor_ =
+            make_rsrc(static_cast<const uint16_t*>(a.xoff) + (z0 + img) * a.xoff_ts, a.xoff_bytes);
+        const int pc = min(tile * 16 + (l & 15), M - 1);
+        const int y = pc / a.W;
+        const uint32_t base = (uint32_t)(y + kPad - 1) * a.Wp + (pc - y * a.W) + kPad - 1;
+        const int kb = 4 * s + (l >> 4);
+        const int tap = kb >> 3;
+        const int cb = kb & 7;
+        const int ky = (tap * 11) >> 5;  // tap / 3 for tap < 9
+        const int kx = tap - ky * 3;
+        if (u < nimg * kOffKsteps * 64)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xor_, (__attribute__((address_space(3))) void*)(stage + u0),
+                16, (int)((base + (uint32_t)(cb * a.Hp + ky) * a.Wp + kx) * 16u), 0, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies (the compiler does not track them)
+    if (tid < nimg * 64) flows[tid] = px_flow < M ? flow_v : (uint16_t)0;
+    __syncthreads();  // A fragments staged, flows in LDS
 
     f32x4 acc[Z][3], sum[Z][3];
 #pragma unroll
