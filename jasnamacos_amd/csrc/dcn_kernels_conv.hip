@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "dcn_device.hpp"
 #include "dcn_warp.hpp"
@@ -588,12 +589,17 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
             for (int nb = 0; nb < NB; ++nb)
                 B1[i][nb] = __builtin_bit_cast(h8, load16(w1, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
     load_rows(z0);
+    // conv2's fragments are requested once conv1's products are issued (first image): in
+    // flight behind conv1's operands they only delayed conv1's first wait; they arrive
+    // during the two reductions before conv2.
+    auto load_b2 = [&]() {
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i)
-        if (s0 + i < s1)
+        for (int i = 0; i < KMAX; ++i)
+            if (s0 + i < s1)
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                B2[i][nb] = __builtin_bit_cast(h8, load16(w2, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
+                for (int nb = 0; nb < NB; ++nb)
+                    B2[i][nb] = __builtin_bit_cast(h8, load16(w2, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
+    };
 
     // Per-thread constants of the two reductions, the same for every image: the biases,
     // and the epilogue's output positions (thread tid < 256 owns output pixels
@@ -625,7 +631,8 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
         epi_r2[v] = (uint32_t)conv_index(a.res2_layout, a.res2_coff + epi_oc, yy, xx, a.H, a.W, a.Hp, a.Wp);
     }
 
-    for (int z = z0; z < z1; ++z) {
+    // One image; the first (peeled, `first_c`) also requests conv2's fragments.
+    auto image = [&](int z, auto first_c) {
         const uint16_t* res1 = a.res1 ? a.res1 + (long)z * a.res1_ts : nullptr;
         const uint16_t* res2 = a.res2 ? a.res2 + (long)z * a.res2_ts : nullptr;
         uint16_t* out = a.out + (long)z * a.out_ts;
@@ -663,6 +670,7 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
                 }
             }
         }
+        if constexpr (decltype(first_c)::value) load_b2();
         if (z + 1 < z1) load_rows(z + 1);  // in flight through the reductions and conv2
 #pragma unroll
         for (int rt = 0; rt < kPairRT1; ++rt)
@@ -765,7 +773,11 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
                 if (out2 != nullptr) out2[epi_out2[v]] = h;
             }
         }
-        if (z + 1 < z1) __syncthreads();  // sums read before the next image's partials
+    };
+    image(z0, std::true_type{});
+    for (int z = z0 + 1; z < z1; ++z) {
+        __syncthreads();  // sums read before the next image's partials
+        image(z, std::false_type{});
     }
 }
 
