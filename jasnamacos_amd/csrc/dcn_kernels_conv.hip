@@ -833,17 +833,14 @@ __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs
     const size_t pl = (size_t)H * W;
     const int Hp = H + 2 * kPad, Wp = W + 2 * kPad;
 
-    // This wave's weight fragments, requested first: they arrive during the sampling.
+    // This wave's weight fragments are requested after the conditions' loads: issued
+    // first, their 32 KB per wave queued ahead of every flow and corner load, and each wait
+    // of the sampling (which waits for everything issued before the loads it needs) also
+    // waited for them.
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
     const int s0 = wave * a.ksteps / NW;
     const int s1 = (wave + 1) * a.ksteps / NW;
     h8 Bf[KMAX][NB];
-#pragma unroll
-    for (int i = 0; i < KMAX; ++i)
-        if (s0 + i < s1)  // uniform across the wave
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
 
     // Flows of the halo pixels first (flow1, and flow2 from one warp of prev_flow), so that
     // every condition below is one round of corner loads.
@@ -929,6 +926,12 @@ __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs
         }
         reinterpret_cast<u32x4*>(dst)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = warp::copy8<u32x4>(src, pl, p);
     }
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i)
+        if (s0 + i < s1)  // uniform across the wave
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
     __syncthreads();
 
     // The conv: lane l supplies tile pixel l % 16 (row (l % 16) / 8, column l % 8).
