@@ -105,6 +105,11 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     // ---- phase A: the offsets conv on this tile ----------------------------------------
     // Column blocks of this wave.
     const int nblocks = wave < kOffBlocks - 2 * kOdWaves ? 3 : 2;
+    // The transform's biases, requested first (loads complete in order: requested after
+    // the DCN's weights, waiting for them would wait for the weights too).
+    float boffv[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) boffv[j] = a.boff[(wave + kOdWaves * min(j, nblocks - 1)) * 16 + (lane & 15)];
 
     h8 Bq[kOffRing][3];
     auto load_b = [&](int slot, int s) {
@@ -195,13 +200,23 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
             }
         }
     }
+    // The DCN's weight fragments, requested now: they pass the texture addresser during
+    // the offset transform and its barrier instead of ahead of the DCN's corner gathers.
+    const int s0 = wave * kDcnPerWave;
+    h8 Bf[kDcnPerWave][kDcnNb];
+#pragma unroll
+    for (int i = 0; i < kDcnPerWave; ++i)
+#pragma unroll
+        for (int nb = 0; nb < kDcnNb; ++nb)
+            Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)(((s0 + i) * kDcnNb + nb) * 64 + lane) * 16u));
+
     // prepare_dcn_offsets_fp16 (MetalShader.swift:815-839) on the FP16 conv output, into
     // the LDS offsets [image][channel][pixel].
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
         if (j >= nblocks) continue;
         const int oc = (wave + kOdWaves * j) * 16 + (lane & 15);
-        const float bias = a.boff[oc];
+        const float bias = boffv[j];
 #pragma unroll
         for (int i = 0; i < Z; ++i) {
             if (i >= nimg) continue;
@@ -235,14 +250,6 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     const int base_y = oy - 1;  // stride 1, pad 1
     const int base_x = ox - 1;
     const uint32_t xinb = (uint32_t)kPad * a.Wp + kPad;  // 16-byte units, border shift
-
-    const int s0 = wave * kDcnPerWave;
-    h8 Bf[kDcnPerWave][kDcnNb];
-#pragma unroll
-    for (int i = 0; i < kDcnPerWave; ++i)
-#pragma unroll
-        for (int nb = 0; nb < kDcnNb; ++nb)
-            Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)(((s0 + i) * kDcnNb + nb) * 64 + lane) * 16u));
 
     for (int img = 0; img < nimg; ++img) {
         const long z = z0 + img;
