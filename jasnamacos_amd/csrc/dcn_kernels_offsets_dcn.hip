@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "dcn_device.hpp"
 #include "dcn_internal.hpp"
@@ -105,22 +106,37 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     // ---- phase A: the offsets conv on this tile ----------------------------------------
     // Column blocks of this wave.
     const int nblocks = wave < kOffBlocks - 2 * kOdWaves ? 3 : 2;
-    // The transform's biases, requested first (loads complete in order: requested after
-    // the DCN's weights, waiting for them would wait for the weights too).
+    // The DCN epilogue's biases (output channel idx / 16 of items idx = tid, tid + 768) and
+    // the transform's, requested first: loads complete in order, and a bias requested late
+    // costs a round trip (or waits for everything requested before it).
+    constexpr int kDcnItems = 16 * kDcnNb * 16;
+    constexpr int kDcnIters = (kDcnItems + kOdThreads - 1) / kOdThreads;
+    float bdcnv[kDcnIters];
+#pragma unroll
+    for (int k = 0; k < kDcnIters; ++k) bdcnv[k] = a.bdcn[min(tid + k * kOdThreads, kDcnItems - 1) >> 4];
     float boffv[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) boffv[j] = a.boff[(wave + kOdWaves * min(j, nblocks - 1)) * 16 + (lane & 15)];
 
+    // Waves own 3 or 2 column blocks; the ring's loads and MFMAs are instantiated for each
+    // count (a uniform branch picks one), so that the compiler's waits count the loads in
+    // flight exactly (with a per-block condition it waited for all but one).
     h8 Bq[kOffRing][3];
-    auto load_b = [&](int slot, int s) {
+    auto load_b = [&](int slot, int s, auto nbl_c) {
+        constexpr int NBL = decltype(nbl_c)::value;
 #pragma unroll
-        for (int j = 0; j < 3; ++j)
-            if (j < nblocks)
-                Bq[slot][j] = __builtin_bit_cast(
-                    h8, load16(wor, (uint32_t)((s * a.nbt + wave + kOdWaves * j) * 64 + lane) * 16u));
+        for (int j = 0; j < NBL; ++j)
+            Bq[slot][j] = __builtin_bit_cast(h8, load16(wor, (uint32_t)((s * a.nbt + wave + kOdWaves * j) * 64 + lane) * 16u));
     };
+    typedef std::integral_constant<int, 3> Three;
+    typedef std::integral_constant<int, 2> Two;
+    if (nblocks == 3) {
 #pragma unroll
-    for (int s = 0; s < kOffRing; ++s) load_b(s, s);
+        for (int s = 0; s < kOffRing; ++s) load_b(s, s, Three{});
+    } else {
+#pragma unroll
+        for (int s = 0; s < kOffRing; ++s) load_b(s, s, Two{});
+    }
 
     // The tile's flows (both flows, both channels, 16 pixels per image; a clamped pixel,
     // zeroed when written), requested before the A fragments.
@@ -170,36 +186,51 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
             acc[i][j] = f32x4{};
             sum[i][j] = f32x4{};
         }
-    // Groups of kOffRing K-steps, one ring slot each; the group loop stays rolled so that
-    // the compiler does not hoist later groups' loads (and their registers) forward.
+    // Groups of kOffRing K-steps, one ring slot each.
     static_assert(kOffKsteps % kOffRing == 0, "whole ring groups");
-#pragma unroll 1
-    for (int sg = 0; sg < kOffKsteps; sg += kOffRing) {
+    auto conv_loop = [&](auto nbl_c) {
+        constexpr int NBL = decltype(nbl_c)::value;
+        auto group = [&](int sg) {
 #pragma unroll
-        for (int slot = 0; slot < kOffRing; ++slot) {
-            const int s = sg + slot;
+            for (int slot = 0; slot < kOffRing; ++slot) {
+                const int s = sg + slot;
 #pragma unroll
-            for (int i = 0; i < Z; ++i) {
-                if (i >= nimg) continue;
-                const h8 A = __builtin_bit_cast(h8, stage[(i * kOffKsteps + s) * 64 + lane]);
+                for (int i = 0; i < Z; ++i) {
+                    if (i >= nimg) continue;
+                    const h8 A = __builtin_bit_cast(h8, stage[(i * kOffKsteps + s) * 64 + lane]);
 #pragma unroll
-                for (int j = 0; j < 3; ++j)
-                    if (j < nblocks)
+                    for (int j = 0; j < NBL; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, Bq[slot][j], acc[i][j], 0, 0, 0);
+                }
+                if (s + kOffRing < kOffKsteps) load_b(slot, s + kOffRing, nbl_c);
+                if constexpr (Z == 1) __builtin_amdgcn_sched_barrier(0);
+                if ((kRangeEnds >> s) & 1) {
+#pragma unroll
+                    for (int i = 0; i < Z; ++i)
+#pragma unroll
+                        for (int j = 0; j < 3; ++j) {
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) sum[i][j][v] += acc[i][j][v];
+                            acc[i][j] = f32x4{};
+                        }
+                }
             }
-            if (s + kOffRing < kOffKsteps) load_b(slot, s + kOffRing);
-            if ((kRangeEnds >> s) & 1) {
+        };
+        // One image: unrolled (a rolled loop's header merges the wait state of its back
+        // edge and waits for every slot), a scheduling barrier per K-step keeping later
+        // loads where they are. Batches stay rolled (unrolled, their accumulators spill).
+        if constexpr (Z == 1) {
 #pragma unroll
-                for (int i = 0; i < Z; ++i)
-#pragma unroll
-                    for (int j = 0; j < 3; ++j) {
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) sum[i][j][v] += acc[i][j][v];
-                        acc[i][j] = f32x4{};
-                    }
-            }
+            for (int sg = 0; sg < kOffKsteps; sg += kOffRing) group(sg);
+        } else {
+#pragma unroll 1
+            for (int sg = 0; sg < kOffKsteps; sg += kOffRing) group(sg);
         }
-    }
+    };
+    if (nblocks == 3)
+        conv_loop(Three{});
+    else
+        conv_loop(Two{});
     // The DCN's weight fragments, requested now: they pass the texture addresser during
     // the offset transform and its barrier instead of ahead of the DCN's corner gathers.
     const int s0 = wave * kDcnPerWave;
@@ -304,7 +335,10 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
         __syncthreads();
 
         uint16_t* out = a.out + z * a.out_ts;
-        for (int idx = tid; idx < 16 * kDcnNb * 16; idx += kOdThreads) {
+#pragma unroll
+        for (int k = 0; k < kDcnIters; ++k) {
+            const int idx = tid + k * kOdThreads;
+            if (idx >= kDcnItems) break;
             const int pl = idx & 15;
             const int oc = idx >> 4;
             const int nb = oc >> 4;
@@ -317,7 +351,7 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
                 const int c = a.out_coff + oc;
                 const size_t dst =
                     ((size_t)((c >> 3) * (a.H + 2 * kPad) + oy + kPad) * (a.W + 2 * kPad) + ox + kPad) * 8 + (c & 7);
-                out[dst] = __builtin_bit_cast(uint16_t, round_f16(s + a.bdcn[oc]));
+                out[dst] = __builtin_bit_cast(uint16_t, round_f16(s + bdcnv[k]));
             }
         }
     }
