@@ -838,21 +838,34 @@ __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs
     // of the sampling (which waits for everything issued before the loads it needs) also
     // waited for them.
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
-    const int s0 = wave * a.ksteps / NW;
-    const int s1 = (wave + 1) * a.ksteps / NW;
+    // 196 channels: 25 blocks x 9 taps = 225 K-blocks, 57 K-steps; a wave owns at least
+    // kMinSteps of them, a count the compiler can use for its waits.
+    constexpr int kSteps = (9 * kTcBlocks + 3) / 4;
+    constexpr int kMinSteps = kSteps / NW;
+    const int s0 = wave * kSteps / NW;
+    const int s1 = (wave + 1) * kSteps / NW;
     h8 Bf[KMAX][NB];
+    auto load_bf = [&]() {
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i)
+            if (i < kMinSteps || s0 + i < s1)  // uniform across the wave
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
+    };
 
-    // Flows of the halo pixels first (flow1, and flow2 from one warp of prev_flow), so that
-    // every condition below is one round of corner loads.
     uint16_t* hflow = reinterpret_cast<uint16_t*>(cond + kTcBlocks * kTcHalo);  // [halo][f1x, f1y, f2x, f2y]
     auto halo_xy = [&](int hp, int& y, int& x) {
         const int hy = hp / kTcHW;
         y = oy0 - 1 + hy;
         x = ox0 - 1 + hp - hy * kTcHW;
     };
-    if (tid < kTcHalo) {
+    constexpr int kCondItems = kTcBlocks * kTcHalo;
+    // The flows of the halo pixels: f1 = flow1 and f2 = flow1 + warp(prev_flow, flow1), so
+    // that every condition below is one round of corner loads. Wave `fw` computes them.
+    auto halo_flows = [&](int hp) {
         int y, x;
-        halo_xy(tid, y, x);
+        halo_xy(hp, y, x);
         uint16_t f1[2] = {0, 0}, f2[2] = {0, 0};
         if (y >= 0 && y < H && x >= 0 && x < W) {
             const int p = y * W + x;
@@ -860,78 +873,241 @@ __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs
             f1[1] = a.flow1[pl + p];
             warp::temporal_flow2(a.flow1, a.prev_flow, a.has_second_order, H, W, y, x, f2);
         }
-        hflow[tid * 4 + 0] = f1[0];
-        hflow[tid * 4 + 1] = f1[1];
-        hflow[tid * 4 + 2] = f2[0];
-        hflow[tid * 4 + 3] = f2[1];
-    }
-    __syncthreads();
+        hflow[hp * 4 + 0] = f1[0];
+        hflow[hp * 4 + 1] = f1[1];
+        hflow[hp * 4 + 2] = f2[0];
+        hflow[hp * 4 + 3] = f2[1];
+    };
+    if constexpr (WARP_CB8) {
+        // Items by load pattern, one loop per pattern with item counts that are multiples of
+        // 64, so that a wave's loads follow one pattern (loads in divergent branches made
+        // the compiler wait for every load in flight wherever the branches' registers
+        // met). Every pattern's loads are requested before any item is finished: a loop that
+        // finished each item before starting the next waited for each round's loads in
+        // turn. W: the 16 warped condition blocks (four corner units each); N: the 8
+        // feat_current condition blocks, then the backbone input's NCHW blocks (eight halves
+        // in 32-bit registers; 128 items per source tensor, so that a wave's source pointer
+        // is uniform); U: the DCN input's 16 CB8 blocks (one unit each). A pixel outside
+        // the image loads a clamped pixel, and its item writes zero or nothing. N and U are
+        // requested before the flows, which the last wave computes (N and U items leave it
+        // idle at nprefix 0).
+        constexpr int kPx = kTcTH * kTcTW;
+        constexpr int kT = 64 * NW;
+        constexpr int kW = 16 * kTcHalo;
+        constexpr int kNc = 8 * kTcHalo;
+        constexpr int kU = 16 * kPx;
+        constexpr int kRW = (kW + kT - 1) / kT;
+        constexpr int kRN = (kNc + 8 * 4 * kPx + kT - 1) / kT;  // nprefix <= 3
+        constexpr int kRU = (kU + kT - 1) / kT;
+        static_assert(kW % 64 == 0 && kNc % 64 == 0 && kU % 64 == 0 && (8 * kPx) % 64 == 0,
+                      "wave-uniform item classes");
+        const int nN = kNc + 8 * (1 + a.nprefix) * kPx;
+        const size_t blk_units = (size_t)Hp * Wp;
+        const u32x4* prop_u = reinterpret_cast<const u32x4*>(a.feat_prop);
+        const u32x4* n2_u = reinterpret_cast<const u32x4*>(a.feat_n2);
+        auto clamp_yx = [&](int& y, int& x) {
+            y = min(max(y, 0), H - 1);
+            x = min(max(x, 0), W - 1);
+        };
+        // N item i: condition block 8 + i / 40 at halo pixel i % 40, or, from kNc, the
+        // backbone input's block (i - kNc) / 16 at tile pixel (i - kNc) % 16.
+        auto n_item = [&](int i, int& y, int& x) {
+            if (i < kNc) {
+                halo_xy(i % kTcHalo, y, x);
+            } else {
+                const int op = (i - kNc) & 15;
+                y = oy0 + (op >> 3);
+                x = ox0 + (op & 7);
+            }
+        };
+        uint32_t hv[kRN][8];
+        u32x4 tu[kRU];
+#pragma unroll
+        for (int r = 0; r < kRN; ++r) {
+            const int i = tid + r * kT;
+            if (i < nN) {
+                int y, x;
+                n_item(i, y, x);
+                clamp_yx(y, x);
+                const uint16_t* src;
+                if (i < kNc) {
+                    src = a.feat_current + (size_t)(i / kTcHalo) * 8 * pl;
+                } else {
+                    const int which = __builtin_amdgcn_readfirstlane(i - kNc) >> 7;
+                    const uint16_t* base = which == 0 ? a.feat_current : (which == 1 ? a.p0 : (which == 2 ? a.p1 : a.p2));
+                    src = base + (size_t)(((i - kNc) >> 4) & 7) * 8 * pl;
+                }
+                src += y * W + x;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) hv[r][c] = src[(size_t)c * pl];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRU; ++r) {
+            const int i = tid + r * kT;
+            if (i < kU) {
+                const int dblock = i >> 4;
+                const int op = i & 15;
+                int y = oy0 + (op >> 3), x = ox0 + (op & 7);
+                clamp_yx(y, x);
+                tu[r] = (dblock < 8 ? prop_u : n2_u)[(size_t)(dblock & 7) * blk_units + (size_t)(y + kPad) * Wp + x + kPad];
+            }
+        }
+        const int fw = NW - 1;
+        if (tid >= fw * 64 && tid - fw * 64 < kTcHalo) halo_flows(tid - fw * 64);
+        __syncthreads();
 
-    // Conditions of the halo, block-major: item (block, halo pixel); then the pointwise
-    // outputs of the tile's pixels: item (kind, pixel), kind 0 flow2, 1-16 the DCN input
-    // blocks, then the backbone input's leading blocks. One loop, so that the loads of
-    // both kinds of item are in flight together.
-    constexpr int kCondItems = kTcBlocks * kTcHalo;
-    const int items = kCondItems + (17 + 8 * (1 + a.nprefix)) * kTcTH * kTcTW;
-    for (int it = tid; it < items; it += 64 * NW) {
-        if (it < kCondItems) {
-            const int blk = it / kTcHalo;
-            const int hp = it - blk * kTcHalo;
-            int y, x;
+        // W item i: warped condition block (i / 40 < 8 ? i / 40 : i / 40 + 8) at halo pixel
+        // i % 40, flow1 for feat_prop, flow2 for feat_n2.
+        auto w_coord = [&](int i, int& blk, int& hp, int& y, int& x, float& yf, float& xf) {
+            const int b16 = i / kTcHalo;
+            hp = i - b16 * kTcHalo;
+            blk = b16 < 8 ? b16 : b16 + 8;
             halo_xy(hp, y, x);
+            const int f = b16 < 8 ? 0 : 2;
+            yf = (float)y + warp::h2f(hflow[hp * 4 + f + 1]);
+            xf = (float)x + warp::h2f(hflow[hp * 4 + f]);
+        };
+        u32x4 tw[kRW][4];
+#pragma unroll
+        for (int r = 0; r < kRW; ++r) {
+            const int i = tid + r * kT;
+            if (i < kW) {
+                int blk, hp, y, x;
+                float yf, xf;
+                w_coord(i, blk, hp, y, x, yf, xf);
+                uint32_t u[4];
+                warp::cb8_corner_units(H, W, yf, xf, u);
+                const u32x4* units = (blk < 8 ? prop_u : n2_u) + (size_t)(blk & 7) * blk_units;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) tw[r][k] = units[u[k]];
+            }
+        }
+
+        load_bf();  // in flight behind the corners, through the finishing of the items
+
+        // Finish: the N and U items (their loads were issued first), then W, then the items
+        // without loads (condition block 24 and flow2).
+#pragma unroll
+        for (int r = 0; r < kRN; ++r) {
+            const int i = tid + r * kT;
+            if (i < nN) {
+                int y, x;
+                n_item(i, y, x);
+                u32x4 v;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) v[d] = __builtin_amdgcn_perm(hv[r][2 * d + 1], hv[r][2 * d], 0x05040100u);
+                if (i < kNc) {
+                    const bool inside = y >= 0 && y < H && x >= 0 && x < W;
+                    cond[(8 + i / kTcHalo) * kTcHalo + i % kTcHalo] = inside ? v : u32x4{0u, 0u, 0u, 0u};
+                } else if (y < H && x < W) {
+                    const int dblock = (i - kNc) >> 4;
+                    reinterpret_cast<u32x4*>(a.bb)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = v;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRU; ++r) {
+            const int i = tid + r * kT;
+            if (i < kU) {
+                const int dblock = i >> 4;
+                const int op = i & 15;
+                const int y = oy0 + (op >> 3), x = ox0 + (op & 7);
+                if (y < H && x < W)
+                    reinterpret_cast<u32x4*>(a.deform)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = tu[r];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRW; ++r) {
+            const int i = tid + r * kT;
+            if (i < kW) {
+                int blk, hp, y, x;
+                float yf, xf;
+                w_coord(i, blk, hp, y, x, yf, xf);
+                u32x4 v = {0u, 0u, 0u, 0u};
+                if (y >= 0 && y < H && x >= 0 && x < W) {
+                    float c8[8];
+                    warp::cb8_blend(tw[r], H, W, yf, xf, c8);
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) v[d] = warp::pack_halves(warp::f2h(c8[2 * d]), warp::f2h(c8[2 * d + 1]));
+                }
+                cond[blk * kTcHalo + hp] = v;
+            }
+        }
+        if (tid < kTcHalo) {  // condition block 24: flow1 (x, y), flow2 (x, y), zero outside
+            int y, x;
+            halo_xy(tid, y, x);
             u32x4 v = {0u, 0u, 0u, 0u};
             if (y >= 0 && y < H && x >= 0 && x < W) {
-                const uint16_t f1[2] = {hflow[hp * 4 + 0], hflow[hp * 4 + 1]};
-                const uint16_t f2[2] = {hflow[hp * 4 + 2], hflow[hp * 4 + 3]};
-                v = warp::condition_from_flows<u32x4, WARP_CB8>(a.feat_prop, a.feat_current, a.feat_n2, H, W, blk, y, x,
-                                                                 f1, f2);
+                v[0] = warp::pack_halves(hflow[tid * 4 + 0], hflow[tid * 4 + 1]);
+                v[1] = warp::pack_halves(hflow[tid * 4 + 2], hflow[tid * 4 + 3]);
             }
-            cond[blk * kTcHalo + hp] = v;
-            continue;
+            cond[24 * kTcHalo + tid] = v;
+        } else if (tid >= 64 && tid < 64 + kPx) {  // flow2 of the tile's pixels
+            const int op = tid - 64;
+            const int y = oy0 + (op >> 3), x = ox0 + (op & 7);
+            if (y < H && x < W) {
+                const int hp = ((op >> 3) + 1) * kTcHW + (op & 7) + 1;  // the pixel's halo slot
+                a.flow2[y * W + x] = hflow[hp * 4 + 2];
+                a.flow2[pl + y * W + x] = hflow[hp * 4 + 3];
+            }
         }
-        const int pt = it - kCondItems;
-        const int kind = pt >> 4;
-        const int op = pt & 15;
-        const int y = oy0 + (op >> 3);
-        const int x = ox0 + (op & 7);
-        if (y >= H || x >= W) continue;
-        const int p = y * W + x;
-        if (kind == 0) {
-            const int hp = ((op >> 3) + 1) * kTcHW + (op & 7) + 1;  // the pixel's halo slot
-            a.flow2[p] = hflow[hp * 4 + 2];
-            a.flow2[pl + p] = hflow[hp * 4 + 3];
-            continue;
+    } else {
+        if (tid < kTcHalo) halo_flows(tid);
+        __syncthreads();
+
+        // Conditions of the halo, block-major: item (block, halo pixel); then the pointwise
+        // outputs of the tile's pixels: item (kind, pixel), kind 0 flow2, 1-16 the DCN input
+        // blocks, then the backbone input's leading blocks. One loop, so that the loads of
+        // both kinds of item are in flight together.
+        const int items = kCondItems + (17 + 8 * (1 + a.nprefix)) * kTcTH * kTcTW;
+        for (int it = tid; it < items; it += 64 * NW) {
+            if (it < kCondItems) {
+                const int blk = it / kTcHalo;
+                const int hp = it - blk * kTcHalo;
+                int y, x;
+                halo_xy(hp, y, x);
+                u32x4 v = {0u, 0u, 0u, 0u};
+                if (y >= 0 && y < H && x >= 0 && x < W) {
+                    const uint16_t f1[2] = {hflow[hp * 4 + 0], hflow[hp * 4 + 1]};
+                    const uint16_t f2[2] = {hflow[hp * 4 + 2], hflow[hp * 4 + 3]};
+                    v = warp::condition_from_flows<u32x4, WARP_CB8>(a.feat_prop, a.feat_current, a.feat_n2, H, W, blk, y, x,
+                                                                     f1, f2);
+                }
+                cond[blk * kTcHalo + hp] = v;
+                continue;
+            }
+            const int pt = it - kCondItems;
+            const int kind = pt >> 4;
+            const int op = pt & 15;
+            const int y = oy0 + (op >> 3);
+            const int x = ox0 + (op & 7);
+            if (y >= H || x >= W) continue;
+            const int p = y * W + x;
+            if (kind == 0) {
+                const int hp = ((op >> 3) + 1) * kTcHW + (op & 7) + 1;  // the pixel's halo slot
+                a.flow2[p] = hflow[hp * 4 + 2];
+                a.flow2[pl + p] = hflow[hp * 4 + 3];
+                continue;
+            }
+            uint16_t* dst;
+            int dblock;
+            const uint16_t* src;
+            if (kind <= 16) {
+                dst = a.deform;
+                dblock = kind - 1;
+                src = dblock < 8 ? a.feat_prop + (size_t)dblock * 8 * pl : a.feat_n2 + (size_t)(dblock - 8) * 8 * pl;
+            } else {
+                dst = a.bb;
+                dblock = kind - 17;
+                const int which = dblock >> 3;
+                const uint16_t* base = which == 0 ? a.feat_current : (which == 1 ? a.p0 : (which == 2 ? a.p1 : a.p2));
+                src = base + (size_t)(dblock & 7) * 8 * pl;
+            }
+            reinterpret_cast<u32x4*>(dst)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = warp::copy8<u32x4>(src, pl, p);
         }
-        uint16_t* dst;
-        int dblock;
-        const uint16_t* src;
-        if (WARP_CB8 && kind <= 16) {
-            dblock = kind - 1;
-            const uint16_t* t = dblock < 8 ? a.feat_prop : a.feat_n2;
-            const size_t unit = ((size_t)(dblock & 7) * Hp + y + kPad) * Wp + x + kPad;
-            reinterpret_cast<u32x4*>(a.deform)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] =
-                reinterpret_cast<const u32x4*>(t)[unit];
-            continue;
-        }
-        if (kind <= 16) {
-            dst = a.deform;
-            dblock = kind - 1;
-            src = dblock < 8 ? a.feat_prop + (size_t)dblock * 8 * pl : a.feat_n2 + (size_t)(dblock - 8) * 8 * pl;
-        } else {
-            dst = a.bb;
-            dblock = kind - 17;
-            const int which = dblock >> 3;
-            const uint16_t* base = which == 0 ? a.feat_current : (which == 1 ? a.p0 : (which == 2 ? a.p1 : a.p2));
-            src = base + (size_t)(dblock & 7) * 8 * pl;
-        }
-        reinterpret_cast<u32x4*>(dst)[((size_t)dblock * Hp + y + kPad) * Wp + x + kPad] = warp::copy8<u32x4>(src, pl, p);
     }
-#pragma unroll
-    for (int i = 0; i < KMAX; ++i)
-        if (s0 + i < s1)  // uniform across the wave
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                Bf[i][nb] = __builtin_bit_cast(h8, load16(wr, (uint32_t)(((s0 + i) * NB + nb) * 64 + lane) * 16u));
+    if constexpr (!WARP_CB8) load_bf();
     __syncthreads();
 
     // The conv: lane l supplies tile pixel l % 16 (row (l % 16) / 8, column l % 8).
@@ -941,7 +1117,7 @@ __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs
     const int r = lane & 15;
 #pragma unroll
     for (int i = 0; i < KMAX; ++i) {
-        if (s0 + i < s1) {  // uniform across the wave
+        if (i < kMinSteps || s0 + i < s1) {  // uniform across the wave
             const int kb = 4 * (s0 + i) + quarter;
             const int kbc = kb < a.KB ? kb : a.KB - 1;
             const int tap = fast_div(kbc, a.magic_cb);
@@ -1112,7 +1288,8 @@ hipError_t launch_temporal_conv(const ConvGeometry& g, const uint16_t* feat_prop
                                 const float* bias, float slope, uint16_t* out_cb8, hipStream_t stream,
                                 bool warp_cb8) {
     constexpr int NW = 8, KMAX = 8;
-    if (g.cin != 196 || g.cout != 64 || g.ksteps > NW * KMAX || nprefix < 0 || nprefix > 3)
+    if (g.cin != 196 || g.cout != 64 || g.ksteps != (9 * kTcBlocks + 3) / 4 || g.ksteps > NW * KMAX || nprefix < 0 ||
+        nprefix > 3)
         return hipErrorInvalidValue;
     TemporalConvArgs a{};
     a.feat_prop = feat_prop;

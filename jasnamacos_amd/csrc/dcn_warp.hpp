@@ -78,9 +78,24 @@ __device__ __forceinline__ void sample8_zero(const uint16_t* planes, size_t plan
 
 // sample8_zero over one 8-channel block of a CB8 tensor ([Hp][Wp][8] with a kPad zero
 // border): the same corners, validity and per-channel arithmetic, four 16-byte gathers.
-__device__ __forceinline__ void sample8_cb8(const uint16_t* block, int H, int W, float y, float x,
-                                            float (&v)[8]) {
+// In two halves, so that a caller can request the corners of several samples before it
+// blends any of them: cb8_corner_units gives the corners' 16-byte unit indices within the
+// block (clamped into the plane: corners outside it are zeroed by the blend), cb8_blend
+// the eight channels from the four loaded units.
+__device__ __forceinline__ void cb8_corner_units(int H, int W, float y, float x, uint32_t (&u)[4]) {
     const int Wp = W + 2 * dev::kPad;
+    const float fy = floorf(y), fx = floorf(x);
+    const int y0 = (int)fminf(fmaxf(fy, -4.0f), (float)H + 4.0f);
+    const int x0 = (int)fminf(fmaxf(fx, -4.0f), (float)W + 4.0f);
+    const int yc0 = min(max(y0, 0), H - 1) + dev::kPad, yc1 = min(max(y0 + 1, 0), H - 1) + dev::kPad;
+    const int xc0 = min(max(x0, 0), W - 1) + dev::kPad, xc1 = min(max(x0 + 1, 0), W - 1) + dev::kPad;
+    u[0] = (uint32_t)(yc0 * Wp + xc0);
+    u[1] = (uint32_t)(yc0 * Wp + xc1);
+    u[2] = (uint32_t)(yc1 * Wp + xc0);
+    u[3] = (uint32_t)(yc1 * Wp + xc1);
+}
+
+__device__ __forceinline__ void cb8_blend(const dev::u32x4 (&t)[4], int H, int W, float y, float x, float (&v)[8]) {
     const float fy = floorf(y), fx = floorf(x);
     const int y0 = (int)fminf(fmaxf(fy, -4.0f), (float)H + 4.0f);
     const int x0 = (int)fminf(fmaxf(fx, -4.0f), (float)W + 4.0f);
@@ -88,23 +103,25 @@ __device__ __forceinline__ void sample8_cb8(const uint16_t* block, int H, int W,
     const float ly = y - fy, lx = x - fx;
     const bool r0 = y0 >= 0 && y0 < H, r1 = y1 >= 0 && y1 < H;
     const bool c0 = x0 >= 0 && x0 < W, c1 = x1 >= 0 && x1 < W;
-    const int yc0 = min(max(y0, 0), H - 1) + dev::kPad, yc1 = min(max(y1, 0), H - 1) + dev::kPad;
-    const int xc0 = min(max(x0, 0), W - 1) + dev::kPad, xc1 = min(max(x1, 0), W - 1) + dev::kPad;
-    typedef const dev::u32x4* row_t;
-    const dev::u32x4 t00 = reinterpret_cast<row_t>(block)[(size_t)yc0 * Wp + xc0];
-    const dev::u32x4 t01 = reinterpret_cast<row_t>(block)[(size_t)yc0 * Wp + xc1];
-    const dev::u32x4 t10 = reinterpret_cast<row_t>(block)[(size_t)yc1 * Wp + xc0];
-    const dev::u32x4 t11 = reinterpret_cast<row_t>(block)[(size_t)yc1 * Wp + xc1];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const int sh = (c & 1) * 16;
-        const float v00 = (r0 && c0) ? h2f((uint16_t)(t00[c >> 1] >> sh)) : 0.0f;
-        const float v01 = (r0 && c1) ? h2f((uint16_t)(t01[c >> 1] >> sh)) : 0.0f;
-        const float v10 = (r1 && c0) ? h2f((uint16_t)(t10[c >> 1] >> sh)) : 0.0f;
-        const float v11 = (r1 && c1) ? h2f((uint16_t)(t11[c >> 1] >> sh)) : 0.0f;
+        const float v00 = (r0 && c0) ? h2f((uint16_t)(t[0][c >> 1] >> sh)) : 0.0f;
+        const float v01 = (r0 && c1) ? h2f((uint16_t)(t[1][c >> 1] >> sh)) : 0.0f;
+        const float v10 = (r1 && c0) ? h2f((uint16_t)(t[2][c >> 1] >> sh)) : 0.0f;
+        const float v11 = (r1 && c1) ? h2f((uint16_t)(t[3][c >> 1] >> sh)) : 0.0f;
         v[c] = v00 * (1.0f - ly) * (1.0f - lx) + v01 * (1.0f - ly) * lx + v10 * ly * (1.0f - lx) +
                v11 * ly * lx;
     }
+}
+
+__device__ __forceinline__ void sample8_cb8(const uint16_t* block, int H, int W, float y, float x,
+                                            float (&v)[8]) {
+    uint32_t u[4];
+    cb8_corner_units(H, W, y, x, u);
+    const dev::u32x4* units = reinterpret_cast<const dev::u32x4*>(block);
+    const dev::u32x4 t[4] = {units[u[0]], units[u[1]], units[u[2]], units[u[3]]};
+    cb8_blend(t, H, W, y, x, v);
 }
 
 // The eight channels of condition block `kind` (0-24) at pixel (y, x), as CB8 halves:
