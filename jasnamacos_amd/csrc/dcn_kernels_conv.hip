@@ -105,6 +105,15 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a0) {
     // 16-byte unit of (cb 0, y - 1, x - 1) in the padded plane.
     const uint32_t base = (uint32_t)(y + kPad - 1) * a.Wp + x + kPad - 1;
 
+    // The epilogue's biases, requested first (clamped index, no branch): loaded in the
+    // epilogue they cost a round trip after the reduction.
+    constexpr int kItems = 16 * kConvChunk;
+    constexpr int kIters = (kItems + 64 * NW - 1) / (64 * NW);
+    float biasv[kIters];
+#pragma unroll
+    for (int j = 0; j < kIters; ++j)
+        biasv[j] = a.bias[min(chunk * kConvChunk + ((tid + j * 64 * NW) >> 4), a.Cout - 1)];
+
     f32x4 acc[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{};
@@ -151,7 +160,10 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a0) {
         for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
     __syncthreads();
 
-    for (int idx = tid; idx < 16 * kConvChunk; idx += 64 * NW) {
+#pragma unroll
+    for (int j = 0; j < kIters; ++j) {
+        const int idx = tid + j * 64 * NW;
+        if (idx >= kItems) break;
         const int pl = idx & 15;
         const int ocl = idx >> 4;
         const int nb = ocl >> 4;
@@ -165,7 +177,7 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a0) {
         if (pp >= M || oc >= a.Cout) continue;
         const int yy = pp / a.W;
         const int xx = pp - yy * a.W;
-        float r = sum + a.bias[oc];
+        float r = sum + biasv[j];
         if (a.act == 1 && r < 0.0f) r = r * a.slope;
         if (a.act == 2 && r < 0.0f) r = 0.0f;
         if (a.res1 != nullptr) {
@@ -1232,8 +1244,15 @@ hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, const ConvBatch& batch, 
             hipLaunchKernelGGL((conv3x3_images_kernel<NW, 8>), grid, dim3(64 * NW), lds, stream, a, batch.images, zpw);
         return hipGetLastError();
     }
+    // One image: a wave requests all its K-steps at once where they fit (kmax up to 8), so
+    // that no wave waits for a second round of loads (128 -> 64: 4 or 5 K-steps per wave).
     const dim3 grid((unsigned)((a.tiles + 7) / 8 * 8), (unsigned)g.chunks, (unsigned)batch.images);
-    hipLaunchKernelGGL((conv3x3_kernel<NW, U>), grid, dim3(64 * NW), lds, stream, a);
+    if (kmax == 5)
+        hipLaunchKernelGGL((conv3x3_kernel<NW, 5>), grid, dim3(64 * NW), lds, stream, a);
+    else if (kmax > U && kmax <= 8)
+        hipLaunchKernelGGL((conv3x3_kernel<NW, 8>), grid, dim3(64 * NW), lds, stream, a);
+    else
+        hipLaunchKernelGGL((conv3x3_kernel<NW, U>), grid, dim3(64 * NW), lds, stream, a);
     return hipGetLastError();
 }
 
