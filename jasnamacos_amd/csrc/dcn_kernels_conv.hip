@@ -800,7 +800,7 @@ __global__ __launch_bounds__(64 * NW) void conv_pair_kernel(PairArgs a) {
 // conv's padding), writes the pointwise outputs of its own 16 pixels (flow2, the DCN
 // input [feat_prop, feat_n2] and the backbone input's [feat_current, prefix...] in CB8),
 // then runs the conv with A fragments from LDS. The conditions are condition_block's bits
-// (the separate body_temporal_kernel's), and the conv keeps conv3x3_kernel<8, 4>'s K split
+// (the separate body_temporal_kernel's), and the conv keeps conv3x3_kernel's K split over 8 waves
 // (wave w owns K-steps [w * 57 / 8, (w + 1) * 57 / 8), K-block 4 s + lane / 16 = tap * 25
 // + block) and its wave-ordered sum, so the output is the two-launch result bit for bit.
 // The halo is 2.5 times the tile, so each workgroup samples 2.5 times the pixels it
