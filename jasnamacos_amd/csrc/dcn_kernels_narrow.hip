@@ -198,6 +198,22 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
         const float bias = a.bias[oc];
         const int c = a.out_coff + oc;
         const size_t plane_cb8 = (size_t)(a.Ho + 2 * kPad) * (a.Wo + 2 * kPad) * 8;
+        auto bits = [&](float x) -> uint32_t {
+            return kBf16 ? round_bf16_bits(x) : __builtin_bit_cast(uint16_t, round_f16(x));
+        };
+        if (!a.out_cb8 && a.HWo % 16 == 0 && ((uintptr_t)a.out & 7) == 0) {
+            // NCHW planes of a multiple of 16 pixels: every tile is whole and inside one
+            // image, so the lane's four pixels are consecutive in the plane (8-byte aligned
+            // on an 8-byte aligned output): one 8-byte store.
+            const int pe = 4 * (lane >> 4);
+            const uint32_t pix = (uint32_t)__shfl((int)pix_out, pe);
+            const int pb = __shfl(b, pe);
+            uint2 w;
+            w.x = bits(sum[0] + bias) | (bits(sum[1] + bias) << 16);
+            w.y = bits(sum[2] + bias) | (bits(sum[3] + bias) << 16);
+            *reinterpret_cast<uint2*>(a.out + ((size_t)pb * a.Cout + oc) * a.HWo + pix) = w;
+            continue;
+        }
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const int pe = 4 * (lane >> 4) + v;  // owned by lane pe
