@@ -524,10 +524,16 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             const int oc = nb * 32 + p;
             const float bias = a.bias[oc];
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const float sum = acc[s][nb][v] + red[(((pblk * NS + s) * NB + nb) * 16 + v) * 64 + lane];
-                const int i = 8 * (v >> 2) + 4 * half + (v & 3);  // pixel within the segment
-                stage[(s * NB * 32 + oc) * 32 + i] = __builtin_bit_cast(uint16_t, round_f16(sum + bias));
+            for (int k = 0; k < 4; ++k) {  // segment pixels 8 k + 4 half .. + 3: one 8-byte write
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int v = 4 * k + e;
+                    const float sum = acc[s][nb][v] + red[(((pblk * NS + s) * NB + nb) * 16 + v) * 64 + lane];
+                    h[e] = __builtin_bit_cast(uint16_t, round_f16(sum + bias));
+                }
+                *reinterpret_cast<uint2*>(stage + (s * NB * 32 + oc) * 32 + 8 * k + 4 * half) =
+                    make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
             }
         }
     // Each item: 4 consecutive pixels of one output channel and tile row. No barrier is
