@@ -389,10 +389,14 @@ __global__ __launch_bounds__(64 * NW, UNI ? 2 : 1) void window_kernel(WindowArgs
         const int oc = nb * 32 + (lane & 31);
         const float bias = a.bias[oc];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int i = 8 * (v >> 2) + 4 * half + (v & 3);  // pixel within the row block
-            stage[oc * 32 + i] = kBf16 ? round_bf16_bits(acc[nb][v] + bias)
-                                       : __builtin_bit_cast(uint16_t, round_f16(acc[nb][v] + bias));
+        for (int k = 0; k < 4; ++k) {  // row-block pixels 8 k + 4 half .. + 3: one 8-byte write
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                h[e] = kBf16 ? round_bf16_bits(acc[nb][4 * k + e] + bias)
+                             : __builtin_bit_cast(uint16_t, round_f16(acc[nb][4 * k + e] + bias));
+            *reinterpret_cast<uint2*>(stage + oc * 32 + 8 * k + 4 * half) =
+                make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
         }
     }
     __syncthreads();
@@ -402,7 +406,9 @@ __global__ __launch_bounds__(64 * NW, UNI ? 2 : 1) void window_kernel(WindowArgs
             const int q = (idx & 7) * 4;
             const uint16_t* src = stage + oc * 32 + q;
             uint16_t* dst = a.out + ((size_t)b * a.Cout + oc) * a.HWo + (size_t)oy_row * a.Wo + ox0 + q;
-            if (ox0 + q + 3 < a.Wo && ((((uintptr_t)dst) & 3u) == 0)) {
+            if (ox0 + q + 3 < a.Wo && ((((uintptr_t)dst) & 7u) == 0)) {
+                *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(src);
+            } else if (ox0 + q + 3 < a.Wo && ((((uintptr_t)dst) & 3u) == 0)) {
                 reinterpret_cast<uint32_t*>(dst)[0] = (uint32_t)src[0] | ((uint32_t)src[1] << 16);
                 reinterpret_cast<uint32_t*>(dst)[1] = (uint32_t)src[2] | ((uint32_t)src[3] << 16);
             } else {
