@@ -33,6 +33,8 @@ using namespace dev;
 
 constexpr int kConvChunk = 64;  // output channels per workgroup
 constexpr int kConvNbc = kConvChunk / 16;
+constexpr int kConvRedStride = 68;  // conv3x3_kernel's partial-sum row (64 lanes + padding)
+static_assert(kConvChunk == 64, "the conv epilogues map 64 channels to a wave");
 
 struct ConvArgs {
     const void* xin;        // CB8 input
@@ -82,7 +84,9 @@ template <int NW, int U>
 __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a0) {
     const ConvArgs a = conv_image(a0);
     constexpr int NB = kConvNbc;
-    extern __shared__ float red[];  // [NW][NB][4][65]
+    // Partial sums [NW][NB][4][kConvRedStride]: rows of 64 lanes padded to 68 floats, so that
+    // the epilogue's channel-fastest reads (bank 16 nb + oc % 16) are conflict-free.
+    extern __shared__ float red[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a0) {
     float biasv[kIters];
 #pragma unroll
     for (int j = 0; j < kIters; ++j)
-        biasv[j] = a.bias[min(chunk * kConvChunk + ((tid + j * 64 * NW) >> 4), a.Cout - 1)];
+        biasv[j] = a.bias[min(chunk * kConvChunk + ((tid + j * 64 * NW) & (kConvChunk - 1)), a.Cout - 1)];
 
     f32x4 acc[NB];
 #pragma unroll
@@ -157,21 +161,23 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_kernel(ConvArgs a0) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+        for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * kConvRedStride + lane] = acc[nb][v];
     __syncthreads();
 
+    // Item idx: channel idx % 64 of pixel idx / 64, so that a wave's stores fill whole CB8
+    // units (eight consecutive channels of a pixel).
 #pragma unroll
     for (int j = 0; j < kIters; ++j) {
         const int idx = tid + j * 64 * NW;
         if (idx >= kItems) break;
-        const int pl = idx & 15;
-        const int ocl = idx >> 4;
+        const int ocl = idx & (kConvChunk - 1);
+        const int pl = idx >> 6;
         const int nb = ocl >> 4;
         const int src = ((pl >> 2) << 4) + (ocl & 15);
         const int v = pl & 3;
         float sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
+        for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * kConvRedStride + src];
         const int oc = chunk * kConvChunk + ocl;
         const int pp = tile * 16 + pl;
         if (pp >= M || oc >= a.Cout) continue;
@@ -1230,7 +1236,7 @@ hipError_t run_conv(const ConvGeometry& g, ConvArgs& a, const ConvBatch& batch, 
     a.Cout = g.cout;
     a.tiles = (g.h * g.w + 15) / 16;
     a.magic_cb = magic_for(g.cb);
-    const size_t lds = (size_t)NW * kConvNbc * 4 * 65 * sizeof(float);
+    const size_t lds = (size_t)NW * kConvNbc * 4 * kConvRedStride * sizeof(float);  // >= the images kernel's 65
     const int kmax = (g.ksteps + NW - 1) / NW;  // K-steps of the busiest wave
     if (batch.images > 1 && kmax <= 8) {
         const int zpw = images_per_group<16>(batch.images);
