@@ -834,8 +834,8 @@ template <int NW, int KMAX, bool WARP_CB8>
 __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs a) {
     constexpr int NB = kConvNbc;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    float* red = reinterpret_cast<float*>(lds);  // [NW][NB][4][65]
-    u32x4* cond = reinterpret_cast<u32x4*>(lds + (size_t)NW * NB * 4 * 65 * sizeof(float));  // [25][halo]
+    float* red = reinterpret_cast<float*>(lds);  // [NW][NB][4][kConvRedStride]
+    u32x4* cond = reinterpret_cast<u32x4*>(lds + (size_t)NW * NB * 4 * kConvRedStride * sizeof(float));  // [25][halo]
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -1155,18 +1155,20 @@ __global__ __launch_bounds__(64 * NW) void temporal_conv_kernel(TemporalConvArgs
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+        for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * kConvRedStride + lane] = acc[nb][v];
     __syncthreads();
 
+    // Channel-fastest items, as conv3x3_kernel's epilogue: conflict-free reads, whole CB8
+    // units per store.
     for (int idx = tid; idx < 16 * kConvChunk; idx += 64 * NW) {
-        const int px = idx & 15;
-        const int ocl = idx >> 4;
+        const int ocl = idx & (kConvChunk - 1);
+        const int px = idx >> 6;
         const int nb = ocl >> 4;
         const int src = ((px >> 2) << 4) + (ocl & 15);
         const int v = px & 3;
         float sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
+        for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * kConvRedStride + src];
         const int yy = oy0 + (px >> 3);
         const int xx = ox0 + (px & 7);
         if (yy >= H || xx >= W) continue;
@@ -1344,7 +1346,7 @@ hipError_t launch_temporal_conv(const ConvGeometry& g, const uint16_t* feat_prop
     a.KB = g.kb;
     a.ksteps = g.ksteps;
     a.slope = slope;
-    const size_t lds = (size_t)NW * kConvNbc * 4 * 65 * sizeof(float) + (size_t)kTcBlocks * kTcHalo * 16 +
+    const size_t lds = (size_t)NW * kConvNbc * 4 * kConvRedStride * sizeof(float) + (size_t)kTcBlocks * kTcHalo * 16 +
                        (size_t)kTcHalo * 4 * sizeof(uint16_t);
     auto kernel = warp_cb8 ? &temporal_conv_kernel<NW, KMAX, true> : &temporal_conv_kernel<NW, KMAX, false>;
     const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
