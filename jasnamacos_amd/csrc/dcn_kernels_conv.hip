@@ -212,7 +212,7 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_images_kernel(ConvArgs a0, in
     constexpr int NB = kConvNbc;
     constexpr int kItems = 16 * kConvChunk;
     constexpr int kIters = (kItems + 64 * NW - 1) / (64 * NW);
-    extern __shared__ float red[];  // [NW][NB][4][65]
+    extern __shared__ float red[];  // [NW][NB][4][kConvRedStride], as conv3x3_kernel
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -265,7 +265,7 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_images_kernel(ConvArgs a0, in
     float biasv[kIters];
 #pragma unroll
     for (int j = 0; j < kIters; ++j) {
-        const int oc = chunk * kConvChunk + ((tid + j * 64 * NW) >> 4);
+        const int oc = chunk * kConvChunk + ((tid + j * 64 * NW) & (kConvChunk - 1));
         biasv[j] = oc < a0.Cout ? a0.bias[oc] : 0.0f;
     }
 
@@ -290,20 +290,20 @@ __global__ __launch_bounds__(64 * NW) void conv3x3_images_kernel(ConvArgs a0, in
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * 65 + lane] = acc[nb][v];
+            for (int v = 0; v < 4; ++v) red[((wave * NB + nb) * 4 + v) * kConvRedStride + lane] = acc[nb][v];
         __syncthreads();
 
 #pragma unroll
-        for (int j = 0; j < kIters; ++j) {
+        for (int j = 0; j < kIters; ++j) {  // channel-fastest items, as conv3x3_kernel
             const int idx = tid + j * 64 * NW;
-            const int pl = idx & 15;
-            const int ocl = idx >> 4;
+            const int ocl = idx & (kConvChunk - 1);
+            const int pl = idx >> 6;
             const int nb = ocl >> 4;
             const int src = ((pl >> 2) << 4) + (ocl & 15);
             const int v = pl & 3;
             float sum = 0.0f;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * 65 + src];
+            for (int w = 0; w < NW; ++w) sum += red[((w * NB + nb) * 4 + v) * kConvRedStride + src];
             const int oc = chunk * kConvChunk + ocl;
             const int pp = tile * 16 + pl;
             if (pp >= M || oc >= a.Cout) continue;
