@@ -46,7 +46,8 @@ constexpr int kDcnPerWave = kDcnKsteps / kOdWaves;
 
 constexpr size_t kStageBytes = (size_t)kOffKsteps * 64 * 16;       // A fragments of an image
 constexpr size_t kOffsBytes = (size_t)kOffChannels * 16 * 2;        // [432][16] FP16 per image
-constexpr size_t kRedBytes = (size_t)kOdWaves * kDcnNb * 4 * 65 * 4;  // narrow_kernel's sums
+constexpr int kOdRedStride = 68;  // partial-sum rows of 64 lanes, padded: conflict-free channel-fastest reads
+constexpr size_t kRedBytes = (size_t)kOdWaves * kDcnNb * 4 * kOdRedStride * 4;
 constexpr size_t kFlowBytes = 2 * 2 * 16 * 2;                      // [flow][channel][16] FP16 per image
 // From three images on, the DCN's partial sums reuse the A-fragment stage (dead by then).
 __host__ __device__ constexpr bool od_red_in_stage(int images) { return images * kStageBytes >= kRedBytes; }
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     u32x4* stage = reinterpret_cast<u32x4*>(lds);                                 // [Z][18][64]
     uint16_t* offs = reinterpret_cast<uint16_t*>(lds + Z * kStageBytes);         // [Z][432][16]
     constexpr bool kRedInStage = od_red_in_stage(Z);
-    float* red = reinterpret_cast<float*>(kRedInStage ? lds : lds + Z * (kStageBytes + kOffsBytes));  // [12][4][4][65]
+    float* red = reinterpret_cast<float*>(kRedInStage ? lds : lds + Z * (kStageBytes + kOffsBytes));  // [12][4][4][kOdRedStride]
     uint16_t* flows = reinterpret_cast<uint16_t*>(lds + Z * (kStageBytes + kOffsBytes) +
                                                   (kRedInStage ? 0 : kRedBytes));  // [Z][2][2][16]
     const int tid = threadIdx.x;
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
     constexpr int kDcnIters = (kDcnItems + kOdThreads - 1) / kOdThreads;
     float bdcnv[kDcnIters];
 #pragma unroll
-    for (int k = 0; k < kDcnIters; ++k) bdcnv[k] = a.bdcn[min(tid + k * kOdThreads, kDcnItems - 1) >> 4];
+    for (int k = 0; k < kDcnIters; ++k) bdcnv[k] = a.bdcn[min(tid + k * kOdThreads, kDcnItems - 1) & (16 * kDcnNb - 1)];
     float boffv[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) boffv[j] = a.boff[(wave + kOdWaves * min(j, nblocks - 1)) * 16 + (lane & 15)];
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
 #pragma unroll
         for (int nb = 0; nb < kDcnNb; ++nb)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) red[((wave * kDcnNb + nb) * 4 + v) * 65 + lane] = dacc[nb][v];
+            for (int v = 0; v < 4; ++v) red[((wave * kDcnNb + nb) * 4 + v) * kOdRedStride + lane] = dacc[nb][v];
         __syncthreads();
 
         uint16_t* out = a.out + z * a.out_ts;
@@ -339,18 +340,21 @@ __global__ __launch_bounds__(kOdThreads) void offsets_dcn_kernel(OffsetsDcnArgs 
         for (int k = 0; k < kDcnIters; ++k) {
             const int idx = tid + k * kOdThreads;
             if (idx >= kDcnItems) break;
-            const int pl = idx & 15;
-            const int oc = idx >> 4;
+            // Channel-fastest items (a wave's stores fill whole CB8 units): pixel pl is the
+            // same for the wave, its position that of lane pl.
+            const int oc = idx & (16 * kDcnNb - 1);
+            const int pl = idx / (16 * kDcnNb);
             const int nb = oc >> 4;
             const int src = ((pl >> 2) << 4) + (oc & 15);
             const int v = pl & 3;
             float s = 0.0f;
 #pragma unroll
-            for (int w = 0; w < kOdWaves; ++w) s += red[((w * kDcnNb + nb) * 4 + v) * 65 + src];
-            if (pvalid) {  // pl == lane % 16: this lane's pixel
+            for (int w = 0; w < kOdWaves; ++w) s += red[((w * kDcnNb + nb) * 4 + v) * kOdRedStride + src];
+            const int py = __shfl(oy, pl), px = __shfl(ox, pl);
+            if (__shfl((int)pvalid, pl)) {
                 const int c = a.out_coff + oc;
                 const size_t dst =
-                    ((size_t)((c >> 3) * (a.H + 2 * kPad) + oy + kPad) * (a.W + 2 * kPad) + ox + kPad) * 8 + (c & 7);
+                    ((size_t)((c >> 3) * (a.H + 2 * kPad) + py + kPad) * (a.W + 2 * kPad) + px + kPad) * 8 + (c & 7);
                 out[dst] = __builtin_bit_cast(uint16_t, round_f16(s + bdcnv[k]));
             }
         }
