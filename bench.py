@@ -19,9 +19,17 @@ prepacked_dev: the same repack, then the narrow kernel (C2) or the window kernel
 C5) with the BF16 sampler and BF16 MFMA); its timed output is checked against the FP32
 oracle on the widened BF16 inputs with bars 8x the FP16 ones.
 
+config.sampler names the sampler arithmetic of the timed kernel: "fast" (the mask folded
+into the four bilinear weights, rounded to FP16, packed-FP16 blend) or "exact" (the
+reference's half(FP32 bilinear x mask), MetalShader.swift:371-379). For FP16 storage the
+exact sampler is also timed beside it (exact_sampler, exact_kernel_us) on the kernel the
+library picks for it.
+
 cpu_baseline: the CPU oracle (a C restatement of the reference's DeformConvCPU.run),
-single thread, on a bounded sample of the benchmarked workload with the same inputs; its
-output of that sample also checks the GPU's timed output (timed_output_check).
+single thread, on a bounded sample of the benchmarked workload with the same inputs. In
+the same leg the oracle's output of the whole call (C3/C5: the same restatement on the
+host's threads) checks the GPU's timed output (timed_output_check) and the exact
+sampler's output (exact_sampler.output_check).
 """
 from __future__ import annotations
 
@@ -90,8 +98,9 @@ def cpu_baseline(config: int, s, inputs: dict, gpu_out, budget_s: float = 25.0,
                  bars: tuple[float, float] = (MAX_ABS_F16, MEAN_ABS_F16)) -> tuple[dict, dict]:
     """The CPU oracle (C restatement of DeformConvCPU.run, DeformConv.swift:76-138) timed on
     a bounded sample of the benchmarked workload, single thread, on the same (FP16-rounded
-    for C2/C3/C5) inputs the GPU ran; value is scaled to one whole call. Its output of the
-    sample is then the checker of the GPU's timed output: returns (baseline, check)."""
+    for C2/C3/C5) inputs the GPU ran; value is scaled to one whole call. The oracle's output
+    of the whole call then checks the GPU's outputs: `gpu_out` is one output or a dict of
+    named outputs; returns (baseline, check) or (baseline, {name: check})."""
     import dataclasses
 
     import numpy as np
@@ -162,18 +171,30 @@ def cpu_baseline(config: int, s, inputs: dict, gpu_out, budget_s: float = 25.0,
         baseline["all_cores"] = {"value": statistics.median(mt) * 1e6, "unit": "us/call", "cores": threads,
                                  "sample": "same call, output channels split over threads, median of 3"}
 
-    got = np.concatenate([np.asarray(gpu_out[sl], np.float32) for sl, _ in ref])
-    want = np.concatenate([r for _, r in ref])
-    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
-    check = {"oracle": "FP32 DeformConvCPU.run restatement on the inputs the GPU ran", "sample": sample,
-             "values": int(want.size), "max_abs_err": float(err.max()), "mean_abs_err": float(err.mean())}
-    if config == 1:
-        check["bound"] = "bit-exact"
-        check["within"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+    # The checker of the timed outputs: the whole call. For C1/C2 the timed sample is the
+    # whole call; for C3/C5 the same restatement runs once more over output channels on the
+    # host's threads (bit-identical to the single-threaded one).
+    if config in (1, 2):
+        want = np.concatenate([r for _, r in ref])
+        check_sample = sample
     else:
-        check["bound"] = {"max": bars[0], "mean": bars[1]}
-        check["within"] = bool(check["max_abs_err"] <= bars[0] and check["mean_abs_err"] <= bars[1])
-    return baseline, check
+        want = oracle.forward_f32_threads(s, *args, threads=min(16, os.cpu_count() or 1))
+        check_sample = "the full call (every output channel and pixel)"
+    outputs = gpu_out if isinstance(gpu_out, dict) else {"timed": gpu_out}
+    checks = {}
+    for name, o in outputs.items():
+        got = np.asarray(o, np.float32).reshape(-1)
+        err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+        check = {"oracle": "FP32 DeformConvCPU.run restatement on the inputs the GPU ran", "sample": check_sample,
+                 "values": int(want.size), "max_abs_err": float(err.max()), "mean_abs_err": float(err.mean())}
+        if config == 1:
+            check["bound"] = "bit-exact"
+            check["within"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+        else:
+            check["bound"] = {"max": bars[0], "mean": bars[1]}
+            check["within"] = bool(check["max_abs_err"] <= bars[0] and check["mean_abs_err"] <= bars[1])
+        checks[name] = check
+    return baseline, (checks if isinstance(gpu_out, dict) else checks["timed"])
 
 
 def calibration_copies(mib: int) -> None:
@@ -814,32 +835,18 @@ def main() -> int:
         kernel_us.append(a.elapsed_time(b) * 1e3 / args.steps)
     k_us = statistics.median(kernel_us)
 
-    # ---- cold cache: a 512 MB scratch write (twice the 256 MB MALL) before each call --
-    cold_us = warm_single_us = None
-    if args.cold_calls > 0:
-        scratch = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
-
-        def single_calls(flush: bool) -> float:
-            samples = []
+    def time_graph(graph) -> float:
+        """Median over kernel_reps replays of `graph` (args.steps launches), us per launch."""
+        reps = []
+        for _ in range(args.kernel_reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             with torch.cuda.stream(stream):
-                for i in range(args.cold_calls):
-                    if flush:
-                        scratch.fill_(i & 0xFF)
-                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    a.record(stream)
-                    step(stream)
-                    b.record(stream)
-                    b.synchronize()
-                    samples.append(a.elapsed_time(b) * 1e3)
+                a.record(stream)
+                graph.replay()
+                b.record(stream)
             torch.cuda.synchronize()
-            return statistics.median(samples)
-
-        cold_us = single_calls(True)
-        warm_single_us = single_calls(False)
-        del scratch
-
-    if args.calibration_copy_mib > 0:
-        calibration_copies(args.calibration_copy_mib)
+            reps.append(a.elapsed_time(b) * 1e3 / args.steps)
+        return statistics.median(reps)
 
     # What was timed: the output of the last timed call (checked against the oracle in the
     # cpu_baseline leg below).
@@ -849,6 +856,70 @@ def main() -> int:
         res = dc.bf16_bits_to_f32(out.cpu().numpy().view(np.uint16))
     else:
         res = out.cpu().numpy().view(np.float16).astype(np.float32)
+
+    # ---- the reference's sampler arithmetic (FP16 storage): half(FP32 bilinear x mask),
+    # MetalShader.swift:371-379, on the kernel the library picks for it, timed like the
+    # default; its output is checked in the cpu_baseline leg too ------------------------
+    exact = None
+    if not f32 and not bf16:
+        ctx.set_fused_config(args.mt, args.ks, dc.SAMPLER_EXACT, args.variant)
+        exact_cfg = ctx.get_fused_config(s)
+        with torch.cuda.stream(stream):
+            fused_only(stream)
+        torch.cuda.synchronize()
+        g_exact = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_exact, stream=stream):
+            cur = torch.cuda.current_stream()
+            for _ in range(args.steps):
+                fused_only(cur)
+        g_exact_step = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_exact_step, stream=stream):
+            cur = torch.cuda.current_stream()
+            for _ in range(args.steps):
+                step(cur)
+        with torch.cuda.stream(stream):
+            g_exact.replay()
+            g_exact_step.replay()
+        torch.cuda.synchronize()
+        exact = {"sampler": "exact", "fused_config": exact_cfg,
+                 "kernel": KERNEL_NAMES.get(exact_cfg["variant"], "fused_kernel"),
+                 "kernel_us": time_graph(g_exact), "us_per_call": time_graph(g_exact_step)}
+        exact["hbm_frac"] = algorithmic_bytes(s) / (exact["kernel_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS
+        exact_res = out.cpu().numpy().view(np.float16).astype(np.float32)
+        del g_exact, g_exact_step
+        ctx.set_fused_config(args.mt, args.ks, -1, args.variant)
+
+    # ---- cold cache: a 512 MB scratch write (twice the 256 MB MALL) before each call --
+    cold_us = warm_single_us = cold_kernel_us = warm_kernel_us = None
+    if args.cold_calls > 0:
+        scratch = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+
+        def single_calls(fn, flush: bool) -> float:
+            samples = []
+            with torch.cuda.stream(stream):
+                for i in range(args.cold_calls):
+                    if flush:
+                        scratch.fill_(i & 0xFF)
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record(stream)
+                    fn(stream)
+                    b.record(stream)
+                    b.synchronize()
+                    samples.append(a.elapsed_time(b) * 1e3)
+            torch.cuda.synchronize()
+            return statistics.median(samples)
+
+        cold_us = single_calls(step, True)
+        warm_single_us = single_calls(step, False)
+        if not f32:
+            # The fused kernel alone on the CB8 input, one eager launch each.
+            cold_kernel_us = single_calls(fused_only, True)
+            warm_kernel_us = single_calls(fused_only, False)
+        del scratch
+
+    if args.calibration_copy_mib > 0:
+        calibration_copies(args.calibration_copy_mib)
+
     finite = bool(np.all(np.isfinite(res)))
 
     nbytes = algorithmic_bytes(s, elem=4 if f32 else 2)
@@ -894,6 +965,8 @@ def main() -> int:
             "batch": s.batch, "in_channels": s.input_channels, "height": s.input_height, "width": s.input_width,
             "out_channels": s.output_channels, "kernel": [s.kernel_height, s.kernel_width],
             "deformable_groups": s.offset_groups, "fused_config": fused_cfg,
+            "sampler": "bf16" if bf16 else None if f32 else ("exact" if fused_cfg["sampler"] == dc.SAMPLER_EXACT
+                                                              else "fast"),
             "timing": f"{args.steps} calls captured in one hipGraph, one replay timed with HIP events",
         },
         "tflops": flops / (us_per_call * 1e-6) / 1e12,
@@ -902,8 +975,11 @@ def main() -> int:
         "kernel_us": k_us,
         "cold_us_per_call": cold_us,
         "warm_single_us_per_call": warm_single_us,
-        "cold_note": ("medians of single eager calls timed with HIP events on the call's stream "
-                      "(launch latency included), cold = each after a 512 MB scratch write, warm = "
+        "cold_kernel_us": cold_kernel_us,
+        "warm_single_kernel_us": warm_kernel_us,
+        "cold_note": ("medians of single eager calls (whole call; *_kernel_us: the fused kernel alone on "
+                      "the CB8 input) timed with HIP events on the call's stream (launch latency "
+                      "included), cold = each after a 512 MB scratch write (twice the MALL), warm = "
                       "back to back") if cold_us is not None else None,
         "kernel_tflops": flops / (k_us * 1e-6) / 1e12,
         "wall_ms_timed_region": wall_ms,
@@ -913,13 +989,21 @@ def main() -> int:
     }
     if args.config == 3 and not bf16:
         line["per_gpu_share"] = bench_share(args, ctx, dc, d, dev)
+    line["exact_sampler"] = exact
+    line["exact_kernel_us"] = exact["kernel_us"] if exact else None
     line["timed_output_check"] = None
     if not args.no_cpu_baseline:
         # BF16 keeps 3 fewer significant bits than FP16: bars 8x the FP16 ones.
         widened = {k: dc.bf16_bits_to_f32(h[k]) if bf16 else h[k].astype(np.float32) for k in keys}
-        line["cpu_baseline"], line["timed_output_check"] = cpu_baseline(
-            args.config, s, widened, res,
+        outputs = {"timed": res, "exact": exact_res} if exact else res
+        line["cpu_baseline"], checks = cpu_baseline(
+            args.config, s, widened, outputs,
             bars=(8 * MAX_ABS_F16, 8 * MEAN_ABS_F16) if bf16 else (MAX_ABS_F16, MEAN_ABS_F16))
+        if exact:
+            line["timed_output_check"] = checks["timed"]
+            exact["output_check"] = checks["exact"]
+        else:
+            line["timed_output_check"] = checks
     if packed is not None:
         packed.free()
     ctx.close()

@@ -288,7 +288,8 @@ dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_sha
  * No counterpart in the reference (its tile size is the compile-time
  * fusedGEMMRowsPerTile, MetalShader.swift:2). */
 dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, int sampler);
-/* The configuration the next FP16 fused call on `shape` would use. */
+/* The configuration the next FP16 fused call on `shape` would use. ctx may be null: the
+ * automatic choice without an override (no device is touched). */
 dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* variant, int* mt,
                                 int* ks, int* sampler);
 

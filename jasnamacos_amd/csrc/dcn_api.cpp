@@ -37,9 +37,9 @@ bool packed_matches(const dcn_packed* p, const dcn_shape* s) {
            p->shape.offset_groups == s->offset_groups;
 }
 
-dcn::FusedConfig choose_config(const dcn_context* ctx, const dcn::FusedGeometry& g, const dcn_shape& shape,
+// `o`: the caller's dcn_set_fused_config override ({0, 0, 0, -1}: none).
+dcn::FusedConfig choose_config(dcn::FusedConfig o, const dcn::FusedGeometry& g, const dcn_shape& shape,
                                bool window_ok, bool tile_ok) {
-    dcn::FusedConfig o = ctx->fused_override;
     // Problems of more than 32K output pixels run fastest on the tile kernel: batches of
     // small maps (C3: 16 x 64 x 64, 48.6 us against 55.2 us for the window kernel) and
     // single large maps (C5: 1 x 180 x 320, 60.2 us against 70.9 us; its wide-flow stages
@@ -163,7 +163,7 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
         bf16 ? (tiles32 <= 1024 ? dcn::FusedConfig{dcn::kVariantNarrow, 1, 12, dcn::kSamplerBf16}
                 : bf16_window   ? dcn::FusedConfig{dcn::kVariantWindow, 4, 4, dcn::kSamplerBf16}
                                 : dcn::FusedConfig{dcn::kVariantRegister, 2, 4, dcn::kSamplerBf16})
-             : choose_config(ctx, g, *shape, packed->weights_group != nullptr && dcn::window_supported(*shape),
+             : choose_config(ctx->fused_override, g, *shape, packed->weights_group != nullptr && dcn::window_supported(*shape),
                              packed->weights_tile != nullptr && dcn::tile_supported(*shape));
     if (!config_supported(cfg, g))
         return fail(ctx, DCN_INVALID_ARGUMENT,
@@ -360,13 +360,15 @@ dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, i
 
 dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* variant, int* mt,
                                 int* ks, int* sampler) {
-    if (!ctx || !variant || !mt || !ks || !sampler) return DCN_INVALID_ARGUMENT;
+    if (!variant || !mt || !ks || !sampler) return DCN_INVALID_ARGUMENT;
     dcn_counts c;
     DCN_TRY(validated_counts(ctx, shape, &c));
     dcn::FusedGeometry g;
     if (!dcn::fused_geometry(*shape, &g)) return fail(ctx, DCN_INVALID_SHAPE, "not a fused shape");
-    const dcn::FusedConfig cfg =
-        choose_config(ctx, g, *shape, dcn::window_supported(*shape), dcn::tile_supported(*shape));
+    // A null context asks for the automatic choice (no override); it touches no device.
+    const dcn::FusedConfig none{0, 0, 0, -1};
+    const dcn::FusedConfig cfg = choose_config(ctx ? ctx->fused_override : none, g, *shape,
+                                               dcn::window_supported(*shape), dcn::tile_supported(*shape));
     *variant = cfg.variant;
     *mt = cfg.mt;
     *ks = cfg.ks;

@@ -66,7 +66,9 @@ enum SamplerMode : int {
     kSamplerFast = 1,
     // BF16 storage (input, offsets, mask, weights, output): the exact sampler's FP32
     // arithmetic on the widened BF16 corners, each sample rounded once to BF16, and the
-    // BF16 MFMA (the register variant only).
+    // BF16 MFMA. The BF16 forwards run the narrow variant up to 1024 tiles of 32 pixels,
+    // above that the window variant (4 x 32 tiles, 4 waves) where the shape allows it,
+    // else the register variant.
     kSamplerBf16 = 2,
 };
 
@@ -355,5 +357,6 @@ struct dcn_packed {
     void* weights_tile = nullptr;   // tap-major B fragments of the tile variant (or null)
     float* bias = nullptr;      // Cout floats
     int device = 0;
-    bool bf16 = false;          // BF16 weights (dcn_prepack_bf16*): the register variant only
+    bool bf16 = false;          // BF16 weights (dcn_prepack_bf16*): narrow, window or register
+                                // variant, no tile fragments
 };

@@ -12,42 +12,46 @@
 //
 // The L2 -> CU path is then the scarce resource, and it is counted in instructions as
 // much as in bytes: 64 addresses take the texture addresser many cycles whatever their
-// size. Reading each sample's offsets and mask with 2-byte loads (27 per pixel and stage,
-// ~216 load instructions per CU and stage) saturated it and doubled the kernel's time.
-// So a stage's 54 offset and mask channels for the tile's 256 pixels (27 KB) are copied
-// to LDS by 27 DMA instructions and every lane reads its values from there. The path
-// also carries the windows (~60 KB per stage) and the weight fragments. With one 32-pixel block per
-// wave, every wave streams the whole weight set (8 x 18 KB per stage), more than the
-// windows. Here each wave holds two 32-pixel blocks (the MFMA B fragment is used for
-// both) and half the taps of a stage: waves 0-3 take taps 0-4, waves 4-7 taps 5-8 of
-// the same pixels. Each weight fragment crosses the path once per pixel block pair, and
-// the two halves of each pixel's sum meet in LDS at the end, in a fixed order.
+// size. Reading each sample's offsets and mask with 2-byte loads (27 per pixel and stage)
+// saturated it and doubled the kernel's time. So a stage's 54 offset and mask channels
+// for the tile's 128 pixels (13.5 KB) are copied to LDS by LDS DMA and every lane reads
+// its values from there. The path also carries the windows and the weight fragments.
+// With one 32-pixel segment per wave, every wave would stream the whole weight set;
+// here each wave holds two 32-pixel segments (the MFMA B fragment is used for both) and
+// about half the taps of a stage, so each weight fragment crosses the path once per two
+// segments, and the two halves of each pixel's sum meet in LDS at the end, in a fixed
+// order (taps 0-4 + taps 5-8).
 //
 // The sampler's VALU is the other limit. One sample (8 channels) feeds 64 output
-// channels, i.e. two v_mfma_f32_32x32x16_f16 (64 MFMA cycles), while its bilinear blend
-// alone is 16 packed FP16 FMAs (64 VALU cycles). So each sample's coordinates and FP16
-// corner weights are computed once, off the K-loop, and the K-loop does two address
-// additions and the blend.
+// channels, i.e. two v_mfma_f32_32x32x16_f16, while its bilinear blend alone is 16 packed
+// FP16 instructions. So each sample's coordinates and FP16 corner weights are computed
+// once, off the K-loop (inside the previous stage's first K-steps), and the K-loop does
+// an address select and the blend.
 //
-// Layout. Workgroup = 8 waves on a 16 x 16 (TW = 16) or 8 x 32 (TW = 32) pixel tile.
-// Pixel block q (0-3) is 64 pixels: two segments of 32, each 32 / TW tile rows. A stage is
-// two offset groups; K-step k of stage s is tap k of both: lanes 0-31 give group 2s,
-// lanes 32-63 group 2s+1 (the A operand of v_mfma_f32_32x32x16_f16 is 32 pixels x 16 K,
-// 8 per lane), and the weights are prepacked in that order (tile_prepack_kernel).
+// Layout. Workgroup = 4 waves (kTileWaves) on a 128-pixel tile (kTilePix): 8 x 16 pixels
+// (TW = 16) or 4 x 32 (TW = 32). Wave w owns pixel block w & 1 (64 pixels = two segments
+// of 32, each 32 / TW tile rows); waves 0-1 take taps 0-4 and waves 2-3 taps 5-8 of the
+// same pixels. A stage is two offset groups; K-step k of stage s is tap k of both: lanes
+// 0-31 give group 2s, lanes 32-63 group 2s+1 (the A operand of v_mfma_f32_32x32x16_f16 is
+// 32 pixels x 16 K, 8 per lane), and the weights are prepacked in that order
+// (tile_prepack_kernel).
 //
-// Pipeline (one workgroup per CU, two 66 KB window buffers), iteration s:
-//   - K-steps 0-1 also compute stage s+1's corner coordinates and their bounding box;
-//   - a barrier; stage s+2's offsets are requested by LDS DMA;
-//   - the remaining K-steps also request a slice of the windows of s+1 by LDS DMA into
-//     the other buffer (all waves, 64-unit chunks) and turn s+1's coordinates into LDS
-//     addresses;
+// Pipeline (two workgroups per CU, each with one 64 KB window buffer, kTileBuf), stage s:
+//   - the K-loop of stage s, whose first two K-steps also compute stage s+1's corner
+//     coordinates and bounding box (from s+1's offsets, already in LDS), and which
+//     requests stage s+1's weight fragment of each tap as soon as tap k of s is done;
+//   - a barrier; the box reduced; stage s+1's windows and stage s+2's offsets requested
+//     by LDS DMA (the window buffer is free: every wave is past s's corner reads);
+//     s+1's coordinates turned into LDS addresses;
 //   - a wait for the DMA and a barrier.
+// One workgroup's copies overlap the other workgroup's K-loop on the same CU.
 // Vector-memory results return in issue order (one vmcnt counter), so a wait for a
 // weight fragment also waits for every older load: each stage's fragments are all in
-// registers before the stage starts (requested during the previous one), so the K-loop
-// never waits on memory.
-// A stage whose two windows do not fit their buffer gathers from the global CB8 input
-// instead (same arithmetic, no copy), so any offset field is handled.
+// registers before the stage starts, so the K-loop never waits on memory.
+// A stage whose two windows do not fit the buffer together but each fits alone runs one
+// pass per group (the other group's lanes read zeros); a stage with a window larger than
+// the buffer gathers from the global CB8 input instead (same arithmetic, no copy), so any
+// offset field is handled.
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -74,6 +78,7 @@ constexpr int kTileOff = kTileOffCh * kTilePix * 2;   // [36 dy/dx + 18 mask][12
 constexpr int kTileBox = 2 * kTileWaves * 2 * 4;      // [group][wave][min, max]
 constexpr int kTileZero = kTileBuf + kTileOff + kTileBox;  // 32 zero bytes (masked lanes' corners)
 constexpr int kTileLds = kTileZero + 32;               // 79,456 B: two workgroups per CU
+constexpr int kTileMaxSide = 32000;                    // input height / width (16-bit corners)
 
 struct TileArgs {
     const void* xin;      // CB8 input [B][CBLK][Hp][Wp][8]
@@ -607,9 +612,13 @@ hipError_t launch_tile_nb(const TileArgs& a, int nb, hipStream_t stream) {
 
 bool tile_supported(const dcn_shape& s) {
     // Output rows of 8-pixel multiples: the offsets are copied as 16-byte chunks of rows.
+    // Clamped corner coordinates (-2 .. H, -2 .. W) travel as signed 16-bit pairs through
+    // the box reduction and the address set-up, so both input sides stay below 2^15 with
+    // room for the clamp.
     return s.groups == 1 && s.kernel_height == 3 && s.kernel_width == 3 &&
            s.input_channels == 8 * s.offset_groups && s.offset_groups % 2 == 0 &&
-           s.output_channels % 32 == 0 && s.output_channels <= 64 && s.output_width % 8 == 0;
+           s.output_channels % 32 == 0 && s.output_channels <= 64 && s.output_width % 8 == 0 &&
+           s.input_height <= kTileMaxSide && s.input_width <= kTileMaxSide;
 }
 
 size_t tile_packed_bytes(const dcn_shape& s) {

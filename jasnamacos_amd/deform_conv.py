@@ -134,6 +134,16 @@ class DeformConvShape:
     def fused_supported(self) -> bool:
         return bool(lib().dcn_shape_fused_supported(C.byref(self.to_c())))
 
+    def automatic_fused_config(self) -> dict:
+        """The fused kernel an FP16 prepacked call on this shape runs when no override is
+        set (dcn_get_fused_config with a null context; no device is touched)."""
+        v, mt, ks, sm = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        st = lib().dcn_get_fused_config(None, C.byref(self.to_c()), C.byref(v), C.byref(mt), C.byref(ks),
+                                        C.byref(sm))
+        if st != OK:
+            raise DeformConvError(st)
+        return {"variant": v.value, "mt": mt.value, "ks": ks.value, "sampler": sm.value}
+
     @property
     def flops(self) -> int:
         """2 * B * Ho * Wo * Cout * (Cin/groups) * Kh * Kw (GEMM-equivalent)."""

@@ -504,8 +504,20 @@ void oracle_conv3x3_f16(int cin, int cout, int height, int width, const uint16_t
                         const uint16_t* weight, const uint16_t* bias, int activation,
                         float slope, const uint16_t* residual, uint16_t* output) {
     /* activation: 0 none, 1 LeakyReLU(slope), 2 ReLU. out = half(residual + act(acc)):
-     * one rounding after the FP32 residual add, not half(residual + half(act(acc))). */
+     * one rounding after the FP32 residual add, not half(residual + half(act(acc))).
+     * FP16 -> FP32 is exact, so the operands are widened once up front; every product and
+     * sum is then the same FP32 operation, in the same order, as widening in the loop. */
     const size_t plane = (size_t)width * height;
+    const size_t in_count = (size_t)cin * plane, w_count = (size_t)cout * cin * 9;
+    float* in32 = (float*)malloc(in_count * sizeof(float));
+    float* w32 = (float*)malloc(w_count * sizeof(float));
+    if (!in32 || !w32) {
+        free(in32);
+        free(w32);
+        return;
+    }
+    for (size_t i = 0; i < in_count; ++i) in32[i] = oracle_f16_to_f32(input[i]);
+    for (size_t i = 0; i < w_count; ++i) w32[i] = oracle_f16_to_f32(weight[i]);
     /* Output channels are independent; each element is computed by the same serial code. */
 #pragma omp parallel for schedule(static)
     for (int oc = 0; oc < cout; ++oc) {
@@ -513,16 +525,15 @@ void oracle_conv3x3_f16(int cin, int cout, int height, int width, const uint16_t
             for (int ox = 0; ox < width; ++ox) {
                 float acc = oracle_f16_to_f32(bias[oc]);
                 for (int ic = 0; ic < cin; ++ic) {
+                    const float* src = in32 + (size_t)ic * plane;
+                    const float* wk = w32 + ((size_t)oc * cin + ic) * 9;
                     for (int ky = 0; ky < 3; ++ky) {
                         const int iy = oy + ky - 1;
                         if (iy < 0 || iy >= height) continue;
                         for (int kx = 0; kx < 3; ++kx) {
                             const int ix = ox + kx - 1;
                             if (ix < 0 || ix >= width) continue;
-                            acc += oracle_f16_to_f32(input[(size_t)ic * plane +
-                                                           (size_t)iy * width + ix]) *
-                                   oracle_f16_to_f32(
-                                       weight[(((size_t)oc * cin + ic) * 3 + ky) * 3 + kx]);
+                            acc += src[(size_t)iy * width + ix] * wk[ky * 3 + kx];
                         }
                     }
                 }
@@ -534,6 +545,8 @@ void oracle_conv3x3_f16(int cin, int cout, int height, int width, const uint16_t
             }
         }
     }
+    free(in32);
+    free(w32);
 }
 
 /* ---- SPyNet flow estimation ---- */

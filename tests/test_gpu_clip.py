@@ -285,3 +285,53 @@ def test_clip_nonfinite_input_ends_the_ladder_in_command_failed(gpu_ctx, dcn, to
         _ladder(torch, gpu_ctx, wd, xd, frames, h, w, blocks)
     assert e.value.status == dcn.COMMAND_FAILED
     assert "non-finite input features" in str(e.value)
+
+
+def test_clip_free_running_c4_size_matches_oracle_chain(gpu_ctx, dcn, torch):
+    """The four-branch clip at config C4's size (64 x 64, 5 blocks) over 8 frames, free
+    running: the GPU clip runs once on its own outputs, and the oracle chain runs the whole
+    TemporalSchedule the same way on the CPU (each step's feat_prop, feat_n2 and prefix are
+    the oracle's own earlier outputs), so any compounding through the recurrence or across
+    branches (branches 1-3 read the earlier branches' outputs, 192-320 backbone input
+    channels) shows. Smooth synthetic flows of up to +-4 px (generate_body_inputs).
+    Per-step max / mean absolute error is logged; each step must stay within the one-step
+    FP16 bars (max 2e-2, mean 1e-3)."""
+    frames, h, w, blocks = 8, 64, 64, 5
+    plane = h * w
+    gens = [dcn.generate_body_inputs(h, w, frames, b, blocks, seed=40 + b) for b in range(4)]
+    weights = [g["weights"] for g in gens]
+    spatial = gens[0]["feats"].reshape(frames, 64 * plane)
+    bflows = gens[1]["flows"].reshape(frames, 2 * plane)[:frames - 1]
+    fflows = gens[2]["flows"].reshape(frames, 2 * plane)[:frames - 1]
+    wd = [{k: dev(torch, v) for k, v in wb.items()} for wb in weights]
+    xd = {"spatial": dev(torch, spatial.ravel()), "bflows": dev(torch, bflows.ravel()),
+          "fflows": dev(torch, fflows.ravel())}
+    log("case: free-running four-branch clip", frames, h, w, "blocks", blocks)
+    got = _run_clip(torch, gpu_ctx, wd, xd, frames, h, w, blocks).astype(np.float64)
+    assert np.all(np.isfinite(got))
+
+    flows = {"backward": bflows, "forward": fflows}
+    zero = np.zeros(64 * plane, np.float16)
+    ref = np.zeros((4, frames, 64 * plane), np.float16)
+    schedule = dcn.TemporalSchedule(frames)
+    worst = (0.0, 0.0)
+    for n, s in enumerate(schedule.steps):
+        b = s.branch.branch_index
+        prefix = [ref[i, s.frame_index] for i in range(b)]
+        if s.position == 0:
+            ref[b, s.frame_index] = br.body_initial_step(weights[b], spatial[s.frame_index], prefix, h, w, blocks)
+        else:
+            steps = [t for t in schedule.steps if t.branch == s.branch]
+            prev = steps[s.position - 1]
+            f = flows[s.branch.direction]
+            x = {"feat_current": spatial[s.frame_index], "flow1": f[s.flow_index],
+                 "prev_flow": f[prev.flow_index] if s.position >= 2 else f[s.flow_index],
+                 "feat_prop": ref[b, prev.frame_index],
+                 "feat_n2": ref[b, s.second_order_frame_index] if s.second_order_frame_index is not None else zero,
+                 "prefix": prefix}
+            _, ref[b, s.frame_index], _ = br.body_step(weights[b], x, h, w, blocks, s.position >= 2)
+        e = np.abs(got[b, s.frame_index] - ref[b, s.frame_index].astype(np.float64))
+        log(f"  step {n:2d} branch {b} frame {s.frame_index}: max {e.max():.3e} mean {e.mean():.3e}")
+        worst = (max(worst[0], e.max()), max(worst[1], e.mean()))
+        assert e.max() <= 2e-2 and e.mean() <= 1e-3, (n, b, s.frame_index, e.max(), e.mean())
+    log(f"  worst over {len(schedule.steps)} steps: max {worst[0]:.3e} mean {worst[1]:.3e}")

@@ -265,11 +265,19 @@ def test_automatic_config_per_workload(gpu_ctx, dcn):
         gpu_ctx.set_fused_config(0, 0, -1)
 
 
-@pytest.mark.parametrize("variant", [0, 3, 5, 6, 7])
-def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle, variant):
+@pytest.fixture(scope="module")
+def c3(dcn, oracle):
+    """C3's 16 tiles with the FP32 oracle over the whole batch (computed once)."""
     d = dcn.generate_config_inputs(3, 3)
-    s = d["shape"]
     h = f16_inputs(d)
+    w = widen(h)
+    ref = oracle.forward_f32_threads(d["shape"], w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    return d["shape"], h, ref
+
+
+@pytest.mark.parametrize("variant", [0, 3, 5, 6, 7])
+def test_fused_c3_batched_tiles(gpu_ctx, dcn, c3, variant):
+    s, h, ref = c3
     log("case: fused C3 16 tiles, variant", variant)
     packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
     gpu_ctx.set_fused_config(0, 0, -1, variant)
@@ -277,16 +285,11 @@ def test_fused_c3_batched_tiles(gpu_ctx, dcn, oracle, variant):
         out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
     finally:
         gpu_ctx.set_fused_config(0, 0, -1, 0)
-    tile = dataclasses.replace(s, batch=1)
-    c = tile.counts()
-    for b in (0, 7, 15):  # tiles are independent: check three against the oracle
-        w = widen(h)
-        ref = oracle.forward_f32_threads(tile, w["input"][b * c["input"]:(b + 1) * c["input"]],
-                                         w["offset"][b * c["offset"]:(b + 1) * c["offset"]],
-                                         w["mask"][b * c["mask"]:(b + 1) * c["mask"]], w["weight"], w["bias"])
-        mx, mean = errors(out[b * c["output"]:(b + 1) * c["output"]], ref)
+    n = dataclasses.replace(s, batch=1).counts()["output"]
+    for b in range(s.batch):  # every tile, every output channel and pixel
+        mx, mean = errors(out[b * n:(b + 1) * n], ref[b * n:(b + 1) * n])
         log(f"  tile {b}: max {mx:.3e} mean {mean:.3e}")
-        assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+        assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, b
 
 
 @pytest.mark.parametrize("cout", [32, 128])
@@ -373,11 +376,19 @@ def test_narrow_batch_equals_single_images(gpu_ctx, dcn, batch, h, w):
         gpu_ctx.set_fused_config(0, 0, -1, 0)
 
 
-@pytest.mark.parametrize("variant", [0, 6, 7])
-def test_fused_c5_large_map(gpu_ctx, dcn, oracle, variant):
+@pytest.fixture(scope="module")
+def c5(dcn, oracle):
+    """C5's large map with the FP32 oracle over all 64 output channels (computed once)."""
     d = dcn.generate_config_inputs(5, 5)
-    s = d["shape"]
     h = f16_inputs(d)
+    w = widen(h)
+    ref = oracle.forward_f32_threads(d["shape"], w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    return d["shape"], h, ref
+
+
+@pytest.mark.parametrize("variant", [0, 6, 7])
+def test_fused_c5_large_map(gpu_ctx, dcn, c5, variant):
+    s, h, ref = c5
     log("case: fused C5 1x128x180x320, variant", variant)
     packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
     gpu_ctx.set_fused_config(0, 0, -1, variant)
@@ -385,17 +396,15 @@ def test_fused_c5_large_map(gpu_ctx, dcn, oracle, variant):
         out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
     finally:
         gpu_ctx.set_fused_config(0, 0, -1, 0)
-    w = widen(h)
     plane = s.output_height * s.output_width
-    # Bounded slices of output channels, every pixel and sample: both ends of both
-    # 32-channel MFMA column blocks.
-    for lo in (0, 28, 60):
-        ocs = range(lo, lo + 4)
-        ref = oracle.forward_f32_ocs(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"], ocs)
-        sl = slice(lo * plane, (lo + 4) * plane)
+    # Every output channel and pixel, reported in slices of 16 channels.
+    for lo in range(0, s.output_channels, 16):
+        sl = slice(lo * plane, (lo + 16) * plane)
         mx, mean = errors(out[sl], ref[sl])
-        log(f"  C5 oc {lo}..{lo + 3}: max {mx:.3e} mean {mean:.3e}")
-        assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+        log(f"  C5 oc {lo}..{lo + 15}: max {mx:.3e} mean {mean:.3e}")
+        assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, lo
+    mx, mean = errors(out, ref)
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
     assert np.all(np.isfinite(out.astype(np.float32)))
 
 
@@ -546,6 +555,41 @@ def test_tile_split_stages(gpu_ctx, dcn, oracle, tw):
     mx, mean = errors(out, ref)
     log(f"  max {mx:.3e} mean {mean:.3e}")
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
+TILE_EDGE_SHAPES = [
+    # (batch, Cin, H, W, Cout, Ho, Wo, Kh, Kw, ph, pw, sh, sw, dh, dw, groups, offset_groups)
+    (1, 16, 13, 40, 32, 13, 40, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2),   # Wo % 16 != 0, H % 8 != 0, Cout 32 (NB 1)
+    (2, 32, 17, 31, 64, 9, 16, 3, 3, 1, 1, 2, 2, 1, 1, 1, 4),    # stride 2, H != Ho
+    (1, 16, 12, 24, 32, 12, 24, 3, 3, 2, 2, 1, 1, 2, 2, 1, 2),   # dilation 2, pad 2
+    (1, 32, 10, 18, 64, 8, 16, 3, 3, 0, 0, 1, 1, 1, 1, 1, 4),    # pad 0
+    (1, 16, 9, 14, 64, 11, 16, 3, 3, 2, 2, 1, 1, 1, 1, 1, 2),    # pad 2: output larger than input
+]
+
+
+@pytest.mark.parametrize("dims", TILE_EDGE_SHAPES, ids=lambda t: "x".join(map(str, t)))
+@pytest.mark.parametrize("tw", [16, 32])
+def test_tile_edge_shapes(gpu_ctx, dcn, oracle, dims, tw):
+    """The tile kernel (variant 7, asserted) on shapes off its C3/C5 path: rows that end
+    inside a tile (clamped lanes, offset chunks past the row), output rows past the map,
+    Cout 32, stride and dilation 2, pad 0 and 2; within the FP16 bars of the FP32 oracle."""
+    s = dcn.DeformConvShape(*dims)
+    d = rand_case(s, sum(dims) + tw, offset_scale=4.0)
+    d["weight"] *= 0.5
+    h = f16_inputs(d)
+    w = widen(h)
+    log("case: tile edge", dims, "width", tw)
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(tw, 8, -1, 7)
+    try:
+        assert gpu_ctx.get_fused_config(s) == {"variant": 7, "mt": tw, "ks": 8, "sampler": 1}
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    ref = oracle.forward_f32(s, w["input"], w["offset"], w["mask"], w["weight"], w["bias"])
+    mx, mean = errors(out, ref)
+    log(f"  max {mx:.3e} mean {mean:.3e}")
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
 def bf16_case(dcn, shape, seed, offset_scale=3.0):

@@ -228,3 +228,27 @@ def test_create_without_device_reports_unavailable(dcn):
     with pytest.raises(dcn.DeformConvError) as e:
         dcn.HipDeformConv(0)
     assert e.value.status == dcn.DEVICE_UNAVAILABLE
+
+
+
+def test_automatic_fused_config_per_workload(dcn):
+    """The automatic kernel choice without a device: the narrow kernel (variant 5) up to
+    1024 tiles of 32 pixels (C2), the tile kernel (variant 7) above that (C3, C5)."""
+    assert dcn.config_shape(2).automatic_fused_config()["variant"] == 5
+    assert dcn.config_shape(3).automatic_fused_config() == {"variant": 7, "mt": 16, "ks": 8, "sampler": 1}
+    assert dcn.config_shape(5).automatic_fused_config()["variant"] == 7
+
+
+@pytest.mark.parametrize("side", ["input_height", "input_width"])
+@pytest.mark.parametrize("n,tile", [(32000, True), (32001, False), (40000, False)])
+def test_tile_kernel_side_limit(dcn, side, n, tile):
+    """The tile kernel carries clamped corner coordinates (-2 .. H, -2 .. W) as signed
+    16-bit pairs: maps with a side above 32000 go to another kernel, those at the limit
+    still take it. The strips have 16 channels (2 offset groups), more than 1024 tiles of
+    32 pixels and 8-pixel output rows: otherwise the tile kernel's domain."""
+    if side == "input_width":
+        s = dcn.DeformConvShape(1, 16, 2, n, 32, 2, 20000, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)
+    else:
+        s = dcn.DeformConvShape(1, 16, n, 8, 32, 5000, 8, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)
+    cfg = s.automatic_fused_config()
+    assert (cfg["variant"] == 7) == tile, cfg
