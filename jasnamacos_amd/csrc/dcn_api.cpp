@@ -41,9 +41,10 @@ bool packed_matches(const dcn_packed* p, const dcn_shape* s) {
 dcn::FusedConfig choose_config(dcn::FusedConfig o, const dcn::FusedGeometry& g, const dcn_shape& shape,
                                bool window_ok, bool tile_ok) {
     // Problems of more than 32K output pixels run fastest on the tile kernel: batches of
-    // small maps (C3: 16 x 64 x 64, 48.6 us against 55.2 us for the window kernel) and
-    // single large maps (C5: 1 x 180 x 320, 60.2 us against 70.9 us; its wide-flow stages
-    // whose two windows do not fit LDS together run one pass per window).
+    // small maps (C3: 16 x 64 x 64, 48.0 us against 55.2 us for the window kernel) and
+    // single large maps (C5: 1 x 180 x 320, 55.2 us with the cost-ordered tile placement,
+    // against 70.9 us; its wide-flow stages whose two windows do not fit LDS together run
+    // one pass per window).
     if (o.variant == 0 && tile_ok && o.sampler != dcn::kSamplerExact && (g.m + 31) / 32 > 1024)
         o.variant = dcn::kVariantTile;
     // The tile variant implements the fast sampler only: with the exact one (or a shape
@@ -97,8 +98,8 @@ dcn::FusedConfig choose_config(dcn::FusedConfig o, const dcn::FusedGeometry& g, 
 }
 
 bool config_supported(const dcn::FusedConfig& c, const dcn::FusedGeometry& g) {
-    if (c.variant == dcn::kVariantTile)
-        return (c.mt == 16 || c.mt == 32) && c.ks == 8 && c.sampler == dcn::kSamplerFast;
+    if (c.variant == dcn::kVariantTile)  // ks: 8 = cost-ordered tile placement, 1 = fixed
+        return (c.mt == 16 || c.mt == 32) && (c.ks == 8 || c.ks == 1) && c.sampler == dcn::kSamplerFast;
     if (c.variant == dcn::kVariantWindowAsync) return c.mt == 8 && c.ks == 8;
     if (c.variant == dcn::kVariantNarrow) return c.mt == 1 && (c.ks == 8 || c.ks == 12);
     if (c.variant == dcn::kVariantWindow || c.variant == dcn::kVariantWindowSplit)

@@ -92,6 +92,7 @@ struct TileArgs {
     int G, CBLK, Hp, Wp, Cout;
     float one;  // 1.0f, opaque to the compiler (see coords)
     int tiles_y, tiles_x, tiles;
+    int plan;   // 1: cost-ordered placement of a band's tiles (tile_band_slot) where it applies
 };
 
 // 16-byte LDS DMA: unit `voff` of the buffer to LDS lds_base + 16 * lane (lds_base uniform).
@@ -125,6 +126,106 @@ __device__ __forceinline__ h8 blend_w(const u32x4 (&q)[4], uint32_t w0, uint32_t
     return r;
 }
 
+// Placement of a band's tiles on its XCD's CUs. Workgroups are dispatched to an XCD in
+// blockIdx order (blockIdx % 8), and within an XCD local index l goes to CU l % 32: with
+// n tiles per band, 32 < n < 64, locals l and l + 32 (l < n - 32) share a CU and locals
+// n - 32 .. 31 run alone (measured on MI355X with per-workgroup hardware ids). A tile
+// whose stages split (windows that do not fit the buffer together) takes 1.2-1.4x the time
+// of the others and, when two such tiles share a CU, sets the kernel's time. So the
+// band's tiles are ranked by an estimate of their window area, the heaviest take the
+// alone slots, and the rest are paired heaviest with lightest.
+// The estimate of a tile: the extent of the clamped sample positions of one offset
+// channel pair (group 0, centre tap; the offset field's flow part is common to all
+// groups and taps, its residue spans the same range in each) over the tile's pixels:
+// (rows + 3) x (columns + 3). Every workgroup of the band reads the same offsets and runs
+// the same arithmetic, so all of them compute the same ranking without communicating.
+// Returns the band-local index of the tile that local slot `loc` runs. All threads of the
+// workgroup call it (it has barriers); `sh` is 1 KB of LDS that nothing else uses yet.
+template <int TW>
+__device__ int tile_band_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr, int band0, int n, int loc,
+                              float* sh) {
+    constexpr int TH = 128 / TW;
+    constexpr int kPieces = TW / 8;          // 16-byte pieces of a tile row
+    constexpr int kUnits = 2 * TH * kPieces; // 32: dy and dx pieces of a tile
+    static_assert(kUnits == 32, "a tile's estimate is 32 units of 8 pixels");
+    const int tid = threadIdx.x;
+    const int u = tid & 31;
+    const int ch = u >> 4;                    // 0: dy, 1: dx
+    const int row = (u & 15) / kPieces, piece = (u & 15) % kPieces;
+    constexpr int kPass = 64 * kTileWaves / kUnits;  // tiles per pass (8)
+    const int tiles_img = a.tiles_y * a.tiles_x;
+    // Centre tap (ky = kx = 1 of the 3x3 kernel) of group 0: offset channels 8 (dy), 9 (dx).
+    float mn[8], mx[8];
+#pragma unroll
+    for (int pass = 0; pass < 8; ++pass) {
+        const int i = pass * kPass + (tid >> 5);
+        mn[pass] = 3.0e38f;
+        mx[pass] = -3.0e38f;
+        if (pass * kPass >= n) continue;  // uniform
+        const int t = band0 + min(i, n - 1);
+        const int b = t / tiles_img, r = t - b * tiles_img;
+        const int ty = r / a.tiles_x, tx = r - ty * a.tiles_x;
+        const int oy = min(ty * TH + row, a.Ho - 1);
+        const int ox0 = tx * TW + piece * 8;
+        const bool valid = i < n && ox0 < a.Wo;  // output rows are whole 8-pixel pieces
+        const uint32_t at = ((uint32_t)(b * 2 * a.G * 9 + 8 + ch) * (uint32_t)a.HWo +
+                             (uint32_t)(oy * a.Wo + min(ox0, a.Wo - 8))) * 2u;
+        const u32x4 q = load16(orr, at, 0);
+        const h8 v = __builtin_bit_cast(h8, q);
+        const float base = ch ? (float)(ox0 * a.sw - a.pw + a.dw) : (float)(oy * a.sh - a.ph + a.dh);
+        const float step = ch ? (float)a.sw : 0.0f;
+        const float hi = ch ? (float)a.W : (float)a.H;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float c = __builtin_amdgcn_fmed3f(base + (float)j * step + (float)v[j], -2.0f, hi);
+            mn[pass] = fminf(mn[pass], c);
+            mx[pass] = fmaxf(mx[pass], c);
+        }
+        if (!valid) {
+            mn[pass] = 3.0e38f;
+            mx[pass] = -3.0e38f;
+        }
+    }
+    // Extent per (tile, channel): a min / max over the 16 lanes of its pieces.
+#pragma unroll
+    for (int pass = 0; pass < 8; ++pass) {
+        if (pass * kPass >= n) continue;
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) {
+            mn[pass] = fminf(mn[pass], __shfl_xor(mn[pass], m));
+            mx[pass] = fmaxf(mx[pass], __shfl_xor(mx[pass], m));
+        }
+        const int i = pass * kPass + (tid >> 5);
+        if ((u & 15) == 0 && i < n) sh[2 * i + ch] = mx[pass] - mn[pass];
+    }
+    float* cost = sh + 128;
+    int* chosen = reinterpret_cast<int*>(sh + 192);
+    if (tid == 0) *chosen = loc;  // (ranks are a permutation: some thread overwrites it)
+    __syncthreads();
+    if (tid < n) {
+        const float c = (sh[2 * tid] + 3.0f) * (sh[2 * tid + 1] + 3.0f);
+        cost[tid] = c == c ? c : 0.0f;
+    }
+    __syncthreads();
+    // Rank = place in descending cost order (ties by index); the slot's rank: alone slots
+    // n-32 .. 31 the heaviest, then CU c < n - 32 pairs rank (64 - n) + c with n - 1 - c.
+    const int pairs = n - 32;
+    const int want = loc >= 32 ? n - 1 - (loc - 32) : loc >= pairs ? loc - pairs : (32 - pairs) + loc;
+    if (tid < n) {
+        const float c = cost[tid];
+        int rank = 0;
+        for (int j = 0; j < n; ++j) {
+            const float d = cost[j];
+            rank += (d > c || (d == c && j < tid)) ? 1 : 0;
+        }
+        if (rank == want) *chosen = tid;
+    }
+    __syncthreads();
+    const int pick = __builtin_amdgcn_readfirstlane(*chosen);
+    __syncthreads();  // every thread has read the pick before the LDS is reused
+    return min(max(pick, 0), n - 1);
+}
+
 template <int NB, int TW>
 __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     constexpr int NW = kTileWaves;
@@ -142,10 +243,18 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     const int p = lane & 31;
     const int pblk = wave & 1;   // pixel block (64 pixels)
 
-    // XCD-aware tile order: blockIdx lands on XCD blockIdx % 8.
+    // XCD-aware tile order: blockIdx lands on XCD blockIdx % 8, which runs a band of
+    // consecutive tiles; within the band a cost-ordered placement where some of the XCD's
+    // CUs run one tile and others two.
     const int per_xcd = (a.tiles + 7) / 8;
-    const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (tile >= a.tiles) return;  // whole workgroup, before any barrier
+    const int band0 = (blockIdx.x & 7) * per_xcd;
+    const int band_n = min(per_xcd, a.tiles - band0);
+    const int loc = blockIdx.x >> 3;
+    if (loc >= band_n) return;  // whole workgroup, before any barrier
+    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
+    const int tile = band0 + (a.plan && band_n > 32 && band_n < 64
+                                  ? tile_band_slot<TW>(a, orr, band0, band_n, loc, reinterpret_cast<float*>(lds))
+                                  : loc);
     const int tiles_img = a.tiles_y * a.tiles_x;
     const int b = tile / tiles_img;
     const int trem = tile - b * tiles_img;
@@ -153,7 +262,6 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     const int tx = trem - ty * a.tiles_x;
 
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
-    const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
     const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
     const int stages = a.G / 2;
@@ -668,6 +776,7 @@ hipError_t launch_tile_f16(const KShape& s, const FusedGeometry& g, const FusedC
     a.Wp = g.wp;
     a.Cout = s.Cout;
     a.one = 1.0f;
+    a.plan = cfg.ks == 8 ? 1 : 0;  // for this variant, ks 8 = planned placement, 1 = fixed
     const int tw = cfg.mt == 32 ? 32 : 16;  // for this variant, mt carries the tile width
     const int th = 4 * 32 / tw;  // 2 pixel blocks x 2 segments of 32 pixels
     a.tiles_y = (s.Ho + th - 1) / th;

@@ -557,6 +557,46 @@ def test_tile_split_stages(gpu_ctx, dcn, oracle, tw):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
 
 
+@pytest.mark.parametrize("batch,h,w,tw", [(1, 180, 320, 16), (9, 64, 64, 16), (1, 120, 320, 32), (1, 150, 264, 16)])
+def test_tile_placement_plan_is_bit_identical(gpu_ctx, dcn, oracle, batch, h, w, tw):
+    """The tile kernel's cost-ordered placement (ks 8, used when an XCD's band has 33-63
+    tiles: C5's 460, 9 maps of 64 x 64 = 288, 300 tiles of 4 x 32, 19 x 17 partial tiles
+    with a short last band) only changes which workgroup runs which tile: the output equals the
+    fixed placement's (ks 1) bit for bit, and the FP32 oracle within the FP16 bars."""
+    s = dcn.DeformConvShape(batch, 128, h, w, 64, h, w, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    th = 128 // tw
+    tiles = batch * ((h + th - 1) // th) * ((w + tw - 1) // tw)
+    per_xcd = (tiles + 7) // 8
+    assert 32 < per_xcd < 64, tiles
+    rng = np.random.default_rng(tiles)
+    c = s.counts()
+    # a smooth +-24 px flow (so that some tiles' windows split) plus a +-6 px residue
+    flow = np.repeat(np.repeat(rng.uniform(-24, 24, (batch, 2, 6, 6)), (h + 5) // 6, axis=2), (w + 5) // 6, axis=3)
+    flow = flow[:, :, :h, :w]
+    off = (flow[:, None] + rng.uniform(-6, 6, (batch, 144, 2, h, w))).reshape(-1)
+    h16 = {"input": rng.standard_normal(c["input"]).astype(np.float16),
+           "offset": off.astype(np.float16),
+           "mask": rng.random(c["mask"]).astype(np.float16),
+           "weight": (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16),
+           "bias": (rng.standard_normal(64) * 0.1).astype(np.float16)}
+    log("case: tile placement plan", batch, h, w, "width", tw, "tiles", tiles)
+    packed = gpu_ctx.prepack(s, h16["weight"], h16["bias"])
+    outs = {}
+    try:
+        for ks in (8, 1):
+            gpu_ctx.set_fused_config(tw, ks, -1, 7)
+            assert gpu_ctx.get_fused_config(s) == {"variant": 7, "mt": tw, "ks": ks, "sampler": 1}
+            outs[ks] = gpu_ctx.run_float16_prepacked(s, h16["input"], h16["offset"], h16["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    assert np.array_equal(outs[8].view(np.uint16), outs[1].view(np.uint16))
+    w32 = widen(h16)
+    ref = oracle.forward_f32_threads(s, w32["input"], w32["offset"], w32["mask"], w32["weight"], w32["bias"])
+    mx, mean = errors(outs[8], ref)
+    log(f"  max {mx:.3e} mean {mean:.3e}")
+    assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
 TILE_EDGE_SHAPES = [
     # (batch, Cin, H, W, Cout, Ho, Wo, Kh, Kw, ph, pw, sh, sw, dh, dw, groups, offset_groups)
     (1, 16, 13, 40, 32, 13, 40, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2),   # Wo % 16 != 0, H % 8 != 0, Cout 32 (NB 1)
