@@ -676,6 +676,95 @@ def bench_share(args, ctx, dc, d, dev, share: int = 2) -> dict:
             "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "fused_config": cfg}
 
 
+def _graph_us(torch, stream, fn, steps: int, reps: int = 5) -> float:
+    """`fn(stream)` captured `steps` times in one hipGraph; median over `reps` replays of the
+    replay time (HIP events on the capture stream) per launch, in us."""
+    with torch.cuda.stream(stream):
+        fn(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        cur = torch.cuda.current_stream()
+        for _ in range(steps):
+            fn(cur)
+    with torch.cuda.stream(stream):
+        graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            a.record(stream)
+            graph.replay()
+            b.record(stream)
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) * 1e3 / steps)
+    return statistics.median(times)
+
+
+# Launch shapes of the kernels a DCN call runs: (name, workgroups, threads, LDS bytes).
+FLOOR_SHAPES = [
+    ("narrow_kernel C2 (256 x 12 waves, 48 KB LDS)", 256, 768, 49152),
+    ("pack_cb8_kernel C2 (19 x 16 blocks of 256)", 304, 256, 0),
+    ("tile_kernel C3 (512 x 4 waves, 77.6 KB LDS)", 512, 256, 79456),
+    ("tile_kernel C5 (464 x 4 waves, 77.6 KB LDS)", 464, 256, 79456),
+    ("one wave", 1, 64, 0),
+]
+
+
+def bench_launch_floor(args) -> int:
+    """Empty kernels (dcn_launch_floor_dev) of the launch shapes of the C2/C3/C5 kernels,
+    each captured `steps` times in a hipGraph: the per-launch floor inside a graph, the
+    part of a kernel's in-graph time that no change to its body removes."""
+    import torch
+
+    from jasnamacos_amd import deform_conv as dc
+
+    ctx = dc.HipDeformConv(0)
+    stream = torch.cuda.Stream()
+    rows = []
+    for name, wg, threads, lds in FLOOR_SHAPES:
+        us = _graph_us(torch, stream, lambda st, wg=wg, t=threads, l=lds: ctx.launch_floor_dev(wg, t, l, stream=st),
+                       args.steps, args.kernel_reps)
+        rows.append({"shape": name, "workgroups": wg, "threads": threads, "lds_bytes": lds, "us_per_launch": us})
+    ctx.close()
+    print(json.dumps({"metric": "launch floor: empty kernel per launch in a hipGraph", "unit": "us", "n_gpus": 1,
+                      "steps": args.steps, "data": "no data (empty kernels)", "shapes": rows}), flush=True)
+    return 0
+
+
+def bench_gather(args) -> int:
+    """The reference's gather phase alone at C2 (dcn_im2col_f16_dev: the modulated FP16
+    im2col matrix [4096][1152] written to HBM, MetalShader.swift:299-381), the counterpart
+    of the reference's gather-only timing (MetalRunner.swift:311-326). Algorithmic bytes:
+    NCHW input, offsets and mask read once, the columns written once."""
+    import numpy as np
+    import torch
+
+    from jasnamacos_amd import deform_conv as dc
+
+    d = dc.generate_config_inputs(2, args.seed)
+    s = d["shape"]
+    dev = {k: torch.from_numpy(np.asarray(d[k], np.float32).astype(np.float16).view(np.int16)).cuda()
+           for k in ("input", "offset", "mask")}
+    ctx = dc.HipDeformConv(0)
+    stream = torch.cuda.Stream()
+    cols = torch.empty(s.batch * s.output_height * s.output_width * s.input_channels * s.kernel_area,
+                       dtype=torch.int16, device="cuda")
+    us = _graph_us(torch, stream, lambda st: ctx.im2col_f16_dev(s, dev["input"], dev["offset"], dev["mask"], cols,
+                                                                 stream=st), args.steps, args.kernel_reps)
+    c = s.counts()
+    nbytes = 2 * (c["input"] + c["offset"] + c["mask"] + cols.numel())
+    ctx.close()
+    print(json.dumps({"metric": "DCNv2 gather phase (reference im2col) at C2", "value": us, "unit": "us/call",
+                      "n_gpus": 1, "steps": args.steps, "higher_is_better": False, "dtype": "f16",
+                      "data": "synthetic (the C2 benchmark distributions)",
+                      "config": {"workload": "C2 gather: im2col_kernel 1x128x64x64, 16 dg -> [4096][1152] FP16"},
+                      "algorithmic_bytes": nbytes, "achieved_gbs": nbytes / (us * 1e-6) / 1e9,
+                      "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -698,6 +787,10 @@ def main() -> int:
     ap.add_argument("--dtype", choices=("f16", "bf16"), default="f16",
                     help="configs 2, 3, 5: FP16 storage (the reference's) or BF16 storage (the BF16 "
                          "fused path)")
+    ap.add_argument("--launch-floor", action="store_true",
+                    help="time empty kernels of the C2/C3/C5 kernels' launch shapes in a hipGraph")
+    ap.add_argument("--gather", action="store_true",
+                    help="time the reference's gather phase alone at C2 (im2col columns to HBM)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run three device copies of this many MiB (the known-size "
                          "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -722,6 +815,13 @@ def main() -> int:
     from jasnamacos_amd import deform_conv as dc
 
     torch.cuda.set_device(0)
+    if args.launch_floor:
+        return bench_launch_floor(args)
+    if args.gather:
+        rc = bench_gather(args)
+        if args.calibration_copy_mib > 0:
+            calibration_copies(args.calibration_copy_mib)
+        return rc
     if args.spynet:
         return bench_spynet(args)
     if args.config == 4:

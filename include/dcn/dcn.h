@@ -296,6 +296,13 @@ dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, i
 dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* variant, int* mt,
                                 int* ks, int* sampler);
 
+/* Diagnostics: an empty kernel of the given launch shape (workgroups of `threads`
+ * threads, `lds_bytes` of dynamic LDS each), enqueued on `stream`. Its duration is the
+ * dispatch, wave-launch and completion floor that every kernel of that shape pays (the
+ * fused kernels' times are read against it). No counterpart in the reference. */
+dcn_status dcn_launch_floor_dev(dcn_context* ctx, int workgroups, int threads, int lds_bytes,
+                                void* stream);
+
 /* Sampler alone: the modulated FP16 im2col matrix [B*Ho*Wo][Cin*Kh*Kw] with
  * column ic*Kh*Kw + k and value half(bilinear * mask), exactly
  * deform_conv2d_fp16_jasna_gather (MetalShader.swift:299-381) generalised to any

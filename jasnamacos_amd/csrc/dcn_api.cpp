@@ -728,6 +728,17 @@ dcn_status dcn_im2col_f16_dev(dcn_context* ctx, const dcn_shape* shape, const vo
     return DCN_OK;
 }
 
+dcn_status dcn_launch_floor_dev(dcn_context* ctx, int workgroups, int threads, int lds_bytes,
+                                void* stream) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    DeviceGuard guard(ctx->device);
+    if (workgroups < 1 || workgroups > (1 << 20) || threads < 1 || threads > 1024 || lds_bytes < 0 ||
+        lds_bytes > 160 * 1024)
+        return fail(ctx, DCN_INVALID_ARGUMENT, "launch shape out of range");
+    DCN_HIP(ctx, dcn::launch_floor(workgroups, threads, lds_bytes, (hipStream_t)stream));
+    return DCN_OK;
+}
+
 dcn_status dcn_flag_nonfinite_f16_dev(dcn_context* ctx, const void* d_values, size_t count,
                                       void* d_flag, void* stream) {
     if (!ctx) return DCN_INVALID_ARGUMENT;

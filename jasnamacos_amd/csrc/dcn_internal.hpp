@@ -136,6 +136,7 @@ hipError_t launch_direct_f32(const KShape& s, const float* in, const float* off,
 hipError_t launch_direct_f16(const KShape& s, const uint16_t* in, const uint16_t* off,
                              const uint16_t* mask, const uint16_t* w, const uint16_t* b,
                              uint16_t* out, hipStream_t stream);
+hipError_t launch_floor(int workgroups, int threads, int lds_bytes, hipStream_t stream);
 hipError_t launch_pack_cb8(const KShape& s, const FusedGeometry& g, const uint16_t* in_nchw,
                            void* cb8, hipStream_t stream);
 // Allocation-free entry point (dcn_scratch.hip): resolve the device address of the

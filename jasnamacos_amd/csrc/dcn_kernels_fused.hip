@@ -366,6 +366,10 @@ __global__ __launch_bounds__(64 * NW) void staged_kernel(StagedArgs sa) {
     }
 }
 
+// An empty kernel: what any kernel of its launch shape (workgroups, threads, dynamic LDS)
+// pays for dispatch, wave launch and completion. Nothing is read or written.
+__global__ void launch_floor_kernel() {}
+
 // NCHW FP16 -> padded CB8. Grid (ceil(Hp*Wp / 256), B * Cin/8): one thread per padded
 // position of one channel block, eight 2-byte loads (coalesced along x) and one 16-byte
 // store; border positions get zeros. 32-bit index math only.
@@ -567,6 +571,14 @@ bool fused_geometry(const dcn_shape& s, FusedGeometry* g) {
     g->wp = s.input_width + 2 * kPad;
     g->m = (long long)s.batch * s.output_height * s.output_width;
     return true;
+}
+
+hipError_t launch_floor(int workgroups, int threads, int lds_bytes, hipStream_t stream) {
+    const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(&launch_floor_kernel), lds_bytes);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(launch_floor_kernel, dim3((unsigned)workgroups), dim3((unsigned)threads),
+                       (size_t)lds_bytes, stream);
+    return hipGetLastError();
 }
 
 hipError_t launch_pack_cb8(const KShape& s, const FusedGeometry& g, const uint16_t* in_nchw,

@@ -402,6 +402,11 @@ class HipDeformConv:
                                                                     _ptr(off), _ptr(msk), packed.handle, _ptr(out),
                                                                     _stream(stream)))
 
+    def launch_floor_dev(self, workgroups: int, threads: int, lds_bytes: int = 0, stream=None) -> None:
+        """An empty kernel of this launch shape (dcn_launch_floor_dev): the dispatch floor."""
+        self._check(self._lib.dcn_launch_floor_dev(self.ctx, int(workgroups), int(threads), int(lds_bytes),
+                                                   _stream(stream)))
+
     def im2col_f16_dev(self, shape, x, off, msk, columns, stream=None) -> None:
         self._check(self._lib.dcn_im2col_f16_dev(self.ctx, C.byref(shape.to_c()), _ptr(x), _ptr(off), _ptr(msk),
                                                  _ptr(columns), _stream(stream)))
