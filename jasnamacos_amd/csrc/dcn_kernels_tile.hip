@@ -401,11 +401,20 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) acc[s][nb] = f32x16{};
 
-    // The stage loop for waves with taps T0 .. T0 + NTW - 1 (compile-time per wave pair).
-    auto run = [&](auto t0_c, auto ntw_c) {
-        constexpr int T0 = decltype(t0_c)::value;
-        constexpr int NTW = decltype(ntw_c)::value;
-        constexpr int NSMP = NS * NTW;  // samples per lane and stage, j = kk * NS + s
+    // The stage loop of a wave pair (compile-time): taps TF .. TF + 3 for both segments
+    // and the centre tap 4 for segment SODD only (waves 0-1: taps 0-3 + tap 4 of segment
+    // 0; waves 2-3: taps 5-8 + tap 4 of segment 1), 9 samples per lane and stage for
+    // every wave. Sample j = 2 k + s (j < 8) is tap TF + k, segment s; j = 8 is the
+    // centre tap. Weight slot k (0-3) holds tap TF + k, slot 4 the centre tap.
+    auto run = [&](auto tf_c, auto sodd_c) {
+        constexpr int TF = decltype(tf_c)::value;
+        constexpr int SODD = decltype(sodd_c)::value;
+        constexpr int NSMP = 9;   // samples per lane and stage
+        constexpr int NSLOT = 5;  // weight slots
+        auto tap_of = [](int j) { return j == 8 ? 4 : TF + j / 2; };
+        auto seg_of = [](int j) { return j == 8 ? SODD : j % 2; };
+        auto slot_of = [](int j) { return j == 8 ? 4 : j / 2; };
+        auto slot_done = [](int j) { return j == 8 || j % 2 == 1; };  // the slot's last sample
 
         // A sample's dy, dx and mask from the LDS copy of the stage's offsets (an LDS
         // pointer, so each read is one ds_read_u16 with an immediate offset from the lane's
@@ -413,7 +422,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         typedef const __attribute__((address_space(3))) _Float16* lds_h;
         const lds_h offs_h = (lds_h)(const __attribute__((address_space(3))) uint8_t*)(lds + kTileBuf);
         auto offset_of = [&](int j, int which) {  // which: 0 = dy, 1 = dx, 2 = mask
-            const int kk = j / NS, s = j % NS, k = T0 + kk;
+            const int s = seg_of(j), k = tap_of(j);
             const uint32_t at = which == 2 ? mask_lane[s] + (uint32_t)(k * kTilePix * 2)
                                            : offs_lane[s] + (uint32_t)((2 * k + which) * kTilePix * 2);
             return offs_h[at / 2];
@@ -429,7 +438,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             bmax = s16x2{SHRT_MIN, SHRT_MIN};
         };
         auto coords = [&](int j, Samples& C) {
-            const int kk = j / NS, s = j % NS, k = T0 + kk;
+            const int s = seg_of(j), k = tap_of(j);
             // float(oy*sh - ph + ky*dh) + dy (MetalShader.swift:327-332), one rounding: an
             // fma with 1 is the same single rounding and takes the FP16 offset as it is
             // (v_fma_mix_f32; with a literal 1 the compiler folds it back into convert + add).
@@ -491,14 +500,15 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             const int ix = (int)(short)(C.a[j] >> 16);
             C.a[j] = (uint32_t)(iy * r.rs + ix * 16 + r.c);
         };
-        // Weight fragments of this wave's taps of one stage, one slot per tap: slot kk of
-        // stage st+1 is requested as soon as tap kk of stage st has used it.
-        h8 Bq[NTW][NB];
-        auto load_b = [&](int st, int kk) {
+        // Weight fragments of this wave's taps of one stage, one slot per tap: a slot of
+        // stage st+1 is requested as soon as its tap's last sample of stage st has used it.
+        h8 Bq[NSLOT][NB];
+        auto load_b = [&](int st, int slot) {
+            const int tap = slot == 4 ? 4 : TF + slot;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
-                Bq[kk][nb] = __builtin_bit_cast(
-                    h8, load16(wr, (uint32_t)(((st * 9 + T0 + kk) * NB + nb) * 64 + lane) * 16u, 0));
+                Bq[slot][nb] = __builtin_bit_cast(
+                    h8, load16(wr, (uint32_t)(((st * 9 + tap) * NB + nb) * 64 + lane) * 16u, 0));
         };
         // The LDS reads are issued in both modes: lanes that are not `active` (all of them
         // when the stage gathers from global memory, the other group's in a pass of a
@@ -527,10 +537,10 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
                 __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             }
         };
-        // K-loop of one stage (or one pass of a split stage): per sample j (tap kk, segment
-        // s) the next sample's corners are requested before this one is blended and
-        // multiplied; after both segments of a tap the weight slot is refilled (in the
-        // stage's last pass) and side(kk) runs (the next stage's work, in its first pass).
+        // K-loop of one stage (or one pass of a split stage): per sample j the next
+        // sample's corners are requested before this one is blended and multiplied; after a
+        // tap's last sample its weight slot is refilled (in the stage's last pass), and
+        // side(j) runs after every sample (the next stage's work, in the first pass).
         auto kloop = [&](int st, const Samples& C, const Addressing& r, bool from_lds, bool active,
                          bool last_pass, bool first_pass, auto&& side) {
             const uint32_t lds_pitch = active ? r.pitch : 0u;
@@ -541,15 +551,13 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
                 u32x4(&cur)[4] = (j & 1) ? qb : qa;
                 u32x4(&nxt)[4] = (j & 1) ? qa : qb;
                 if (j + 1 < NSMP) corners(j + 1, C, r, from_lds, active, lds_pitch, nxt);
-                const int kk = j / NS, s = j % NS;
+                const int kk = slot_of(j), s = seg_of(j);
                 const h8 A = blend_w(cur, C.w0[j], C.w1[j]);
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
                     acc[s][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bq[kk][nb], acc[s][nb], 0, 0, 0);
-                if (s == NS - 1) {
-                    if (last_pass && st + 1 < stages) load_b(st + 1, kk);
-                    if (first_pass) side(kk);
-                }
+                if (slot_done(j) && last_pass && st + 1 < stages) load_b(st + 1, kk);
+                if (first_pass) side(j);
                 __builtin_amdgcn_sched_barrier(0);
             }
         };
@@ -573,7 +581,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         // ---- prologue: stage 0's offsets, coordinates, windows and addresses ----
         Samples ca, cb;
 #pragma unroll
-        for (int kk = 0; kk < NTW; ++kk) load_b(0, kk);
+        for (int slot = 0; slot < NSLOT; ++slot) load_b(0, slot);
         copy_offsets(0);
         if (tid < 8) reinterpret_cast<uint32_t*>(lds + kTileZero)[tid] = 0u;
         __builtin_amdgcn_s_waitcnt(0);
@@ -583,19 +591,20 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         for (int j = 0; j < NSMP; ++j) coords(j, ca);
         next_stage(0, ca);
 
-        // Stage st: `ca` holds its addresses; K-steps 0-1 also compute stage st+1's
-        // coordinates into `cb` (from the offsets copied with st's windows), which then
-        // become `ca`. A split stage has a second pass: group 0's window is in LDS
+        // Stage st: `ca` holds its addresses; after its samples 1 and 3 the K-loop also
+        // computes stage st+1's coordinates into `cb` (from the offsets copied with st's
+        // windows), which then become `ca`. A split stage has a second pass: group 0's window is in LDS
         // (next_stage), then group 1's.
         for (int st = 0; st < stages; ++st) {
             const bool more = st + 1 < stages;
             if (more) box_reset();
             constexpr int kPerCoord = (NSMP + 1) / 2;
-            auto side = [&](int kk) {
-                if (!more || kk >= 2) return;
+            auto side = [&](int j) {
+                if (!more || (j != 1 && j != 3)) return;
+                const int h = j == 1 ? 0 : 1;
 #pragma unroll
                 for (int i = 0; i < kPerCoord; ++i)
-                    if (kk * kPerCoord + i < NSMP) coords(kk * kPerCoord + i, cb);
+                    if (h * kPerCoord + i < NSMP) coords(h * kPerCoord + i, cb);
             };
             const bool in_lds = win.lds || win.split;
             kloop(st, ca, ad, in_lds, win.lds || (win.split && half == 0), !win.split, true, side);
@@ -612,8 +621,8 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             }
         }
     };
-    if (wave < 2) run(std::integral_constant<int, 0>{}, std::integral_constant<int, 5>{});
-    else run(std::integral_constant<int, 5>{}, std::integral_constant<int, 4>{});
+    if (wave < 2) run(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    else run(std::integral_constant<int, 5>{}, std::integral_constant<int, 1>{});
 
     // ---- epilogue: the two tap halves summed (taps 0-4 + taps 5-8), bias, FP16, NCHW
     // stores through LDS ----
