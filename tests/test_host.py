@@ -252,3 +252,30 @@ def test_tile_kernel_side_limit(dcn, side, n, tile):
         s = dcn.DeformConvShape(1, 16, n, 8, 32, 5000, 8, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2)
     cfg = s.automatic_fused_config()
     assert (cfg["variant"] == 7) == tile, cfg
+
+
+def _tile_plan_rank(loc: int, n: int) -> int:
+    """The rank (0 = heaviest) of the tile that band-local slot `loc` runs under the tile
+    kernel's placement plan for a band of n tiles, 32 < n < 64 (tile_band_slot in
+    dcn_kernels_tile.hip): locals l and l + 32 share a CU for l < n - 32, locals n - 32 ..
+    31 run alone."""
+    pairs = n - 32
+    if loc >= 32:
+        return n - 1 - (loc - 32)
+    if loc >= pairs:
+        return loc - pairs
+    return (32 - pairs) + loc
+
+
+@pytest.mark.parametrize("n", range(33, 64))
+def test_tile_plan_slots_cover_every_tile_once(n):
+    """Every band size the plan applies to: the slots take ranks 0 .. n-1 exactly once, the
+    single-tile slots take the heaviest ranks, and each shared CU pairs the k-th heaviest of
+    the rest with the k-th lightest."""
+    ranks = [_tile_plan_rank(loc, n) for loc in range(n)]
+    assert sorted(ranks) == list(range(n))
+    pairs = n - 32
+    alone = [ranks[loc] for loc in range(pairs, 32)]
+    assert sorted(alone) == list(range(32 - pairs))
+    for c in range(pairs):
+        assert ranks[c] == 32 - pairs + c and ranks[c + 32] == n - 1 - c
