@@ -2,7 +2,7 @@
 // Swift tests so each reads like its original:
 //   DeformConvCPUTests.swift:4-33, 35-41     (1x1 known answer, recoverability)
 //   BenchmarkStatisticsTests.swift:5-20      (summary of [4,1,3,2]; nil for [] and [1, inf])
-//   MetalNonFiniteFlagTests.swift:5-55       (flag_non_finite_fp16 on finite / inf / nan)
+//   MetalNonFiniteFlagTests.swift:5-53       (flag_non_finite_fp16 on finite / inf / nan)
 //   JasnaCLI.swift:68-110                    (correctnessTest: seeded 1x2x5x5 -> 3, 2e-5 gate)
 //   TemporalScheduleTests.swift:4-40         (traversal, widths, second order, 30 frames)
 //   RestorationResumeTests.swift:51-72       (temporalChunkRanges)

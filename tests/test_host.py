@@ -138,7 +138,7 @@ def test_statistics_known_answer(dcn):
     assert abs(s.standard_deviation - np.sqrt(1.25)) < 1e-12
     assert abs(s.percentile10 - 1.3) < 1e-12 and abs(s.percentile90 - 3.7) < 1e-12
     assert dcn.BenchmarkStatistics.of([5]).median == 5
-    # BenchmarkStatisticsTests.swift:22-25
+    # BenchmarkStatisticsTests.swift:17-20
     assert dcn.BenchmarkStatistics.of([]) is None
     assert dcn.BenchmarkStatistics.of([1, np.inf]) is None
 
