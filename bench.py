@@ -30,6 +30,12 @@ single thread, on a bounded sample of the benchmarked workload with the same inp
 the same leg the oracle's output of the whole call (C3/C5: the same restatement on the
 host's threads) checks the GPU's timed output (timed_output_check) and the exact
 sampler's output (exact_sampler.output_check).
+
+Diagnostics (one JSON line each, instead of the bench line): --launch-floor (empty
+kernels of the fused kernels' launch shapes in a hipGraph), --gather (the reference's
+gather phase alone, im2col to HBM, at C2) and --tile-clock (configs 3, 5: the tile
+kernel's per-workgroup start/end stamps, so the spread of workgroup times behind the
+kernel's duration).
 """
 from __future__ import annotations
 
@@ -733,6 +739,128 @@ def bench_launch_floor(args) -> int:
     return 0
 
 
+def bench_tile_clock(args) -> int:
+    """Per-workgroup clock stamps of the tile kernel (variant 7) at config 3 or 5
+    (dcn_set_tile_clock_dev): each workgroup's start and end on the 100 MHz constant clock,
+    its tile and its CU (HW_ID, XCC_ID), from the last of 10 back-to-back fused launches on
+    the CB8 input, repeated --clock-runs times. Prints one JSON line: the spread of the
+    workgroup durations, how many CUs ran one and two workgroups and the durations of
+    each kind, the slowest workgroups; the output with the stamps on is compared bit for
+    bit with the output with them off."""
+    import numpy as np
+    import torch
+
+    from jasnamacos_amd import deform_conv as dc
+
+    d = dc.generate_config_inputs(args.config, args.seed)
+    s = d["shape"]
+    dev = {k: torch.from_numpy(np.asarray(d[k], np.float32).astype(np.float16).view(np.int16)).cuda()
+           for k in ("input", "offset", "mask", "weight", "bias")}
+    ctx = dc.HipDeformConv(0)
+    stream = torch.cuda.Stream()
+    packed = ctx.prepack_dev(s, dev["weight"], dev["bias"])
+    ctx.reserve(s)
+    if args.variant or args.mt or args.ks:
+        ctx.set_fused_config(args.mt, args.ks, -1, args.variant)
+    cfg = ctx.get_fused_config(s)
+    if cfg["variant"] != 7:
+        print(f"--tile-clock: config {args.config} runs fused variant {cfg['variant']}, not the tile kernel",
+              file=sys.stderr)
+        return 2
+    tw = 32 if cfg["mt"] == 32 else 16
+    th = 128 // tw
+    tiles = s.batch * -(-s.output_height // th) * -(-s.output_width // tw)
+    grid = (tiles + 7) // 8 * 8
+    out = torch.empty(s.output_count, dtype=torch.int16, device="cuda")
+    cb8 = torch.empty(ctx.cb8_count(s), dtype=torch.int16, device="cuda")
+    clock = torch.zeros(4 * grid, dtype=torch.int64, device="cuda")
+    launches = 10
+
+    def fused(n):
+        with torch.cuda.stream(stream):
+            for _ in range(n):
+                ctx.forward_f16_prepacked_cb8_dev(s, cb8, dev["offset"], dev["mask"], packed, out, stream=stream)
+
+    with torch.cuda.stream(stream):
+        ctx.pack_input_cb8_dev(s, dev["input"], cb8, stream=stream)
+    fused(20)
+    torch.cuda.synchronize()
+    ref = out.clone()
+    ctx.set_tile_clock_dev(clock)
+    runs, identical, launch_us = [], True, []
+    try:
+        for _ in range(args.clock_runs):
+            clock.zero_()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fused(launches)
+            b.record(stream)
+            torch.cuda.synchronize()
+            launch_us.append(a.elapsed_time(b) * 1e3 / launches)
+            runs.append(clock.cpu().numpy().view(np.uint64).reshape(grid, 4).copy())
+            identical = identical and bool(torch.equal(out, ref))
+    finally:
+        ctx.set_tile_clock_dev(None)
+
+    def analyse(rec):
+        valid = rec[:, 0] != 0
+        blocks = np.nonzero(valid)[0]
+        start = rec[valid, 0].astype(np.int64)
+        end = np.maximum(rec[valid, 1], rec[valid, 2]).astype(np.int64)
+        meta = rec[valid, 3]
+        tile = (meta & np.uint64(0x0FFFFFFF)).astype(np.int64)
+        xcc = ((meta >> np.uint64(28)) & np.uint64(15)).astype(np.int64)
+        cu = xcc * 256 + ((meta >> np.uint64(40)) & np.uint64(0xFF)).astype(np.int64)  # HW_ID bits 15:8
+        dur = (end - start) * 0.01  # 100 MHz ticks -> us
+        _, inverse, counts = np.unique(cu, return_inverse=True, return_counts=True)
+        per_wg = counts[inverse]
+        # On a CU that runs two workgroups, the one with the lower blockIdx was dispatched first.
+        first = np.array([blocks[i] == blocks[inverse == inverse[i]].min() for i in range(len(blocks))])
+        mod8 = blocks % 8
+        xcd_map = {int(m): sorted(set(xcc[mod8 == m].tolist())) for m in range(8)}
+        return {
+            "span_us": round(float((end.max() - start.min()) * 0.01), 2),
+            "start_skew_us": round(float((start.max() - start.min()) * 0.01), 2),
+            "dur": dur, "per_wg": per_wg, "tile": tile, "counts": counts, "first": first,
+            "tiles_once": bool(np.array_equal(np.sort(tile), np.arange(tiles))),
+            "xcd_is_block_mod_8": all(len(v) == 1 for v in xcd_map.values()) and
+                                  len({v[0] for v in xcd_map.values()}) == 8,
+        }
+
+    if args.clock_dump:
+        np.save(args.clock_dump, np.stack(runs))  # [runs][workgroups][4] uint64, as written
+    res = [analyse(r) for r in runs]
+    med = sorted(res, key=lambda r: r["span_us"])[len(res) // 2]  # the run of median span
+    q = lambda x, p: round(float(np.percentile(x, p)), 2) if len(x) else None  # noqa: E731
+    dur, per_wg = med["dur"], med["per_wg"]
+    stats = lambda x: {"n": int(len(x)), "min": q(x, 0), "median": q(x, 50), "p90": q(x, 90),  # noqa: E731
+                       "max": q(x, 100)}
+    order = np.argsort(-dur)[:8]
+    print(json.dumps({
+        "metric": "tile kernel per-workgroup clock (us, 100 MHz constant clock)",
+        "config": {"workload": WORKLOADS[args.config], "tile": f"{th}x{tw}", "tiles": tiles, "workgroups": grid,
+                   "fused_config": cfg},
+        "runs": args.clock_runs, "launches_per_run": launches,
+        "us_per_launch_back_to_back": round(statistics.median(launch_us), 2),
+        "span_us": {"median_run": med["span_us"], "all_runs": [r["span_us"] for r in res]},
+        "start_skew_us": med["start_skew_us"],
+        "workgroup_us": stats(dur),
+        "workgroup_us_alone_on_cu": stats(dur[per_wg == 1]),
+        "workgroup_us_sharing_cu": stats(dur[per_wg >= 2]),
+        "workgroup_us_sharing_cu_dispatched_first": stats(dur[(per_wg == 2) & med["first"]]),
+        "workgroup_us_sharing_cu_dispatched_second": stats(dur[(per_wg == 2) & ~med["first"]]),
+        "cus": {"one_workgroup": int(np.sum(med["counts"] == 1)), "two": int(np.sum(med["counts"] == 2)),
+                "more": int(np.sum(med["counts"] > 2))},
+        "slowest": [{"tile": int(med["tile"][i]), "us": round(float(dur[i]), 2), "sharing_cu": bool(per_wg[i] >= 2)}
+                    for i in order],
+        "tiles_once": all(r["tiles_once"] for r in res),
+        "xcd_is_block_mod_8": all(r["xcd_is_block_mod_8"] for r in res),
+        "bit_identical_with_clock_off": identical,
+    }))
+    return 0 if identical and all(r["tiles_once"] for r in res) else 1
+
+
 def bench_gather(args) -> int:
     """The reference's gather phase alone at C2 (dcn_im2col_f16_dev: the modulated FP16
     im2col matrix [4096][1152] written to HBM, MetalShader.swift:299-381), the counterpart
@@ -791,6 +919,12 @@ def main() -> int:
                     help="time empty kernels of the C2/C3/C5 kernels' launch shapes in a hipGraph")
     ap.add_argument("--gather", action="store_true",
                     help="time the reference's gather phase alone at C2 (im2col columns to HBM)")
+    ap.add_argument("--tile-clock", action="store_true",
+                    help="configs 3, 5: per-workgroup clock stamps of the tile kernel (the spread of "
+                         "workgroup times, CU sharing, the slowest tiles)")
+    ap.add_argument("--clock-runs", type=int, default=5, help="--tile-clock: runs of 10 launches")
+    ap.add_argument("--clock-dump", default="",
+                    help="--tile-clock: also save every run's raw records to this .npy file")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run three device copies of this many MiB (the known-size "
                          "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -817,6 +951,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.launch_floor:
         return bench_launch_floor(args)
+    if args.tile_clock:
+        return bench_tile_clock(args)
     if args.gather:
         rc = bench_gather(args)
         if args.calibration_copy_mib > 0:

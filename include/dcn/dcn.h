@@ -302,6 +302,16 @@ dcn_status dcn_get_fused_config(dcn_context* ctx, const dcn_shape* shape, int* v
  * fused kernels' times are read against it). No counterpart in the reference. */
 dcn_status dcn_launch_floor_dev(dcn_context* ctx, int workgroups, int threads, int lds_bytes,
                                 void* stream);
+/* Diagnostics: per-workgroup clock stamps of the tile kernel (variant 7). While set, every
+ * tile launch of this context writes, for workgroup b, d_clock[4b .. 4b+3] = {start, end
+ * of wave 0, end of wave 1, HW_ID << 32 | (XCC_ID & 15) << 28 | tile} as uint64, start
+ * and ends on the 100 MHz constant clock (s_memrealtime), the ends when the wave has
+ * issued its output stores; HW_ID and XCC_ID are the hardware registers of that name
+ * (bits 15:8 of HW_ID and XCC_ID together name the CU). Workgroups without a tile write nothing, so the caller clears the buffer.
+ * `count` is in uint64 elements; a tile launch needs 4 x its workgroup count
+ * (8 x ceil(tiles / 8)) and fails with DCN_INVALID_ARGUMENT when the buffer is smaller.
+ * A null d_clock turns the stamps off. No counterpart in the reference. */
+dcn_status dcn_set_tile_clock_dev(dcn_context* ctx, void* d_clock, size_t count);
 
 /* Sampler alone: the modulated FP16 im2col matrix [B*Ho*Wo][Cin*Kh*Kw] with
  * column ic*Kh*Kw + k and value half(bilinear * mask), exactly

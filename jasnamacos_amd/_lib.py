@@ -140,6 +140,7 @@ SIGNATURES: dict[str, tuple] = {
                                        C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "dcn_im2col_f16_dev": (C.c_int, [CtxP, ShapeP, c_void, c_void, c_void, c_void, c_void]),
     "dcn_launch_floor_dev": (C.c_int, [CtxP, C.c_int, C.c_int, C.c_int, c_void]),
+    "dcn_set_tile_clock_dev": (C.c_int, [CtxP, c_void, C.c_size_t]),
     "dcn_flag_nonfinite_f16_dev": (C.c_int, [CtxP, c_void, c_size, c_void, c_void]),
     "dcn_check_nonfinite_f16_dev": (C.c_int, [CtxP, c_void, c_size, c_void]),
     "dcn_splitmix64_seed": (C.c_uint64, [C.c_uint64]),

@@ -172,6 +172,11 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
                         std::to_string(cfg.mt) + ", ks " + std::to_string(cfg.ks) + ")");
     if (g.kb >= (1 << 16)) return fail(ctx, DCN_INVALID_SHAPE, "K too large for the fused path");
     const dcn::KShape ks = dcn::to_kshape(*shape);
+    if (cfg.variant == dcn::kVariantTile && ctx->tile_clock &&
+        ctx->tile_clock_count < 4 * dcn::tile_grid(ks, cfg))
+        return fail(ctx, DCN_INVALID_ARGUMENT,
+                    "tile clock buffer holds " + std::to_string(ctx->tile_clock_count) +
+                        " stamps; this launch needs " + std::to_string(4 * dcn::tile_grid(ks, cfg)));
     const void* cb8 = d_input;
     if (!input_is_cb8) {
         void* dst = repack;
@@ -193,7 +198,7 @@ dcn_status fused_prepacked_dev(dcn_context* ctx, const dcn_shape* shape, const v
             return fail(ctx, DCN_INVALID_ARGUMENT, "the tile variant does not support this shape");
         DCN_HIP(ctx, dcn::launch_tile_f16(ks, g, cfg, cb8, (const uint16_t*)d_offset,
                                           (const uint16_t*)d_mask, packed->weights_tile,
-                                          packed->bias, (uint16_t*)d_output, stream));
+                                          packed->bias, (uint16_t*)d_output, stream, ctx->tile_clock));
         return DCN_OK;
     }
     if (cfg.variant == dcn::kVariantNarrow) {
@@ -356,6 +361,14 @@ dcn_status dcn_set_fused_config(dcn_context* ctx, int variant, int mt, int ks, i
     if (variant < 0 || variant > 7 || mt < 0 || mt > 32 || ks < 0 || sampler < -1 || sampler > 1)
         return fail(ctx, DCN_INVALID_ARGUMENT, "invalid fused config");
     ctx->fused_override = dcn::FusedConfig{variant, mt, ks, sampler};
+    return DCN_OK;
+}
+
+dcn_status dcn_set_tile_clock_dev(dcn_context* ctx, void* d_clock, size_t count) {
+    if (!ctx) return DCN_INVALID_ARGUMENT;
+    if (d_clock && count == 0) return fail(ctx, DCN_INVALID_ARGUMENT, "tile clock buffer is empty");
+    ctx->tile_clock = static_cast<unsigned long long*>(d_clock);
+    ctx->tile_clock_count = d_clock ? count : 0;
     return DCN_OK;
 }
 

@@ -124,10 +124,12 @@ bool tile_supported(const dcn_shape& s);
 size_t tile_packed_bytes(const dcn_shape& s);
 hipError_t launch_tile_prepack(const KShape& s, const uint16_t* w, int layout, void* wpk,
                                hipStream_t stream);
+// clock: per-workgroup clock stamps [tile_grid(s, cfg)][4] (TileArgs::clock) or null.
 hipError_t launch_tile_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
                            const void* cb8, const uint16_t* off, const uint16_t* mask,
                            const void* packed_w, const float* packed_b, uint16_t* out,
-                           hipStream_t stream);
+                           hipStream_t stream, unsigned long long* clock = nullptr);
+size_t tile_grid(const KShape& s, const FusedConfig& cfg);  // workgroups of a tile launch
 
 // ---- launchers (return hipSuccess or the launch error) ---------------------------
 hipError_t launch_direct_f32(const KShape& s, const float* in, const float* off,
@@ -347,6 +349,8 @@ struct dcn_context {
     size_t workspace_bytes = 0;
     uint32_t* flag = nullptr;   // device flag for the non-finite check
     dcn::FusedConfig fused_override{0, 0, 0, -1};
+    unsigned long long* tile_clock = nullptr;  // dcn_set_tile_clock_dev (diagnostics)
+    size_t tile_clock_count = 0;
 };
 
 struct dcn_packed {

@@ -20,7 +20,7 @@
 // here each wave holds two 32-pixel segments (the MFMA B fragment is used for both) and
 // about half the taps of a stage, so each weight fragment crosses the path once per two
 // segments, and the two halves of each pixel's sum meet in LDS at the end, in a fixed
-// order (taps 0-4 + taps 5-8).
+// order (the half of waves 0-1 + the half of waves 2-3).
 //
 // The sampler's VALU is the other limit. One sample (8 channels) feeds 64 output
 // channels, i.e. two v_mfma_f32_32x32x16_f16, while its bilinear blend alone is 16 packed
@@ -30,11 +30,12 @@
 //
 // Layout. Workgroup = 4 waves (kTileWaves) on a 128-pixel tile (kTilePix): 8 x 16 pixels
 // (TW = 16) or 4 x 32 (TW = 32). Wave w owns pixel block w & 1 (64 pixels = two segments
-// of 32, each 32 / TW tile rows); waves 0-1 take taps 0-4 and waves 2-3 taps 5-8 of the
-// same pixels. A stage is two offset groups; K-step k of stage s is tap k of both: lanes
-// 0-31 give group 2s, lanes 32-63 group 2s+1 (the A operand of v_mfma_f32_32x32x16_f16 is
-// 32 pixels x 16 K, 8 per lane), and the weights are prepacked in that order
-// (tile_prepack_kernel).
+// of 32, each 32 / TW tile rows); waves 0-1 take taps 0-3 of both segments and the
+// centre tap 4 of the first, waves 2-3 taps 5-8 of both and tap 4 of the second: 9
+// samples per lane and stage in every wave. A stage is two offset groups; K-step k of
+// stage s is tap k of both: lanes 0-31 give group 2s, lanes 32-63 group 2s+1 (the A
+// operand of v_mfma_f32_32x32x16_f16 is 32 pixels x 16 K, 8 per lane), and the weights
+// are prepacked in that order (tile_prepack_kernel).
 //
 // Pipeline (two workgroups per CU, each with one 64 KB window buffer, kTileBuf), stage s:
 //   - the K-loop of stage s, whose first two K-steps also compute stage s+1's corner
@@ -93,6 +94,11 @@ struct TileArgs {
     float one;  // 1.0f, opaque to the compiler (see coords)
     int tiles_y, tiles_x, tiles;
     int plan;   // 1: cost-ordered placement of a band's tiles (tile_band_slot) where it applies
+    // Per-workgroup clock stamps (diagnostics) or null: workgroup b writes
+    // clock[4b .. 4b+3] = {start, end of wave 0, end of wave 1, HW_ID << 32 | XCC_ID << 28 |
+    // tile} on the 100 MHz constant clock (s_memrealtime); workgroups without a tile write
+    // nothing. (Tiles stay below 2^28: a tensor holds fewer than 2^29 elements.)
+    unsigned long long* clock;
 };
 
 // 16-byte LDS DMA: unit `voff` of the buffer to LDS lds_base + 16 * lane (lds_base uniform).
@@ -136,32 +142,42 @@ __device__ __forceinline__ h8 blend_w(const u32x4 (&q)[4], uint32_t w0, uint32_t
 // alone slots, and the rest are paired heaviest with lightest.
 // The estimate of a tile: the extent of the clamped sample positions of one offset
 // channel pair (group 0, centre tap; the offset field's flow part is common to all
-// groups and taps, its residue spans the same range in each) over the tile's pixels:
-// (rows + 3) x (columns + 3). Every workgroup of the band reads the same offsets and runs
+// groups and taps, its residue spans the same range in each) over half of the tile's rows
+// (the first, the last and evenly spaced ones between): (rows + 3) x (columns + 3). On C5
+// it ranks the tiles with a rank correlation of 0.98 to their window bytes (0.99 with
+// every row, at twice the loads). Every workgroup of the band reads the same offsets and runs
 // the same arithmetic, so all of them compute the same ranking without communicating.
 // Returns the band-local index of the tile that local slot `loc` runs. All threads of the
-// workgroup call it (it has barriers); `sh` is 1 KB of LDS that nothing else uses yet.
+// workgroup call it (it has a barrier); `sh` is 2.5 KB of LDS that nothing else writes
+// before the workgroup's next barrier.
 template <int TW>
 __device__ int tile_band_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr, int band0, int n, int loc,
                               float* sh) {
     constexpr int TH = 128 / TW;
-    constexpr int kPieces = TW / 8;          // 16-byte pieces of a tile row
-    constexpr int kUnits = 2 * TH * kPieces; // 32: dy and dx pieces of a tile
-    static_assert(kUnits == 32, "a tile's estimate is 32 units of 8 pixels");
+    constexpr int kPieces = TW / 8;           // 16-byte pieces of a tile row
+    constexpr int kRows = 8 / kPieces;        // rows sampled: 4 of 8 (TW 16), 2 of 4 (TW 32)
+    constexpr int kUnits = 2 * kRows * kPieces;  // 16: dy and dx pieces of a tile
+    static_assert(kUnits == 16 && TH >= kRows, "a tile's estimate is 16 units of 8 pixels");
     const int tid = threadIdx.x;
-    const int u = tid & 31;
-    const int ch = u >> 4;                    // 0: dy, 1: dx
-    const int row = (u & 15) / kPieces, piece = (u & 15) % kPieces;
-    constexpr int kPass = 64 * kTileWaves / kUnits;  // tiles per pass (8)
+    const int u = tid & 15;
+    const int ch = u >> 3;                    // 0: dy, 1: dx
+    const int w = u & 7;
+    // Sampled row r of kRows: tile row round(r (TH - 1) / (kRows - 1)), so the first and
+    // last rows and evenly spaced ones between (0, 2, 5, 7 of 8; 0, 3 of 4).
+    const int row = ((w / kPieces) * (TH - 1) * 2 + (kRows - 1)) / (2 * (kRows - 1));
+    const int piece = w % kPieces;
+    constexpr int kPass = 64 * kTileWaves / kUnits;  // tiles per pass (16)
+    constexpr int kPasses = 64 / kPass;              // 4: a band has at most 63 tiles
     const int tiles_img = a.tiles_y * a.tiles_x;
     // Centre tap (ky = kx = 1 of the 3x3 kernel) of group 0: offset channels 8 (dy), 9 (dx).
-    float mn[8], mx[8];
+    // Every pass loads (tiles past the band read its last tile again and are masked), so
+    // the loads are in flight together: one memory round trip for the whole plan.
+    float mn[kPasses], mx[kPasses];
 #pragma unroll
-    for (int pass = 0; pass < 8; ++pass) {
-        const int i = pass * kPass + (tid >> 5);
+    for (int pass = 0; pass < kPasses; ++pass) {
+        const int i = pass * kPass + (tid >> 4);
         mn[pass] = 3.0e38f;
         mx[pass] = -3.0e38f;
-        if (pass * kPass >= n) continue;  // uniform
         const int t = band0 + min(i, n - 1);
         const int b = t / tiles_img, r = t - b * tiles_img;
         const int ty = r / a.tiles_x, tx = r - ty * a.tiles_x;
@@ -186,43 +202,53 @@ __device__ int tile_band_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr, int
             mx[pass] = -3.0e38f;
         }
     }
-    // Extent per (tile, channel): a min / max over the 16 lanes of its pieces.
+    // Extent per (tile, channel): a min / max over the 8 lanes of its pieces, a half DPP
+    // row (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror: lane i meets lanes i ^ 1,
+    // i ^ 2, then the other quad of its 8).
+    auto lanes8 = [](float v, bool take_min) {
+        auto step = [&](float x, auto ctrl_c) {
+            const float y = __builtin_bit_cast(
+                float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl_c)::value, 0xF, 0xF, false));
+            return take_min ? fminf(x, y) : fmaxf(x, y);
+        };
+        v = step(v, std::integral_constant<int, 0xB1>{});
+        v = step(v, std::integral_constant<int, 0x4E>{});
+        return step(v, std::integral_constant<int, 0x141>{});
+    };
 #pragma unroll
-    for (int pass = 0; pass < 8; ++pass) {
+    for (int pass = 0; pass < kPasses; ++pass) {
         if (pass * kPass >= n) continue;
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) {
-            mn[pass] = fminf(mn[pass], __shfl_xor(mn[pass], m));
-            mx[pass] = fmaxf(mx[pass], __shfl_xor(mx[pass], m));
-        }
-        const int i = pass * kPass + (tid >> 5);
-        if ((u & 15) == 0 && i < n) sh[2 * i + ch] = mx[pass] - mn[pass];
+        mn[pass] = lanes8(mn[pass], true);
+        mx[pass] = lanes8(mx[pass], false);
+        const int i = pass * kPass + (tid >> 4);
+        if (w == 0 && i < n) sh[2 * i + ch] = mx[pass] - mn[pass];
     }
-    float* cost = sh + 128;
-    int* chosen = reinterpret_cast<int*>(sh + 192);
-    if (tid == 0) *chosen = loc;  // (ranks are a permutation: some thread overwrites it)
-    __syncthreads();
-    if (tid < n) {
-        const float c = (sh[2 * tid] + 3.0f) * (sh[2 * tid + 1] + 3.0f);
-        cost[tid] = c == c ? c : 0.0f;
+    __syncthreads();  // every tile's extents in sh[0 .. 2n) (the plan's only barrier)
+    // Each wave ranks the band's tiles itself (the same arithmetic in every wave, so the
+    // same ranks): lane l < n holds tile l's key and writes it to the wave's own row of
+    // LDS, which the wave then reads back in order (LDS operations of one wave complete
+    // in issue order; no other wave touches the row). Key = cost bits << 32 | ~l: the costs
+    // are positive, so their bit patterns order like their values, and a larger key is a
+    // larger cost or the same cost at a smaller index.
+    const int l = tid & 63;
+    unsigned long long* keys = reinterpret_cast<unsigned long long*>(sh + 128) + 64 * (tid >> 6);
+    unsigned long long key = 0;
+    if (l < n) {
+        float c = (sh[2 * l] + 3.0f) * (sh[2 * l + 1] + 3.0f);
+        c = c == c ? c : 0.0f;
+        key = ((unsigned long long)__builtin_bit_cast(uint32_t, c) << 32) | (uint32_t)~l;
+        keys[l] = key;
     }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
     // Rank = place in descending cost order (ties by index); the slot's rank: alone slots
     // n-32 .. 31 the heaviest, then CU c < n - 32 pairs rank (64 - n) + c with n - 1 - c.
     const int pairs = n - 32;
     const int want = loc >= 32 ? n - 1 - (loc - 32) : loc >= pairs ? loc - pairs : (32 - pairs) + loc;
-    if (tid < n) {
-        const float c = cost[tid];
-        int rank = 0;
-        for (int j = 0; j < n; ++j) {
-            const float d = cost[j];
-            rank += (d > c || (d == c && j < tid)) ? 1 : 0;
-        }
-        if (rank == want) *chosen = tid;
-    }
-    __syncthreads();
-    const int pick = __builtin_amdgcn_readfirstlane(*chosen);
-    __syncthreads();  // every thread has read the pick before the LDS is reused
+    int rank = 0;
+    for (int j = 0; j < n; ++j) rank += keys[j] > key ? 1 : 0;
+    const unsigned long long hit = __builtin_amdgcn_ballot_w64(l < n && rank == want);
+    // (The ranks are a permutation of 0 .. n-1, so exactly one lane hits.)
+    const int pick = hit ? (int)__builtin_ctzll(hit) : loc;
     return min(max(pick, 0), n - 1);
 }
 
@@ -251,10 +277,17 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     const int band_n = min(per_xcd, a.tiles - band0);
     const int loc = blockIdx.x >> 3;
     if (loc >= band_n) return;  // whole workgroup, before any barrier
+    unsigned long long* const clock = a.clock ? a.clock + 4 * (size_t)blockIdx.x : nullptr;
+    if (clock && tid == 0) clock[0] = __builtin_amdgcn_s_memrealtime();
     const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
     const int tile = band0 + (a.plan && band_n > 32 && band_n < 64
                                   ? tile_band_slot<TW>(a, orr, band0, band_n, loc, reinterpret_cast<float*>(lds))
                                   : loc);
+    if (clock && tid == 0) {  // HW_ID: wave, SIMD, CU, shader array and engine; XCC_ID: the XCD
+        const uint32_t hw = (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);
+        const uint32_t xcc = (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 20) & 15u;
+        clock[3] = ((unsigned long long)hw << 32) | (xcc << 28) | (uint32_t)tile;
+    }
     const int tiles_img = a.tiles_y * a.tiles_x;
     const int b = tile / tiles_img;
     const int trem = tile - b * tiles_img;
@@ -624,7 +657,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     if (wave < 2) run(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
     else run(std::integral_constant<int, 5>{}, std::integral_constant<int, 1>{});
 
-    // ---- epilogue: the two tap halves summed (taps 0-4 + taps 5-8), bias, FP16, NCHW
+    // ---- epilogue: the two tap halves summed (waves 0-1's + waves 2-3's), bias, FP16, NCHW
     // stores through LDS ----
     __syncthreads();  // every wave is done with the windows
     float* red = reinterpret_cast<float*>(lds);  // [2 pixel blocks][NS][NB][16][64]
@@ -679,6 +712,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
                 if (x + e < a.Wo) dst[e] = src[e];
         }
     }
+    if (clock && lane == 0) clock[1 + wave] = __builtin_amdgcn_s_memrealtime();  // stores issued
 }
 
 // Weights -> the tile kernel's B fragments [G/2][9][NB][64][8]: lane l of K-step k, stage
@@ -755,8 +789,9 @@ hipError_t launch_tile_prepack(const KShape& s, const uint16_t* w, int layout, v
 hipError_t launch_tile_f16(const KShape& s, const FusedGeometry& g, const FusedConfig& cfg,
                            const void* cb8, const uint16_t* off, const uint16_t* mask,
                            const void* packed_w, const float* packed_b, uint16_t* out,
-                           hipStream_t stream) {
+                           hipStream_t stream, unsigned long long* clock) {
     TileArgs a;
+    a.clock = clock;
     a.xin = cb8;
     a.off = off;
     a.msk = mask;
@@ -792,6 +827,13 @@ hipError_t launch_tile_f16(const KShape& s, const FusedGeometry& g, const FusedC
     a.tiles_x = (s.Wo + tw - 1) / tw;
     a.tiles = a.tiles_y * a.tiles_x * s.B;
     return tw == 32 ? launch_tile_nb<32>(a, g.nb, stream) : launch_tile_nb<16>(a, g.nb, stream);
+}
+
+size_t tile_grid(const KShape& s, const FusedConfig& cfg) {
+    const int tw = cfg.mt == 32 ? 32 : 16;
+    const int th = 4 * 32 / tw;
+    const size_t tiles = (size_t)((s.Ho + th - 1) / th) * ((s.Wo + tw - 1) / tw) * s.B;
+    return (tiles + 7) / 8 * 8;
 }
 
 }  // namespace dcn

@@ -407,6 +407,16 @@ class HipDeformConv:
         self._check(self._lib.dcn_launch_floor_dev(self.ctx, int(workgroups), int(threads), int(lds_bytes),
                                                    _stream(stream)))
 
+    def set_tile_clock_dev(self, clock, count: int | None = None) -> None:
+        """Per-workgroup clock stamps of the tile kernel (dcn_set_tile_clock_dev): `clock`
+        is a device buffer of uint64 (an int64 tensor; count defaults to its numel), or
+        None to turn the stamps off."""
+        if clock is None:
+            self._check(self._lib.dcn_set_tile_clock_dev(self.ctx, None, 0))
+            return
+        n = int(clock.numel()) if count is None else int(count)
+        self._check(self._lib.dcn_set_tile_clock_dev(self.ctx, _ptr(clock), n))
+
     def im2col_f16_dev(self, shape, x, off, msk, columns, stream=None) -> None:
         self._check(self._lib.dcn_im2col_f16_dev(self.ctx, C.byref(shape.to_c()), _ptr(x), _ptr(off), _ptr(msk),
                                                  _ptr(columns), _stream(stream)))

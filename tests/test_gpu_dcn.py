@@ -597,6 +597,61 @@ def test_tile_placement_plan_is_bit_identical(gpu_ctx, dcn, oracle, batch, h, w,
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
 
 
+@pytest.mark.parametrize("batch,h,w", [(2, 64, 64), (1, 24, 48)])
+def test_tile_clock_stamps_every_tile(gpu_ctx, dcn, batch, h, w):
+    """dcn_set_tile_clock_dev: with a clock buffer set, the tile kernel writes one record per
+    workgroup that runs a tile (start <= both wave ends, every tile exactly once, the
+    grid's padding workgroups write nothing), the output is bit-identical to a launch
+    without stamps, and a buffer smaller than 4 stamps per workgroup is refused."""
+    import torch
+
+    s = dcn.DeformConvShape(batch, 128, h, w, 64, h, w, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    tiles = batch * ((h + 7) // 8) * ((w + 15) // 16)
+    grid = (tiles + 7) // 8 * 8
+    rng = np.random.default_rng(tiles)
+    c = s.counts()
+    h16 = {"input": rng.standard_normal(c["input"]).astype(np.float16),
+           "offset": rng.uniform(-8, 8, c["offset"]).astype(np.float16),
+           "mask": rng.random(c["mask"]).astype(np.float16),
+           "weight": (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16),
+           "bias": (rng.standard_normal(64) * 0.1).astype(np.float16)}
+    log("case: tile clock", batch, h, w, "tiles", tiles, "grid", grid)
+    dev = {k: _dev(torch, h16[k].view(np.int16)) for k in ("input", "offset", "mask", "weight", "bias")}
+    out = torch.empty(c["output"], dtype=torch.int16, device="cuda")
+    packed = gpu_ctx.prepack_dev(s, dev["weight"], dev["bias"])
+    gpu_ctx.reserve(s)
+    gpu_ctx.set_fused_config(16, 8, -1, 7)
+    try:
+        assert gpu_ctx.get_fused_config(s)["variant"] == 7
+        gpu_ctx.forward_f16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out)
+        torch.cuda.synchronize()
+        ref = out.clone()
+        out.zero_()
+        clock = torch.zeros(4 * grid, dtype=torch.int64, device="cuda")
+        gpu_ctx.set_tile_clock_dev(clock)
+        gpu_ctx.forward_f16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        rec = clock.cpu().numpy().view(np.uint64).reshape(grid, 4)
+        small = torch.zeros(4 * grid - 1, dtype=torch.int64, device="cuda")
+        gpu_ctx.set_tile_clock_dev(small)
+        with pytest.raises(dcn.DeformConvError):
+            gpu_ctx.forward_f16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out)
+        torch.cuda.synchronize()
+    finally:
+        gpu_ctx.set_tile_clock_dev(None)
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    assert not np.any(small.cpu().numpy())  # the refused launch ran nothing
+    per_xcd = (tiles + 7) // 8
+    has_tile = np.array([b // 8 < min(per_xcd, tiles - (b % 8) * per_xcd) for b in range(grid)])
+    assert np.all(rec[has_tile, 0] > 0) and not np.any(rec[~has_tile])
+    r = rec[has_tile]
+    assert np.all(r[:, 1] >= r[:, 0]) and np.all(r[:, 2] >= r[:, 0])
+    assert np.all(r[:, 1] - r[:, 0] < 100_000_000)  # < 1 s on the 100 MHz clock
+    tile_ids = (r[:, 3] & np.uint64(0x0FFFFFFF)).astype(np.int64)
+    assert np.array_equal(np.sort(tile_ids), np.arange(tiles))
+
+
 TILE_EDGE_SHAPES = [
     # (batch, Cin, H, W, Cout, Ho, Wo, Kh, Kw, ph, pw, sh, sw, dh, dw, groups, offset_groups)
     (1, 16, 13, 40, 32, 13, 40, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2),   # Wo % 16 != 0, H % 8 != 0, Cout 32 (NB 1)
