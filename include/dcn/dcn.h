@@ -254,10 +254,14 @@ dcn_status dcn_forward_bf16_prepacked_cb8_dev(dcn_context* ctx, const dcn_shape*
  * that the library holds on every device it runs on (resolved by dcn_create) instead
  * of the context's workspace; the call allocates nothing (no hipMalloc / hipFree).
  * A shape whose padded input (dcn_cb8_count * 2 bytes) exceeds the array fails with
- * DCN_INVALID_SHAPE. All calls on one device share that device's array: calls that
- * overlap in time on one device (other streams, other contexts, other threads) race and
- * must be serialized by the caller. Each call writes every element it reads, so the
- * array needs no clearing between calls. */
+ * DCN_INVALID_SHAPE. All calls on one device share that device's array, so the library
+ * orders them: a call on another stream than the previous call's (any context, any host
+ * thread) makes its stream wait, on the device, for the previous call's work
+ * (hipStreamWaitEvent on an event created with the context; nothing is allocated), and
+ * calls from several threads enqueue one at a time. Under hipGraph capture a call neither
+ * waits nor records: captured calls that could overlap in time on one device race unless
+ * the caller orders them. Each call writes every element it reads, so the array needs no
+ * clearing between calls. */
 #define DCN_NOALLOC_SCRATCH_BYTES (24u << 20)
 dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_shape* shape,
                                                  const void* d_input, const void* d_offset,

@@ -647,12 +647,16 @@ dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_sha
                                                  void* d_output, void* stream) {
     if (!ctx) return DCN_INVALID_ARGUMENT;
     DeviceGuard guard(ctx->device);
-    // The device address of the scratch array, resolved by dcn_create on this device.
-    void* scratch = dcn::noalloc_scratch(ctx->device);
-    if (!scratch)
+    // The device address of the scratch array, resolved by dcn_create on this device; the
+    // call's use of it is ordered after the previous call's (another stream's included).
+    dcn::NoallocScratchUse use(ctx->device, (hipStream_t)stream);
+    if (!use.ptr())
         return fail(ctx, DCN_COMMAND_FAILED, "allocation-free scratch is not resolved on this device");
+    if (use.error() != hipSuccess)
+        return fail(ctx, DCN_COMMAND_FAILED,
+                    std::string("ordering after the previous allocation-free call: ") + hipGetErrorString(use.error()));
     return fused_prepacked_dev(ctx, shape, d_input, false, d_offset, d_mask, packed, d_output,
-                               (hipStream_t)stream, scratch, DCN_NOALLOC_SCRATCH_BYTES);
+                               (hipStream_t)stream, use.ptr(), DCN_NOALLOC_SCRATCH_BYTES);
 }
 
 dcn_status dcn_forward_bf16_prepacked_dev(dcn_context* ctx, const dcn_shape* shape,

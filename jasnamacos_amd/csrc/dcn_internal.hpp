@@ -145,7 +145,25 @@ hipError_t launch_pack_cb8(const KShape& s, const FusedGeometry& g, const uint16
 // file-scope scratch array for `device` (which must be current; once per device), and
 // look it up afterwards (null when it was never resolved).
 hipError_t noalloc_scratch_init(int device);
-void* noalloc_scratch(int device);
+// One call's use of the device's allocation-free scratch (dcn_scratch.hip): while it
+// lives, the library's lock is held; on construction the stream waits for the previous
+// call if that ran on another stream, on destruction the call's completion is recorded.
+class NoallocScratchUse {
+public:
+    NoallocScratchUse(int device, hipStream_t stream);
+    ~NoallocScratchUse();
+    NoallocScratchUse(const NoallocScratchUse&) = delete;
+    NoallocScratchUse& operator=(const NoallocScratchUse&) = delete;
+    void* ptr() const { return ptr_; }        // null: not resolved on this device
+    hipError_t error() const { return error_; }
+private:
+    std::unique_lock<std::mutex> lock_;
+    int device_;
+    hipStream_t stream_;
+    void* ptr_ = nullptr;
+    bool ordered_ = false;
+    hipError_t error_ = hipSuccess;
+};
 hipError_t launch_prepack_weights(const KShape& s, const FusedGeometry& g, const uint16_t* w,
                                   int layout, const uint16_t* bias, void* packed_w,
                                   float* packed_b, hipStream_t stream, bool bias_bf16 = false);

@@ -1,8 +1,8 @@
 """The allocation-free fused entry point (dcn_forward_f16_prepacked_noalloc_dev), through
 the C ABI: bit-identical to dcn_forward_f16_prepacked_dev on the same inputs for two
 calls in a row, the second with a smaller input (the shared scratch array still holds
-the first call's larger copy), inside a captured hipGraph too, and shapes whose padded
-input exceeds the scratch array are rejected before anything runs."""
+the first call's larger copy), inside a captured hipGraph too, ordered across two streams,
+and shapes whose padded input exceeds the scratch array are rejected before anything runs."""
 from __future__ import annotations
 
 import ctypes as C
@@ -78,6 +78,34 @@ def test_noalloc_in_captured_graph(dcn):
                 g.replay()
             torch.cuda.synchronize()
             assert np.array_equal(out.cpu().numpy(), want), i
+        packed.free()
+    finally:
+        ctx.close()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(dcn):
+    """Calls on two streams, issued back to back without a host synchronisation, share the
+    device's scratch array: the library makes each stream wait for the other's previous
+    call, so every output equals the workspace path's."""
+    import torch
+
+    ctx = dcn.HipDeformConv(0)
+    try:
+        s = dcn.DeformConvShape(2, 128, 64, 64, 64, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+        cases = [_case(dcn, torch, s, 10 + i) for i in range(4)]
+        packed = ctx.prepack_dev(s, cases[0]["weight"], cases[0]["bias"])
+        want = [_run(ctx, s, d, packed, False, torch) for d in cases]
+        streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+        for rep in range(3):
+            print("case: noalloc two streams, round", rep, flush=True)
+            outs = [torch.zeros(s.output_count, dtype=torch.int16, device="cuda") for _ in cases]
+            torch.cuda.synchronize()
+            for i, d in enumerate(cases):  # streams 0, 1, 0, 1
+                ctx.forward_f16_prepacked_noalloc_dev(s, d["input"], d["offset"], d["mask"], packed, outs[i],
+                                                      stream=streams[i % 2])
+            torch.cuda.synchronize()
+            for i in range(len(cases)):
+                assert np.array_equal(outs[i].cpu().numpy(), want[i]), (rep, i)
         packed.free()
     finally:
         ctx.close()
