@@ -155,19 +155,22 @@ __device__ int tile_band_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr, int
                               float* sh) {
     constexpr int TH = 128 / TW;
     constexpr int kPieces = TW / 8;           // 16-byte pieces of a tile row
-    constexpr int kRows = 8 / kPieces;        // rows sampled: 4 of 8 (TW 16), 2 of 4 (TW 32)
-    constexpr int kUnits = 2 * kRows * kPieces;  // 16: dy and dx pieces of a tile
-    static_assert(kUnits == 16 && TH >= kRows, "a tile's estimate is 16 units of 8 pixels");
+    constexpr int kRows = TW == 16 ? 4 : 2;      // rows sampled: 4 of 8 (TW 16), 2 of 4 (TW 32)
+    constexpr int kHalf = kRows * kPieces;       // 8: pieces of one channel (dy or dx) of a tile
+    constexpr int kUnits = 2 * kHalf;            // 16: dy and dx pieces of a tile
+    static_assert((kHalf == 4 || kHalf == 8) && TH >= kRows && kRows >= 2,
+                  "a tile's estimate is 8 or 16 units of 8 pixels");
     const int tid = threadIdx.x;
-    const int u = tid & 15;
-    const int ch = u >> 3;                    // 0: dy, 1: dx
-    const int w = u & 7;
+    const int u = tid % kUnits;
+    const int ch = u / kHalf;                    // 0: dy, 1: dx
+    const int w = u % kHalf;
     // Sampled row r of kRows: tile row round(r (TH - 1) / (kRows - 1)), so the first and
     // last rows and evenly spaced ones between (0, 2, 5, 7 of 8; 0, 3 of 4).
     const int row = ((w / kPieces) * (TH - 1) * 2 + (kRows - 1)) / (2 * (kRows - 1));
     const int piece = w % kPieces;
     constexpr int kPass = 64 * kTileWaves / kUnits;  // tiles per pass (16)
     constexpr int kPasses = 64 / kPass;              // 4: a band has at most 63 tiles
+    static_assert(kPass * kPasses == 64, "the passes cover 64 tiles");
     const int tiles_img = a.tiles_y * a.tiles_x;
     // Centre tap (ky = kx = 1 of the 3x3 kernel) of group 0: offset channels 8 (dy), 9 (dx).
     // Every pass loads (tiles past the band read its last tile again and are masked), so
@@ -175,7 +178,7 @@ __device__ int tile_band_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr, int
     float mn[kPasses], mx[kPasses];
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
-        const int i = pass * kPass + (tid >> 4);
+        const int i = pass * kPass + tid / kUnits;
         mn[pass] = 3.0e38f;
         mx[pass] = -3.0e38f;
         const int t = band0 + min(i, n - 1);
@@ -202,10 +205,10 @@ __device__ int tile_band_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr, int
             mx[pass] = -3.0e38f;
         }
     }
-    // Extent per (tile, channel): a min / max over the 8 lanes of its pieces, a half DPP
-    // row (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror: lane i meets lanes i ^ 1,
-    // i ^ 2, then the other quad of its 8).
-    auto lanes8 = [](float v, bool take_min) {
+    // Extent per (tile, channel): a min / max over the kHalf lanes of its pieces by DPP
+    // (quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror for 8: lane i meets lanes
+    // i ^ 1, i ^ 2, then the other quad of its 8).
+    auto lanes = [](float v, bool take_min) {
         auto step = [&](float x, auto ctrl_c) {
             const float y = __builtin_bit_cast(
                 float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(ctrl_c)::value, 0xF, 0xF, false));
@@ -213,14 +216,15 @@ __device__ int tile_band_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr, int
         };
         v = step(v, std::integral_constant<int, 0xB1>{});
         v = step(v, std::integral_constant<int, 0x4E>{});
-        return step(v, std::integral_constant<int, 0x141>{});
+        if constexpr (kHalf == 8) v = step(v, std::integral_constant<int, 0x141>{});
+        return v;
     };
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
         if (pass * kPass >= n) continue;
-        mn[pass] = lanes8(mn[pass], true);
-        mx[pass] = lanes8(mx[pass], false);
-        const int i = pass * kPass + (tid >> 4);
+        mn[pass] = lanes(mn[pass], true);
+        mx[pass] = lanes(mx[pass], false);
+        const int i = pass * kPass + tid / kUnits;
         if (w == 0 && i < n) sh[2 * i + ch] = mx[pass] - mn[pass];
     }
     __syncthreads();  // every tile's extents in sh[0 .. 2n) (the plan's only barrier)
