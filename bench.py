@@ -1204,6 +1204,9 @@ def main() -> int:
             "sampler": "bf16" if bf16 else None if f32 else ("exact" if fused_cfg["sampler"] == dc.SAMPLER_EXACT
                                                               else "fast"),
             "timing": f"{args.steps} calls captured in one hipGraph, one replay timed with HIP events",
+            # samples whose four corners all lie outside the input (they contribute zero)
+            "sample_oob_fraction": round(dc.out_of_bounds_fraction(
+                s, dc.bf16_bits_to_f32(h["offset"]) if bf16 else np.asarray(h["offset"], np.float32)), 4),
         },
         "tflops": flops / (us_per_call * 1e-6) / 1e12,
         "step_hbm_frac": nbytes / (us_per_call * 1e-6) / 1e9 / HBM_PEAK_GBS,

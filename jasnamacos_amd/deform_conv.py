@@ -1021,6 +1021,26 @@ def generate_config_inputs(config: int, seed: int) -> dict:
     return arrays
 
 
+def out_of_bounds_fraction(shape, offset) -> float:
+    """Fraction of a layer's samples (output pixel x offset group x tap) whose sampling
+    point lies where all four bilinear corners are outside the input (y <= -1, y >= H,
+    x <= -1 or x >= W), so that the sample contributes zero: the out-of-bounds rate the
+    benchmark configs are drawn for. offset: [B][2*G*Kh*Kw][Ho][Wo] (dy, dx), any float."""
+    s = shape
+    ka = s.kernel_height * s.kernel_width
+    off = np.asarray(offset, np.float64).reshape(s.batch, s.offset_groups, ka, 2, s.output_height,
+                                                 s.output_width)
+    k = np.arange(ka)
+    ky = (k // s.kernel_width).reshape(1, 1, -1, 1, 1)
+    kx = (k % s.kernel_width).reshape(1, 1, -1, 1, 1)
+    oy = np.arange(s.output_height).reshape(1, 1, 1, -1, 1)
+    ox = np.arange(s.output_width).reshape(1, 1, 1, 1, -1)
+    y = oy * s.stride_height - s.pad_height + ky * s.dilation_height + off[:, :, :, 0]
+    x = ox * s.stride_width - s.pad_width + kx * s.dilation_width + off[:, :, :, 1]
+    inside = (y > -1) & (y < s.input_height) & (x > -1) & (x < s.input_width)
+    return float(1.0 - inside.mean())
+
+
 def reference_benchmark_inputs(seed: int = 0x4A41534E41) -> dict:
     """benchmarkJasnaShape's seeded inputs (MetalRunner.swift:210-213, 233-234): input
     U(-1,1), offset U(-0.25,0.25), mask U(0.25,0.75), weight and bias U(-0.02,0.02),

@@ -164,6 +164,28 @@ def _oob_fraction(shape, offset):
     return 1.0 - inside.mean()
 
 
+def test_out_of_bounds_fraction(dcn):
+    """deform_conv.out_of_bounds_fraction against this file's restatement (stride 1, pad 1)
+    on C2's inputs, and against a per-sample count on a small shape with stride, dilation
+    and padding 2, with points exactly on the -1 and H / W boundaries."""
+    d = dcn.generate_config_inputs(2, 7)
+    assert dcn.out_of_bounds_fraction(d["shape"], d["offset"]) == pytest.approx(_oob_fraction(d["shape"], d["offset"]))
+    s = dcn.DeformConvShape(1, 8, 7, 9, 8, 4, 5, 3, 3, 2, 2, 2, 2, 2, 2, 1, 1)
+    rng = np.random.default_rng(3)
+    off = rng.uniform(-4, 4, (2 * 9, 4, 5))
+    off[0, 0, 0] = -1.0 - (0 * 2 - 2 + 0)  # y exactly -1: outside
+    off[1, 0, 0] = 0.0
+    off[2, 0, 1] = 7.0 - (0 * 2 - 2 + 0)   # y exactly H: outside
+    n_out = 0
+    for k in range(9):
+        for oy in range(4):
+            for ox in range(5):
+                y = oy * 2 - 2 + (k // 3) * 2 + off[2 * k, oy, ox]
+                x = ox * 2 - 2 + (k % 3) * 2 + off[2 * k + 1, oy, ox]
+                n_out += not (-1 < y < 7 and -1 < x < 9)
+    assert dcn.out_of_bounds_fraction(s, off.reshape(-1)) == pytest.approx(n_out / (9 * 4 * 5))
+
+
 def test_config_inputs_c2(dcn):
     d = dcn.generate_config_inputs(2, 1)
     d2 = dcn.generate_config_inputs(2, 1)
