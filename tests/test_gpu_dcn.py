@@ -597,16 +597,18 @@ def test_tile_placement_plan_is_bit_identical(gpu_ctx, dcn, oracle, batch, h, w,
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
 
 
-@pytest.mark.parametrize("batch,h,w", [(2, 64, 64), (1, 24, 48)])
-def test_tile_clock_stamps_every_tile(gpu_ctx, dcn, batch, h, w):
+@pytest.mark.parametrize("batch,h,w,cout,tw", [(2, 64, 64, 64, 16), (1, 24, 48, 64, 16), (2, 64, 64, 32, 16),
+                                                (1, 40, 96, 64, 32)])
+def test_tile_clock_stamps_every_tile(gpu_ctx, dcn, batch, h, w, cout, tw):
     """dcn_set_tile_clock_dev: with a clock buffer set, the tile kernel writes one record per
     workgroup that runs a tile (start <= both wave ends, every tile exactly once, the
     grid's padding workgroups write nothing), the output is bit-identical to a launch
     without stamps, and a buffer smaller than 4 stamps per workgroup is refused."""
     import torch
 
-    s = dcn.DeformConvShape(batch, 128, h, w, 64, h, w, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
-    tiles = batch * ((h + 7) // 8) * ((w + 15) // 16)
+    s = dcn.DeformConvShape(batch, 128, h, w, cout, h, w, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    th = 128 // tw
+    tiles = batch * ((h + th - 1) // th) * ((w + tw - 1) // tw)
     grid = (tiles + 7) // 8 * 8
     rng = np.random.default_rng(tiles)
     c = s.counts()
@@ -614,15 +616,15 @@ def test_tile_clock_stamps_every_tile(gpu_ctx, dcn, batch, h, w):
            "offset": rng.uniform(-8, 8, c["offset"]).astype(np.float16),
            "mask": rng.random(c["mask"]).astype(np.float16),
            "weight": (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16),
-           "bias": (rng.standard_normal(64) * 0.1).astype(np.float16)}
-    log("case: tile clock", batch, h, w, "tiles", tiles, "grid", grid)
+           "bias": (rng.standard_normal(cout) * 0.1).astype(np.float16)}
+    log("case: tile clock", batch, h, w, "cout", cout, "width", tw, "tiles", tiles, "grid", grid)
     dev = {k: _dev(torch, h16[k].view(np.int16)) for k in ("input", "offset", "mask", "weight", "bias")}
     out = torch.empty(c["output"], dtype=torch.int16, device="cuda")
     packed = gpu_ctx.prepack_dev(s, dev["weight"], dev["bias"])
     gpu_ctx.reserve(s)
-    gpu_ctx.set_fused_config(16, 8, -1, 7)
+    gpu_ctx.set_fused_config(tw, 8, -1, 7)
     try:
-        assert gpu_ctx.get_fused_config(s)["variant"] == 7
+        assert gpu_ctx.get_fused_config(s) == {"variant": 7, "mt": tw, "ks": 8, "sampler": 1}
         gpu_ctx.forward_f16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out)
         torch.cuda.synchronize()
         ref = out.clone()
