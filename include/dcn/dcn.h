@@ -281,10 +281,12 @@ dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_sha
  * (mt = 16) or 4 x 32 (mt = 32), two offset groups per stage split by tap across the
  * waves, each stage's offsets, masks and sample windows copied into LDS by DMA, global
  * gathers for a stage whose windows do not fit (3x3 kernels, 8 channels per group, an
- * even group count, Cout 32 or 64, input sides up to 32000, fast sampler; ks = 8: the
- * tiles of an XCD's band are placed on its CUs by estimated cost where some CUs run one
- * tile and others two (33-63 tiles per band), ks = 1: fixed placement; the outputs are
- * the same bits either way). sampler: 0 = reference arithmetic
+ * even group count, Cout 32 or 64, input sides up to 32000; ks = 8: the tiles of an
+ * XCD's band are placed on its CUs by estimated cost where some CUs run one tile and
+ * others two (33-63 tiles per band), ks = 1: fixed placement; the outputs are the same
+ * bits either way; the automatic choice for problems of more than 1024 tiles of 32
+ * pixels with the fast sampler, and with the exact sampler only when pinned, since the
+ * window kernel is faster there). sampler: 0 = reference arithmetic
  * (FP32 bilinear in the reference's association, half(sampled*mask): the im2col
  * values of deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into
  * the bilinear weights, packed-FP16 blend). mt = 32-pixel row blocks per tile (1, 2),

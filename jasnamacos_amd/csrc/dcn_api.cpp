@@ -45,14 +45,17 @@ dcn::FusedConfig choose_config(dcn::FusedConfig o, const dcn::FusedGeometry& g, 
     // single large maps (C5: 1 x 180 x 320, 55.2 us with the cost-ordered tile placement,
     // against 70.9 us; its wide-flow stages whose two windows do not fit LDS together run
     // one pass per window).
+    // With the exact sampler (the reference's FP32 blend, about 136 VALU per sample) the
+    // tile variant is slower than the window kernel (C3 78.1 against 74.9 us, C5 80.3
+    // against 76.4): it runs only when pinned.
     if (o.variant == 0 && tile_ok && o.sampler != dcn::kSamplerExact && (g.m + 31) / 32 > 1024)
         o.variant = dcn::kVariantTile;
-    // The tile variant implements the fast sampler only: with the exact one (or a shape
-    // it does not cover) the automatic choice below applies, with only the sampler pinned.
+    // A shape the tile variant does not cover gets the automatic choice below, with only
+    // the sampler pinned.
     if (o.variant == dcn::kVariantTile) {
-        if (tile_ok && o.sampler != dcn::kSamplerExact)
+        if (tile_ok)
             return dcn::FusedConfig{dcn::kVariantTile, o.mt > 0 ? o.mt : 16, o.ks > 0 ? o.ks : 8,
-                                    dcn::kSamplerFast};
+                                    o.sampler == dcn::kSamplerExact ? dcn::kSamplerExact : dcn::kSamplerFast};
         o = dcn::FusedConfig{0, 0, 0, o.sampler};
     }
     const long long tiles32 = (g.m + 31) / 32;
@@ -99,7 +102,8 @@ dcn::FusedConfig choose_config(dcn::FusedConfig o, const dcn::FusedGeometry& g, 
 
 bool config_supported(const dcn::FusedConfig& c, const dcn::FusedGeometry& g) {
     if (c.variant == dcn::kVariantTile)  // ks: 8 = cost-ordered tile placement, 1 = fixed
-        return (c.mt == 16 || c.mt == 32) && (c.ks == 8 || c.ks == 1) && c.sampler == dcn::kSamplerFast;
+        return (c.mt == 16 || c.mt == 32) && (c.ks == 8 || c.ks == 1) &&
+               (c.sampler == dcn::kSamplerFast || c.sampler == dcn::kSamplerExact);
     if (c.variant == dcn::kVariantWindowAsync) return c.mt == 8 && c.ks == 8;
     if (c.variant == dcn::kVariantNarrow) return c.mt == 1 && (c.ks == 8 || c.ks == 12);
     if (c.variant == dcn::kVariantWindow || c.variant == dcn::kVariantWindowSplit)

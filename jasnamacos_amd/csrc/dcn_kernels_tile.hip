@@ -132,6 +132,27 @@ __device__ __forceinline__ h8 blend_w(const u32x4 (&q)[4], uint32_t w0, uint32_t
     return r;
 }
 
+// The reference's sampler arithmetic (blend_exact: FP32 bilinear in the reference's
+// association, times the mask, rounded once to FP16), two channels at a time: the
+// scheduling barriers keep the widened corners of only two channels live at once, so the
+// tile kernel's register budget holds it. Same operations, so the same bits.
+__device__ __forceinline__ h8 blend_exact_pairs(const u32x4 (&q)[4], float ly, float lx, float m) {
+    const float oy = 1.0f - ly, ox = 1.0f - lx;
+    h8 r;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+#pragma unroll
+        for (int f = e; f < e + 2; ++f) {
+            const float v00 = (float)__builtin_bit_cast(h8, q[0])[f], v01 = (float)__builtin_bit_cast(h8, q[1])[f];
+            const float v10 = (float)__builtin_bit_cast(h8, q[2])[f], v11 = (float)__builtin_bit_cast(h8, q[3])[f];
+            const float sv = v00 * oy * ox + v01 * oy * lx + v10 * ly * ox + v11 * ly * lx;
+            r[f] = round_f16(sv * m);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return r;
+}
+
 // Placement of a band's tiles on its XCD's CUs. Workgroups are dispatched to an XCD in
 // blockIdx order (blockIdx % 8), and within an XCD local index l goes to CU l % 32: with
 // n tiles per band, 32 < n < 64, locals l and l + 32 (l < n - 32) share a CU and locals
@@ -256,7 +277,7 @@ __device__ int tile_band_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr, int
     return min(max(pick, 0), n - 1);
 }
 
-template <int NB, int TW>
+template <int NB, int TW, bool EXACT>
 __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     constexpr int NW = kTileWaves;
     constexpr int RPW = 32 / TW;  // tile rows per 32-pixel segment
@@ -466,8 +487,13 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         };
         // Sample state of a stage: a[] = clamped corner (iy, ix) as a 16-bit pair, then
         // the sample's address; w0/w1 = the FP16 corner weights.
+        // a = the clamped corner (iy, ix) as a 16-bit pair, then the sample's address.
+        // Fast sampler: w0 / w1 = the four mask-folded FP16 corner weights. Exact sampler
+        // (EXACT): w0 / w1 = the FP32 fractions ly / lx, m = the FP16 masks of samples 2i
+        // and 2i + 1, for the reference's FP32 blend.
         struct Samples {
             uint32_t a[NSMP], w0[NSMP], w1[NSMP];
+            uint32_t m[EXACT ? (NSMP + 1) / 2 : 1];
         };
         s16x2 bmin, bmax;
         auto box_reset = [&]() {
@@ -489,10 +515,17 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             C.a[j] = __builtin_amdgcn_perm((uint32_t)ix, (uint32_t)iy, 0x05040100u);
             bmin = __builtin_elementwise_min(bmin, as_s16x2(C.a[j]));
             bmax = __builtin_elementwise_max(bmax, as_s16x2(C.a[j]));
+            if constexpr (EXACT) {
+                C.w0[j] = __builtin_bit_cast(uint32_t, ly);
+                C.w1[j] = __builtin_bit_cast(uint32_t, lx);
+                const uint32_t mb = __builtin_bit_cast(uint16_t, offset_of(j, 2));
+                C.m[j / 2] = (j & 1) ? (C.m[j / 2] & 0xffffu) | (mb << 16) : mb;
+                return;
+            }
+            const float m = (float)offset_of(j, 2);
             // Mask folded into the four bilinear weights, each rounded once to FP16 (the
             // mask products as fmas with +0: the products are not negative, so the same
             // single rounding, with the FP16 mask taken as it is).
-            const float m = (float)offset_of(j, 2);
             const float t0 = __builtin_fmaf(m, 1.0f - ly, 0.0f);
             const float t1 = __builtin_fmaf(m, ly, 0.0f);
             C.w0[j] = __builtin_bit_cast(uint32_t, h2{(_Float16)(t0 * (1.0f - lx)), (_Float16)(t0 * lx)});
@@ -587,9 +620,19 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             for (int j = 0; j < NSMP; ++j) {
                 u32x4(&cur)[4] = (j & 1) ? qb : qa;
                 u32x4(&nxt)[4] = (j & 1) ? qa : qb;
-                if (j + 1 < NSMP) corners(j + 1, C, r, from_lds, active, lds_pitch, nxt);
+                // The next sample's corners are requested before this one's blend; with the
+                // exact sampler (a blend long enough to cover the LDS round trip) after it,
+                // so the two samples' corners need not be live together.
+                if (!EXACT && j + 1 < NSMP) corners(j + 1, C, r, from_lds, active, lds_pitch, nxt);
                 const int kk = slot_of(j), s = seg_of(j);
-                const h8 A = blend_w(cur, C.w0[j], C.w1[j]);
+                h8 A;
+                if constexpr (EXACT) {
+                    const float m = (float)__builtin_bit_cast(_Float16, (uint16_t)(C.m[j / 2] >> (16 * (j & 1))));
+                    A = blend_exact_pairs(cur, __builtin_bit_cast(float, C.w0[j]), __builtin_bit_cast(float, C.w1[j]), m);
+                } else {
+                    A = blend_w(cur, C.w0[j], C.w1[j]);
+                }
+                if (EXACT && j + 1 < NSMP) corners(j + 1, C, r, from_lds, active, lds_pitch, nxt);
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
                     acc[s][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, Bq[kk][nb], acc[s][nb], 0, 0, 0);
@@ -744,9 +787,9 @@ __global__ __launch_bounds__(256) void tile_prepack_kernel(const uint16_t* __res
     wpk[gid] = v;
 }
 
-template <int NB, int TW>
+template <int NB, int TW, bool EXACT>
 hipError_t launch_tile_t(const TileArgs& a, hipStream_t stream) {
-    auto kernel = &tile_kernel<NB, TW>;
+    auto kernel = &tile_kernel<NB, TW, EXACT>;
     const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), kTileLds);
     if (attr != hipSuccess) return attr;
     const unsigned grid = (unsigned)(((a.tiles + 7) / 8) * 8);
@@ -755,10 +798,12 @@ hipError_t launch_tile_t(const TileArgs& a, hipStream_t stream) {
 }
 
 template <int TW>
-hipError_t launch_tile_nb(const TileArgs& a, int nb, hipStream_t stream) {
-    switch (nb) {
-        case 1: return launch_tile_t<1, TW>(a, stream);
-        case 2: return launch_tile_t<2, TW>(a, stream);
+hipError_t launch_tile_nb(const TileArgs& a, int nb, bool exact, hipStream_t stream) {
+    switch (nb * 2 + (exact ? 1 : 0)) {
+        case 2: return launch_tile_t<1, TW, false>(a, stream);
+        case 3: return launch_tile_t<1, TW, true>(a, stream);
+        case 4: return launch_tile_t<2, TW, false>(a, stream);
+        case 5: return launch_tile_t<2, TW, true>(a, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -830,7 +875,8 @@ hipError_t launch_tile_f16(const KShape& s, const FusedGeometry& g, const FusedC
     a.tiles_y = (s.Ho + th - 1) / th;
     a.tiles_x = (s.Wo + tw - 1) / tw;
     a.tiles = a.tiles_y * a.tiles_x * s.B;
-    return tw == 32 ? launch_tile_nb<32>(a, g.nb, stream) : launch_tile_nb<16>(a, g.nb, stream);
+    const bool exact = cfg.sampler == kSamplerExact;
+    return tw == 32 ? launch_tile_nb<32>(a, g.nb, exact, stream) : launch_tile_nb<16>(a, g.nb, exact, stream);
 }
 
 size_t tile_grid(const KShape& s, const FusedConfig& cfg) {

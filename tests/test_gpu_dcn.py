@@ -253,8 +253,8 @@ def test_fused_configs(gpu_ctx, dcn, c2, variant, mt, ks, sampler):
 
 def test_automatic_config_per_workload(gpu_ctx, dcn):
     """The automatic choice: narrow 16-pixel tiles for one 64 x 64 map (C2), the tile kernel
-    for batches of small maps (C3) and for one large map (C5); the exact sampler never gets
-    the tile kernel (it implements the fast one only)."""
+    for batches of small maps (C3) and for one large map (C5); with the exact sampler the
+    window kernel (faster there than the tile kernel's exact path, which runs when pinned)."""
     want = {2: dcn.VARIANT_NARROW, 3: 7, 5: 7}
     for c, v in want.items():
         assert gpu_ctx.get_fused_config(dcn.config_shape(c))["variant"] == v, c
@@ -555,6 +555,44 @@ def test_tile_split_stages(gpu_ctx, dcn, oracle, tw):
     mx, mean = errors(out, ref)
     log(f"  max {mx:.3e} mean {mean:.3e}")
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16
+
+
+@pytest.mark.parametrize("tw", [16, 32])
+def test_tile_exact_sampler_matches_gather_gemm(gpu_ctx, dcn, oracle, tw):
+    """The tile variant pinned with the reference's sampler arithmetic (FP32 bilinear in the
+    reference's association, half(sampled * mask)), on the split-stage case above (one
+    pass per group in stages 4-7): the samples are the oracle im2col's FP16 values, so the
+    output is within two FP16 ulps of the oracle's gather + FP32 GEMM (only the summation
+    order differs), and deterministic."""
+    s = dcn.DeformConvShape(2, 128, 64, 64, 64, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    rng = np.random.default_rng(200 + tw)
+    c = s.counts()
+    off = rng.uniform(-3, 3, c["offset"]).reshape(2, 16, 18, 64 * 64)
+    off[:, 8:] = rng.uniform(-20, 20, off[:, 8:].shape)
+    off = off.reshape(-1).astype(np.float16)
+    sizes = tile_stage_windows(off, 64, 64, 16, 8 * 16 // tw, tw)
+    split = (sizes.sum(axis=1) > 65536) & (sizes.max(axis=1) <= 65536)
+    assert split.sum() >= 8, "the case must exercise split stages"
+    h = {"input": rng.standard_normal(c["input"]).astype(np.float16),
+         "offset": off,
+         "mask": rng.random(c["mask"]).astype(np.float16),
+         "weight": (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16),
+         "bias": (rng.standard_normal(64) * 0.1).astype(np.float16)}
+    log("case: tile variant, exact sampler, width", tw, "split stages", int(split.sum()))
+    packed = gpu_ctx.prepack(s, h["weight"], h["bias"])
+    gpu_ctx.set_fused_config(tw, 8, dcn.SAMPLER_EXACT, 7)
+    try:
+        assert gpu_ctx.get_fused_config(s) == {"variant": 7, "mt": tw, "ks": 8, "sampler": dcn.SAMPLER_EXACT}
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+        again = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    assert np.array_equal(out.view(np.uint16), again.view(np.uint16))
+    cols = oracle.im2col_f16(s, h["input"], h["offset"], h["mask"])
+    ref = oracle.gemm_f16(s, cols, h["weight"], h["bias"]).astype(np.float64)
+    diff = np.abs(out.astype(np.float64) - ref)
+    ulp = np.maximum(np.abs(ref), 2.0 ** -14) * 2.0 ** -10
+    assert np.all(diff <= 2 * ulp + 1e-6), float((diff / ulp).max())
 
 
 @pytest.mark.parametrize("batch,h,w,tw", [(1, 180, 320, 16), (9, 64, 64, 16), (1, 120, 320, 32), (1, 150, 264, 16)])
