@@ -251,6 +251,34 @@ def test_fused_configs(gpu_ctx, dcn, c2, variant, mt, ks, sampler):
     assert mx <= MAX_ABS_F16 and mean <= MEAN_ABS_F16, (mx, mean)
 
 
+@pytest.mark.parametrize("variant,mt,ks", FUSED_CONFIGS)
+def test_exact_sampler_through_one_hot_weights(gpu_ctx, dcn, oracle, c2, variant, mt, ks):
+    """Each fused kernel with the reference's sampler arithmetic and one-hot weights (output
+    channel oc weighs one K element, ic * 9 + tap = 18 oc, with 1.0; no bias): every other
+    product is a signed zero, so each output is one sample, exactly, and must equal the
+    oracle's gather (deform_conv2d_fp16_jasna_gather) at that K element and pixel, value
+    for value (zeros of either sign compare equal)."""
+    s, h, _ = c2
+    log("case: one-hot exact sampler", variant, mt, ks)
+    w = np.zeros((64, 128, 9), np.float16)
+    kk = 18 * np.arange(64)
+    w[np.arange(64), kk // 9, kk % 9] = 1.0
+    bias = np.zeros(64, np.float16)
+    packed = gpu_ctx.prepack(s, w.reshape(-1), bias)
+    gpu_ctx.set_fused_config(mt, ks, dcn.SAMPLER_EXACT, variant)
+    try:
+        cfg = gpu_ctx.get_fused_config(s)
+        assert (cfg["variant"], cfg["sampler"]) == (variant, dcn.SAMPLER_EXACT), cfg
+        out = gpu_ctx.run_float16_prepacked(s, h["input"], h["offset"], h["mask"], packed)
+    finally:
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    cols = oracle.im2col_f16(s, h["input"], h["offset"], h["mask"]).view(np.float16).reshape(64 * 64, 128 * 9)
+    want = cols[:, kk].T.astype(np.float32)  # [oc][pixel]
+    got = out.reshape(64, 64 * 64).astype(np.float32)
+    bad = np.nonzero(got != want)
+    assert bad[0].size == 0, (bad[0].size, got[bad][:4], want[bad][:4])
+
+
 def test_automatic_config_per_workload(gpu_ctx, dcn):
     """The automatic choice: narrow 16-pixel tiles for one 64 x 64 map (C2), the tile kernel
     for batches of small maps (C3) and for one large map (C5); with the exact sampler the
