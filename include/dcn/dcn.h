@@ -285,8 +285,7 @@ dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_sha
  * XCD's band are placed on its CUs by estimated cost where some CUs run one tile and
  * others two (33-63 tiles per band), ks = 1: fixed placement; the outputs are the same
  * bits either way; the automatic choice for problems of more than 1024 tiles of 32
- * pixels with the fast sampler, and with the exact sampler only when pinned, since the
- * window kernel is faster there). sampler: 0 = reference arithmetic
+ * pixels, with either sampler). sampler: 0 = reference arithmetic
  * (FP32 bilinear in the reference's association, half(sampled*mask): the im2col
  * values of deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into
  * the bilinear weights, packed-FP16 blend). mt = 32-pixel row blocks per tile (1, 2),

@@ -41,15 +41,13 @@ bool packed_matches(const dcn_packed* p, const dcn_shape* s) {
 dcn::FusedConfig choose_config(dcn::FusedConfig o, const dcn::FusedGeometry& g, const dcn_shape& shape,
                                bool window_ok, bool tile_ok) {
     // Problems of more than 32K output pixels run fastest on the tile kernel: batches of
-    // small maps (C3: 16 x 64 x 64, 48.0 us against 55.2 us for the window kernel) and
-    // single large maps (C5: 1 x 180 x 320, 55.2 us with the cost-ordered tile placement,
+    // small maps (C3: 16 x 64 x 64, 47.2 us against 55.2 us for the window kernel) and
+    // single large maps (C5: 1 x 180 x 320, 51.2 us with the cost-ordered tile placement,
     // against 70.9 us; its wide-flow stages whose two windows do not fit LDS together run
     // one pass per window).
-    // With the exact sampler (the reference's FP32 blend, about 136 VALU per sample) the
-    // tile variant is slower than the window kernel (C3 78.1 against 74.9 us, C5 80.3
-    // against 76.4): it runs only when pinned.
-    if (o.variant == 0 && tile_ok && o.sampler != dcn::kSamplerExact && (g.m + 31) / 32 > 1024)
-        o.variant = dcn::kVariantTile;
+    // The same holds for the exact sampler (the reference's FP32 blend, about 104 VALU per
+    // sample): C3 67.4 against 67.6 us for the window kernel, C5 71.9 against 73.2.
+    if (o.variant == 0 && tile_ok && (g.m + 31) / 32 > 1024) o.variant = dcn::kVariantTile;
     // A shape the tile variant does not cover gets the automatic choice below, with only
     // the sampler pinned.
     if (o.variant == dcn::kVariantTile) {

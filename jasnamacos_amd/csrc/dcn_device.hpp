@@ -48,17 +48,28 @@ __device__ __forceinline__ int fast_div(int x, uint32_t magic) {
     return magic ? (int)__umulhi((uint32_t)x, magic) : x;
 }
 
+// -0.0f the compiler cannot see (so that fma(x, y, -0) is not turned into a multiply).
+__device__ __forceinline__ float opaque_neg_zero() {
+    float z;
+    asm("v_mov_b32 %0, 0x80000000" : "=v"(z));
+    return z;
+}
+
 // Reference arithmetic (MetalShader.swift:369-379): FP32 bilinear in the reference's
 // association, times the mask, rounded once to FP16. Eight channels of one sample.
+// Each corner's first product, float(v) * (1 - ly) or float(v) * ly, is an fma with -0:
+// x * y + (-0) is x * y exactly, signed zeros included, and v_fma_mix_f32 widens the FP16
+// corner inside it (one instruction instead of a conversion and a multiply).
 __device__ __forceinline__ h8 blend_exact(u32x4 q00, u32x4 q01, u32x4 q10, u32x4 q11, float ly,
                                           float lx, float m) {
     const h8 a = __builtin_bit_cast(h8, q00), b = __builtin_bit_cast(h8, q01);
     const h8 c = __builtin_bit_cast(h8, q10), d = __builtin_bit_cast(h8, q11);
+    const float oy = 1.0f - ly, ox = 1.0f - lx, nz = opaque_neg_zero();
     h8 r;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float s = (float)a[e] * (1.0f - ly) * (1.0f - lx) + (float)b[e] * (1.0f - ly) * lx +
-                        (float)c[e] * ly * (1.0f - lx) + (float)d[e] * ly * lx;
+        const float s = __builtin_fmaf((float)a[e], oy, nz) * ox + __builtin_fmaf((float)b[e], oy, nz) * lx +
+                        __builtin_fmaf((float)c[e], ly, nz) * ox + __builtin_fmaf((float)d[e], ly, nz) * lx;
         r[e] = round_f16(s * m);
     }
     return r;

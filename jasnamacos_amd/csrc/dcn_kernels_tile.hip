@@ -132,27 +132,6 @@ __device__ __forceinline__ h8 blend_w(const u32x4 (&q)[4], uint32_t w0, uint32_t
     return r;
 }
 
-// The reference's sampler arithmetic (blend_exact: FP32 bilinear in the reference's
-// association, times the mask, rounded once to FP16), two channels at a time: the
-// scheduling barriers keep the widened corners of only two channels live at once, so the
-// tile kernel's register budget holds it. Same operations, so the same bits.
-__device__ __forceinline__ h8 blend_exact_pairs(const u32x4 (&q)[4], float ly, float lx, float m) {
-    const float oy = 1.0f - ly, ox = 1.0f - lx;
-    h8 r;
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-#pragma unroll
-        for (int f = e; f < e + 2; ++f) {
-            const float v00 = (float)__builtin_bit_cast(h8, q[0])[f], v01 = (float)__builtin_bit_cast(h8, q[1])[f];
-            const float v10 = (float)__builtin_bit_cast(h8, q[2])[f], v11 = (float)__builtin_bit_cast(h8, q[3])[f];
-            const float sv = v00 * oy * ox + v01 * oy * lx + v10 * ly * ox + v11 * ly * lx;
-            r[f] = round_f16(sv * m);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    return r;
-}
-
 // Placement of a band's tiles on its XCD's CUs. Workgroups are dispatched to an XCD in
 // blockIdx order (blockIdx % 8), and within an XCD local index l goes to CU l % 32: with
 // n tiles per band, 32 < n < 64, locals l and l + 32 (l < n - 32) share a CU and locals
@@ -628,7 +607,8 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
                 h8 A;
                 if constexpr (EXACT) {
                     const float m = (float)__builtin_bit_cast(_Float16, (uint16_t)(C.m[j / 2] >> (16 * (j & 1))));
-                    A = blend_exact_pairs(cur, __builtin_bit_cast(float, C.w0[j]), __builtin_bit_cast(float, C.w1[j]), m);
+                    A = blend_exact(cur[0], cur[1], cur[2], cur[3], __builtin_bit_cast(float, C.w0[j]),
+                                    __builtin_bit_cast(float, C.w1[j]), m);
                 } else {
                     A = blend_w(cur, C.w0[j], C.w1[j]);
                 }

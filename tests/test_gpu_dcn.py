@@ -281,14 +281,15 @@ def test_exact_sampler_through_one_hot_weights(gpu_ctx, dcn, oracle, c2, variant
 
 def test_automatic_config_per_workload(gpu_ctx, dcn):
     """The automatic choice: narrow 16-pixel tiles for one 64 x 64 map (C2), the tile kernel
-    for batches of small maps (C3) and for one large map (C5); with the exact sampler the
-    window kernel (faster there than the tile kernel's exact path, which runs when pinned)."""
+    for batches of small maps (C3) and for one large map (C5), with either sampler."""
     want = {2: dcn.VARIANT_NARROW, 3: 7, 5: 7}
     for c, v in want.items():
         assert gpu_ctx.get_fused_config(dcn.config_shape(c))["variant"] == v, c
     gpu_ctx.set_fused_config(0, 0, dcn.SAMPLER_EXACT)
     try:
-        assert gpu_ctx.get_fused_config(dcn.config_shape(3))["variant"] == 3
+        for c, v in want.items():
+            cfg = gpu_ctx.get_fused_config(dcn.config_shape(c))
+            assert (cfg["variant"], cfg["sampler"]) == (v, dcn.SAMPLER_EXACT), (c, cfg)
     finally:
         gpu_ctx.set_fused_config(0, 0, -1)
 
