@@ -50,7 +50,50 @@ struct NarrowArgs {
     // Output placement: NCHW [B][Cout][HWo], or channels out_coff.. of a CB8 tensor with
     // out_cblk 8-channel blocks per image ([B][out_cblk][Ho+4][Wo+4][8]).
     int out_cb8, out_coff, out_cblk;
+    // Rows above and below the sampled band that the L2 warm-up loads (0: no warm-up).
+    int pf_halo;
 };
+
+// L2 warm-up of narrow_kernel. The CB8 input is usually fresh (written by the repack or by
+// its producer just before this launch) and in no XCD's L2, so each XCD fetches the lines
+// its corner gathers touch over the fabric (measured: 1.4 us of the 10.5 us C2 call). The
+// workgroups of one XCD hold consecutive tiles, i.e. a band of output rows of one image;
+// their waves together copy the input rows that band samples (receptive field plus
+// pf_halo rows each side, every channel block) to a 1 KB slot of LDS that nothing reads:
+// exactly two LDS-DMA instructions of 1 KB per wave (chunks past the band, and units
+// past the buffer, read nothing: buffer bounds). A fixed count keeps the compiler's wait
+// counts exact. Issued after the wave's offset loads and before its corner gathers:
+// loads complete in issue order, so earlier they would delay the offsets.
+constexpr int kNarrowWarmLoads = 2;  // LDS-DMA instructions per wave
+
+template <int NW, int LOADS>
+__device__ __forceinline__ void warm_band(const NarrowArgs& a, __amdgpu_buffer_rsrc_t xr, int per_xcd,
+                                          int wave, int lane, uint8_t* slot) {
+    const int t_lo = (blockIdx.x & 7) * per_xcd;
+    const int t_hi = min(t_lo + per_xcd, a.tiles) - 1;
+    const int p_lo = t_lo * 16;
+    const int p_hi = min(t_hi * 16 + 15, a.M - 1);
+    const int img = p_lo / a.HWo;
+    if (img != p_hi / a.HWo) return;  // a band across two images: no warm-up
+    const int kh = a.KA / a.KW;
+    const int r0 = max((p_lo - img * a.HWo) / a.Wo * a.sh - a.ph - a.pf_halo + kPad, 0);
+    const int r1 = min((p_hi - img * a.HWo) / a.Wo * a.sh - a.ph + (kh - 1) * a.dh + a.pf_halo + kPad + 1,
+                       a.Hp - 1);
+    const uint32_t run = (uint32_t)max(r1 - r0 + 1, 0) * a.Wp;  // 16-byte units per channel block
+    const uint32_t per_block = (run + 63) / 64;                 // 1 KB chunks per channel block
+    const uint32_t chunks = per_block * a.CBLK;
+    const uint32_t j0 = (uint32_t)(blockIdx.x >> 3) * NW + (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+    const uint32_t step = (uint32_t)(t_hi - t_lo + 1) * NW;  // waves on this XCD
+#pragma unroll
+    for (int t = 0; t < LOADS; ++t) {
+        const uint32_t j = j0 + t * step;
+        const uint32_t jc = j < chunks ? j : 0;
+        const uint32_t c = jc / per_block;
+        const uint32_t unit = ((uint32_t)(img * a.CBLK + c) * a.Hp + r0) * a.Wp + (jc - c * per_block) * 64 + lane;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)slot, 16,
+                                                 (int)(j < chunks ? unit * 16u : 0xFFFFFFF0u), 0, 0, 0);
+    }
+}
 
 template <int NB, int NW, int U, int SAMPLER>
 __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
@@ -58,7 +101,7 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
     // samples are the exact sampler's FP32 bilinear rounded once to BF16, the products
     // run on the BF16 MFMA, the output is bf16(sum + bias).
     constexpr bool kBf16 = SAMPLER == kSamplerBf16;
-    extern __shared__ __attribute__((aligned(16))) float red[];  // [NW][NB][64] f32x4
+    extern __shared__ __attribute__((aligned(16))) float red[];  // [NW][NB][64] f32x4, 1 KB slot
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -139,6 +182,14 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
             dx[i] = kBf16 ? load_bf16(orr, dxo) : load_half(orr, dxo);
             m[i] = kBf16 ? load_bf16(mr, mo) : load_half(mr, mo);
         }
+        if constexpr (SAMPLER == kSamplerFast) {
+            // (C2 call 10.3 -> 10.1 us with halo 16 and two loads per wave; halo 12 or 20
+            // and three loads per wave measured slower. The exact sampler loses 0.6 us
+            // with it.)
+            if (sb == s0 && a.pf_halo > 0)
+                warm_band<NW, kNarrowWarmLoads>(a, xr, per_xcd, wave, lane,
+                                                reinterpret_cast<uint8_t*>(red) + NW * NB * 64 * 16);
+        }
         u32x4 q[U][4];
         float ly[U], lx[U];
 #pragma unroll
@@ -162,6 +213,10 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
             q[i][2] = load16(xr, (u + a.Wp) * 16u);
             q[i][3] = load16(xr, (u + a.Wp) * 16u + 16u);
         }
+        // Every corner of the U K-steps is requested before the first blend: left alone,
+        // the scheduler issues the first K-step's corners, waits for them and multiplies
+        // before it requests the rest, a second gather round trip per wave.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < U; ++i) {
             if (sb + i < s1) {  // uniform across the wave
@@ -411,7 +466,7 @@ hipError_t launch_narrow_t(const NarrowArgs& a, hipStream_t stream) {
     // K-steps whose loads are in flight at once, sized to the register budget of
     // NW / 4 waves per SIMD (more output columns hold more weight fragments).
     constexpr int U = NB >= 6 ? (NW == 12 ? 2 : 3) : (NW == 12 ? 3 : 5);
-    const size_t lds = (size_t)NW * NB * 64 * 4 * sizeof(float);
+    const size_t lds = (size_t)NW * NB * 64 * 4 * sizeof(float) + 1024;  // + the warm-up slot
     auto kernel = &narrow_kernel<NB, NW, U, SAMPLER>;
     const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), (int)lds);
     if (attr != hipSuccess) return attr;
@@ -441,6 +496,9 @@ hipError_t launch_narrow_s(const NarrowArgs& a, int nb, int nw, hipStream_t stre
 }
 
 }  // namespace
+
+// Rows each side of a band's receptive field that narrow_kernel's L2 warm-up loads.
+constexpr int kNarrowWarmHalo = 16;
 
 int narrow_ksteps(const FusedGeometry& g) { return (g.kb + 3) / 4; }
 
@@ -493,6 +551,7 @@ hipError_t launch_narrow_f16(const KShape& s, const FusedGeometry& g, const Fuse
     a.magic_cb = magic_for(g.cb);
     a.magic_ka = magic_for(g.ka);
     a.magic_kw = magic_for(s.KW);
+    a.pf_halo = kNarrowWarmHalo;
     // Batches of images whose K range fits three K-steps per wave (the body's 128 -> 64
     // DCN over many tiles): weights stay in registers across the images of a workgroup.
     // From four images on (C3's tiles at batch 2: 19.5 us against 18.6 us for
