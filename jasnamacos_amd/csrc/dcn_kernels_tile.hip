@@ -80,6 +80,12 @@ constexpr int kTileBox = 2 * kTileWaves * 2 * 4;      // [group][wave][min, max]
 constexpr int kTileZero = kTileBuf + kTileOff + kTileBox;  // 32 zero bytes (masked lanes' corners)
 constexpr int kTileLds = kTileZero + 32;               // 79,456 B: two workgroups per CU
 constexpr int kTileMaxSide = 32000;                    // input height / width (16-bit corners)
+constexpr int kTileSlots = 5;                          // weight slots per wave and stage
+// Pair placement: where every wave's stage-0 weight fragments wait in the window buffer
+// (free until stage 0's windows; its first 4 KB hold the waves' estimate channels).
+constexpr int kTilePairB = 14 * 1024;
+static_assert(kTilePairB >= kTileWaves * 1024 && kTilePairB + kTileWaves * kTileSlots * 2 * 1024 <= kTileBuf,
+              "the pair placement's copies fit the window buffer");
 
 struct TileArgs {
     const void* xin;      // CB8 input [B][CBLK][Hp][Wp][8]
@@ -93,7 +99,8 @@ struct TileArgs {
     int G, CBLK, Hp, Wp, Cout;
     float one;  // 1.0f, opaque to the compiler (see coords)
     int tiles_y, tiles_x, tiles;
-    int plan;   // 1: cost-ordered placement of a band's tiles (tile_band_slot) where it applies
+    int plan;   // 1: planned placement of a band's tiles where it applies: cost-ordered
+                // (tile_band_slot, 33-63 tiles) or heavier-of-two first (tile_pair_slot, 64)
     // Per-workgroup clock stamps (diagnostics) or null: workgroup b writes
     // clock[4b .. 4b+3] = {start, end of wave 0, end of wave 1, HW_ID << 32 | XCC_ID << 28 |
     // tile} on the 100 MHz constant clock (s_memrealtime); workgroups without a tile write
@@ -256,7 +263,161 @@ __device__ int tile_band_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr, int
     return min(max(pick, 0), n - 1);
 }
 
-template <int NB, int TW, bool EXACT>
+// LDS DMA of stage st's offsets (channels 36st .. 36st+35) and masks (18st .. 18st+17) of
+// tile (b, ty, tx): 864 chunks of 8 pixels, chunk c -> dst + 16c ([channel][128 px], a
+// channel's pixels row by row). Rows past the map repeat its last row (the clamped pixels
+// read those).
+template <int TW>
+__device__ __forceinline__ void tile_copy_offsets(const TileArgs& a, __amdgpu_buffer_rsrc_t orr,
+                                                  __amdgpu_buffer_rsrc_t mr, int b, int ty, int tx, int st,
+                                                  uint8_t* dst, int wave, int lane) {
+    constexpr int NW = kTileWaves;
+    constexpr int TH = kTilePix / TW;
+    constexpr int kChunksPerCh = kTilePix / 8;  // 16
+    constexpr int kRowChunks = TW / 8;
+    constexpr int kChunks = kTileOffCh * kChunksPerCh;  // 864
+    constexpr int kOffInstr = 36 * kChunksPerCh / 64;   // instructions of the 36 offset channels
+    // Chunk c = 64 i + lane is channel c / 16 = 4 i + lane / 16 at tile position c % 16 =
+    // lane % 16 for every i, so a lane's source only steps by 4 NW channels per
+    // instruction: the address is set up once and then advanced by one add.
+    const int rem = lane % kChunksPerCh;
+    const int y = min(ty * TH + rem / kRowChunks, a.Ho - 1);
+    const int x = tx * TW + (rem % kRowChunks) * 8;
+    const uint32_t pix = (uint32_t)(y * a.Wo + x);
+    const int ch0 = wave * 4 + lane / kChunksPerCh;  // channel of instruction i = wave
+    const uint32_t step = (uint32_t)(4 * NW) * (uint32_t)a.HWo * 2u;
+    // (Modular arithmetic: the mask address is only used once it is past channel 36.)
+    uint32_t off_src = ((uint32_t)(b * 2 * a.G * 9 + 36 * st + ch0) * (uint32_t)a.HWo + pix) * 2u;
+    uint32_t msk_src = ((uint32_t)(b * a.G * 9 + 18 * st + ch0 - 36) * (uint32_t)a.HWo + pix) * 2u;
+    for (int i = wave; i * 64 < kChunks; i += NW) {
+        const bool is_off = i < kOffInstr;  // uniform per instruction
+        if (i * 64 + lane < kChunks) dma16(is_off ? orr : mr, is_off ? off_src : msk_src, dst + i * 64 * 16);
+        off_src += step;
+        msk_src += step;
+    }
+}
+
+// A tile's estimate for the pair placement: the extent of its clamped corner positions
+// (floor of the sample position, clamped like the stage loop's corners) for group 0's
+// centre tap over every pixel, (rows + 3) x (columns + 3). It is the window box of one
+// offset channel pair (the flow part of the offset field is common to all groups and taps,
+// and its residue spans the same range in each). `src` holds stage 0's offset channels 8
+// (dy) and 9 (dx) of the tile, 128 FP16 each in tile_copy_offsets' pixel order; lane l
+// takes pixels l and l + 64, and (row, column) pairs are reduced as 16-bit pairs.
+template <int TW>
+__device__ __forceinline__ int tile_pair_cost(const TileArgs& a, const uint8_t* src_bytes, int ty, int tx,
+                                              int lane) {
+    constexpr int TH = kTilePix / TW;
+    const _Float16* src = reinterpret_cast<const _Float16*>(src_bytes);
+    s16x2 mn = s16x2{SHRT_MAX, SHRT_MAX}, mx = s16x2{SHRT_MIN, SHRT_MIN};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int px = lane + 64 * h;
+        const int oy = min(ty * TH + px / TW, a.Ho - 1);
+        const int ox = min(tx * TW + px % TW, a.Wo - 1);
+        const float y = (float)(oy * a.sh - a.ph + a.dh) + (float)src[px];
+        const float x = (float)(ox * a.sw - a.pw + a.dw) + (float)src[kTilePix + px];
+        const int iy = (int)__builtin_amdgcn_fmed3f(floorf(y), (float)-kPad, (float)a.H);
+        const int ix = (int)__builtin_amdgcn_fmed3f(floorf(x), (float)-kPad, (float)a.W);
+        const s16x2 v = as_s16x2(__builtin_amdgcn_perm((uint32_t)ix, (uint32_t)iy, 0x05040100u));
+        mn = __builtin_elementwise_min(mn, v);
+        mx = __builtin_elementwise_max(mx, v);
+    }
+    // Over the 64 lanes: DPP within each row of 16 (quad_perm [1,0,3,2], [2,3,0,1],
+    // row_half_mirror, row_mirror), then the four rows.
+    auto step = [&](auto ctrl_c) {
+        constexpr int kCtrl = decltype(ctrl_c)::value;
+        mn = __builtin_elementwise_min(mn, as_s16x2(__builtin_amdgcn_update_dpp(0, (int)as_u32(mn), kCtrl, 0xF, 0xF, false)));
+        mx = __builtin_elementwise_max(mx, as_s16x2(__builtin_amdgcn_update_dpp(0, (int)as_u32(mx), kCtrl, 0xF, 0xF, false)));
+    };
+    step(std::integral_constant<int, 0xB1>{});
+    step(std::integral_constant<int, 0x4E>{});
+    step(std::integral_constant<int, 0x141>{});
+    step(std::integral_constant<int, 0x140>{});
+    s16x2 lo = as_s16x2(__builtin_amdgcn_readlane((int)as_u32(mn), 0));
+    s16x2 hi = as_s16x2(__builtin_amdgcn_readlane((int)as_u32(mx), 0));
+#pragma unroll
+    for (int row = 1; row < 4; ++row) {
+        lo = __builtin_elementwise_min(lo, as_s16x2(__builtin_amdgcn_readlane((int)as_u32(mn), 16 * row)));
+        hi = __builtin_elementwise_max(hi, as_s16x2(__builtin_amdgcn_readlane((int)as_u32(mx), 16 * row)));
+    }
+    return ((int)hi.x - (int)lo.x + 3) * ((int)hi.y - (int)lo.y + 3);
+}
+
+// A tile whose estimate exceeds this is likely to have split stages: three quarters of a
+// group's share of the window buffer in 16-byte units (kTileBuf / 2 / 16 = 2048). On C3's
+// inputs (8 seeds, 4096 tiles) every tile with 4 or more split stages estimates 1560 or
+// more, and 95 % of all tiles less than 1520.
+constexpr int kTilePairHeavy = 3 * kTileBuf / 128;
+
+// Placement in a band of exactly 64 tiles: every CU of the XCD runs two workgroups, locals
+// c and c + 32 (c < 32), and the one with the lower blockIdx is dispatched first. The
+// kernel ends with a heavy tile dispatched second; dispatched first, the same tile ends
+// 5-7 us earlier. So locals c and c + 32 run tiles c and c + 32 of the band, swapped when
+// tile c + 32 is heavy (estimate above kTilePairHeavy) and heavier than tile c. Each
+// workgroup copies its own tile's stage-0 offsets to dst0 (the offsets area), and each
+// wave the two tiles' estimate channels to its own 1 KB of the window buffer at dst1 (free
+// until stage 0's windows), so that its own wait suffices, and its stage-0 weight
+// fragments to dst1 + kTilePairB: one wait for all of it, the memory round trip every
+// workgroup makes for stage 0 anyway. Both workgroups estimate both tiles from the same
+// values with the same arithmetic, so they agree. A swapped pair (a few per launch) then
+// fetches the other tile's stage-0 offsets, which its partner has brought into L2.
+// Returns the tile; all threads call it.
+template <int NB, int TW>
+__device__ __forceinline__ int tile_pair_slot(const TileArgs& a, __amdgpu_buffer_rsrc_t orr,
+                                              __amdgpu_buffer_rsrc_t mr, __amdgpu_buffer_rsrc_t wr, int band0,
+                                              int loc, uint8_t* dst0, uint8_t* dst1) {
+    constexpr int TH = kTilePix / TW;
+    constexpr int kRowChunks = TW / 8;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tiles_img = a.tiles_y * a.tiles_x;
+    int b[2], ty[2], tx[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // k = 0: tile c, 1: tile c + 32
+        const int t = band0 + (loc & 31) + 32 * k;
+        b[k] = t / tiles_img;
+        const int r = t - b[k] * tiles_img;
+        ty[k] = r / a.tiles_x;
+        tx[k] = r - ty[k] * a.tiles_x;
+    }
+    const int mine = loc < 32 ? 0 : 1;
+    tile_copy_offsets<TW>(a, orr, mr, b[mine], ty[mine], tx[mine], 0, dst0, wave, lane);
+    // Estimate channels: lane l copies 8 pixels (chunk l % 16) of channel 8 + (l / 16) % 2 of
+    // tile l / 32 to slot + 16 l, i.e. [tile][channel][128 px].
+    uint8_t* slot = dst1 + wave * 1024;
+    {
+        const int k = lane / 32, rem = lane % 16, ch = 8 + (lane / 16) % 2;
+        const int bk = k ? b[1] : b[0], tyk = k ? ty[1] : ty[0], txk = k ? tx[1] : tx[0];
+        const int y = min(tyk * TH + rem / kRowChunks, a.Ho - 1);
+        const int x = txk * TW + (rem % kRowChunks) * 8;
+        dma16(orr, ((uint32_t)(bk * 2 * a.G * 9 + ch) * (uint32_t)a.HWo + (uint32_t)(y * a.Wo + x)) * 2u, slot);
+    }
+    // The wave's stage-0 weight slots as the stage loop numbers them (taps 0-3 and the
+    // centre tap for waves 0-1, taps 5-8 and the centre tap for waves 2-3), to dst1 +
+    // kTilePairB, where the stage loop's prologue reads them.
+#pragma unroll
+    for (int s = 0; s < kTileSlots; ++s) {
+        const int tap = s == 4 ? 4 : (wave < 2 ? 0 : 5) + s;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+            dma16(wr, (uint32_t)((tap * NB + nb) * 64 + lane) * 16u,
+                  dst1 + kTilePairB + ((wave * kTileSlots + s) * NB + nb) * 1024);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies
+    const int c0 = tile_pair_cost<TW>(a, slot, ty[0], tx[0], lane);
+    const int c1 = tile_pair_cost<TW>(a, slot + 2 * kTilePix * 2, ty[1], tx[1], lane);
+    const int own = band0 + loc;
+    if (!(c1 > kTilePairHeavy && c1 > c0)) return own;
+    __syncthreads();  // (uniform) every wave's copy of its own tile's offsets is done
+    const int other = 1 - mine;
+    tile_copy_offsets<TW>(a, orr, mr, b[other], ty[other], tx[other], 0, dst0, wave, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    return band0 + (loc ^ 32);
+}
+
+template <int NB, int TW, bool EXACT, bool PAIR>
 __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     constexpr int NW = kTileWaves;
     constexpr int RPW = 32 / TW;  // tile rows per 32-pixel segment
@@ -284,9 +445,17 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     unsigned long long* const clock = a.clock ? a.clock + 4 * (size_t)blockIdx.x : nullptr;
     if (clock && tid == 0) clock[0] = __builtin_amdgcn_s_memrealtime();
     const __amdgpu_buffer_rsrc_t orr = make_rsrc(a.off, a.off_bytes);
-    const int tile = band0 + (a.plan && band_n > 32 && band_n < 64
-                                  ? tile_band_slot<TW>(a, orr, band0, band_n, loc, reinterpret_cast<float*>(lds))
-                                  : loc);
+    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
+    // Bands of exactly 64 tiles (the PAIR instantiation): the pair placement, which also
+    // leaves stage 0's offsets in the offsets area and this wave's stage-0 weight fragments
+    // in the window buffer.
+    const bool pair_plan = PAIR && a.plan && band_n == 64;
+    const int tile = pair_plan ? tile_pair_slot<NB, TW>(a, orr, mr, wr, band0, loc, offs, lds)
+                               : band0 + (a.plan && band_n > 32 && band_n < 64
+                                              ? tile_band_slot<TW>(a, orr, band0, band_n, loc,
+                                                                   reinterpret_cast<float*>(lds))
+                                              : loc);
     if (clock && tid == 0) {  // HW_ID: wave, SIMD, CU, shader array and engine; XCC_ID: the XCD
         const uint32_t hw = (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4);
         const uint32_t xcc = (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 20) & 15u;
@@ -299,8 +468,6 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
     const int tx = trem - ty * a.tiles_x;
 
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xin, a.xin_bytes);
-    const __amdgpu_buffer_rsrc_t mr = make_rsrc(a.msk, a.msk_bytes);
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.wpk, a.wpk_bytes);
     const int stages = a.G / 2;
 
     // Pixel of this lane in segment s (tile rows (2 * pblk + s) * RPW ..): lanes past the
@@ -330,33 +497,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
             ybf[s][t] = (float)(ybi[s] + t * a.dh);
             xbf[s][t] = (float)(xbi[s] + t * a.dw);
         }
-    // LDS DMA of stage st's offsets (channels 36st .. 36st+35) and masks (18st .. 18st+17)
-    // of the tile: 864 chunks of 8 pixels, chunk c -> LDS offs + 16c ([channel][128 px]).
-    // Rows past the map repeat its last row (the clamped pixels read those).
-    auto copy_offsets = [&](int st) {
-        constexpr int kChunksPerCh = kTilePix / 8;  // 16
-        constexpr int kRowChunks = TW / 8;
-        constexpr int kChunks = kTileOffCh * kChunksPerCh;  // 864
-        constexpr int kOffInstr = 36 * kChunksPerCh / 64;   // instructions of the 36 offset channels
-        // Chunk c = 64 i + lane is channel c / 16 = 4 i + lane / 16 at tile position c % 16 =
-        // lane % 16 for every i, so a lane's source only steps by 4 NW channels per
-        // instruction: the address is set up once and then advanced by one add.
-        const int rem = lane % kChunksPerCh;
-        const int y = min(ty * TH + rem / kRowChunks, a.Ho - 1);
-        const int x = tx * TW + (rem % kRowChunks) * 8;
-        const uint32_t pix = (uint32_t)(y * a.Wo + x);
-        const int ch0 = wave * 4 + lane / kChunksPerCh;  // channel of instruction i = wave
-        const uint32_t step = (uint32_t)(4 * NW) * (uint32_t)a.HWo * 2u;
-        // (Modular arithmetic: the mask address is only used once it is past channel 36.)
-        uint32_t off_src = ((uint32_t)(b * 2 * a.G * 9 + 36 * st + ch0) * (uint32_t)a.HWo + pix) * 2u;
-        uint32_t msk_src = ((uint32_t)(b * a.G * 9 + 18 * st + ch0 - 36) * (uint32_t)a.HWo + pix) * 2u;
-        for (int i = wave; i * 64 < kChunks; i += NW) {
-            const bool is_off = i < kOffInstr;  // uniform per instruction
-            if (i * 64 + lane < kChunks) dma16(is_off ? orr : mr, is_off ? off_src : msk_src, offs + i * 64 * 16);
-            off_src += step;
-            msk_src += step;
-        }
-    };
+    auto copy_offsets = [&](int st) { tile_copy_offsets<TW>(a, orr, mr, b, ty, tx, st, offs, wave, lane); };
 
     // Window geometry of a stage (wave-uniform): origin, size in units, LDS placement.
     struct Win {
@@ -447,7 +588,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         constexpr int TF = decltype(tf_c)::value;
         constexpr int SODD = decltype(sodd_c)::value;
         constexpr int NSMP = 9;   // samples per lane and stage
-        constexpr int NSLOT = 5;  // weight slots
+        constexpr int NSLOT = kTileSlots;  // weight slots
         auto tap_of = [](int j) { return j == 8 ? 4 : TF + j / 2; };
         auto seg_of = [](int j) { return j == 8 ? SODD : j % 2; };
         auto slot_of = [](int j) { return j == 8 ? 4 : j / 2; };
@@ -641,8 +782,18 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void tile_kernel(TileArgs a) {
         // ---- prologue: stage 0's offsets, coordinates, windows and addresses ----
         Samples ca, cb;
 #pragma unroll
-        for (int slot = 0; slot < NSLOT; ++slot) load_b(0, slot);
-        copy_offsets(0);
+        for (int slot = 0; slot < NSLOT; ++slot) {
+            if (pair_plan) {  // the pair placement's copy (its wait is done)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    Bq[slot][nb] = __builtin_bit_cast(
+                        h8, *reinterpret_cast<const u32x4*>(lds + kTilePairB + ((wave * NSLOT + slot) * NB + nb) * 1024 +
+                                                            lane * 16));
+            } else {
+                load_b(0, slot);
+            }
+        }
+        if (!pair_plan) copy_offsets(0);
         if (tid < 8) reinterpret_cast<uint32_t*>(lds + kTileZero)[tid] = 0u;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();  // stage 0's offsets in LDS; the zero bytes
@@ -767,14 +918,22 @@ __global__ __launch_bounds__(256) void tile_prepack_kernel(const uint16_t* __res
     wpk[gid] = v;
 }
 
-template <int NB, int TW, bool EXACT>
-hipError_t launch_tile_t(const TileArgs& a, hipStream_t stream) {
-    auto kernel = &tile_kernel<NB, TW, EXACT>;
+template <int NB, int TW, bool EXACT, bool PAIR>
+hipError_t launch_tile_p(const TileArgs& a, hipStream_t stream) {
+    auto kernel = &tile_kernel<NB, TW, EXACT, PAIR>;
     const hipError_t attr = allow_dynamic_lds(reinterpret_cast<const void*>(kernel), kTileLds);
     if (attr != hipSuccess) return attr;
     const unsigned grid = (unsigned)(((a.tiles + 7) / 8) * 8);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kTileWaves), kTileLds, stream, a);
     return hipGetLastError();
+}
+
+// The pair placement's instantiation where the planned placement has bands of exactly 64
+// tiles (every CU of an XCD runs two); every other shape runs the kernel without it.
+template <int NB, int TW, bool EXACT>
+hipError_t launch_tile_t(const TileArgs& a, hipStream_t stream) {
+    return a.plan && (a.tiles + 7) / 8 == 64 ? launch_tile_p<NB, TW, EXACT, true>(a, stream)
+                                             : launch_tile_p<NB, TW, EXACT, false>(a, stream);
 }
 
 template <int TW>
