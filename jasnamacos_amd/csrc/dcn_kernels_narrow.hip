@@ -259,10 +259,11 @@ __global__ __launch_bounds__(64 * NW) void narrow_kernel(NarrowArgs a) {
         if (!a.out_cb8 && a.HWo % 16 == 0 && ((uintptr_t)a.out & 7) == 0) {
             // NCHW planes of a multiple of 16 pixels: every tile is whole and inside one
             // image, so the lane's four pixels are consecutive in the plane (8-byte aligned
-            // on an 8-byte aligned output): one 8-byte store.
+            // on an 8-byte aligned output): one 8-byte store. Pixel pe of the tile is pixel
+            // sp0 + pe of image p0 / HWo.
             const int pe = 4 * (lane >> 4);
-            const uint32_t pix = (uint32_t)__shfl((int)pix_out, pe);
-            const int pb = __shfl(b, pe);
+            const uint32_t pix = (uint32_t)(sp0 + pe);
+            const int pb = p0 / a.HWo;
             uint2 w;
             w.x = bits(sum[0] + bias) | (bits(sum[1] + bias) << 16);
             w.y = bits(sum[2] + bias) | (bits(sum[3] + bias) << 16);
