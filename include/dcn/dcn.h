@@ -283,8 +283,9 @@ dcn_status dcn_forward_f16_prepacked_noalloc_dev(dcn_context* ctx, const dcn_sha
  * gathers for a stage whose windows do not fit (3x3 kernels, 8 channels per group, an
  * even group count, Cout 32 or 64, input sides up to 32000; ks = 8: the tiles of an
  * XCD's band are placed on its CUs by estimated cost where some CUs run one tile and
- * others two (33-63 tiles per band), ks = 1: fixed placement; the outputs are the same
- * bits either way; the automatic choice for problems of more than 1024 tiles of 32
+ * others two (33-63 tiles per band), and where every CU runs two (64 tiles per band) a
+ * heavy tile goes to the slot dispatched first; ks = 1: fixed placement; the outputs are
+ * the same bits either way; the automatic choice for problems of more than 1024 tiles of 32
  * pixels, with either sampler). sampler: 0 = reference arithmetic
  * (FP32 bilinear in the reference's association, half(sampled*mask): the im2col
  * values of deform_conv2d_fp16_jasna_gather bit for bit), 1 = fast (mask folded into
