@@ -724,6 +724,68 @@ def test_tile_clock_stamps_every_tile(gpu_ctx, dcn, batch, h, w, cout, tw):
     assert np.array_equal(np.sort(tile_ids), np.arange(tiles))
 
 
+def test_tile_pair_placement_runs_heavy_tiles_first(gpu_ctx, dcn):
+    """Bands of exactly 64 tiles (C3's 16 maps of 64 x 64): locals c and c + 32 share a CU
+    and c is dispatched first, so a heavy tile c + 32 (window-box estimate of group 0's
+    centre tap above three quarters of a group's buffer share) is swapped into local c.
+    Planted: a few tiles whose estimate channels (offset channels 8, 9) spread +-32 px
+    (estimates 2205-3283 on the host) while every other offset stays within +-1 px (at most
+    228). The clock records show each heavy second-slot
+    tile run by local c and its light partner by local c + 32, a heavy tile already in a
+    first slot left where it is, every other tile in its natural slot, and the output equal
+    to the fixed placement's bit for bit."""
+    import torch
+
+    s = dcn.DeformConvShape(16, 128, 64, 64, 64, 64, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 16)
+    tiles, grid = 512, 512  # 8 x 16 tiles, 32 per map, bands of 64
+    rng = np.random.default_rng(64)
+    c = s.counts()
+    off = rng.uniform(-1, 1, (16, 288, 64, 64))
+    heavy = [40, 100, 300, 455]  # band-local 40, 36, 44 (second slots) and 7 (a first slot)
+    for t in heavy:
+        b, r = divmod(t, 32)
+        ty, tx = divmod(r, 4)
+        off[b, 8:10, ty * 8:(ty + 1) * 8, tx * 16:(tx + 1) * 16] = rng.uniform(-32, 32, (2, 8, 16))
+    h16 = {"input": rng.standard_normal(c["input"]).astype(np.float16),
+           "offset": off.reshape(-1).astype(np.float16),
+           "mask": rng.random(c["mask"]).astype(np.float16),
+           "weight": (rng.standard_normal(c["weight"]) * 0.03).astype(np.float16),
+           "bias": (rng.standard_normal(64) * 0.1).astype(np.float16)}
+    log("case: tile pair placement, heavy tiles", heavy)
+    dev = {k: _dev(torch, h16[k].view(np.int16)) for k in ("input", "offset", "mask", "weight", "bias")}
+    out = torch.empty(c["output"], dtype=torch.int16, device="cuda")
+    packed = gpu_ctx.prepack_dev(s, dev["weight"], dev["bias"])
+    gpu_ctx.reserve(s)
+    clock = torch.zeros(4 * grid, dtype=torch.int64, device="cuda")
+    try:
+        gpu_ctx.set_fused_config(16, 1, -1, 7)
+        gpu_ctx.forward_f16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out)
+        torch.cuda.synchronize()
+        fixed = out.clone()
+        out.zero_()
+        gpu_ctx.set_fused_config(16, 8, -1, 7)
+        assert gpu_ctx.get_fused_config(s) == {"variant": 7, "mt": 16, "ks": 8, "sampler": 1}
+        gpu_ctx.set_tile_clock_dev(clock)
+        gpu_ctx.forward_f16_prepacked_dev(s, dev["input"], dev["offset"], dev["mask"], packed, out)
+        torch.cuda.synchronize()
+    finally:
+        gpu_ctx.set_tile_clock_dev(None)
+        gpu_ctx.set_fused_config(0, 0, -1, 0)
+    assert torch.equal(out, fixed)
+    rec = clock.cpu().numpy().view(np.uint64).reshape(grid, 4)
+    ran = (rec[:, 3] & np.uint64(0x0FFFFFFF)).astype(np.int64)  # the tile workgroup b ran
+    blocks = np.arange(grid)
+    natural = (blocks % 8) * 64 + blocks // 8
+    assert np.array_equal(np.sort(ran), np.arange(tiles))
+    want = natural.copy()
+    for t in heavy:
+        band, cl = divmod(t, 64)
+        if cl >= 32:  # swapped with the light tile band * 64 + cl - 32
+            want[(cl - 32) * 8 + band] = t
+            want[cl * 8 + band] = t - 32
+    assert np.array_equal(ran, want), [(int(b), int(ran[b]), int(want[b])) for b in np.nonzero(ran != want)[0][:8]]
+
+
 TILE_EDGE_SHAPES = [
     # (batch, Cin, H, W, Cout, Ho, Wo, Kh, Kw, ph, pw, sh, sw, dh, dw, groups, offset_groups)
     (1, 16, 13, 40, 32, 13, 40, 3, 3, 1, 1, 1, 1, 1, 1, 1, 2),   # Wo % 16 != 0, H % 8 != 0, Cout 32 (NB 1)
