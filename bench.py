@@ -35,7 +35,8 @@ Diagnostics (one JSON line each, instead of the bench line): --launch-floor (emp
 kernels of the fused kernels' launch shapes in a hipGraph), --gather (the reference's
 gather phase alone, im2col to HBM, at C2) and --tile-clock (configs 3, 5: the tile
 kernel's per-workgroup start/end stamps, so the spread of workgroup times behind the
-kernel's duration).
+kernel's duration). --seed-sweep N runs the bench at input seeds 0 .. N-1 and reports
+the per-seed times and their spread (the C3/C5 kernel times depend on the offset field).
 """
 from __future__ import annotations
 
@@ -893,6 +894,52 @@ def bench_gather(args) -> int:
     return 0
 
 
+def seed_sweep(args) -> int:
+    """--seed-sweep N: the bench of config 2, 3 or 5 at input seeds 0 .. N-1, each in a child
+    process (this process never touches the GPU), without the CPU baseline or the cold
+    calls. The seed changes the offset field and with it the tile kernel's windows, so the
+    C3/C5 kernel times depend on it. Prints one JSON line: each seed's call and kernel
+    times (and the exact sampler's kernel time for FP16) and their mean, min and max."""
+    import subprocess
+
+    if args.config not in (2, 3, 5) or args.spynet or args.seed_sweep < 1:
+        print("--seed-sweep N (N >= 1) sweeps configs 2, 3 and 5", file=sys.stderr)
+        return 2
+    passthrough = ["--config", str(args.config), "--steps", str(args.steps), "--warmup", str(args.warmup),
+                   "--kernel-reps", str(args.kernel_reps), "--dtype", args.dtype, "--no-cpu-baseline",
+                   "--cold-calls", "0"]
+    for flag in ("variant", "mt", "ks"):
+        if getattr(args, flag):
+            passthrough += [f"--{flag}", str(getattr(args, flag))]
+    rows = []
+    for seed in range(args.seed_sweep):
+        r = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--seed", str(seed), *passthrough],
+                           capture_output=True, text=True)
+        lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+        if r.returncode != 0 or not lines:
+            print(f"seed {seed}: bench.py exited {r.returncode}\n{r.stderr[-2000:]}", file=sys.stderr)
+            return r.returncode or 1
+        d = json.loads(lines[-1])
+        row = {"seed": seed, "us_per_call": round(d["ms_per_step"] * 1e3, 3), "kernel_us": round(d["kernel_us"], 3)}
+        if d.get("exact_kernel_us"):
+            row["exact_kernel_us"] = round(d["exact_kernel_us"], 3)
+        rows.append(row)
+        print(f"seed {seed}: {row}", file=sys.stderr, flush=True)
+
+    def summary(key):
+        v = [r[key] for r in rows if key in r]
+        return {"mean": round(statistics.mean(v), 3), "min": min(v), "max": max(v)} if v else None
+
+    print(json.dumps({"metric": "DCNv2 fwd us/call and fused kernel us over input seeds", "unit": "us",
+                      "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": False,
+                      "data": "synthetic (dcn_generate_config_inputs at each seed)",
+                      "config": {"workload": WORKLOADS[args.config], "dtype": args.dtype,
+                                 "seeds": list(range(args.seed_sweep))},
+                      "per_seed": rows, "us_per_call": summary("us_per_call"), "kernel_us": summary("kernel_us"),
+                      "exact_kernel_us": summary("exact_kernel_us")}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -925,6 +972,9 @@ def main() -> int:
     ap.add_argument("--clock-runs", type=int, default=5, help="--tile-clock: runs of 10 launches")
     ap.add_argument("--clock-dump", default="",
                     help="--tile-clock: also save every run's raw records to this .npy file")
+    ap.add_argument("--seed-sweep", type=int, default=0,
+                    help="configs 2, 3, 5: run the bench at input seeds 0 .. N-1 (one child process "
+                         "each) and print the per-seed and mean/min/max kernel and call times")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, run three device copies of this many MiB (the known-size "
                          "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -937,6 +987,8 @@ def main() -> int:
     if args.steps < 1:
         print("--steps must be >= 1", file=sys.stderr)
         return 2
+    if args.seed_sweep:
+        return seed_sweep(args)
     bf16 = args.dtype == "bf16"
     if bf16 and (args.spynet or args.config in (1, 4) or args.variant or args.mt or args.ks):
         print("--dtype bf16 measures the BF16 fused forward of configs 2, 3 and 5 (its automatic "

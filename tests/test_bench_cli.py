@@ -21,3 +21,14 @@ def test_bench_rejects_zero_steps():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--steps", "0"], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 2
+
+
+def test_bench_seed_sweep_rejects_other_configs():
+    """--seed-sweep covers the fused configs 2, 3 and 5; other configs are refused before
+    any child process starts."""
+    for extra in (["--config", "4"], ["--config", "1"], ["--spynet"]):
+        r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--seed-sweep", "2", *extra],
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode == 2, extra
+        assert "--seed-sweep" in r.stderr
+        assert r.stdout.strip() == ""
